@@ -1,0 +1,101 @@
+/*
+ * qvh — the C-ABI between Quiver's C++ indexes and the gfx950 (MI355X) kernels.
+ *
+ * This is the drop-in boundary: the host C++ classes (quiver::FlatIndex, quiver::IvfPqIndex,
+ * quiver_amd/csrc/host/) keep the reference's public API and call these functions where the
+ * reference runs its CPU scan loops. Only plain pointers and sizes cross it; no exceptions, no
+ * C++ or torch types. Every function returns QVH_OK (0) or a negative status; the message of the
+ * last failure on the calling thread is qvh_last_error().
+ *
+ * Conventions kept from the reference (include/quiver/common.h:25-29, flat_index.h:30-36):
+ *   metric 0 = squared L2, 1 = inner product (distance 1 - <q,x>), 2 = cosine (1 - cos; rows and
+ *   queries unit-normalized exactly as simd::normalize does, src/simd/dispatch.cc:119-135);
+ *   results are ascending by distance; empty slots carry row/ref "all ones" and +infinity.
+ * Ties between exactly equal distances are broken by the smaller row (or list ref); the reference
+ * leaves that order to libstdc++ heap internals (src/internal/search_util.h:26-28).
+ *
+ * "Host" entry points take host buffers and return after the results are in host memory.
+ * "_device" entry points take device pointers and enqueue on `stream` (NULL = the handle's own
+ * stream) without synchronizing. Calls on one handle are serialized internally; distinct
+ * handles may be used from distinct threads concurrently.
+ */
+#ifndef QVH_H_
+#define QVH_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int qvh_status;
+#define QVH_OK 0
+#define QVH_EINVAL (-22)   /* bad argument (the reference throws quiver::Error for these) */
+#define QVH_ENOMEM (-12)   /* device allocation failed */
+#define QVH_EDEVICE (-5)   /* no usable HIP device, or a HIP runtime failure */
+#define QVH_EUNSUPPORTED (-95)
+
+#define QVH_METRIC_L2 0
+#define QVH_METRIC_IP 1
+#define QVH_METRIC_COSINE 2
+
+#define QVH_EMPTY_ROW 0xFFFFFFFFu
+#define QVH_EMPTY_REF 0xFFFFFFFFFFFFFFFFull
+
+typedef struct qvh_flat qvh_flat;
+typedef struct qvh_ivfpq qvh_ivfpq;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* qvh_last_error(void);
+
+/* Selects and initializes the HIP device used by handles created afterwards on this thread's
+ * process (default: device 0, initialized on first use). Fails with QVH_EDEVICE when no gfx950
+ * device is present. */
+qvh_status qvh_init(int device);
+
+/* Writes the device name and the gfx target (e.g. "gfx950") into caller buffers. */
+qvh_status qvh_device_info(char* name, size_t name_len, char* arch, size_t arch_len,
+                           int* compute_units);
+
+/* Unit-normalizes n rows of `dim` floats in place, bit-identical to the reference's
+ * simd::normalize with the AVX2 kernels (src/simd/dispatch.cc:119-135,
+ * src/simd/kernels_avx2.cc:58-83). Host buffers. */
+qvh_status qvh_normalize(float* rows, uint64_t n, uint32_t dim);
+
+/* ------------------------------------------------------------------------------------------ *
+ * Flat exact search: replaces the per-query scan of FlatIndex::search_one
+ * (src/flat_index.cc:69-107) under FlatIndex::search_batch (src/flat_index.cc:126-140).
+ * ------------------------------------------------------------------------------------------ */
+
+/* FlatIndex(dim, metric) (src/flat_index.cc:41-47): an empty device-resident row store. */
+qvh_status qvh_flat_create(uint32_t dim, int metric, qvh_flat** out);
+void qvh_flat_destroy(qvh_flat* flat);
+
+/* The append step of FlatIndex::add (src/flat_index.cc:62-65): copies n rows to the device
+ * (normalizing them for cosine). `stored_out` (nullable, n*dim floats) receives the rows as
+ * stored, i.e. normalized for cosine, for the host copy the C++ class keeps. */
+qvh_status qvh_flat_append(qvh_flat* flat, const float* rows, uint64_t n, float* stored_out);
+
+/* Number of stored rows. */
+uint64_t qvh_flat_size(const qvh_flat* flat);
+
+/* The scan of FlatIndex::search_batch (src/flat_index.cc:84-106) for nq raw queries (normalized
+ * here for cosine, as search_one does at :74-78). `row_bitmap` (nullable, ceil(size/64) words,
+ * bit r of word r/64 set = row r admitted) is the Filter materialized over rows (:85).
+ * Outputs: nq*k rows (QVH_EMPTY_ROW when fewer than k rows are admitted) and distances (+inf). */
+qvh_status qvh_flat_search(qvh_flat* flat, const float* queries, uint64_t nq, uint32_t k,
+                           const uint64_t* row_bitmap, uint32_t* out_rows, float* out_dist);
+
+/* Same, on device-resident buffers, enqueued on `stream` (a hipStream_t; NULL = the handle's). */
+qvh_status qvh_flat_search_device(qvh_flat* flat, const float* d_queries, uint64_t nq,
+                                  uint32_t k, const uint64_t* d_row_bitmap, uint32_t* d_out_rows,
+                                  float* d_out_dist, void* stream);
+
+/* Synchronizes the handle's stream. */
+qvh_status qvh_flat_sync(qvh_flat* flat);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QVH_H_ */

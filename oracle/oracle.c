@@ -348,32 +348,41 @@ int orc_flat_search(const float* base, size_t n, size_t dim, int metric, const f
   const int l2 = metric == ORC_L2;
   const int nt = nthreads_or_max(nthreads);
   const size_t cap = k < n ? k : n;
+  enum { QB = 16 }; /* queries per pass over the rows (each query still sees rows in order) */
+  const size_t nblocks = (nq + QB - 1) / QB;
 #pragma omp parallel num_threads(nt)
   {
-    cand* heap = (cand*)malloc(sizeof(cand) * (cap + 1));
-    float* qbuf = (float*)malloc(sizeof(float) * dim);
+    cand* heaps = (cand*)malloc(sizeof(cand) * (cap + 1) * QB);
+    size_t sizes[QB];
+    float* qbuf = (float*)malloc(sizeof(float) * dim * QB);
 #pragma omp for schedule(dynamic, 1)
-    for (size_t qi = 0; qi < nq; ++qi) {
-      const float* q = queries + qi * dim;
-      if (metric == ORC_COSINE) { /* src/flat_index.cc:74-78 */
-        memcpy(qbuf, q, sizeof(float) * dim);
-        normalize_one(qbuf, dim);
-        q = qbuf;
+    for (size_t blk = 0; blk < nblocks; ++blk) {
+      const size_t q0 = blk * QB, nb = nq - q0 < QB ? nq - q0 : QB;
+      for (size_t b = 0; b < nb; ++b) {
+        memcpy(qbuf + b * dim, queries + (q0 + b) * dim, sizeof(float) * dim);
+        if (metric == ORC_COSINE) normalize_one(qbuf + b * dim, dim); /* src/flat_index.cc:74-78 */
+        sizes[b] = 0;
       }
-      size_t size = 0;
       for (size_t i = 0; i < n; ++i) { /* src/flat_index.cc:84-96 */
         if (row_bitmap && !bit_set(row_bitmap, i)) continue;
-        const cand c = {flat_dist(q, base + i * dim, dim, l2), i};
-        topk_push(heap, &size, cap, c);
+        const float* x = base + i * dim;
+        for (size_t b = 0; b < nb; ++b) {
+          const cand c = {flat_dist(qbuf + b * dim, x, dim, l2), i};
+          topk_push(heaps + b * (cap + 1), &sizes[b], cap, c);
+        }
       }
-      qsort(heap, size, sizeof(cand), cand_cmp); /* src/flat_index.cc:97 */
-      for (size_t j = 0; j < k; ++j) {
-        out_rows[qi * k + j] = j < size ? (uint32_t)heap[j].id : UINT32_MAX;
-        out_dist[qi * k + j] = j < size ? heap[j].d : INFINITY;
+      for (size_t b = 0; b < nb; ++b) {
+        cand* heap = heaps + b * (cap + 1);
+        const size_t qi = q0 + b;
+        qsort(heap, sizes[b], sizeof(cand), cand_cmp); /* src/flat_index.cc:97 */
+        for (size_t j = 0; j < k; ++j) {
+          out_rows[qi * k + j] = j < sizes[b] ? (uint32_t)heap[j].id : UINT32_MAX;
+          out_dist[qi * k + j] = j < sizes[b] ? heap[j].d : INFINITY;
+        }
       }
     }
     free(qbuf);
-    free(heap);
+    free(heaps);
   }
   return 0;
 }

@@ -1,0 +1,119 @@
+// Internal helpers shared by the qvh translation units: error propagation across the C-ABI,
+// device selection, growable device buffers, and small device utilities.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <stdexcept>
+#include <string>
+
+#include "qvh.h"
+
+namespace qvh {
+
+/// A failure carried to the C-ABI boundary as (status, message).
+struct Failure : std::runtime_error {
+  int status;
+  Failure(int s, const std::string& m) : std::runtime_error(m), status(s) {}
+};
+
+void set_last_error(const std::string& msg);
+
+#define QVH_HIP(call)                                                                       \
+  do {                                                                                      \
+    const hipError_t qvh_e_ = (call);                                                       \
+    if (qvh_e_ != hipSuccess) {                                                             \
+      throw ::qvh::Failure(qvh_e_ == hipErrorOutOfMemory ? QVH_ENOMEM : QVH_EDEVICE,        \
+                           std::string(#call) + ": " + hipGetErrorString(qvh_e_));          \
+    }                                                                                       \
+  } while (0)
+
+#define QVH_REQUIRE(cond, msg)                                   \
+  do {                                                           \
+    if (!(cond)) throw ::qvh::Failure(QVH_EINVAL, (msg));        \
+  } while (0)
+
+/// Runs `f`, mapping every exception to a status code and qvh_last_error().
+template <class F>
+int guarded(F&& f) noexcept {
+  try {
+    f();
+    return QVH_OK;
+  } catch (const Failure& e) {
+    set_last_error(e.what());
+    return e.status;
+  } catch (const std::bad_alloc&) {
+    set_last_error("host allocation failed");
+    return QVH_ENOMEM;
+  } catch (const std::exception& e) {
+    set_last_error(e.what());
+    return QVH_EDEVICE;
+  } catch (...) {
+    set_last_error("unknown failure");
+    return QVH_EDEVICE;
+  }
+}
+
+/// The device chosen by qvh_init (initialized on first use). Throws Failure(QVH_EDEVICE) when
+/// there is no gfx950 device.
+int current_device();
+
+/// Device allocation that honours the QVH_FAULT_ALLOC fault hook (see core.hip): the N-th
+/// allocation of the process fails with QVH_ENOMEM when QVH_FAULT_ALLOC=N is set.
+void* device_alloc(size_t bytes);
+void device_free(void* p) noexcept;
+
+/// A device buffer that only grows; contents are not preserved by reserve().
+struct DeviceBuffer {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  DeviceBuffer() = default;
+  DeviceBuffer(const DeviceBuffer&) = delete;
+  DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+  ~DeviceBuffer() { device_free(ptr); }
+  void* reserve(size_t want) {
+    if (want > bytes) {
+      device_free(ptr);
+      ptr = nullptr;
+      bytes = 0;
+      ptr = device_alloc(want);
+      bytes = want;
+    }
+    return ptr;
+  }
+  template <class T>
+  T* as() const { return static_cast<T*>(ptr); }
+};
+
+__host__ __device__ inline uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+
+// ---- device utilities ------------------------------------------------------------------------
+
+/// Monotone map from float to uint32 (a < b as floats <=> map(a) < map(b) for non-NaN values),
+/// so (distance, id) pairs order lexicographically as one 64-bit key.
+__device__ __forceinline__ uint32_t float_to_ordered(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float ordered_to_float(uint32_t o) {
+  return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
+}
+__device__ __forceinline__ uint64_t make_key(float d, uint32_t id) {
+  return (static_cast<uint64_t>(float_to_ordered(d)) << 32) | id;
+}
+
+/// Wave-wide (64 lanes) minimum of a 64-bit key.
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint64_t o = __shfl_xor(v, off, 64);
+    v = o < v ? o : v;
+  }
+  return v;
+}
+
+}  // namespace qvh

@@ -1,0 +1,118 @@
+// Device restatements of the reference's x86-64 float arithmetic, bit for bit.
+//
+// The reference's flat scan, refine and normalize use its AVX2+FMA kernels
+// (src/simd/kernels_avx2.cc:35-83, chosen by src/simd/dispatch.cc:108-117 on any x86-64 CPU with
+// AVX2 and FMA). Their reduction order is: four 8-lane FMA accumulators over blocks of 32
+// elements, an 8-wide loop into the first accumulator, the horizontal sum
+// ((s0+s1)+(s2+s3)) -> lo[j] = v[j]+v[j+4] -> (lo0+lo1)+(lo2+lo3), then a scalar tail of fewer
+// than 8 elements which GCC 11 -O3 compiles as: the first four products separately rounded and
+// added in order, the remaining ones fused. One GPU thread replays that sequence exactly.
+//
+// All qvh sources are compiled with -ffp-contract=off, so every a*b+c written here is two
+// roundings; fused steps are explicit fmaf().
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace qvh {
+
+__device__ __forceinline__ float avx2_reduce(const float (&s)[4][8]) {
+  float v[8];
+#pragma unroll
+  for (int l = 0; l < 8; ++l) v[l] = (s[0][l] + s[1][l]) + (s[2][l] + s[3][l]);
+  float lo[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) lo[j] = v[j] + v[j + 4];
+  return (lo[0] + lo[1]) + (lo[2] + lo[3]);
+}
+
+/// sum_i (a_i - b_i)^2 in the order of src/simd/kernels_avx2.cc:35-56.
+__device__ inline float exact_l2sqr(const float* __restrict__ a, const float* __restrict__ b,
+                                    uint32_t dim) {
+  float s[4][8];
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+#pragma unroll
+    for (int l = 0; l < 8; ++l) s[u][l] = 0.0f;
+  uint32_t i = 0;
+  for (; i + 32 <= dim; i += 32) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int l = 0; l < 8; ++l) {
+        const float d = a[i + 8 * u + l] - b[i + 8 * u + l];
+        s[u][l] = fmaf(d, d, s[u][l]);
+      }
+  }
+  for (; i + 8 <= dim; i += 8) {
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+      const float d = a[i + l] - b[i + l];
+      s[0][l] = fmaf(d, d, s[0][l]);
+    }
+  }
+  float sum = avx2_reduce(s);
+  const uint32_t v4 = i + (dim - i) / 4 * 4;
+  for (; i < v4; ++i) {
+    const float d = a[i] - b[i];
+    sum = sum + d * d;
+  }
+  for (; i < dim; ++i) {
+    const float d = a[i] - b[i];
+    sum = fmaf(d, d, sum);
+  }
+  return sum;
+}
+
+/// sum_i a_i * b_i in the order of src/simd/kernels_avx2.cc:58-83.
+__device__ inline float exact_dot(const float* __restrict__ a, const float* __restrict__ b,
+                                  uint32_t dim) {
+  float s[4][8];
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+#pragma unroll
+    for (int l = 0; l < 8; ++l) s[u][l] = 0.0f;
+  uint32_t i = 0;
+  for (; i + 32 <= dim; i += 32) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int l = 0; l < 8; ++l) s[u][l] = fmaf(a[i + 8 * u + l], b[i + 8 * u + l], s[u][l]);
+  }
+  for (; i + 8 <= dim; i += 8) {
+#pragma unroll
+    for (int l = 0; l < 8; ++l) s[0][l] = fmaf(a[i + l], b[i + l], s[0][l]);
+  }
+  float sum = avx2_reduce(s);
+  const uint32_t v4 = i + (dim - i) / 4 * 4;
+  for (; i < v4; ++i) sum = sum + a[i] * b[i];
+  for (; i < dim; ++i) sum = fmaf(a[i], b[i], sum);
+  return sum;
+}
+
+/// simd::normalize (src/simd/dispatch.cc:119-135) of one row in place.
+__device__ inline void exact_normalize(float* v, uint32_t dim) {
+  const float norm_sq = exact_dot(v, v, dim);
+  if (!isfinite(norm_sq)) {
+    double acc = 0.0;
+    for (uint32_t i = 0; i < dim; ++i) acc = acc + static_cast<double>(v[i]) * static_cast<double>(v[i]);
+    const double inv = acc > 0.0 && isfinite(acc) ? 1.0 / sqrt(acc) : 0.0;
+    if (inv == 0.0) return;
+    for (uint32_t i = 0; i < dim; ++i) v[i] = static_cast<float>(static_cast<double>(v[i]) * inv);
+    return;
+  }
+  if (norm_sq <= 0.0f) return;
+  const float inv = 1.0f / sqrtf(norm_sq);
+  for (uint32_t i = 0; i < dim; ++i) v[i] = v[i] * inv;
+}
+
+/// The flat scan's distance (src/flat_index.cc:87-88): squared L2, or 1 - dot for inner product
+/// and cosine; NaN becomes +inf.
+__device__ inline float exact_flat_distance(const float* q, const float* x, uint32_t dim, bool l2) {
+  const float d = l2 ? exact_l2sqr(q, x, dim) : 1.0f - exact_dot(q, x, dim);
+  return d == d ? d : __builtin_huge_valf();
+}
+
+}  // namespace qvh

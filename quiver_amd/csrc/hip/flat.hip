@@ -1,0 +1,630 @@
+// Flat exact search on gfx950: the FlatIndex::search_batch scan (src/flat_index.cc:69-140).
+//
+// Pipeline for one call:
+//   1. prep:  queries -> device, unit-normalized for cosine (exact simd::normalize order),
+//             zero-padded to DP floats, ||q||^2.
+//   2. scan:  fp32 MFMA GEMM (v_mfma_f32_32x32x2_f32) of a 32-query column block held in VGPRs
+//             against 64-row base tiles staged through LDS (double buffered, padded stride),
+//             with the distance epilogue ||q||^2 + ||x||^2 - 2<q,x> (or 1 - <q,x>) and a per-lane
+//             register top-KL list fused in, so the nq x n distance matrix never reaches HBM.
+//             Each (query block, row split) is one workgroup; each query ends with 2 * nsplit
+//             sorted lists of KL candidates.
+//   3. merge: one wave per query pops the KL best candidates of those lists, re-scores them with
+//             the reference's exact AVX2-order arithmetic, and writes the k best by
+//             (exact distance, row).
+// The GEMM form differs from the reference's sum of squared differences only in rounding; the
+// re-score makes every returned distance bit-identical to the reference's for that row, and KL > k
+// keeps a margin of near-tied candidates for the re-score to choose from.
+#include <algorithm>
+#include <vector>
+
+#include "common.hpp"
+#include "exact.hpp"
+
+namespace qvh {
+void launch_normalize_rows(float* d_rows, uint64_t n, uint32_t dim, hipStream_t stream);
+}
+
+namespace {
+
+using namespace qvh;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kWaves = 8;                                 // 2 waves per SIMD
+constexpr int kThreads = kWaves * 64;
+constexpr int kTileRows = 64;                             // two 32-row MFMA blocks
+constexpr int kQueriesPerBlock = kWaves * 32;             // each wave owns 32 queries
+constexpr int kMaxListsPerLane = 4;                       // merge: lists per lane
+constexpr uint32_t kMaxSplits = 64 * kMaxListsPerLane / 2;
+constexpr int kMaxDp = 128;                               // register-resident query width
+
+struct ScanArgs {
+  const float* X;           // [cap][DP] rows as stored, zero padded
+  const float* xnorm;       // [cap] ||x||^2
+  uint64_t n;
+  const float* Q;           // [nq][DP] prepared queries
+  const float* qnorm;       // [nq] ||q||^2
+  uint32_t nq;
+  const uint64_t* bitmap;   // admitted rows, or null
+  int l2;
+  uint32_t nsplit;
+  uint32_t qblocks;
+  uint64_t rows_per_split;  // multiple of kTileRows
+  float* part_d;            // [nq][2*nsplit][KL]
+  uint32_t* part_r;
+};
+
+/// Inserts (d, r) into the ascending list (Ld, Lr) in (distance, row) order, dropping the last.
+template <int KL>
+__device__ __forceinline__ void list_insert(float (&Ld)[KL], uint32_t (&Lr)[KL], float d, uint32_t r) {
+#pragma unroll
+  for (int x = 0; x < KL; ++x) {
+    const bool lt = (d < Ld[x]) | ((d == Ld[x]) & (r < Lr[x]));
+    const float td = Ld[x];
+    const uint32_t tr = Lr[x];
+    Ld[x] = lt ? d : td;
+    Lr[x] = lt ? r : tr;
+    d = lt ? td : d;
+    r = lt ? tr : r;
+  }
+}
+
+template <int DP, int KL>
+__global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
+  constexpr int H = DP / 2;                   // dims per lane half (K split in two halves)
+  constexpr int STRIDE = DP + 4;              // LDS row stride in floats: conflict-free b128 reads
+  constexpr int C4 = DP / 4;                  // float4 chunks per row
+  constexpr int CHUNKS = kTileRows * C4;
+  constexpr int PER_THREAD = (CHUNKS + kThreads - 1) / kThreads;
+  __shared__ __attribute__((aligned(16))) float s_tile[2][kTileRows * STRIDE];
+  __shared__ float s_norm[2][kTileRows];
+  __shared__ uint64_t s_bits[2];
+  __shared__ __attribute__((aligned(16))) float s_spill[kThreads * 16];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 31, h = lane >> 5;
+
+  // Workgroup w runs on XCD w % 8; give each XCD its own row splits so the workgroups resident
+  // on one XCD at a time stream the same base rows through that XCD's L2.
+  uint32_t qb, split;
+  const uint32_t wg = blockIdx.x;
+  if (a.nsplit % 8 == 0) {
+    const uint32_t x = wg % 8, li = wg / 8;
+    split = (li / a.qblocks) * 8 + x;
+    qb = li % a.qblocks;
+  } else {
+    split = wg / a.qblocks;
+    qb = wg % a.qblocks;
+  }
+
+  const uint32_t q = qb * kQueriesPerBlock + wave * 32 + j;
+  const bool wave_active = qb * kQueriesPerBlock + wave * 32 < a.nq;
+  const bool qvalid = q < a.nq;
+
+  // This lane's half of its query: dims [h*H, h*H + H). MFMA step s pairs dim h*H+s of the query
+  // (B operand, lane = (k=h, col=j)) with the same dim of a base row (A operand, lane = (row j, k=h)).
+  float qreg[H];
+  {
+    const f32x4* qp = reinterpret_cast<const f32x4*>(a.Q + static_cast<size_t>(qvalid ? q : 0) * DP + h * H);
+#pragma unroll
+    for (int s = 0; s < H / 4; ++s) {
+      const f32x4 v = qvalid ? qp[s] : f32x4{0.f, 0.f, 0.f, 0.f};
+      qreg[4 * s + 0] = v[0];
+      qreg[4 * s + 1] = v[1];
+      qreg[4 * s + 2] = v[2];
+      qreg[4 * s + 3] = v[3];
+    }
+  }
+  const float qn = qvalid ? a.qnorm[q] : 0.0f;
+
+  float Ld[KL];
+  uint32_t Lr[KL];
+#pragma unroll
+  for (int x = 0; x < KL; ++x) {
+    Ld[x] = __builtin_huge_valf();
+    Lr[x] = QVH_EMPTY_ROW;
+  }
+
+  const uint64_t r0 = static_cast<uint64_t>(split) * a.rows_per_split;
+  const uint64_t r1 = r0 < a.n ? (a.n < r0 + a.rows_per_split ? a.n : r0 + a.rows_per_split) : r0;
+  const uint32_t ntiles = static_cast<uint32_t>(ceil_div(r1 - r0, kTileRows));
+
+  f32x4 stage[PER_THREAD];
+  float stage_norm = 0.0f;
+  uint64_t stage_bits = ~0ull;
+  auto load_tile = [&](uint32_t t) {
+    const uint64_t base = r0 + static_cast<uint64_t>(t) * kTileRows;
+#pragma unroll
+    for (int p = 0; p < PER_THREAD; ++p) {
+      const int c = tid + p * kThreads;
+      const int row = c / C4, col = c % C4;
+      const uint64_t gr = base + row;
+      stage[p] = (c < CHUNKS && gr < r1)
+                     ? *reinterpret_cast<const f32x4*>(a.X + gr * DP + 4 * col)
+                     : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    if (tid < kTileRows) {
+      const uint64_t gr = base + tid;
+      stage_norm = gr < r1 ? a.xnorm[gr] : 0.0f;
+    }
+    if (tid == kTileRows && a.bitmap) stage_bits = a.bitmap[base >> 6];
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < PER_THREAD; ++p) {
+      const int c = tid + p * kThreads;
+      if (c < CHUNKS) {
+        const int row = c / C4, col = c % C4;
+        *reinterpret_cast<f32x4*>(&s_tile[buf][row * STRIDE + 4 * col]) = stage[p];
+      }
+    }
+    if (tid < kTileRows) s_norm[buf][tid] = stage_norm;
+    if (tid == kTileRows) s_bits[buf] = stage_bits;
+  };
+
+  if (ntiles > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  for (uint32_t t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < ntiles) load_tile(t + 1);
+    if (wave_active) {
+      f32x16 acc0 = {}, acc1 = {};
+      const float* a0 = &s_tile[buf][j * STRIDE + h * H];
+      const float* a1 = &s_tile[buf][(32 + j) * STRIDE + h * H];
+      // Software-pipelined: the next step's two b128 LDS reads are issued before this step's
+      // eight MFMAs (8 x 64 cycles), and the scheduling barrier keeps the compiler from hoisting
+      // every read of the tile at once (which would spill).
+      f32x4 x0 = *reinterpret_cast<const f32x4*>(a0);
+      f32x4 x1 = *reinterpret_cast<const f32x4*>(a1);
+#pragma unroll
+      for (int s = 0; s < H; s += 4) {
+        f32x4 n0 = x0, n1 = x1;
+        if (s + 4 < H) {
+          n0 = *reinterpret_cast<const f32x4*>(a0 + s + 4);
+          n1 = *reinterpret_cast<const f32x4*>(a1 + s + 4);
+        }
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0[0], qreg[s + 0], acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1[0], qreg[s + 0], acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0[1], qreg[s + 1], acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1[1], qreg[s + 1], acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0[2], qreg[s + 2], acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1[2], qreg[s + 2], acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0[3], qreg[s + 3], acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1[3], qreg[s + 3], acc1, 0, 0, 0);
+        x0 = n0;
+        x1 = n1;
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // D[row][col] of a 32x32 block: col = lane % 32 (query j), row = 8*(r/4) + 4*h + r%4 in
+      // register r. Per lane the rows visited increase, so ties resolve to the smaller row.
+      const uint64_t tile_row0 = r0 + static_cast<uint64_t>(t) * kTileRows;
+      const uint64_t bits = s_bits[buf];
+      const float* tn = s_norm[buf];
+      float* spill = &s_spill[tid * 16];
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk) {
+        const f32x16 acc = blk ? acc1 : acc0;
+        // Fast path: distances and a mask of the rows that beat this lane's current k-th.
+        const float thr = Ld[KL - 1];
+        float d[16];
+        uint32_t pass = 0;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int i = 32 * blk + 8 * (r >> 2) + 4 * h + (r & 3);
+          float v = a.l2 ? (qn + tn[i]) - 2.0f * acc[r] : 1.0f - acc[r];
+          v = v == v ? v : __builtin_huge_valf();
+          d[r] = v;
+          const bool ok = (tile_row0 + i < r1) & (((bits >> i) & 1ull) != 0);
+          pass |= (ok & (v <= thr)) ? (1u << r) : 0u;
+        }
+        // Slow path (rare after the first tiles): park the 16 distances in LDS and insert the
+        // passing ones in row order.
+        if (pass) {
+#pragma unroll
+          for (int r = 0; r < 16; r += 4) {
+            *reinterpret_cast<f32x4*>(spill + r) = f32x4{d[r], d[r + 1], d[r + 2], d[r + 3]};
+          }
+          while (pass) {
+            const int r = __builtin_ctz(pass);
+            pass &= pass - 1;
+            const float v = spill[r];
+            if (v <= Ld[KL - 1]) {
+              const uint32_t row = static_cast<uint32_t>(
+                  tile_row0 + 32 * blk + 8 * (r >> 2) + 4 * h + (r & 3));
+              list_insert<KL>(Ld, Lr, v, row);
+            }
+          }
+        }
+      }
+    }
+    if (t + 1 < ntiles) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (qvalid) {
+    const size_t o = (static_cast<size_t>(q) * (2 * a.nsplit) + 2 * split + h) * KL;
+#pragma unroll
+    for (int x = 0; x < KL; ++x) {
+      a.part_d[o + x] = Ld[x];
+      a.part_r[o + x] = Lr[x];
+    }
+  }
+}
+
+struct MergeArgs {
+  const float* X;
+  uint32_t dim, dp;
+  const float* Q;
+  uint32_t nq, k;
+  int l2;
+  uint32_t nlists;          // 2 * nsplit
+  const float* part_d;
+  const uint32_t* part_r;
+  uint32_t* out_rows;
+  float* out_dist;
+};
+
+template <int KL>
+__global__ void __launch_bounds__(256) flat_merge_kernel(MergeArgs m) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t q = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (q >= m.nq) return;  // whole wave; this kernel has no block barriers
+  const float* pd = m.part_d + static_cast<size_t>(q) * m.nlists * KL;
+  const uint32_t* pr = m.part_r + static_cast<size_t>(q) * m.nlists * KL;
+
+  uint32_t ptr[kMaxListsPerLane];
+  uint64_t head[kMaxListsPerLane];
+#pragma unroll
+  for (int u = 0; u < kMaxListsPerLane; ++u) {
+    const uint32_t li = lane + 64 * u;
+    ptr[u] = 0;
+    head[u] = li < m.nlists ? make_key(pd[li * KL], pr[li * KL]) : ~0ull;
+  }
+  uint64_t sel = ~0ull;
+  int count = 0;
+  for (int x = 0; x < KL; ++x) {
+    uint64_t mine = head[0];
+    int arg = 0;
+#pragma unroll
+    for (int u = 1; u < kMaxListsPerLane; ++u) {
+      if (head[u] < mine) {
+        mine = head[u];
+        arg = u;
+      }
+    }
+    const uint64_t best = wave_min_u64(mine);
+    if (static_cast<uint32_t>(best) == QVH_EMPTY_ROW) break;  // only empty slots remain
+    if (lane == x) sel = best;
+    ++count;
+    if (mine == best) {
+#pragma unroll
+      for (int u = 0; u < kMaxListsPerLane; ++u) {
+        if (u == arg) {
+          const uint32_t li = lane + 64 * u;
+          const uint32_t p = ++ptr[u];
+          head[u] = p < KL ? make_key(pd[li * KL + p], pr[li * KL + p]) : ~0ull;
+        }
+      }
+    }
+  }
+  // Re-score the selected candidates exactly and rank them by (distance, row).
+  const bool valid = lane < count;
+  const uint32_t row = static_cast<uint32_t>(sel);
+  float e = __builtin_huge_valf();
+  if (valid) {
+    e = exact_flat_distance(m.Q + static_cast<size_t>(q) * m.dp,
+                            m.X + static_cast<size_t>(row) * m.dp, m.dim, m.l2 != 0);
+  }
+  const uint64_t key = valid ? make_key(e, row) : ~0ull;
+  uint32_t rank = 0;
+  for (int y = 0; y < KL; ++y) {
+    const uint64_t o = __shfl(key, y, 64);
+    rank += o < key ? 1u : 0u;
+  }
+  uint32_t* orow = m.out_rows + static_cast<size_t>(q) * m.k;
+  float* odist = m.out_dist + static_cast<size_t>(q) * m.k;
+  if (valid && rank < m.k) {
+    orow[rank] = row;
+    odist[rank] = e;
+  }
+  for (uint32_t p = lane; p < m.k; p += 64) {
+    if (p >= static_cast<uint32_t>(count)) {
+      orow[p] = QVH_EMPTY_ROW;
+      odist[p] = __builtin_huge_valf();
+    }
+  }
+}
+
+// ---- ingest / prep kernels ------------------------------------------------------------------
+
+/// dst[r][c] = c < dim ? src[r][c] : 0 for r < n, c < dp.
+__global__ void pack_rows_kernel(const float* __restrict__ src, float* __restrict__ dst, uint64_t n,
+                                 uint32_t dim, uint32_t dp) {
+  const uint64_t idx = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= n * dp) return;
+  const uint64_t r = idx / dp;
+  const uint32_t c = static_cast<uint32_t>(idx % dp);
+  dst[idx] = c < dim ? src[r * dim + c] : 0.0f;
+}
+
+/// out[r] = sum of squares of row r (any order: only the GEMM-form screening uses it).
+__global__ void row_norms_kernel(const float* __restrict__ rows, float* __restrict__ out, uint64_t n,
+                                 uint32_t dp) {
+  const uint64_t r = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r >= n) return;
+  const f32x4* p = reinterpret_cast<const f32x4*>(rows + r * dp);
+  float s = 0.0f;
+  for (uint32_t c = 0; c < dp / 4; ++c) {
+    const f32x4 v = p[c];
+    s = fmaf(v[0], v[0], s);
+    s = fmaf(v[1], v[1], s);
+    s = fmaf(v[2], v[2], s);
+    s = fmaf(v[3], v[3], s);
+  }
+  out[r] = s;
+}
+
+uint32_t padded_dim(uint32_t dim) {
+  for (uint32_t dp : {16u, 32u, 48u, 64u, 80u, 96u, 112u, 128u})
+    if (dim <= dp) return dp;
+  return 0;
+}
+
+template <int DP>
+void launch_scan_dp(int kl, dim3 grid, const ScanArgs& a, hipStream_t s) {
+  if (kl == 16) {
+    hipLaunchKernelGGL((flat_scan_kernel<DP, 16>), grid, dim3(kThreads), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((flat_scan_kernel<DP, 32>), grid, dim3(kThreads), 0, s, a);
+  }
+}
+
+void launch_scan(uint32_t dp, int kl, dim3 grid, const ScanArgs& a, hipStream_t s) {
+  switch (dp) {
+    case 16: launch_scan_dp<16>(kl, grid, a, s); break;
+    case 32: launch_scan_dp<32>(kl, grid, a, s); break;
+    case 48: launch_scan_dp<48>(kl, grid, a, s); break;
+    case 64: launch_scan_dp<64>(kl, grid, a, s); break;
+    case 80: launch_scan_dp<80>(kl, grid, a, s); break;
+    case 96: launch_scan_dp<96>(kl, grid, a, s); break;
+    case 112: launch_scan_dp<112>(kl, grid, a, s); break;
+    case 128: launch_scan_dp<128>(kl, grid, a, s); break;
+    default: throw Failure(QVH_EUNSUPPORTED, "flat scan: unsupported padded dimension");
+  }
+}
+
+}  // namespace
+
+struct qvh_flat {
+  uint32_t dim = 0, dp = 0;
+  int metric = 0;
+  int device = 0;
+  uint64_t n = 0, cap = 0;
+  DeviceBuffer rows, norms;
+  hipStream_t stream = nullptr;
+  std::mutex mu;
+  // per-call workspace (grown on demand, serialized by mu)
+  DeviceBuffer w_stage, w_q, w_qn, w_pd, w_pr, w_rows, w_dist, w_bits;
+};
+
+namespace {
+
+void flat_grow(qvh_flat* f, uint64_t need) {
+  if (need <= f->cap) return;
+  uint64_t cap = std::max<uint64_t>(need, f->cap ? f->cap * 2 : 1024);
+  void* nr = device_alloc(cap * f->dp * sizeof(float));
+  void* nn = nullptr;
+  try {
+    nn = device_alloc(cap * sizeof(float));
+  } catch (...) {
+    device_free(nr);
+    throw;
+  }
+  if (f->n) {
+    QVH_HIP(hipMemcpyAsync(nr, f->rows.ptr, f->n * f->dp * sizeof(float), hipMemcpyDeviceToDevice, f->stream));
+    QVH_HIP(hipMemcpyAsync(nn, f->norms.ptr, f->n * sizeof(float), hipMemcpyDeviceToDevice, f->stream));
+    QVH_HIP(hipStreamSynchronize(f->stream));
+  }
+  device_free(f->rows.ptr);
+  device_free(f->norms.ptr);
+  f->rows.ptr = nr;
+  f->rows.bytes = cap * f->dp * sizeof(float);
+  f->norms.ptr = nn;
+  f->norms.bytes = cap * sizeof(float);
+  f->cap = cap;
+}
+
+/// Prepared queries (normalized for cosine, padded) and their norms in the handle workspace.
+void flat_prep_queries(qvh_flat* f, const float* d_raw, uint64_t nq, hipStream_t s) {
+  float* qs = static_cast<float*>(f->w_stage.reserve(nq * f->dim * sizeof(float)));
+  if (qs != d_raw) QVH_HIP(hipMemcpyAsync(qs, d_raw, nq * f->dim * sizeof(float), hipMemcpyDeviceToDevice, s));
+  if (f->metric == QVH_METRIC_COSINE) launch_normalize_rows(qs, nq, f->dim, s);
+  float* qp = static_cast<float*>(f->w_q.reserve(nq * f->dp * sizeof(float)));
+  float* qn = static_cast<float*>(f->w_qn.reserve(nq * sizeof(float)));
+  const uint64_t total = nq * f->dp;
+  hipLaunchKernelGGL(pack_rows_kernel, dim3(static_cast<unsigned>(ceil_div(total, 256))), dim3(256), 0, s,
+                     qs, qp, nq, f->dim, f->dp);
+  hipLaunchKernelGGL(row_norms_kernel, dim3(static_cast<unsigned>(ceil_div(nq, 256))), dim3(256), 0, s,
+                     qp, qn, nq, f->dp);
+  QVH_HIP(hipGetLastError());
+}
+
+void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t k,
+                      const uint64_t* d_bitmap, uint32_t* d_rows, float* d_dist, hipStream_t s) {
+  QVH_REQUIRE(k <= 32, "flat search: k > 32 is not supported on the device path yet");
+  QVH_REQUIRE(nq <= 0xFFFFFFFFull, "flat search: too many queries in one call");
+  const int kl = k <= 16 ? 16 : 32;
+  flat_prep_queries(f, d_queries, nq, s);
+
+  int cus = 256;
+  (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, f->device);
+  const uint32_t qblocks = static_cast<uint32_t>(ceil_div(nq, kQueriesPerBlock));
+  const uint64_t tiles = std::max<uint64_t>(1, ceil_div(f->n, kTileRows));
+  uint64_t nsplit = ceil_div(static_cast<uint64_t>(4 * cus), qblocks);
+  nsplit = std::min<uint64_t>({nsplit, tiles, kMaxSplits});
+  if (nsplit >= 8) nsplit -= nsplit % 8;
+  nsplit = std::max<uint64_t>(nsplit, 1);
+  const uint64_t rows_per_split = ceil_div(tiles, nsplit) * kTileRows;
+
+  const size_t parts = static_cast<size_t>(nq) * 2 * nsplit * kl;
+  ScanArgs a;
+  a.X = f->rows.as<float>();
+  a.xnorm = f->norms.as<float>();
+  a.n = f->n;
+  a.Q = f->w_q.as<float>();
+  a.qnorm = f->w_qn.as<float>();
+  a.nq = static_cast<uint32_t>(nq);
+  a.bitmap = d_bitmap;
+  a.l2 = f->metric == QVH_METRIC_L2;
+  a.nsplit = static_cast<uint32_t>(nsplit);
+  a.qblocks = qblocks;
+  a.rows_per_split = rows_per_split;
+  a.part_d = static_cast<float*>(f->w_pd.reserve(parts * sizeof(float)));
+  a.part_r = static_cast<uint32_t*>(f->w_pr.reserve(parts * sizeof(uint32_t)));
+  launch_scan(f->dp, kl, dim3(static_cast<unsigned>(qblocks * nsplit)), a, s);
+  QVH_HIP(hipGetLastError());
+
+  MergeArgs m;
+  m.X = a.X;
+  m.dim = f->dim;
+  m.dp = f->dp;
+  m.Q = a.Q;
+  m.nq = a.nq;
+  m.k = k;
+  m.l2 = a.l2;
+  m.nlists = static_cast<uint32_t>(2 * nsplit);
+  m.part_d = a.part_d;
+  m.part_r = a.part_r;
+  m.out_rows = d_rows;
+  m.out_dist = d_dist;
+  const dim3 mgrid(static_cast<unsigned>(ceil_div(nq, 4)));
+  if (kl == 16) {
+    hipLaunchKernelGGL(flat_merge_kernel<16>, mgrid, dim3(256), 0, s, m);
+  } else {
+    hipLaunchKernelGGL(flat_merge_kernel<32>, mgrid, dim3(256), 0, s, m);
+  }
+  QVH_HIP(hipGetLastError());
+}
+
+}  // namespace
+
+extern "C" {
+
+qvh_status qvh_flat_create(uint32_t dim, int metric, qvh_flat** out) {
+  return guarded([&] {
+    QVH_REQUIRE(out != nullptr, "qvh_flat_create: null output");
+    *out = nullptr;
+    QVH_REQUIRE(dim >= 1 && dim <= 65536, "dimension must be in [1, 65536]");
+    QVH_REQUIRE(metric >= QVH_METRIC_L2 && metric <= QVH_METRIC_COSINE, "unknown metric");
+    const uint32_t dp = padded_dim(dim);
+    if (dp == 0) throw Failure(QVH_EUNSUPPORTED, "flat device path supports dim <= 128 for now");
+    const int dev = current_device();
+    auto* f = new qvh_flat;
+    f->dim = dim;
+    f->dp = dp;
+    f->metric = metric;
+    f->device = dev;
+    const hipError_t e = hipStreamCreateWithFlags(&f->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+      delete f;
+      throw Failure(QVH_EDEVICE, std::string("hipStreamCreate: ") + hipGetErrorString(e));
+    }
+    *out = f;
+  });
+}
+
+void qvh_flat_destroy(qvh_flat* f) {
+  if (!f) return;
+  (void)hipSetDevice(f->device);
+  if (f->stream) {
+    (void)hipStreamSynchronize(f->stream);
+    (void)hipStreamDestroy(f->stream);
+  }
+  delete f;
+}
+
+uint64_t qvh_flat_size(const qvh_flat* f) { return f ? f->n : 0; }
+
+qvh_status qvh_flat_append(qvh_flat* f, const float* rows, uint64_t n, float* stored_out) {
+  return guarded([&] {
+    QVH_REQUIRE(f != nullptr, "qvh_flat_append: null handle");
+    if (n == 0) return;
+    QVH_REQUIRE(rows != nullptr, "qvh_flat_append: null rows");
+    std::lock_guard<std::mutex> lock(f->mu);
+    QVH_REQUIRE(f->n + n <= 0xFFFFFFFFull, "FlatIndex holds at most 2^32 vectors");
+    QVH_HIP(hipSetDevice(f->device));
+    flat_grow(f, f->n + n);
+    const size_t raw_bytes = n * f->dim * sizeof(float);
+    float* stage = static_cast<float*>(f->w_stage.reserve(raw_bytes));
+    QVH_HIP(hipMemcpyAsync(stage, rows, raw_bytes, hipMemcpyHostToDevice, f->stream));
+    if (f->metric == QVH_METRIC_COSINE) launch_normalize_rows(stage, n, f->dim, f->stream);
+    float* dst = f->rows.as<float>() + f->n * f->dp;
+    const uint64_t total = n * f->dp;
+    hipLaunchKernelGGL(pack_rows_kernel, dim3(static_cast<unsigned>(ceil_div(total, 256))), dim3(256), 0,
+                       f->stream, stage, dst, n, f->dim, f->dp);
+    hipLaunchKernelGGL(row_norms_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0,
+                       f->stream, dst, f->norms.as<float>() + f->n, n, f->dp);
+    QVH_HIP(hipGetLastError());
+    if (stored_out) QVH_HIP(hipMemcpyAsync(stored_out, stage, raw_bytes, hipMemcpyDeviceToHost, f->stream));
+    QVH_HIP(hipStreamSynchronize(f->stream));
+    f->n += n;
+  });
+}
+
+qvh_status qvh_flat_search(qvh_flat* f, const float* queries, uint64_t nq, uint32_t k,
+                           const uint64_t* row_bitmap, uint32_t* out_rows, float* out_dist) {
+  return guarded([&] {
+    QVH_REQUIRE(f != nullptr, "qvh_flat_search: null handle");
+    if (nq == 0 || k == 0) return;
+    QVH_REQUIRE(queries && out_rows && out_dist, "qvh_flat_search: null buffer");
+    std::lock_guard<std::mutex> lock(f->mu);
+    QVH_HIP(hipSetDevice(f->device));
+    const size_t qbytes = nq * f->dim * sizeof(float);
+    float* d_raw = static_cast<float*>(f->w_stage.reserve(qbytes));
+    QVH_HIP(hipMemcpyAsync(d_raw, queries, qbytes, hipMemcpyHostToDevice, f->stream));
+    const uint64_t* d_bits = nullptr;
+    if (row_bitmap) {
+      const size_t words = ceil_div(std::max<uint64_t>(f->n, 1), 64);
+      uint64_t* b = static_cast<uint64_t*>(f->w_bits.reserve(words * sizeof(uint64_t)));
+      QVH_HIP(hipMemcpyAsync(b, row_bitmap, words * sizeof(uint64_t), hipMemcpyHostToDevice, f->stream));
+      d_bits = b;
+    }
+    uint32_t* d_rows = static_cast<uint32_t*>(f->w_rows.reserve(nq * k * sizeof(uint32_t)));
+    float* d_dist = static_cast<float*>(f->w_dist.reserve(nq * k * sizeof(float)));
+    flat_search_impl(f, d_raw, nq, k, d_bits, d_rows, d_dist, f->stream);
+    QVH_HIP(hipMemcpyAsync(out_rows, d_rows, nq * k * sizeof(uint32_t), hipMemcpyDeviceToHost, f->stream));
+    QVH_HIP(hipMemcpyAsync(out_dist, d_dist, nq * k * sizeof(float), hipMemcpyDeviceToHost, f->stream));
+    QVH_HIP(hipStreamSynchronize(f->stream));
+  });
+}
+
+qvh_status qvh_flat_search_device(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t k,
+                                  const uint64_t* d_row_bitmap, uint32_t* d_out_rows,
+                                  float* d_out_dist, void* stream) {
+  return guarded([&] {
+    QVH_REQUIRE(f != nullptr, "qvh_flat_search_device: null handle");
+    if (nq == 0 || k == 0) return;
+    QVH_REQUIRE(d_queries && d_out_rows && d_out_dist, "qvh_flat_search_device: null buffer");
+    std::lock_guard<std::mutex> lock(f->mu);
+    QVH_HIP(hipSetDevice(f->device));
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : f->stream;
+    flat_search_impl(f, d_queries, nq, k, d_row_bitmap, d_out_rows, d_out_dist, s);
+  });
+}
+
+qvh_status qvh_flat_sync(qvh_flat* f) {
+  return guarded([&] {
+    QVH_REQUIRE(f != nullptr, "qvh_flat_sync: null handle");
+    QVH_HIP(hipSetDevice(f->device));
+    QVH_HIP(hipStreamSynchronize(f->stream));
+  });
+}
+
+}  // extern "C"

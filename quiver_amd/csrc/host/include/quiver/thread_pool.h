@@ -1,0 +1,52 @@
+// Fork-join pool for the host-side work around the device calls (filter materialization, label
+// mapping, k-means centroid updates), with the reference's interface and semantics
+// (include/quiver/thread_pool.h:14-57): the caller participates, nested parallel_for calls run
+// inline, and the first exception thrown by a chunk is rethrown to the caller.
+#pragma once
+
+#include <condition_variable>
+#include <cstddef>
+#include <cstdint>
+#include <exception>
+#include <functional>
+#include <mutex>
+#include <thread>
+#include <vector>
+
+namespace quiver {
+
+class ThreadPool {
+ public:
+  using RangeFn = std::function<void(std::size_t begin, std::size_t end)>;
+
+  /// `num_threads` counts the calling thread; 0 means std::thread::hardware_concurrency().
+  explicit ThreadPool(std::size_t num_threads = 0);
+  ~ThreadPool();
+  ThreadPool(const ThreadPool&) = delete;
+  ThreadPool& operator=(const ThreadPool&) = delete;
+
+  std::size_t num_threads() const noexcept { return threads_.size() + 1; }
+
+  /// Runs fn over [0, n) in chunks of at most `grain` items and blocks until all finish.
+  void parallel_for(std::size_t n, std::size_t grain, const RangeFn& fn);
+
+  /// Process-wide pool sized to the machine.
+  static ThreadPool& global();
+
+ private:
+  struct Task;
+  void worker();
+  static void drain(Task& task) noexcept;
+
+  std::vector<std::thread> threads_;
+  std::mutex submit_;            // one parallel_for at a time per pool
+  std::mutex mu_;
+  std::condition_variable wake_;
+  std::condition_variable idle_;
+  Task* task_ = nullptr;
+  std::uint64_t epoch_ = 0;
+  std::size_t busy_ = 0;
+  bool stopping_ = false;
+};
+
+}  // namespace quiver

@@ -1,0 +1,162 @@
+// pybind11 bindings with the reference's binding surface (python/quiver_ext.cc:24-389, nanobind
+// there; nanobind is not available in this toolchain). Argument normalization happens in Python
+// (quiver_amd/__init__.py); every compute call releases the GIL.
+#include <pybind11/numpy.h>
+#include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
+
+#include <algorithm>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+
+#include "qvh.h"
+#include "quiver/filter.h"
+#include "quiver/flat_index.h"
+
+namespace py = pybind11;
+
+namespace {
+
+using FloatMatrix = py::array_t<float, py::array::c_style>;
+using LabelArray = py::array_t<std::uint64_t, py::array::c_style>;
+
+/// One cached pool per requested size (python/quiver_ext.cc:28-37).
+quiver::ThreadPool* pool_for(std::size_t num_threads) {
+  if (num_threads == 0) return &quiver::ThreadPool::global();
+  if (num_threads > 1024) throw py::value_error("num_threads must be at most 1024");
+  static std::mutex mu;
+  static std::map<std::size_t, std::unique_ptr<quiver::ThreadPool>> pools;
+  std::lock_guard<std::mutex> lock(mu);
+  auto& p = pools[num_threads];
+  if (!p) p = std::make_unique<quiver::ThreadPool>(num_threads);
+  return p.get();
+}
+
+/// The cheaper filter for a set of allowed labels: a bitset unless labels are very sparse
+/// (the same rule as python/quiver_ext.cc:40-51).
+std::unique_ptr<quiver::Filter> make_filter(const LabelArray& allowed) {
+  const std::uint64_t* p = allowed.data();
+  const std::size_t n = static_cast<std::size_t>(allowed.size());
+  const std::uint64_t max_label = n == 0 ? 0 : *std::max_element(p, p + n);
+  if (max_label < (std::uint64_t{1} << 32) && max_label / 64 <= 16 * n + 1024) {
+    auto f = std::make_unique<quiver::BitsetFilter>(static_cast<std::size_t>(max_label) + 1);
+    for (std::size_t i = 0; i < n; ++i) f->insert(p[i]);
+    return f;
+  }
+  return std::make_unique<quiver::LabelSetFilter>(p, p + n);
+}
+
+void check_matrix(const FloatMatrix& x, std::size_t dim) {
+  if (x.ndim() != 2) throw py::value_error("expected a 2-D float32 array");
+  if (static_cast<std::size_t>(x.shape(1)) != dim) {
+    throw py::value_error("expected vectors of dimension " + std::to_string(dim) + ", got " +
+                          std::to_string(x.shape(1)));
+  }
+}
+
+/// nq * k, rejecting sizes that would overflow or that no machine could allocate
+/// (python/quiver_ext.cc:62-68).
+std::size_t result_size(std::size_t nq, std::size_t k) {
+  std::size_t total = 0;
+  if (__builtin_mul_overflow(nq, k, &total) || total > (std::size_t{1} << 40)) {
+    throw py::value_error("nq * k is too large");
+  }
+  return total;
+}
+
+/// (labels int64 [nq, k] with -1 for empty slots, distances float32 [nq, k]).
+py::tuple make_results(std::size_t nq, std::size_t k, std::vector<std::uint64_t>&& labels,
+                       std::vector<float>&& dist) {
+  auto* l = new std::vector<std::uint64_t>(std::move(labels));
+  auto* d = new std::vector<float>(std::move(dist));
+  py::capsule lc(l, [](void* p) { delete static_cast<std::vector<std::uint64_t>*>(p); });
+  py::capsule dc(d, [](void* p) { delete static_cast<std::vector<float>*>(p); });
+  // kInvalidLabel (2^64 - 1) reinterpreted as int64 is exactly -1.
+  py::array_t<std::int64_t> la({nq, k}, reinterpret_cast<std::int64_t*>(l->data()), lc);
+  py::array_t<float> da({nq, k}, d->data(), dc);
+  return py::make_tuple(la, da);
+}
+
+const std::uint64_t* optional_labels(const py::object& labels, std::size_t n, LabelArray& hold) {
+  if (labels.is_none()) return nullptr;
+  hold = labels.cast<LabelArray>();
+  if (static_cast<std::size_t>(hold.size()) != n) {
+    throw py::value_error("labels and vectors differ in length");
+  }
+  return hold.data();
+}
+
+}  // namespace
+
+PYBIND11_MODULE(_quiver, m) {
+  m.doc() = "Quiver search path on MI355X (gfx950): flat exact and IVF-PQ search";
+
+  py::register_exception_translator([](std::exception_ptr p) {
+    try {
+      if (p) std::rethrow_exception(p);
+    } catch (const quiver::Error& e) {
+      PyErr_SetString(PyExc_ValueError, e.what());
+    }
+  });
+
+  m.def(
+      "simd_isa",
+      [] {
+        char name[128] = {0}, arch[64] = {0};
+        int cus = 0;
+        if (qvh_device_info(name, sizeof(name), arch, sizeof(arch), &cus) != QVH_OK) {
+          throw quiver::Error(std::string("no device: ") + qvh_last_error());
+        }
+        std::string a(arch);
+        return a.substr(0, a.find(':'));
+      },
+      "Instruction set the distance kernels run on (the GPU target, e.g. gfx950).");
+
+  py::class_<quiver::FlatIndex>(m, "FlatIndex")
+      .def(py::init([](std::size_t dim, const std::string& metric) {
+             return new quiver::FlatIndex(dim, quiver::parse_metric(metric));
+           }),
+           py::arg("dim"), py::arg("metric") = "l2")
+      .def(
+          "_add",
+          [](quiver::FlatIndex& self, const FloatMatrix& x, const py::object& labels) {
+            check_matrix(x, self.dim());
+            LabelArray hold;
+            const std::uint64_t* lp = optional_labels(labels, x.shape(0), hold);
+            py::gil_scoped_release release;
+            self.add(x.data(), x.shape(0), lp);
+          },
+          py::arg("vectors"), py::arg("labels").none(true))
+      .def(
+          "_search",
+          [](const quiver::FlatIndex& self, const FloatMatrix& q, std::size_t k,
+             const py::object& allowed, std::size_t threads) {
+            check_matrix(q, self.dim());
+            std::unique_ptr<quiver::Filter> filter;
+            if (!allowed.is_none()) filter = make_filter(allowed.cast<LabelArray>());
+            const std::size_t nq = q.shape(0);
+            std::vector<std::uint64_t> labels(result_size(nq, k));
+            std::vector<float> dist(labels.size());
+            quiver::ThreadPool* pool = pool_for(threads);
+            {
+              py::gil_scoped_release release;
+              self.search_batch(q.data(), nq, k, labels.data(), dist.data(), filter.get(), pool);
+            }
+            return make_results(nq, k, std::move(labels), std::move(dist));
+          },
+          py::arg("queries"), py::arg("k"), py::arg("allowed").none(true), py::arg("num_threads"))
+      .def("__len__", &quiver::FlatIndex::size, py::call_guard<py::gil_scoped_release>())
+      .def("get_vector",
+           [](const quiver::FlatIndex& self, std::size_t i) {
+             if (i >= self.size()) throw py::index_error("row out of range");
+             py::array_t<float> out(self.dim());
+             std::memcpy(out.mutable_data(), self.vector(i), self.dim() * sizeof(float));
+             return out;
+           })
+      .def_property_readonly("dim", &quiver::FlatIndex::dim)
+      .def_property_readonly("metric", [](const quiver::FlatIndex& s) {
+        return std::string(quiver::to_string(s.metric()));
+      });
+}

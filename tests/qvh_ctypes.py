@@ -1,0 +1,90 @@
+"""ctypes view of the qvh C-ABI (include/qvh.h), for tests that call the boundary directly."""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB = os.path.join(ROOT, "quiver_amd", "lib", "libqvh.so")
+HEADER = os.path.join(ROOT, "include", "qvh.h")
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_u32p = np.ctypeslib.ndpointer(dtype=np.uint32, flags="C_CONTIGUOUS")
+
+
+def declared_functions():
+    """Names of the functions include/qvh.h declares."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(qvh_[a-z0-9_]+)\s*\(", text)))
+
+
+class Qvh:
+    def __init__(self, path=LIB):
+        self.lib = L = C.CDLL(path)
+        L.qvh_last_error.restype = C.c_char_p
+        L.qvh_init.argtypes = [C.c_int]
+        L.qvh_flat_create.argtypes = [C.c_uint32, C.c_int, C.POINTER(C.c_void_p)]
+        L.qvh_flat_destroy.argtypes = [C.c_void_p]
+        L.qvh_flat_append.argtypes = [C.c_void_p, _f32p, C.c_uint64, C.c_void_p]
+        L.qvh_flat_size.argtypes = [C.c_void_p]
+        L.qvh_flat_size.restype = C.c_uint64
+        L.qvh_flat_search.argtypes = [C.c_void_p, _f32p, C.c_uint64, C.c_uint32, C.c_void_p,
+                                      _u32p, _f32p]
+        L.qvh_normalize.argtypes = [_f32p, C.c_uint64, C.c_uint32]
+
+    def error(self) -> str:
+        return self.lib.qvh_last_error().decode()
+
+    def check(self, status):
+        if status != 0:
+            raise RuntimeError(f"qvh status {status}: {self.error()}")
+
+    def normalize(self, x):
+        x = np.array(x, dtype=np.float32, copy=True, order="C")
+        self.check(self.lib.qvh_normalize(x, x.shape[0], x.shape[1]))
+        return x
+
+    def flat(self, dim, metric):
+        return QvhFlat(self, dim, metric)
+
+
+class QvhFlat:
+    METRIC = {"l2": 0, "ip": 1, "cosine": 2}
+
+    def __init__(self, q: Qvh, dim, metric):
+        self.q, self.dim = q, dim
+        h = C.c_void_p()
+        q.check(q.lib.qvh_flat_create(dim, self.METRIC[metric], C.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self.q.lib.qvh_flat_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def append(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        stored = np.empty_like(x)
+        self.q.check(self.q.lib.qvh_flat_append(self.h, x, x.shape[0], stored.ctypes.data_as(C.c_void_p)))
+        return stored
+
+    def size(self):
+        return int(self.q.lib.qvh_flat_size(self.h))
+
+    def search(self, queries, k, bitmap=None):
+        queries = np.ascontiguousarray(queries, dtype=np.float32)
+        nq = queries.shape[0]
+        rows = np.empty((nq, k), dtype=np.uint32)
+        dist = np.empty((nq, k), dtype=np.float32)
+        bm = None if bitmap is None else np.ascontiguousarray(bitmap, dtype=np.uint64)
+        self.q.check(self.q.lib.qvh_flat_search(
+            self.h, queries, nq, k, None if bm is None else bm.ctypes.data_as(C.c_void_p), rows, dist))
+        return rows, dist

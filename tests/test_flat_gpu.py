@@ -1,0 +1,166 @@
+"""Flat exact search on the GPU vs the oracle (the C restatement of FlatIndex::search_batch,
+src/flat_index.cc:69-140), on the same seeded inputs.
+
+The device returns distances re-scored in the reference's own arithmetic, so they must be
+bit-identical to the oracle's for the same rows, and the (distance, row) order makes the rows
+identical too: assert_same_topk allows label differences only inside groups of exactly equal
+distance at the k-th boundary, and checks that boundary members really carry that distance.
+"""
+
+import numpy as np
+import pytest
+
+import quiver_amd as quiver
+from oracle.oracle import rows_bitmap
+from parity import assert_same_topk
+from quiver_amd import datasets as D
+from qvh_ctypes import Qvh
+
+pytestmark = pytest.mark.gpu
+
+
+def _true_dist(oracle, stored, queries, metric):
+    def f(qi, labels):
+        return oracle.flat_pair_dist(stored, queries, np.full(labels.size, qi), labels, metric)
+    return f
+
+
+def _check(oracle, base, queries, k, metric, allowed=None, labels=None):
+    print(f"case: n={base.shape[0]} dim={base.shape[1]} nq={queries.shape[0]} k={k} "
+          f"metric={metric} filtered={allowed is not None}", flush=True)
+    idx = quiver.FlatIndex(base.shape[1], metric)
+    idx.add(base, labels=labels)
+    got_l, got_d = idx.search(queries, k, filter=allowed)
+    stored = oracle.normalize(base) if metric == "cosine" else base
+    bm = None
+    if allowed is not None:
+        lab = np.arange(base.shape[0], dtype=np.uint64) if labels is None else labels
+        bm = rows_bitmap(np.flatnonzero(np.isin(lab, allowed)), base.shape[0])
+    rows, dist = oracle.flat_search(stored, queries, k, metric, bm)
+    if labels is None:
+        exp_l = rows.astype(np.int64)
+        exp_l[rows == np.uint32(0xFFFFFFFF)] = -1
+    else:
+        exp_l = np.where(rows == np.uint32(0xFFFFFFFF), np.uint64(2**64 - 1),
+                         labels[np.minimum(rows, base.shape[0] - 1)]).view(np.int64)
+    stats = assert_same_topk(got_l, got_d, exp_l, dist,
+                             None if labels is not None else _true_dist(oracle, stored, queries, metric))
+    return stats
+
+
+@pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
+@pytest.mark.parametrize("filtered", [False, True])
+def test_flat_gaussian_10k_matches_oracle(oracle, metric, filtered):
+    """10,000 x 128 N(0,1), 100 queries, k=10 (the reference's CPU-runnable case)."""
+    base, q = D.flat_small()
+    allowed = D.allowed_ids(base.shape[0], 0.1, seed=5) if filtered else None
+    stats = _check(oracle, base, q, 10, metric, allowed)
+    print(stats)
+
+
+def test_cosine_rows_are_normalized_like_the_reference(oracle):
+    base, _ = D.flat_small()
+    idx = quiver.FlatIndex(128, "cosine")
+    idx.add(base[:500])
+    exp = oracle.normalize(base[:500])
+    got = np.stack([idx.get_vector(i) for i in range(500)])
+    assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))
+
+
+def test_normalize_entry_point_is_bit_exact(oracle):
+    rng = np.random.default_rng(7)
+    for d in (1, 3, 4, 7, 13, 31, 100, 128, 257):
+        x = (rng.standard_normal((300, d)) * rng.uniform(1e-3, 1e3, (300, 1))).astype(np.float32)
+        x[0] = 0.0  # zero vector stays zero
+        x[1, 0] = 3e19  # squares overflow float: the double-precision branch
+        got = Qvh().normalize(x)
+        exp = oracle.normalize(x)
+        assert np.array_equal(got.view(np.uint32), exp.view(np.uint32)), d
+
+
+@pytest.mark.parametrize("dim", [1, 5, 13, 16, 24, 33, 64, 100, 127, 128])
+def test_awkward_dimensions(oracle, dim):
+    rng = np.random.default_rng(dim)
+    base = rng.standard_normal((3000, dim)).astype(np.float32)
+    q = rng.standard_normal((37, dim)).astype(np.float32)
+    for metric in ("l2", "ip"):
+        _check(oracle, base, q, 7, metric)
+
+
+@pytest.mark.parametrize("k", [1, 2, 10, 16, 17, 32])
+def test_k_values(oracle, k):
+    base, q = D.flat_small()
+    _check(oracle, base[:4000], q[:50], k, "l2")
+
+
+def test_integer_data_exact_ties(oracle):
+    """Integer-valued mixture (config 2's distribution): distances are exact integers, ties are
+    common; ties resolve to the smaller row."""
+    base, q = D.int_mix(200_000, 300)
+    stats = _check(oracle, base, q, 10, "l2")
+    print(stats)
+
+
+def test_fewer_rows_than_k_and_selective_filter(oracle):
+    rng = np.random.default_rng(3)
+    base = rng.standard_normal((10, 8)).astype(np.float32)
+    labels = np.arange(100, 110, dtype=np.uint64)
+    idx = quiver.FlatIndex(8)
+    idx.add(base, labels=labels)
+    got_l, got_d = idx.search(base[:1], k=50)
+    assert (got_l[0, :10] >= 100).all() and (got_l[0, 10:] == -1).all()
+    assert np.isinf(got_d[0, 10:]).all()
+    got_l, got_d = idx.search(base[:1], k=5, filter=[103, 107])
+    assert set(got_l[0, :2].tolist()) == {103, 107} and (got_l[0, 2:] == -1).all()
+    _check(oracle, base, base, 5, "l2", allowed=np.array([103, 107], np.uint64), labels=labels)
+
+
+def test_empty_filter_and_unknown_labels():
+    rng = np.random.default_rng(4)
+    base = rng.standard_normal((200, 8)).astype(np.float32)
+    idx = quiver.FlatIndex(8)
+    idx.add(base)
+    got_l, got_d = idx.search(base[:3], k=4, filter=[])
+    assert (got_l == -1).all() and np.isinf(got_d).all()
+    got_l, _ = idx.search(base[:3], k=4, filter=[10**12])
+    assert (got_l == -1).all()
+
+
+def test_known_answers_cosine_and_inner_product():
+    """tests/test_flat.cc:37-52 of the reference."""
+    base = np.array([[1, 0, 0, 0], [0, 2, 0, 0], [1, 1, 0, 0]], np.float32)
+    q = np.array([[3, 0.1, 0, 0]], np.float32)
+    cos = quiver.FlatIndex(4, "cosine")
+    cos.add(base)
+    l, d = cos.search(q, 3)
+    assert l[0, 0] == 0
+    assert abs(d[0, 0] - (1.0 - 3.0 / np.sqrt(9.01))) < 1e-5
+    ip = quiver.FlatIndex(4, "ip")
+    ip.add(base)
+    l, d = ip.search(q, 3)
+    assert l[0, 0] == 2 and abs(d[0, 0] - (1.0 - 3.1)) < 1e-5
+
+
+def test_incremental_adds_and_labels(oracle):
+    rng = np.random.default_rng(9)
+    base = rng.standard_normal((5000, 32)).astype(np.float32)
+    idx = quiver.FlatIndex(32)
+    for b in range(0, 5000, 1237):  # several appends, growing the device store
+        idx.add(base[b:b + 1237], labels=np.arange(b, min(b + 1237, 5000), dtype=np.uint64) * 3)
+    assert len(idx) == 5000
+    q = rng.standard_normal((20, 32)).astype(np.float32)
+    got_l, got_d = idx.search(q, 10)
+    rows, dist = oracle.flat_search(base, q, 10, "l2")
+    assert np.array_equal(got_l, rows.astype(np.int64) * 3)
+    assert np.array_equal(got_d.view(np.uint32), dist.view(np.uint32))
+
+
+def test_c_abi_rows_match_python_path(oracle):
+    base, q = D.flat_small()
+    f = Qvh().flat(128, "l2")
+    f.append(base)
+    assert f.size() == base.shape[0]
+    rows, dist = f.search(q, 10)
+    exp_r, exp_d = oracle.flat_search(base, q, 10, "l2")
+    assert np.array_equal(rows, exp_r) and np.array_equal(dist.view(np.uint32), exp_d.view(np.uint32))
+    f.close()
