@@ -1,0 +1,236 @@
+#!/usr/bin/env python3
+"""Benchmark of the Quiver search path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Headline workload (one "step" = one batched search of the whole query set):
+  flat exact L2, k=10, 1,000,000 x 128 fp32 base (integer-valued 64-component mixture,
+  quiver_amd/datasets.py), 10,000 queries, batched; queries, base and outputs resident in HBM.
+
+Prints ONE JSON line. `value` is queries per second of the whole batched search (query prep +
+fused MFMA scan + merge/exact re-score), timed over K steps with the device synchronized on both
+sides. `roofline` is the dominant kernel (the fused scan): algorithmic 2*n*d*nq FLOP per launch
+over its average launch time, measured with HIP events on the stream it runs on, against the
+MI355X dense FP32 matrix peak (157.3 TFLOP/s). `cpu_baseline` is the reference's own CPU path
+(its sources compiled by oracle/Makefile; the C restatement in oracle/ when that library is
+absent) timed on this host's cores over a bounded sample of the same queries.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "batched QPS @k=10: flat 1M×128 L2 and IVF-PQ nprobe=32; % of MFMA/HBM peak"
+FP32_MFMA_PEAK_TFLOPS = 157.3
+HBM_PEAK_GBS = 8000.0
+
+
+class Hip:
+    """The few HIP runtime calls the bench needs for device-resident buffers."""
+
+    def __init__(self):
+        rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+        self.lib = L = C.CDLL(os.path.join(rocm, "lib", "libamdhip64.so"))
+        L.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+        L.hipFree.argtypes = [C.c_void_p]
+        L.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+        L.hipDeviceSynchronize.argtypes = []
+
+    def malloc(self, nbytes: int) -> C.c_void_p:
+        p = C.c_void_p()
+        rc = self.lib.hipMalloc(C.byref(p), nbytes)
+        if rc != 0:
+            raise RuntimeError(f"hipMalloc({nbytes}) failed: {rc}")
+        return p
+
+    def h2d(self, dst, arr: np.ndarray):
+        arr = np.ascontiguousarray(arr)
+        assert self.lib.hipMemcpy(dst, arr.ctypes.data_as(C.c_void_p), arr.nbytes, 1) == 0
+
+    def d2h(self, arr: np.ndarray, src):
+        assert self.lib.hipMemcpy(arr.ctypes.data_as(C.c_void_p), src, arr.nbytes, 2) == 0
+
+    def sync(self):
+        assert self.lib.hipDeviceSynchronize() == 0
+
+
+class Qvh:
+    def __init__(self):
+        self.lib = L = C.CDLL(os.path.join(ROOT, "quiver_amd", "lib", "libqvh.so"))
+        L.qvh_last_error.restype = C.c_char_p
+        L.qvh_flat_create.argtypes = [C.c_uint32, C.c_int, C.POINTER(C.c_void_p)]
+        L.qvh_flat_append.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p]
+        L.qvh_flat_search_device.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint32,
+                                             C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.qvh_flat_sync.argtypes = [C.c_void_p]
+        L.qvh_flat_set_timing.argtypes = [C.c_void_p, C.c_int]
+        L.qvh_flat_last_timing.argtypes = [C.c_void_p, C.POINTER(C.c_float), C.POINTER(C.c_float),
+                                           C.POINTER(C.c_float), C.POINTER(C.c_uint32)]
+        L.qvh_flat_destroy.argtypes = [C.c_void_p]
+        L.qvh_device_info.argtypes = [C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t,
+                                      C.POINTER(C.c_int)]
+
+    def check(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what}: {self.lib.qvh_last_error().decode()}")
+
+    def device(self):
+        name = C.create_string_buffer(128)
+        arch = C.create_string_buffer(64)
+        cus = C.c_int()
+        self.check(self.lib.qvh_device_info(name, 128, arch, 64, C.byref(cus)), "device")
+        return name.value.decode(), arch.value.decode(), cus.value
+
+
+def load_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary, if present."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_pmc.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("traffic_bytes_per_launch")
+
+
+def bench_flat(args, hip: Hip, qvh: Qvh):
+    from quiver_amd import datasets as D
+
+    n, dim, nq, k = 1_000_000, 128, 10_000, 10
+    base, queries = D.int_mix(n, nq)
+    h = C.c_void_p()
+    qvh.check(qvh.lib.qvh_flat_create(dim, 0, C.byref(h)), "create")
+    qvh.check(qvh.lib.qvh_flat_append(h, base.ctypes.data_as(C.c_void_p), n, None), "append")
+    d_q = hip.malloc(queries.nbytes)
+    hip.h2d(d_q, queries)
+    d_rows = hip.malloc(nq * k * 4)
+    d_dist = hip.malloc(nq * k * 4)
+    qvh.check(qvh.lib.qvh_flat_set_timing(h, 1), "timing")
+
+    def step():
+        qvh.check(qvh.lib.qvh_flat_search_device(h, d_q, nq, k, None, d_rows, d_dist, None), "search")
+
+    for _ in range(args.warmup):
+        step()
+    qvh.check(qvh.lib.qvh_flat_sync(h), "sync")
+    hip.sync()
+    stages = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+        p, s, m, ns = C.c_float(), C.c_float(), C.c_float(), C.c_uint32()
+        qvh.check(qvh.lib.qvh_flat_last_timing(h, C.byref(p), C.byref(s), C.byref(m), C.byref(ns)),
+                  "timing")
+        stages.append((p.value, s.value, m.value, ns.value))
+    qvh.check(qvh.lib.qvh_flat_sync(h), "sync")
+    hip.sync()
+    elapsed = time.perf_counter() - t0
+
+    rows = np.empty((nq, k), np.uint32)
+    dist = np.empty((nq, k), np.float32)
+    hip.d2h(rows, d_rows)
+    hip.d2h(dist, d_dist)
+    assert (rows != 0xFFFFFFFF).all() and (np.diff(dist, axis=1) >= 0).all(), "malformed results"
+
+    st = np.array(stages, dtype=np.float64)
+    scan_ms = float(st[:, 1].mean())
+    flops = 2.0 * n * dim * nq
+    achieved = flops / (scan_ms * 1e-3) / 1e12
+    ms_per_step = elapsed / args.steps * 1e3
+    result = {
+        "value": nq / (ms_per_step * 1e-3),
+        "ms_per_step": ms_per_step,
+        "stage_ms": {"prep": float(st[:, 0].mean()), "scan": scan_ms, "merge": float(st[:, 2].mean())},
+        "nsplit": int(st[0, 3]),
+        "roofline": {"bound": "mfma", "kernel": "flat_scan_kernel<128,16>", "achieved": achieved,
+                     "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / FP32_MFMA_PEAK_TFLOPS,
+                     "traffic": load_traffic("flat_scan_int_mix_1m")},
+        "config": {"workload": "flat exact L2 k=10: 1,000,000 x 128 fp32 integer-valued mixture, "
+                               "10,000 queries batched", "n": n, "dim": dim, "nq": nq, "k": k},
+    }
+    qvh.lib.qvh_flat_destroy(h)
+    for p in (d_q, d_rows, d_dist):
+        hip.lib.hipFree(p)
+    return result, base, queries
+
+
+def cpu_baseline_flat(base, queries, k, seconds, threads):
+    """QPS of the reference CPU flat search over a bounded prefix of the query batch."""
+    from oracle.oracle import Oracle, Reference
+
+    try:
+        ref = Reference()
+        kind = "reference"
+        idx = ref.flat(base.shape[1], "l2")
+        idx.add(base)
+        run = lambda q: idx.search(q, k, threads=threads)
+    except FileNotFoundError:
+        orc = Oracle()
+        kind = "port"
+        run = lambda q: orc.flat_search(base, q, k, "l2", threads=threads)
+    batch = 2 * threads
+    done = 0
+    t0 = time.perf_counter()
+    while done < queries.shape[0] and (time.perf_counter() - t0 < seconds or done == 0):
+        run(queries[done:done + batch])
+        done += batch
+    elapsed = time.perf_counter() - t0
+    return {"value": done / elapsed, "unit": "queries/s", "cores": threads, "kind": kind,
+            "sample": f"first {done} of {queries.shape[0]} queries against all {base.shape[0]} rows "
+                      f"({elapsed:.1f} s, {threads} threads, ThreadPool grain 1)"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build's search path runs on a single MI355X and "
+              f"has no multi-GPU mode (asked for --gpus {args.gpus})", file=sys.stderr)
+        sys.exit(2)
+
+    hip, qvh = Hip(), Qvh()
+    name, arch, cus = qvh.device()
+    flat, base, queries = bench_flat(args, hip, qvh)
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline_flat(base, queries[:4096], 10, args.cpu_seconds, args.cpu_threads)
+    line = {
+        "metric": METRIC,
+        "value": flat["value"],
+        "unit": "queries/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": flat["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded, quiver_amd/datasets.py)",
+        "config": flat["config"],
+        "roofline": flat["roofline"],
+        "cpu_baseline": cpu,
+        "stage_ms": flat["stage_ms"],
+        "nsplit": flat["nsplit"],
+        "device": {"name": name, "arch": arch, "compute_units": cus},
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

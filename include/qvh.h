@@ -95,6 +95,14 @@ qvh_status qvh_flat_search_device(qvh_flat* flat, const float* d_queries, uint64
 /* Synchronizes the handle's stream. */
 qvh_status qvh_flat_sync(qvh_flat* flat);
 
+/* Measurement hook (no counterpart in the reference): when enabled, each search records HIP
+ * events around its three stages (query prep, fused scan, merge + exact re-score) on the stream
+ * the kernels run on; qvh_flat_last_timing waits for the last search and returns the stage
+ * durations in milliseconds and the number of row splits the scan used. */
+qvh_status qvh_flat_set_timing(qvh_flat* flat, int enable);
+qvh_status qvh_flat_last_timing(qvh_flat* flat, float* prep_ms, float* scan_ms, float* merge_ms,
+                                uint32_t* nsplit);
+
 #ifdef __cplusplus
 }
 #endif

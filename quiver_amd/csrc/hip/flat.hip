@@ -54,7 +54,11 @@ struct ScanArgs {
   uint64_t rows_per_split;  // multiple of kTileRows
   float* part_d;            // [nq][2*nsplit][KL]
   uint32_t* part_r;
+  uint32_t* qthr;           // [nq] shared prune threshold (ordered float bits), starts at +inf
 };
+
+constexpr int kShareEvery = 4;  // tiles between exchanges of the shared per-query threshold
+constexpr int kQueueCap = 20;   // queued candidates per lane before a wave-wide flush
 
 /// Inserts (d, r) into the ascending list (Ld, Lr) in (distance, row) order, dropping the last.
 template <int KL>
@@ -71,7 +75,7 @@ __device__ __forceinline__ void list_insert(float (&Ld)[KL], uint32_t (&Lr)[KL],
   }
 }
 
-template <int DP, int KL>
+template <int DP, int KL, bool L2, bool FILTER>
 __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
   constexpr int H = DP / 2;                   // dims per lane half (K split in two halves)
   constexpr int STRIDE = DP + 4;              // LDS row stride in floats: conflict-free b128 reads
@@ -81,7 +85,10 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
   __shared__ __attribute__((aligned(16))) float s_tile[2][kTileRows * STRIDE];
   __shared__ float s_norm[2][kTileRows];
   __shared__ uint64_t s_bits[2];
-  __shared__ __attribute__((aligned(16))) float s_spill[kThreads * 16];
+  // Per-lane candidate queues, entry-major (entry e of thread t at e * kThreads + t) so lanes
+  // appending at different depths never share a bank.
+  __shared__ float s_qd[kQueueCap * kThreads];
+  __shared__ uint32_t s_qr[kQueueCap * kThreads];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -128,6 +135,42 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
     Lr[x] = QVH_EMPTY_ROW;
   }
 
+  // Prune threshold: the smaller of this lane's KL-th best and the shared per-query value. Any
+  // list's KL-th best bounds the KL-th best of the union of all lists, so candidates above it can
+  // never be among the query's KL best (equal distances pass: ties are decided by row).
+  float pthr = qvalid ? ordered_to_float(a.qthr[q]) : __builtin_huge_valf();
+  auto share_threshold = [&]() {
+    // The two lanes of a query hold disjoint rows: their union has KL candidates at or below
+    // max(own[KL/2-1], other[KL/2-1]) as well as below either list's KL-th.
+    const float own_k = Ld[KL - 1], own_h = Ld[KL / 2 - 1];
+    const float oth_k = __shfl_xor(own_k, 32, 64), oth_h = __shfl_xor(own_h, 32, 64);
+    float t = fminf(fminf(own_k, oth_k), fmaxf(own_h, oth_h));
+    if (qvalid) {
+      uint32_t g;
+      if (h == 0) g = atomicMin(&a.qthr[q], float_to_ordered(t));
+      g = __shfl(g, j, 64);
+      t = fminf(t, ordered_to_float(g));
+    }
+    pthr = fminf(pthr, t);
+  };
+
+  // Candidate queue of this lane: appended in row order, inserted into the list by a wave-wide
+  // flush (all lanes at once) when any queue could overflow on the next block.
+  int qcount = 0;
+  auto flush_queue = [&]() {
+    int m = qcount;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = max(m, __shfl_xor(m, off, 64));
+    for (int e = 0; e < m; ++e) {
+      if (e < qcount) {
+        float v = s_qd[e * kThreads + tid];
+        v = v == v ? v : __builtin_huge_valf();
+        if (v <= Ld[KL - 1]) list_insert<KL>(Ld, Lr, v, s_qr[e * kThreads + tid]);
+      }
+    }
+    qcount = 0;
+  };
+
   const uint64_t r0 = static_cast<uint64_t>(split) * a.rows_per_split;
   const uint64_t r1 = r0 < a.n ? (a.n < r0 + a.rows_per_split ? a.n : r0 + a.rows_per_split) : r0;
   const uint32_t ntiles = static_cast<uint32_t>(ceil_div(r1 - r0, kTileRows));
@@ -135,22 +178,25 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
   f32x4 stage[PER_THREAD];
   float stage_norm = 0.0f;
   uint64_t stage_bits = ~0ull;
+  // Unconditional loads (rows past the split repeat its last row; the epilogue masks them), so no
+  // load sits under an exec-mask branch and the prefetch of the next tile stays in flight while
+  // this tile's MFMAs run.
+  const uint64_t last_row = r1 > r0 ? r1 - 1 : r0;
   auto load_tile = [&](uint32_t t) {
     const uint64_t base = r0 + static_cast<uint64_t>(t) * kTileRows;
 #pragma unroll
     for (int p = 0; p < PER_THREAD; ++p) {
-      const int c = tid + p * kThreads;
+      int c = tid + p * kThreads;
+      if (CHUNKS % kThreads != 0) c = c < CHUNKS ? c : CHUNKS - 1;
       const int row = c / C4, col = c % C4;
-      const uint64_t gr = base + row;
-      stage[p] = (c < CHUNKS && gr < r1)
-                     ? *reinterpret_cast<const f32x4*>(a.X + gr * DP + 4 * col)
-                     : f32x4{0.f, 0.f, 0.f, 0.f};
+      uint64_t gr = base + row;
+      gr = gr < last_row ? gr : last_row;
+      stage[p] = *reinterpret_cast<const f32x4*>(a.X + gr * DP + 4 * col);
     }
-    if (tid < kTileRows) {
-      const uint64_t gr = base + tid;
-      stage_norm = gr < r1 ? a.xnorm[gr] : 0.0f;
-    }
-    if (tid == kTileRows && a.bitmap) stage_bits = a.bitmap[base >> 6];
+    uint64_t gn = base + (tid & (kTileRows - 1));
+    gn = gn < last_row ? gn : last_row;
+    stage_norm = a.xnorm[gn];
+    if constexpr (FILTER) stage_bits = a.bitmap[base >> 6];
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
@@ -162,7 +208,7 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
       }
     }
     if (tid < kTileRows) s_norm[buf][tid] = stage_norm;
-    if (tid == kTileRows) s_bits[buf] = stage_bits;
+    if (FILTER && tid == kTileRows) s_bits[buf] = stage_bits;
   };
 
   if (ntiles > 0) {
@@ -173,8 +219,19 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
 
   for (uint32_t t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
-    if (t + 1 < ntiles) load_tile(t + 1);
+    const bool prefetch = t + 1 < ntiles;
+    if (!wave_active && prefetch) load_tile(t + 1);
     if (wave_active) {
+      // Row norms of this lane's 32 rows: rows 8*g + 4*h + (0..3) of each 32-row block, g=0..3,
+      // four b128 reads per block, issued before the MFMAs so their latency is covered.
+      f32x4 xn[2][4];
+      if constexpr (L2) {
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            xn[blk][g] = *reinterpret_cast<const f32x4*>(&s_norm[buf][32 * blk + 8 * g + 4 * h]);
+      }
       f32x16 acc0 = {}, acc1 = {};
       const float* a0 = &s_tile[buf][j * STRIDE + h * H];
       const float* a1 = &s_tile[buf][(32 + j) * STRIDE + h * H];
@@ -201,53 +258,72 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
         x0 = n0;
         x1 = n1;
         __builtin_amdgcn_sched_barrier(0);
+        // The next tile's global loads go out once the MFMA pipe is busy, so no wait for them
+        // lands in front of this tile's first MFMAs.
+        if (s == 4 && prefetch) load_tile(t + 1);
+        if (s == 4) __builtin_amdgcn_sched_barrier(0);
       }
       // D[row][col] of a 32x32 block: col = lane % 32 (query j), row = 8*(r/4) + 4*h + r%4 in
       // register r. Per lane the rows visited increase, so ties resolve to the smaller row.
       const uint64_t tile_row0 = r0 + static_cast<uint64_t>(t) * kTileRows;
-      const uint64_t bits = s_bits[buf];
-      const float* tn = s_norm[buf];
-      float* spill = &s_spill[tid * 16];
+      const uint64_t left = r1 - tile_row0;  // rows of this tile inside the split
+      // Admitted rows of the tile (bit i = row tile_row0 + i), shifted to this lane half.
+      uint64_t admit = FILTER ? s_bits[buf] : ~0ull;
+      if (left < 64) admit &= (1ull << left) - 1;
+      const bool masked = FILTER || left < 64;
 #pragma unroll
       for (int blk = 0; blk < 2; ++blk) {
         const f32x16 acc = blk ? acc1 : acc0;
-        // Fast path: distances and a mask of the rows that beat this lane's current k-th.
-        const float thr = Ld[KL - 1];
+        const uint32_t lane_bits = static_cast<uint32_t>(admit >> (32 * blk)) >> (4 * h);
+        // Fast path: distance and "may pass" test. NaN passes here (!(d > thr)) so the slow
+        // path can turn it into +inf as the reference does.
+        const float thr = fminf(pthr, Ld[KL - 1]);
         float d[16];
-        uint32_t pass = 0;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int i = 32 * blk + 8 * (r >> 2) + 4 * h + (r & 3);
-          float v = a.l2 ? (qn + tn[i]) - 2.0f * acc[r] : 1.0f - acc[r];
-          v = v == v ? v : __builtin_huge_valf();
-          d[r] = v;
-          const bool ok = (tile_row0 + i < r1) & (((bits >> i) & 1ull) != 0);
-          pass |= (ok & (v <= thr)) ? (1u << r) : 0u;
-        }
-        // Slow path (rare after the first tiles): park the 16 distances in LDS and insert the
-        // passing ones in row order.
-        if (pass) {
-#pragma unroll
-          for (int r = 0; r < 16; r += 4) {
-            *reinterpret_cast<f32x4*>(spill + r) = f32x4{d[r], d[r + 1], d[r + 2], d[r + 3]};
+          if constexpr (L2) {
+            d[r] = fmaf(-2.0f, acc[r], qn + xn[blk][r >> 2][r & 3]);
+          } else {
+            d[r] = 1.0f - acc[r];
           }
-          while (pass) {
-            const int r = __builtin_ctz(pass);
-            pass &= pass - 1;
-            const float v = spill[r];
-            if (v <= Ld[KL - 1]) {
-              const uint32_t row = static_cast<uint32_t>(
-                  tile_row0 + 32 * blk + 8 * (r >> 2) + 4 * h + (r & 3));
-              list_insert<KL>(Ld, Lr, v, row);
+        }
+        bool any = false;
+        if (!masked) {  // wave-uniform: full tile, no filter
+#pragma unroll
+          for (int r = 0; r < 16; ++r) any = any || !(d[r] > thr);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            any = any || (!(d[r] > thr) && ((lane_bits >> (8 * (r >> 2) + (r & 3))) & 1u));
+          }
+        }
+        // Slow path: append this lane's passing, admitted candidates to its queue.
+        if (__builtin_amdgcn_ballot_w64(qcount > kQueueCap - 16)) flush_queue();
+        if (any) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int bit = 8 * (r >> 2) + (r & 3);
+            bool p = !(d[r] > thr);
+            if (masked) p = p && ((lane_bits >> bit) & 1u);
+            if (p) {
+              s_qd[qcount * kThreads + tid] = d[r];
+              s_qr[qcount * kThreads + tid] =
+                  static_cast<uint32_t>(tile_row0 + 32 * blk + 4 * h + bit);
+              ++qcount;
             }
           }
         }
       }
     }
+    if (wave_active && (t % kShareEvery) == kShareEvery - 1) {
+      flush_queue();
+      share_threshold();
+    }
     if (t + 1 < ntiles) store_tile(buf ^ 1);
     __syncthreads();
   }
 
+  if (wave_active) flush_queue();
   if (qvalid) {
     const size_t o = (static_cast<size_t>(q) * (2 * a.nsplit) + 2 * split + h) * KL;
 #pragma unroll
@@ -371,31 +447,54 @@ __global__ void row_norms_kernel(const float* __restrict__ rows, float* __restri
   out[r] = s;
 }
 
+__global__ void fill_u32_kernel(uint32_t* p, uint64_t n, uint32_t v) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
 uint32_t padded_dim(uint32_t dim) {
   for (uint32_t dp : {16u, 32u, 48u, 64u, 80u, 96u, 112u, 128u})
     if (dim <= dp) return dp;
   return 0;
 }
 
-template <int DP>
-void launch_scan_dp(int kl, dim3 grid, const ScanArgs& a, hipStream_t s) {
-  if (kl == 16) {
-    hipLaunchKernelGGL((flat_scan_kernel<DP, 16>), grid, dim3(kThreads), 0, s, a);
+template <int DP, int KL>
+void launch_scan_kl(bool l2, bool filter, dim3 grid, const ScanArgs& a, hipStream_t s) {
+  if (l2) {
+    if (filter) {
+      hipLaunchKernelGGL((flat_scan_kernel<DP, KL, true, true>), grid, dim3(kThreads), 0, s, a);
+    } else {
+      hipLaunchKernelGGL((flat_scan_kernel<DP, KL, true, false>), grid, dim3(kThreads), 0, s, a);
+    }
   } else {
-    hipLaunchKernelGGL((flat_scan_kernel<DP, 32>), grid, dim3(kThreads), 0, s, a);
+    if (filter) {
+      hipLaunchKernelGGL((flat_scan_kernel<DP, KL, false, true>), grid, dim3(kThreads), 0, s, a);
+    } else {
+      hipLaunchKernelGGL((flat_scan_kernel<DP, KL, false, false>), grid, dim3(kThreads), 0, s, a);
+    }
+  }
+}
+
+template <int DP>
+void launch_scan_dp(int kl, bool l2, bool filter, dim3 grid, const ScanArgs& a, hipStream_t s) {
+  if (kl == 16) {
+    launch_scan_kl<DP, 16>(l2, filter, grid, a, s);
+  } else {
+    launch_scan_kl<DP, 32>(l2, filter, grid, a, s);
   }
 }
 
 void launch_scan(uint32_t dp, int kl, dim3 grid, const ScanArgs& a, hipStream_t s) {
+  const bool l2 = a.l2 != 0, filter = a.bitmap != nullptr;
   switch (dp) {
-    case 16: launch_scan_dp<16>(kl, grid, a, s); break;
-    case 32: launch_scan_dp<32>(kl, grid, a, s); break;
-    case 48: launch_scan_dp<48>(kl, grid, a, s); break;
-    case 64: launch_scan_dp<64>(kl, grid, a, s); break;
-    case 80: launch_scan_dp<80>(kl, grid, a, s); break;
-    case 96: launch_scan_dp<96>(kl, grid, a, s); break;
-    case 112: launch_scan_dp<112>(kl, grid, a, s); break;
-    case 128: launch_scan_dp<128>(kl, grid, a, s); break;
+    case 16: launch_scan_dp<16>(kl, l2, filter, grid, a, s); break;
+    case 32: launch_scan_dp<32>(kl, l2, filter, grid, a, s); break;
+    case 48: launch_scan_dp<48>(kl, l2, filter, grid, a, s); break;
+    case 64: launch_scan_dp<64>(kl, l2, filter, grid, a, s); break;
+    case 80: launch_scan_dp<80>(kl, l2, filter, grid, a, s); break;
+    case 96: launch_scan_dp<96>(kl, l2, filter, grid, a, s); break;
+    case 112: launch_scan_dp<112>(kl, l2, filter, grid, a, s); break;
+    case 128: launch_scan_dp<128>(kl, l2, filter, grid, a, s); break;
     default: throw Failure(QVH_EUNSUPPORTED, "flat scan: unsupported padded dimension");
   }
 }
@@ -411,7 +510,12 @@ struct qvh_flat {
   hipStream_t stream = nullptr;
   std::mutex mu;
   // per-call workspace (grown on demand, serialized by mu)
-  DeviceBuffer w_stage, w_q, w_qn, w_pd, w_pr, w_rows, w_dist, w_bits;
+  DeviceBuffer w_stage, w_q, w_qn, w_pd, w_pr, w_rows, w_dist, w_bits, w_thr;
+  // optional per-stage timing of the last search: events before prep, scan, merge and after
+  bool timing = false;
+  bool timed = false;
+  hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
+  uint64_t last_nsplit = 0;
 };
 
 namespace {
@@ -461,18 +565,36 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
   QVH_REQUIRE(k <= 32, "flat search: k > 32 is not supported on the device path yet");
   QVH_REQUIRE(nq <= 0xFFFFFFFFull, "flat search: too many queries in one call");
   const int kl = k <= 16 ? 16 : 32;
+  f->timed = f->timing;
+  if (f->timed) QVH_HIP(hipEventRecord(f->ev[0], s));
   flat_prep_queries(f, d_queries, nq, s);
+  if (f->timed) QVH_HIP(hipEventRecord(f->ev[1], s));
 
   int cus = 256;
   (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, f->device);
   const uint32_t qblocks = static_cast<uint32_t>(ceil_div(nq, kQueriesPerBlock));
   const uint64_t tiles = std::max<uint64_t>(1, ceil_div(f->n, kTileRows));
-  uint64_t nsplit = ceil_div(static_cast<uint64_t>(4 * cus), qblocks);
-  nsplit = std::min<uint64_t>({nsplit, tiles, kMaxSplits});
-  if (nsplit >= 8) nsplit -= nsplit % 8;
-  nsplit = std::max<uint64_t>(nsplit, 1);
+  // One workgroup per CU at a time: pick the split count (a multiple of 8 for the XCD mapping)
+  // whose workgroup count best fills whole rounds of the CUs; fewer splits on ties.
+  uint64_t nsplit = 1;
+  {
+    const uint64_t cap = std::min<uint64_t>(tiles, kMaxSplits);
+    double best = -1.0;
+    for (uint64_t c = 1; c <= cap; c = c < 8 ? c + 1 : c + 8) {
+      if (c >= 8 && c % 8) continue;
+      const uint64_t total = qblocks * c;
+      const uint64_t rounds = ceil_div(total, static_cast<uint64_t>(cus));
+      // prefer enough parallelism (>= 4 rounds when the rows allow) and full rounds
+      const double fill = static_cast<double>(total) / static_cast<double>(rounds * cus);
+      const double par = std::min(1.0, static_cast<double>(total) / (4.0 * cus));
+      const double score = fill * par;
+      if (score > best + 1e-9) {
+        best = score;
+        nsplit = c;
+      }
+    }
+  }
   const uint64_t rows_per_split = ceil_div(tiles, nsplit) * kTileRows;
-
   const size_t parts = static_cast<size_t>(nq) * 2 * nsplit * kl;
   ScanArgs a;
   a.X = f->rows.as<float>();
@@ -488,8 +610,13 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
   a.rows_per_split = rows_per_split;
   a.part_d = static_cast<float*>(f->w_pd.reserve(parts * sizeof(float)));
   a.part_r = static_cast<uint32_t*>(f->w_pr.reserve(parts * sizeof(uint32_t)));
+  a.qthr = static_cast<uint32_t*>(f->w_thr.reserve(nq * sizeof(uint32_t)));
+  hipLaunchKernelGGL(fill_u32_kernel, dim3(static_cast<unsigned>(ceil_div(nq, 256))), dim3(256), 0, s,
+                     a.qthr, nq, 0xFF800000u);  // ordered bits of +inf
   launch_scan(f->dp, kl, dim3(static_cast<unsigned>(qblocks * nsplit)), a, s);
   QVH_HIP(hipGetLastError());
+  if (f->timed) QVH_HIP(hipEventRecord(f->ev[2], s));
+  f->last_nsplit = nsplit;
 
   MergeArgs m;
   m.X = a.X;
@@ -511,6 +638,7 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
     hipLaunchKernelGGL(flat_merge_kernel<32>, mgrid, dim3(256), 0, s, m);
   }
   QVH_HIP(hipGetLastError());
+  if (f->timed) QVH_HIP(hipEventRecord(f->ev[3], s));
 }
 
 }  // namespace
@@ -547,7 +675,39 @@ void qvh_flat_destroy(qvh_flat* f) {
     (void)hipStreamSynchronize(f->stream);
     (void)hipStreamDestroy(f->stream);
   }
+  for (hipEvent_t& e : f->ev) {
+    if (e) (void)hipEventDestroy(e);
+  }
   delete f;
+}
+
+qvh_status qvh_flat_set_timing(qvh_flat* f, int enable) {
+  return guarded([&] {
+    QVH_REQUIRE(f != nullptr, "qvh_flat_set_timing: null handle");
+    std::lock_guard<std::mutex> lock(f->mu);
+    QVH_HIP(hipSetDevice(f->device));
+    if (enable && !f->ev[0]) {
+      for (hipEvent_t& e : f->ev) QVH_HIP(hipEventCreate(&e));
+    }
+    f->timing = enable != 0;
+  });
+}
+
+qvh_status qvh_flat_last_timing(qvh_flat* f, float* prep_ms, float* scan_ms, float* merge_ms,
+                                uint32_t* nsplit) {
+  return guarded([&] {
+    QVH_REQUIRE(f != nullptr, "qvh_flat_last_timing: null handle");
+    std::lock_guard<std::mutex> lock(f->mu);
+    QVH_REQUIRE(f->timed, "qvh_flat_last_timing: the last search was not timed");
+    QVH_HIP(hipSetDevice(f->device));
+    QVH_HIP(hipEventSynchronize(f->ev[3]));
+    float t[3];
+    for (int i = 0; i < 3; ++i) QVH_HIP(hipEventElapsedTime(&t[i], f->ev[i], f->ev[i + 1]));
+    if (prep_ms) *prep_ms = t[0];
+    if (scan_ms) *scan_ms = t[1];
+    if (merge_ms) *merge_ms = t[2];
+    if (nsplit) *nsplit = static_cast<uint32_t>(f->last_nsplit);
+  });
 }
 
 uint64_t qvh_flat_size(const qvh_flat* f) { return f ? f->n : 0; }
