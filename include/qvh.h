@@ -103,6 +103,73 @@ qvh_status qvh_flat_set_timing(qvh_flat* flat, int enable);
 qvh_status qvh_flat_last_timing(qvh_flat* flat, float* prep_ms, float* scan_ms, float* merge_ms,
                                 uint32_t* nsplit);
 
+/* ------------------------------------------------------------------------------------------ *
+ * IVF-PQ: replaces the encode step of IvfPqIndex::Impl::add (src/ivfpq_index.cc:208-271) and
+ * the query path of IvfPqIndex::Impl::search_into (src/ivfpq_index.cc:275-381). Lists live on
+ * the device in CSR order (the LOFF/CODE/VECT layout of src/ivfpq_index.cc:479-503); labels stay
+ * with the caller, who maps refs back to them.
+ * ------------------------------------------------------------------------------------------ */
+
+/* IvfPqIndex(params) (src/ivfpq_index.cc:95-103): dim, metric, nlist, m (dim % m == 0),
+ * store_vectors. */
+qvh_status qvh_ivfpq_create(uint32_t dim, int metric, uint32_t nlist, uint32_t m, int store_vectors,
+                            qvh_ivfpq** out);
+void qvh_ivfpq_destroy(qvh_ivfpq* ivf);
+
+/* Installs the trained state, as Impl::train commits it (src/ivfpq_index.cc:199-205): coarse
+ * centroids [nlist][dim] and PQ codebook [m][256][dim/m]. With use_precomputed (L2 only) the
+ * device builds the nlist x m x 256 term table of Impl::precompute (src/ivfpq_index.cc:112-129). */
+qvh_status qvh_ivfpq_set_trained(qvh_ivfpq* ivf, const float* centroids, const float* codebook,
+                                 int use_precomputed);
+/* Copies the precomputed table [nlist][m][256] to the host. */
+qvh_status qvh_ivfpq_precomputed(qvh_ivfpq* ivf, float* out);
+
+/* Cells and PQ codes of n vectors without storing them (src/ivfpq_index.cc:235-246):
+ * assign[n] (nullable), codes[n][m] (nullable), stored_out[n][dim] = the vectors as stored
+ * (normalized for cosine; nullable). */
+qvh_status qvh_ivfpq_encode(qvh_ivfpq* ivf, const float* x, uint64_t n, uint32_t* assign,
+                            uint8_t* codes, float* stored_out);
+
+/* Impl::add (src/ivfpq_index.cc:208-271): encodes n vectors and appends them to their lists in
+ * input order. assign_out[n] (nullable) receives each vector's list, which the caller needs to
+ * place its labels. */
+qvh_status qvh_ivfpq_add(qvh_ivfpq* ivf, const float* x, uint64_t n, uint32_t* assign_out);
+
+uint64_t qvh_ivfpq_size(const qvh_ivfpq* ivf);
+/* CSR offsets [nlist + 1] of the lists. */
+qvh_status qvh_ivfpq_list_offsets(qvh_ivfpq* ivf, uint64_t* offsets);
+/* Stored codes [count][m] and vectors [count][dim] (nullable each) in CSR order. */
+qvh_status qvh_ivfpq_lists(qvh_ivfpq* ivf, uint8_t* codes, float* vectors);
+
+/* search_into for nq raw queries (normalized here for cosine): nprobe clamped to [1, nlist],
+ * keep = min(size, k * refine_factor) with refine only when vectors are stored,
+ * `pos_bitmap` (nullable, ceil(size/64) words over CSR positions) is the Filter. Outputs nq*k
+ * refs ((list << 32) | offset in list, QVH_EMPTY_REF when empty) and distances. */
+qvh_status qvh_ivfpq_search(qvh_ivfpq* ivf, const float* queries, uint64_t nq, uint32_t k,
+                            uint32_t nprobe, uint64_t refine_factor, const uint64_t* pos_bitmap,
+                            uint64_t* out_refs, float* out_dist);
+/* Same on device-resident buffers, enqueued on `stream` (NULL = the handle's). */
+qvh_status qvh_ivfpq_search_device(qvh_ivfpq* ivf, const float* d_queries, uint64_t nq,
+                                   uint32_t k, uint32_t nprobe, uint64_t refine_factor,
+                                   const uint64_t* d_pos_bitmap, uint64_t* d_out_refs,
+                                   float* d_out_dist, void* stream);
+qvh_status qvh_ivfpq_sync(qvh_ivfpq* ivf);
+/* Measurement hook (no counterpart in the reference): HIP events around the probe selection
+ * (query prep, coarse scores, top-nprobe) and the list scan of each search. */
+qvh_status qvh_ivfpq_set_timing(qvh_ivfpq* ivf, int enable);
+qvh_status qvh_ivfpq_last_timing(qvh_ivfpq* ivf, float* select_ms, float* scan_ms);
+
+/* ------------------------------------------------------------------------------------------ *
+ * Nearest-centroid assignment for k-means (src/product_quantizer.cc:72-77), restating
+ * CentroidTable::nearest_batch (src/internal/centroid_table.h:94-144) bit for bit: a device
+ * resident point set assigned repeatedly against changing centroids.
+ * ------------------------------------------------------------------------------------------ */
+typedef struct qvh_points qvh_points;
+qvh_status qvh_points_create(const float* x, uint64_t n, uint32_t dim, qvh_points** out);
+void qvh_points_destroy(qvh_points* points);
+qvh_status qvh_points_nearest(qvh_points* points, const float* centroids, uint32_t k,
+                              int max_inner_product, uint32_t* out_assign);
+
 #ifdef __cplusplus
 }
 #endif

@@ -35,7 +35,7 @@ def _load_extension():
 _quiver = _load_extension()
 simd_isa = _quiver.simd_isa
 
-__all__ = ["FlatIndex", "simd_isa"]
+__all__ = ["FlatIndex", "IvfPqIndex", "kmeans", "simd_isa"]
 __version__ = "0.1.0"
 
 ArrayLike = Union[np.ndarray, Iterable]
@@ -85,6 +85,86 @@ def _as_labels(labels: Optional[ArrayLike], n: Optional[int] = None) -> Optional
     if n is not None and a.shape[0] != n:
         raise ValueError(f"got {a.shape[0]} labels for {n} vectors")
     return a
+
+
+class IvfPqIndex:
+    """Inverted-file index over product-quantized residuals: ~``m`` bytes per vector.
+
+    Args:
+        dim: vector dimensionality (must be divisible by ``m``).
+        metric: ``"l2"``, ``"ip"``, or ``"cosine"``.
+        nlist: number of coarse cells (roughly ``4 * sqrt(n)``).
+        m: bytes per vector (PQ sub-quantizers).
+        store_vectors: keep float32 copies to enable exact re-ranking (``refine_factor``).
+
+    Call :meth:`train` on a representative sample before :meth:`add`. Encoding and search run on
+    the GPU; training runs the reference's k-means with its assignment steps on the GPU.
+    """
+
+    def __init__(self, dim: int, metric: str = "l2", nlist: int = 1024, m: int = 16,
+                 store_vectors: bool = False, train_iterations: int = 20, seed: int = 1234,
+                 *, _native=None):
+        self._index = _native if _native is not None else _quiver.IvfPqIndex(
+            dim, metric, nlist, m, store_vectors, train_iterations, seed)
+
+    def train(self, vectors: ArrayLike, num_threads: int = 0) -> None:
+        self._index._train(_as_matrix(vectors, self.dim), num_threads)
+
+    def add(self, vectors: ArrayLike, labels: Optional[ArrayLike] = None, num_threads: int = 0) -> None:
+        x = _as_matrix(vectors, self.dim)
+        self._index._add(x, _as_labels(labels, x.shape[0]), num_threads)
+
+    def search(self, queries: ArrayLike, k: int = 10, nprobe: int = 16, refine_factor: int = 0,
+               filter: Optional[ArrayLike] = None, num_threads: int = 0) -> Tuple[np.ndarray, np.ndarray]:
+        q = _as_matrix(queries, self.dim)
+        if k <= 0:
+            raise ValueError("k must be positive")
+        allowed = _as_labels(filter) if filter is not None else None
+        return self._index._search(q, int(k), int(nprobe), int(refine_factor), allowed, num_threads)
+
+    def set_trained(self, centroids: ArrayLike, codebook: ArrayLike) -> None:
+        """Install trained state (coarse centroids [nlist, dim], PQ codebook [m, 256, dim/m])
+        instead of training, e.g. state trained elsewhere."""
+        self._index._set_trained(np.ascontiguousarray(centroids, dtype=np.float32),
+                                 np.ascontiguousarray(codebook, dtype=np.float32))
+
+    @property
+    def centroids(self) -> np.ndarray:
+        return self._index._centroids()
+
+    @property
+    def codebook(self) -> np.ndarray:
+        return self._index._codebook()
+
+    def lists(self):
+        """(offsets [nlist+1], labels, codes [n, m]) in list order."""
+        return self._index._list_offsets(), self._index._list_labels(), self._index._list_codes()
+
+    def list_vectors(self) -> np.ndarray:
+        return self._index._list_vectors()
+
+    def list_sizes(self):
+        return self._index.list_sizes()
+
+    def __len__(self) -> int:
+        return len(self._index)
+
+    dim = property(lambda self: self._index.dim)
+    metric = property(lambda self: self._index.metric)
+    nlist = property(lambda self: self._index.nlist)
+    m = property(lambda self: self._index.m)
+    is_trained = property(lambda self: self._index.is_trained)
+    memory_bytes = property(lambda self: self._index.memory_bytes)
+
+    def __repr__(self) -> str:
+        return f"IvfPqIndex(dim={self.dim}, nlist={self.nlist}, m={self.m}, size={len(self)})"
+
+
+def kmeans(vectors: ArrayLike, k: int, iterations: int = 25, max_points_per_centroid: int = 256,
+           seed: int = 1234, num_threads: int = 0) -> np.ndarray:
+    """Lloyd's k-means with the reference's initialization and empty-cluster rule (k x dim)."""
+    x = np.ascontiguousarray(vectors, dtype=np.float32)
+    return _quiver.kmeans(x, int(k), int(iterations), int(max_points_per_centroid), int(seed), num_threads)
 
 
 class FlatIndex:

@@ -1,0 +1,1190 @@
+// IVF-PQ on gfx950: batched encode on add (IvfPqIndex::Impl::add, src/ivfpq_index.cc:208-271) and
+// the query path of IvfPqIndex::Impl::search_into (src/ivfpq_index.cc:275-381).
+//
+// Device layout (one handle):
+//   centroids   [nlist][dim] and transposed [dim][nlist]; ||c||^2 per centroid
+//   codebook    [m][256][dsub] and, per sub-space, transposed [m][dsub][256]
+//   precomputed [nlist][m][256] (L2 only, when it fits the reference's 256 MiB budget)
+//   lists in CSR order: offsets [nlist+1] (u64), codes [count][mp] (u8, mp = m rounded up to 4),
+//   term1 [count] (L2 precomputed: sum_j pre[l][j][code_j]), vectors [count][dim] (store_vectors)
+// Labels stay on the host; the device speaks of CSR positions and refs (list << 32 | offset).
+//
+// Arithmetic: assignment, PQ codes, coarse scores, the precomputed table, the per-query tables and
+// the ADC sums replay the reference's unfused, in-order float operations (all qvh sources are
+// compiled with -ffp-contract=off), so codes and assignments are bit-identical. For L2 with the
+// precomputed table the scan ranks candidates by base + term1 + sum_j qtab[j][c_j] (the same
+// quantity, grouped differently), then re-scores the best keep + margin candidates exactly as the
+// reference adds them (base + sum_j (pre[l][j][c_j] + qtab[j][c_j])).
+#include <algorithm>
+#include <cstring>
+#include <numeric>
+#include <vector>
+
+#include "common.hpp"
+#include "exact.hpp"
+
+namespace qvh {
+void launch_normalize_rows(float* d_rows, uint64_t n, uint32_t dim, hipStream_t stream);
+}
+
+namespace {
+
+using namespace qvh;
+
+constexpr int kModePre = 0;       // L2 with precomputed table (approximate scan + exact re-score)
+constexpr int kModeIp = 1;        // inner product / cosine: exact scan
+constexpr int kModeResidual = 2;  // L2 without precomputed table: per-list residual tables, exact
+
+// ---- exact nearest centroid / PQ encode -------------------------------------------------------
+
+constexpr int kNearThreads = 256;
+constexpr int kNearCT = 64;  // centroids per tile (accumulators per thread)
+constexpr int kNearJC = 32;  // dims per staged chunk
+
+struct NearestArgs {
+  const float* x;        // point p, dim t at x[p * x_stride + x_off + t]
+  uint64_t n;
+  uint32_t dim;
+  uint64_t x_stride;
+  uint32_t x_off;
+  const float* ct;       // transposed centroids [dim][k] (for the sub-space: + sub * dim * k)
+  const float* norms;    // [k] ||c||^2 (nearest mode)
+  uint32_t k;
+  int max_ip;
+  uint32_t* out32;       // nearest mode: out32[p]
+  uint8_t* out8;         // sqdiff mode: out8[p * out_stride + sub]
+  uint32_t out_stride;
+};
+
+/// SQDIFF = false: CentroidTable::nearest_batch (src/internal/centroid_table.h:94-144):
+///   dot_c = sum_j x_j * c_j in order of j, d_c = max_ip ? -dot_c : ||c||^2 - 2 dot_c, first strictly
+///   smaller wins, 0 if every d_c is NaN.
+/// SQDIFF = true: CentroidTable::l2 + argmin_n (centroid_table.h:65-75,155-170) for PQ encode:
+///   d_c = sum_t (x_t - c_t)^2 in order of t; the first index holding the minimum over the non-NaN
+///   values; 0 if there is none. blockIdx.y is the sub-space.
+template <bool SQDIFF>
+__global__ void __launch_bounds__(kNearThreads) nearest_kernel(NearestArgs a) {
+  __shared__ float s_x[kNearJC][kNearThreads];
+  __shared__ __attribute__((aligned(16))) float s_c[kNearJC][kNearCT];
+  const int tid = threadIdx.x;
+  const uint64_t p = static_cast<uint64_t>(blockIdx.x) * kNearThreads + tid;
+  const uint32_t sub = blockIdx.y;
+  const bool valid = p < a.n;
+  const uint64_t prow = valid ? p : 0;
+  const float* xrow = a.x + prow * a.x_stride + a.x_off + static_cast<uint64_t>(sub) * a.dim;
+  const float* ct = a.ct + static_cast<uint64_t>(sub) * a.dim * a.k;
+
+  float best = __builtin_huge_valf();
+  int64_t arg = -1;
+  for (uint32_t c0 = 0; c0 < a.k; c0 += kNearCT) {
+    float acc[kNearCT];
+#pragma unroll
+    for (int c = 0; c < kNearCT; ++c) acc[c] = 0.0f;
+    for (uint32_t j0 = 0; j0 < a.dim; j0 += kNearJC) {
+      const uint32_t jn = min(static_cast<uint32_t>(kNearJC), a.dim - j0);
+      __syncthreads();
+      for (uint32_t jj = 0; jj < jn; ++jj) s_x[jj][tid] = xrow[j0 + jj];
+      for (uint32_t e = tid; e < jn * kNearCT; e += kNearThreads) {
+        const uint32_t jj = e / kNearCT, c = e % kNearCT;
+        s_c[jj][c] = c0 + c < a.k ? ct[static_cast<uint64_t>(j0 + jj) * a.k + c0 + c] : 0.0f;
+      }
+      __syncthreads();
+      for (uint32_t jj = 0; jj < jn; ++jj) {
+        const float xv = s_x[jj][tid];
+#pragma unroll
+        for (int c = 0; c < kNearCT; c += 4) {
+          const float4 cv = *reinterpret_cast<const float4*>(&s_c[jj][c]);
+          if constexpr (SQDIFF) {
+            const float d0 = xv - cv.x, d1 = xv - cv.y, d2 = xv - cv.z, d3 = xv - cv.w;
+            acc[c + 0] = acc[c + 0] + d0 * d0;
+            acc[c + 1] = acc[c + 1] + d1 * d1;
+            acc[c + 2] = acc[c + 2] + d2 * d2;
+            acc[c + 3] = acc[c + 3] + d3 * d3;
+          } else {
+            acc[c + 0] = acc[c + 0] + xv * cv.x;
+            acc[c + 1] = acc[c + 1] + xv * cv.y;
+            acc[c + 2] = acc[c + 2] + xv * cv.z;
+            acc[c + 3] = acc[c + 3] + xv * cv.w;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < kNearCT; ++c) {
+      if (c0 + c < a.k) {
+        float d;
+        if constexpr (SQDIFF) {
+          d = acc[c];
+          // argmin_n: strictly smaller wins; the first +inf counts when nothing finite came first
+          if (d < best || (arg < 0 && d == best)) {
+            best = d;
+            arg = c0 + c;
+          }
+        } else {
+          d = a.max_ip ? -acc[c] : a.norms[c0 + c] - 2.0f * acc[c];
+          if (d < best) {
+            best = d;
+            arg = c0 + c;
+          }
+        }
+      }
+    }
+  }
+  if (!valid) return;
+  const uint32_t r = arg < 0 ? 0u : static_cast<uint32_t>(arg);
+  if constexpr (SQDIFF) {
+    a.out8[p * a.out_stride + sub] = static_cast<uint8_t>(r);
+  } else {
+    a.out32[p] = r;
+  }
+}
+
+/// ||c||^2 summed in order (centroid_table.h:50-57) and the transposed table t[j][c].
+__global__ void centroid_prep_kernel(const float* __restrict__ cent, uint32_t k, uint32_t dim,
+                                     float* __restrict__ ct, float* __restrict__ norms) {
+  const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= k) return;
+  float norm = 0.0f;
+  for (uint32_t j = 0; j < dim; ++j) {
+    const float v = cent[static_cast<uint64_t>(c) * dim + j];
+    ct[static_cast<uint64_t>(j) * k + c] = v;
+    norm = norm + v * v;
+  }
+  if (norms) norms[c] = norm;
+}
+
+/// Codebook [m][256][dsub] -> per sub-space transposed [m][dsub][256].
+__global__ void codebook_prep_kernel(const float* __restrict__ cb, uint32_t m, uint32_t dsub,
+                                     float* __restrict__ cbt) {
+  const uint64_t e = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= static_cast<uint64_t>(m) * 256 * dsub) return;
+  const uint32_t t = e % dsub, c = (e / dsub) % 256, j = static_cast<uint32_t>(e / (256ull * dsub));
+  cbt[(static_cast<uint64_t>(j) * dsub + t) * 256 + c] = cb[e];
+}
+
+/// residual[p] = x[p] - centroid[assign[p]] (src/ivfpq_index.cc:243).
+__global__ void residual_kernel(const float* __restrict__ x, const uint32_t* __restrict__ assign,
+                                const float* __restrict__ cent, uint64_t n, uint32_t dim,
+                                float* __restrict__ res) {
+  const uint64_t e = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= n * dim) return;
+  const uint64_t p = e / dim;
+  const uint32_t j = static_cast<uint32_t>(e % dim);
+  res[e] = x[e] - cent[static_cast<uint64_t>(assign[p]) * dim + j];
+}
+
+/// Impl::precompute (src/ivfpq_index.cc:117-127): sum_t r_t*r_t + (2*cl_t)*r_t, in order of t.
+__global__ void precompute_kernel(const float* __restrict__ cent, const float* __restrict__ cb,
+                                  uint32_t nlist, uint32_t dim, uint32_t m, float* __restrict__ pre) {
+  const uint64_t e = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= static_cast<uint64_t>(nlist) * m * 256) return;
+  const uint32_t dsub = dim / m;
+  const uint32_t c = e % 256, j = (e / 256) % m;
+  const uint64_t l = e / (256ull * m);
+  const float* cl = cent + l * dim + static_cast<uint64_t>(j) * dsub;
+  const float* r = cb + (static_cast<uint64_t>(j) * 256 + c) * dsub;
+  float v = 0.0f;
+  for (uint32_t t = 0; t < dsub; ++t) v = v + (r[t] * r[t] + 2.0f * cl[t] * r[t]);
+  pre[e] = v;
+}
+
+/// term1[p] = sum_j pre[assign[p]][j][code_j], accumulated in double and rounded once.
+__global__ void term1_kernel(const uint8_t* __restrict__ codes, uint32_t mp, const uint32_t* __restrict__ assign,
+                             const float* __restrict__ pre, uint32_t m, uint64_t n, float* __restrict__ out) {
+  const uint64_t p = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (p >= n) return;
+  const float* pl = pre + static_cast<uint64_t>(assign[p]) * m * 256;
+  const uint8_t* c = codes + p * mp;
+  double s = 0.0;
+  for (uint32_t j = 0; j < m; ++j) s += static_cast<double>(pl[j * 256 + c[j]]);
+  out[p] = static_cast<float>(s);
+}
+
+/// Codes of n points from [n][m] (sub-space minor) to the padded CSR stride.
+__global__ void pad_codes_kernel(const uint8_t* __restrict__ src, uint32_t m, uint32_t mp, uint64_t n,
+                                 uint8_t* __restrict__ dst) {
+  const uint64_t e = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= n * mp) return;
+  const uint64_t p = e / mp;
+  const uint32_t j = static_cast<uint32_t>(e % mp);
+  dst[e] = j < m ? src[p * m + j] : 0;
+}
+
+/// New CSR from the old one plus a batch: old entry at old position i of list l moves by
+/// shift[l]; batch entry b goes to dest[b].
+struct ScatterArgs {
+  const uint64_t* old_off;  // [nlist+1]
+  const uint64_t* shift;    // [nlist] cumulative batch sizes of the lists before l
+  uint32_t nlist;
+  uint64_t old_count, n_new;
+  const uint64_t* dest;     // [n_new]
+  uint32_t mp, dim;
+  const uint8_t* old_codes; const uint8_t* new_codes; uint8_t* codes;
+  const float* old_t1; const float* new_t1; float* t1;
+  const float* old_vec; const float* new_vec; float* vec;
+};
+
+__device__ __forceinline__ uint32_t list_of(const uint64_t* off, uint32_t nlist, uint64_t pos) {
+  // last l with off[l] <= pos (lists may be empty)
+  uint32_t lo = 0, hi = nlist;
+  while (hi - lo > 1) {
+    const uint32_t mid = (lo + hi) / 2;
+    if (off[mid] <= pos) lo = mid; else hi = mid;
+  }
+  return lo;
+}
+
+__global__ void scatter_old_kernel(ScatterArgs a) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= a.old_count) return;
+  const uint32_t l = list_of(a.old_off, a.nlist, i);
+  const uint64_t dst = i + a.shift[l];
+  for (uint32_t b = 0; b < a.mp; ++b) a.codes[dst * a.mp + b] = a.old_codes[i * a.mp + b];
+  if (a.t1) a.t1[dst] = a.old_t1[i];
+  if (a.vec) {
+    for (uint32_t j = 0; j < a.dim; ++j) a.vec[dst * a.dim + j] = a.old_vec[i * a.dim + j];
+  }
+}
+
+__global__ void scatter_new_kernel(ScatterArgs a) {
+  const uint64_t b = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (b >= a.n_new) return;
+  const uint64_t dst = a.dest[b];
+  for (uint32_t x = 0; x < a.mp; ++x) a.codes[dst * a.mp + x] = a.new_codes[b * a.mp + x];
+  if (a.t1) a.t1[dst] = a.new_t1[b];
+  if (a.vec) {
+    for (uint32_t j = 0; j < a.dim; ++j) a.vec[dst * a.dim + j] = a.new_vec[b * a.dim + j];
+  }
+}
+
+// ---- search: coarse scores and probe selection ------------------------------------------------
+
+constexpr int kCoarseQ = 8;  // queries per coarse workgroup
+
+/// Coarse scores (src/ivfpq_index.cc:285-297): L2: sum_j (q_j - c_j)^2; IP/cosine: -sum_j q_j c_j,
+/// both in order of j (centroid_table.h:65-85). Stored as the reference's probe key.
+__global__ void __launch_bounds__(256) coarse_kernel(const float* __restrict__ Q, uint32_t nq, uint32_t dim,
+                                                     const float* __restrict__ ct, uint32_t nlist, int ip,
+                                                     float* __restrict__ scores) {
+  extern __shared__ float s_q[];  // [kCoarseQ][dim]
+  const uint32_t c = blockIdx.x * 256 + threadIdx.x;
+  const uint32_t q0 = blockIdx.y * kCoarseQ;
+  const uint32_t nb = min(static_cast<uint32_t>(kCoarseQ), nq - q0);
+  for (uint32_t e = threadIdx.x; e < nb * dim; e += 256) s_q[e] = Q[static_cast<uint64_t>(q0) * dim + e];
+  __syncthreads();
+  if (c >= nlist) return;
+  float acc[kCoarseQ];
+#pragma unroll
+  for (int b = 0; b < kCoarseQ; ++b) acc[b] = 0.0f;
+  for (uint32_t j = 0; j < dim; ++j) {
+    const float cj = ct[static_cast<uint64_t>(j) * nlist + c];
+#pragma unroll
+    for (int b = 0; b < kCoarseQ; ++b) {
+      const float qv = s_q[(b < static_cast<int>(nb) ? b : 0) * dim + j];
+      if (ip) {
+        acc[b] = acc[b] + qv * cj;
+      } else {
+        const float d = qv - cj;
+        acc[b] = acc[b] + d * d;
+      }
+    }
+  }
+  for (uint32_t b = 0; b < nb; ++b) scores[static_cast<uint64_t>(q0 + b) * nlist + c] = ip ? -acc[b] : acc[b];
+}
+
+/// The nprobe smallest (score, list) per query, ascending (std::partial_sort of
+/// src/ivfpq_index.cc:298-300, with ties broken by the list id). One wave per query: every lane
+/// keeps the smallest key of its strided share above the last key popped.
+__global__ void __launch_bounds__(256) probe_select_kernel(const float* __restrict__ scores, uint32_t nq,
+                                                           uint32_t nlist, uint32_t nprobe,
+                                                           uint32_t* __restrict__ probes) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t q = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (q >= nq) return;
+  const float* sq = scores + static_cast<uint64_t>(q) * nlist;
+  auto my_next = [&](uint64_t above, bool first) {
+    uint64_t best = ~0ull;
+    for (uint32_t l = lane; l < nlist; l += 64) {
+      float s = sq[l];
+      s = s == s ? s : __builtin_huge_valf();
+      const uint64_t key = make_key(s, l);
+      if ((first || key > above) && key < best) best = key;
+    }
+    return best;
+  };
+  uint64_t cur = my_next(0, true);
+  for (uint32_t p = 0; p < nprobe; ++p) {
+    const uint64_t best = wave_min_u64(cur);
+    if (lane == 0) probes[static_cast<uint64_t>(q) * nprobe + p] = static_cast<uint32_t>(best);
+    if (cur == best) cur = my_next(best, false);
+  }
+}
+
+// ---- search: the scan ---------------------------------------------------------------------------
+
+constexpr int kScanThreads = 256;
+constexpr int kCandCap = 2048;       // LDS candidate buffer (u64 keys)
+constexpr int kScanRound = 4;        // codes per thread between buffer checks
+constexpr uint32_t kMaxKeepSel = kCandCap - kScanThreads * kScanRound;  // 1024
+
+struct ScanArgs {
+  uint32_t nq, k, m, mp, dsub, dim, nlist, nprobe;
+  int mode;
+  const float* Q;          // [nq][dim] prepared
+  const float* scores;     // [nq][nlist] probe keys
+  const uint32_t* probes;  // [nq][nprobe]
+  const uint64_t* off;     // [nlist+1]
+  const uint8_t* codes;    // [count][mp]
+  const float* t1;         // [count] (mode pre)
+  const float* pre;        // [nlist][m][256] (mode pre)
+  const float* cbt;        // [m][dsub][256]
+  const float* cent;       // [nlist][dim] (mode residual)
+  const float* vec;        // [count][dim] or null
+  const uint64_t* bitmap;  // admitted positions, or null
+  uint32_t keep, keep_sel;
+  int refine;
+  uint64_t* out_refs;
+  float* out_dist;
+};
+
+/// Ascending bitonic sort of s[0, n) (n a power of two) by all 256 threads.
+__device__ void block_sort_u64(uint64_t* s, uint32_t n) {
+  for (uint32_t size = 2; size <= n; size <<= 1) {
+    for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+      __syncthreads();
+      for (uint32_t i = threadIdx.x; i < n / 2; i += blockDim.x) {
+        const uint32_t lo = 2 * i - (i & (stride - 1));
+        const uint32_t hi = lo + stride;
+        const bool up = (lo & size) == 0;
+        const uint64_t a = s[lo], b = s[hi];
+        if ((a > b) == up) {
+          s[lo] = b;
+          s[hi] = a;
+        }
+      }
+    }
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ uint32_t pow2_at_least(uint32_t v) {
+  uint32_t p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+
+/// Loads the mp code bytes of position pos as dwords.
+template <int MPW>
+__device__ __forceinline__ void load_code(const uint8_t* codes, uint64_t pos, uint32_t mp, uint32_t (&w)[MPW]) {
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(codes + pos * mp);
+  if (mp % 16 == 0) {
+#pragma unroll
+    for (int i = 0; i < MPW; i += 4) {
+      if (4 * i < static_cast<int>(mp)) {
+        const uint4 v = *reinterpret_cast<const uint4*>(p + i);
+        w[i] = v.x;
+        if (i + 1 < MPW) w[i + 1] = v.y;
+        if (i + 2 < MPW) w[i + 2] = v.z;
+        if (i + 3 < MPW) w[i + 3] = v.w;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < MPW; ++i) {
+      if (4 * i < static_cast<int>(mp)) w[i] = p[i];
+    }
+  }
+}
+
+/// sum_j table[j*256 + code_j] in order of j (ProductQuantizer::adc, src/product_quantizer.cc:188-192).
+template <int MPW>
+__device__ __forceinline__ float adc_sum(const float* lut, const uint32_t (&w)[MPW], uint32_t m) {
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4 * MPW; ++j) {
+    if (j < static_cast<int>(m)) {
+      const uint32_t c = (w[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+      s = s + lut[j * 256 + c];
+    }
+  }
+  return s;
+}
+
+template <int MPW>
+__global__ void __launch_bounds__(kScanThreads) ivf_scan_kernel(ScanArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char s_raw[];
+  uint64_t* s_cand = reinterpret_cast<uint64_t*>(s_raw);                       // [kCandCap]
+  uint64_t* s_pstart = s_cand + kCandCap;                                      // [nprobe + 1] flattened starts
+  uint32_t* s_plist = reinterpret_cast<uint32_t*>(s_pstart + a.nprobe + 1);    // [nprobe]
+  float* s_lut = reinterpret_cast<float*>(s_plist + ((a.nprobe + 1) & ~1u));  // [m][256]
+  __shared__ uint32_t s_count;
+  __shared__ uint64_t s_thr;
+
+  const int tid = threadIdx.x;
+  const uint32_t q = blockIdx.x;
+  const float* qv = a.Q + static_cast<uint64_t>(q) * a.dim;
+  const float* qscore = a.scores + static_cast<uint64_t>(q) * a.nlist;
+  const uint32_t table = a.m * 256;
+
+  // Per-query table (src/ivfpq_index.cc:309-318): <q_j, C_{j,c}> in order of t, times -2 for L2.
+  if (a.mode != kModeResidual) {
+    for (uint32_t e = tid; e < table; e += kScanThreads) {
+      const uint32_t j = e / 256, c = e % 256;
+      const float* cb = a.cbt + static_cast<uint64_t>(j) * a.dsub * 256 + c;
+      const float* qj = qv + static_cast<uint64_t>(j) * a.dsub;
+      float v = 0.0f;
+      for (uint32_t t = 0; t < a.dsub; ++t) v = v + qj[t] * cb[t * 256];
+      s_lut[e] = a.mode == kModePre ? v * -2.0f : v;
+    }
+  }
+  // Probed lists and their flattened start offsets.
+  if (tid == 0) {
+    uint64_t acc = 0;
+    for (uint32_t p = 0; p < a.nprobe; ++p) {
+      const uint32_t l = a.probes[static_cast<uint64_t>(q) * a.nprobe + p];
+      s_plist[p] = l;
+      s_pstart[p] = acc;
+      acc += a.off[l + 1] - a.off[l];
+    }
+    s_pstart[a.nprobe] = acc;
+    s_count = 0;
+    s_thr = ~0ull;
+  }
+  __syncthreads();
+
+  const uint32_t keep_sel = a.keep_sel;
+  // Keeps the keep_sel smallest keys of the buffer and tightens the append threshold.
+  auto compact = [&]() {
+    __syncthreads();
+    const uint32_t cnt = min(s_count, static_cast<uint32_t>(kCandCap));
+    const uint32_t n2 = pow2_at_least(max(cnt, 2u));
+    for (uint32_t i = cnt + tid; i < n2; i += kScanThreads) s_cand[i] = ~0ull;
+    block_sort_u64(s_cand, n2);
+    if (tid == 0) {
+      const uint32_t kept = min(cnt, keep_sel);
+      s_count = kept;
+      if (kept == keep_sel && kept > 0) s_thr = min(s_thr, s_cand[kept - 1]);
+    }
+    __syncthreads();
+  };
+  auto offer = [&](float dist, uint64_t pos) {
+    dist = dist == dist ? dist : __builtin_huge_valf();
+    const uint64_t key = make_key(dist, static_cast<uint32_t>(pos));
+    if (key < s_thr) {
+      const uint32_t slot = atomicAdd(&s_count, 1u);
+      if (slot < kCandCap) s_cand[slot] = key;
+    }
+  };
+
+  if (a.mode != kModeResidual) {
+    // All probed lists as one sequence, dealt round-robin to the threads.
+    const uint64_t total = s_pstart[a.nprobe];
+    uint32_t p = 0;
+    for (uint64_t base_v = 0; base_v < total; base_v += static_cast<uint64_t>(kScanThreads) * kScanRound) {
+#pragma unroll
+      for (int r = 0; r < kScanRound; ++r) {
+        const uint64_t v = base_v + static_cast<uint64_t>(r) * kScanThreads + tid;
+        if (v < total) {
+          while (s_pstart[p + 1] <= v) ++p;
+          const uint32_t l = s_plist[p];
+          const uint64_t pos = a.off[l] + (v - s_pstart[p]);
+          if (!a.bitmap || ((a.bitmap[pos >> 6] >> (pos & 63)) & 1ull)) {
+            uint32_t w[MPW];
+            load_code<MPW>(a.codes, pos, a.mp, w);
+            const float s = adc_sum<MPW>(s_lut, w, a.m);
+            const float score = qscore[l];
+            float dist;
+            if (a.mode == kModeIp) {
+              dist = 1.0f - (-score + s);  // base = <q, c> (src/ivfpq_index.cc:333,346)
+            } else {
+              dist = score + (a.t1[pos] + s);
+            }
+            offer(dist, pos);
+          }
+        }
+      }
+      __syncthreads();
+      if (s_count + kScanThreads * kScanRound > kCandCap) compact();
+    }
+  } else {
+    // L2 without the precomputed table: a residual table per list (src/ivfpq_index.cc:338-342).
+    for (uint32_t p = 0; p < a.nprobe; ++p) {
+      const uint32_t l = s_plist[p];
+      const uint64_t b = a.off[l], len = a.off[l + 1] - b;
+      if (len == 0) continue;
+      __syncthreads();
+      const float* cl = a.cent + static_cast<uint64_t>(l) * a.dim;
+      for (uint32_t e = tid; e < table; e += kScanThreads) {
+        const uint32_t j = e / 256, c = e % 256;
+        const float* cb = a.cbt + static_cast<uint64_t>(j) * a.dsub * 256 + c;
+        float v = 0.0f;
+        for (uint32_t t = 0; t < a.dsub; ++t) {
+          const uint32_t dj = j * a.dsub + t;
+          const float r = qv[dj] - cl[dj];
+          const float d = r - cb[t * 256];
+          v = v + d * d;
+        }
+        s_lut[e] = v;
+      }
+      __syncthreads();
+      for (uint64_t i0 = 0; i0 < len; i0 += static_cast<uint64_t>(kScanThreads) * kScanRound) {
+#pragma unroll
+        for (int r = 0; r < kScanRound; ++r) {
+          const uint64_t i = i0 + static_cast<uint64_t>(r) * kScanThreads + tid;
+          if (i < len) {
+            const uint64_t pos = b + i;
+            if (!a.bitmap || ((a.bitmap[pos >> 6] >> (pos & 63)) & 1ull)) {
+              uint32_t w[MPW];
+              load_code<MPW>(a.codes, pos, a.mp, w);
+              offer(0.0f + adc_sum<MPW>(s_lut, w, a.m), pos);
+            }
+          }
+        }
+        __syncthreads();
+        if (s_count + kScanThreads * kScanRound > kCandCap) compact();
+      }
+    }
+  }
+  compact();
+  uint32_t cnt = s_count;  // sorted ascending, <= keep_sel
+
+  auto list_pos = [&](uint64_t pos) {
+    uint32_t p = 0;
+    while (p + 1 < a.nprobe && !(a.off[s_plist[p]] <= pos && pos < a.off[s_plist[p] + 1])) ++p;
+    return s_plist[p];
+  };
+
+  // Exact re-score of the approximate ranking (L2 with the precomputed table): the reference's
+  // table entry pre + qtab, summed in order of j, plus ||q - c||^2 (src/ivfpq_index.cc:334-346).
+  if (a.mode == kModePre) {
+    for (uint32_t i = tid; i < cnt; i += kScanThreads) {
+      const uint32_t pos = static_cast<uint32_t>(s_cand[i]);
+      const uint32_t l = list_pos(pos);
+      const float* pre = a.pre + static_cast<uint64_t>(l) * table;
+      uint32_t w[MPW];
+      load_code<MPW>(a.codes, pos, a.mp, w);
+      float s = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4 * MPW; ++j) {
+        if (j < static_cast<int>(a.m)) {
+          const uint32_t c = (w[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+          s = s + (pre[j * 256 + c] + s_lut[j * 256 + c]);
+        }
+      }
+      float dist = qscore[l] + s;
+      dist = dist == dist ? dist : __builtin_huge_valf();
+      s_cand[i] = make_key(dist, pos);
+    }
+    const uint32_t n2 = pow2_at_least(max(cnt, 2u));
+    __syncthreads();
+    for (uint32_t i = cnt + tid; i < n2; i += kScanThreads) s_cand[i] = ~0ull;
+    block_sort_u64(s_cand, n2);
+    cnt = min(cnt, a.keep);
+  }
+
+  // Exact re-ranking with the stored vectors (src/ivfpq_index.cc:139-142,363-373).
+  if (a.refine) {
+    for (uint32_t i = tid; i < cnt; i += kScanThreads) {
+      const uint32_t pos = static_cast<uint32_t>(s_cand[i]);
+      const float* x = a.vec + static_cast<uint64_t>(pos) * a.dim;
+      const float e = a.mode == kModeIp ? 1.0f - exact_dot(qv, x, a.dim) : exact_l2sqr(qv, x, a.dim);
+      s_cand[i] = make_key(e, pos);
+    }
+    const uint32_t n2 = pow2_at_least(max(cnt, 2u));
+    __syncthreads();
+    for (uint32_t i = cnt + tid; i < n2; i += kScanThreads) s_cand[i] = ~0ull;
+    block_sort_u64(s_cand, n2);
+  }
+
+  const uint32_t nout = min(cnt, a.k);
+  for (uint32_t j = tid; j < a.k; j += kScanThreads) {
+    uint64_t ref = QVH_EMPTY_REF;
+    float dist = __builtin_huge_valf();
+    if (j < nout) {
+      const uint64_t key = s_cand[j];
+      const uint32_t pos = static_cast<uint32_t>(key);
+      const uint32_t l = list_pos(pos);
+      ref = (static_cast<uint64_t>(l) << 32) | (pos - a.off[l]);
+      dist = ordered_to_float(static_cast<uint32_t>(key >> 32));
+    }
+    a.out_refs[static_cast<uint64_t>(q) * a.k + j] = ref;
+    a.out_dist[static_cast<uint64_t>(q) * a.k + j] = dist;
+  }
+}
+
+void launch_nearest(bool sqdiff, const NearestArgs& a, uint32_t nsub, hipStream_t s) {
+  if (a.n == 0) return;
+  const dim3 grid(static_cast<unsigned>(ceil_div(a.n, kNearThreads)), nsub);
+  if (sqdiff) {
+    hipLaunchKernelGGL(nearest_kernel<true>, grid, dim3(kNearThreads), 0, s, a);
+  } else {
+    hipLaunchKernelGGL(nearest_kernel<false>, grid, dim3(kNearThreads), 0, s, a);
+  }
+  QVH_HIP(hipGetLastError());
+}
+
+}  // namespace
+
+// ---- handle ---------------------------------------------------------------------------------------
+
+struct qvh_ivfpq {
+  uint32_t dim = 0, nlist = 0, m = 0, dsub = 0, mp = 0;
+  int metric = 0;
+  int store_vectors = 0;
+  int device = 0;
+  bool trained = false;
+  bool has_pre = false;
+  uint64_t count = 0;
+  std::vector<uint64_t> h_off;  // host copy of the list offsets
+  DeviceBuffer cent, cent_t, cent_norm, cb, cbt, pre;
+  DeviceBuffer off, codes, t1, vec;
+  hipStream_t stream = nullptr;
+  std::mutex mu;
+  DeviceBuffer w_x, w_res, w_assign, w_codes, w_codes_p, w_t1, w_dest, w_shift;
+  DeviceBuffer w_q, w_scores, w_probes, w_bits, w_refs, w_dist;
+  bool timing = false, timed = false;
+  hipEvent_t ev[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
+};
+
+namespace {
+
+int ivf_mode(const qvh_ivfpq* h) {
+  if (h->metric != QVH_METRIC_L2) return kModeIp;
+  return h->has_pre ? kModePre : kModeResidual;
+}
+
+/// Cells (src/ivfpq_index.cc:238) and codes (:239-245) of n device-resident rows `d_x` (already
+/// normalized for cosine). Results stay on the device in the handle workspace.
+void ivf_encode_device(qvh_ivfpq* h, const float* d_x, uint64_t n, hipStream_t s) {
+  uint32_t* assign = static_cast<uint32_t*>(h->w_assign.reserve(n * sizeof(uint32_t)));
+  NearestArgs na{};
+  na.x = d_x;
+  na.n = n;
+  na.dim = h->dim;
+  na.x_stride = h->dim;
+  na.x_off = 0;
+  na.ct = h->cent_t.as<float>();
+  na.norms = h->cent_norm.as<float>();
+  na.k = h->nlist;
+  na.max_ip = h->metric == QVH_METRIC_IP;
+  na.out32 = assign;
+  launch_nearest(false, na, 1, s);
+  float* res = static_cast<float*>(h->w_res.reserve(n * h->dim * sizeof(float)));
+  hipLaunchKernelGGL(residual_kernel, dim3(static_cast<unsigned>(ceil_div(n * h->dim, 256))), dim3(256), 0, s,
+                     d_x, assign, h->cent.as<float>(), n, h->dim, res);
+  uint8_t* codes = static_cast<uint8_t*>(h->w_codes.reserve(n * h->m));
+  NearestArgs pa{};
+  pa.x = res;
+  pa.n = n;
+  pa.dim = h->dsub;  // per sub-space
+  pa.x_stride = h->dim;
+  pa.x_off = 0;
+  pa.ct = h->cbt.as<float>();
+  pa.k = 256;
+  pa.out8 = codes;
+  pa.out_stride = h->m;
+  launch_nearest(true, pa, h->m, s);
+  QVH_HIP(hipGetLastError());
+}
+
+void ivf_check_trained(const qvh_ivfpq* h) {
+  if (!h->trained) throw Failure(QVH_EINVAL, "IVF-PQ index must be trained before add()");
+}
+
+void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k, uint32_t nprobe_req,
+                     uint64_t refine_factor, const uint64_t* d_bitmap, uint64_t* d_refs, float* d_dist,
+                     hipStream_t s) {
+  QVH_REQUIRE(nq <= 0x7FFFFFFFull, "too many queries in one call");
+  const uint32_t nprobe = std::min(std::max<uint32_t>(nprobe_req, 1), h->nlist);
+  // keep = min(count, sat(k * factor)) (src/ivfpq_index.cc:303-308)
+  const bool refine = refine_factor > 0 && h->store_vectors;
+  const uint64_t factor = refine ? refine_factor : 1;
+  const uint64_t count = h->count;
+  uint64_t keep = factor > count / std::max<uint64_t>(k, 1) ? count : static_cast<uint64_t>(k) * factor;
+  keep = std::min(keep, count);
+  const int mode = ivf_mode(h);
+  uint64_t keep_sel = keep;
+  if (mode == kModePre) keep_sel = std::min<uint64_t>(count, keep + std::max<uint64_t>(16, keep / 2));
+  if (keep_sel > kMaxKeepSel) {
+    throw Failure(QVH_EUNSUPPORTED, "IVF-PQ search: k * refine_factor above " + std::to_string(kMaxKeepSel) +
+                                        " candidates is not supported on the device path yet");
+  }
+  QVH_REQUIRE(h->count < 0xFFFFFFFFull, "IVF-PQ device path holds fewer than 2^32 vectors");
+  h->timed = h->timing;
+  if (h->timed) QVH_HIP(hipEventRecord(h->ev[0], s));
+  // prepared queries
+  float* dq = static_cast<float*>(h->w_q.reserve(nq * h->dim * sizeof(float)));
+  if (dq != d_q_raw) QVH_HIP(hipMemcpyAsync(dq, d_q_raw, nq * h->dim * sizeof(float), hipMemcpyDeviceToDevice, s));
+  if (h->metric == QVH_METRIC_COSINE) launch_normalize_rows(dq, nq, h->dim, s);
+  // coarse scores + probes
+  float* scores = static_cast<float*>(h->w_scores.reserve(nq * h->nlist * sizeof(float)));
+  {
+    const dim3 grid(static_cast<unsigned>(ceil_div(h->nlist, 256)), static_cast<unsigned>(ceil_div(nq, kCoarseQ)));
+    hipLaunchKernelGGL(coarse_kernel, grid, dim3(256), kCoarseQ * h->dim * sizeof(float), s, dq,
+                       static_cast<uint32_t>(nq), h->dim, h->cent_t.as<float>(), h->nlist,
+                       h->metric != QVH_METRIC_L2 ? 1 : 0, scores);
+  }
+  uint32_t* probes = static_cast<uint32_t*>(h->w_probes.reserve(nq * nprobe * sizeof(uint32_t)));
+  hipLaunchKernelGGL(probe_select_kernel, dim3(static_cast<unsigned>(ceil_div(nq, 4))), dim3(256), 0, s, scores,
+                     static_cast<uint32_t>(nq), h->nlist, nprobe, probes);
+  QVH_HIP(hipGetLastError());
+  if (h->timed) QVH_HIP(hipEventRecord(h->ev[1], s));
+  ScanArgs a{};
+  a.nq = static_cast<uint32_t>(nq);
+  a.k = k;
+  a.m = h->m;
+  a.mp = h->mp;
+  a.dsub = h->dsub;
+  a.dim = h->dim;
+  a.nlist = h->nlist;
+  a.nprobe = nprobe;
+  a.mode = mode;
+  a.Q = dq;
+  a.scores = scores;
+  a.probes = probes;
+  a.off = h->off.as<uint64_t>();
+  a.codes = h->codes.as<uint8_t>();
+  a.t1 = h->t1.as<float>();
+  a.pre = h->pre.as<float>();
+  a.cbt = h->cbt.as<float>();
+  a.cent = h->cent.as<float>();
+  a.vec = h->vec.as<float>();
+  a.bitmap = d_bitmap;
+  a.keep = static_cast<uint32_t>(keep);
+  a.keep_sel = static_cast<uint32_t>(keep_sel);
+  a.refine = refine ? 1 : 0;
+  a.out_refs = d_refs;
+  a.out_dist = d_dist;
+  const size_t lds = kCandCap * sizeof(uint64_t) + (nprobe + 1) * sizeof(uint64_t) +
+                     ((nprobe + 1) & ~1u) * sizeof(uint32_t) + static_cast<size_t>(h->m) * 256 * sizeof(float);
+  QVH_REQUIRE(lds <= 150 * 1024, "IVF-PQ search: m and nprobe too large for the on-chip tables");
+  const dim3 grid(static_cast<unsigned>(nq));
+  if (keep == 0) {
+    // nothing stored: every slot is empty
+    a.keep_sel = 0;
+  }
+  const uint32_t mpw = h->mp / 4;
+  // Dynamic LDS above the default 64 KiB needs the kernel's limit raised first.
+  auto raise_lds = [&](const void* fn) {
+    if (lds > 64 * 1024) {
+      QVH_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    }
+  };
+  if (mpw <= 2) {
+    raise_lds(reinterpret_cast<const void*>(ivf_scan_kernel<2>));
+    hipLaunchKernelGGL(ivf_scan_kernel<2>, grid, dim3(kScanThreads), lds, s, a);
+  } else if (mpw <= 4) {
+    raise_lds(reinterpret_cast<const void*>(ivf_scan_kernel<4>));
+    hipLaunchKernelGGL(ivf_scan_kernel<4>, grid, dim3(kScanThreads), lds, s, a);
+  } else if (mpw <= 8) {
+    raise_lds(reinterpret_cast<const void*>(ivf_scan_kernel<8>));
+    hipLaunchKernelGGL(ivf_scan_kernel<8>, grid, dim3(kScanThreads), lds, s, a);
+  } else if (mpw <= 16) {
+    raise_lds(reinterpret_cast<const void*>(ivf_scan_kernel<16>));
+    hipLaunchKernelGGL(ivf_scan_kernel<16>, grid, dim3(kScanThreads), lds, s, a);
+  } else if (mpw <= 32) {
+    raise_lds(reinterpret_cast<const void*>(ivf_scan_kernel<32>));
+    hipLaunchKernelGGL(ivf_scan_kernel<32>, grid, dim3(kScanThreads), lds, s, a);
+  } else {
+    throw Failure(QVH_EUNSUPPORTED, "IVF-PQ device path supports m <= 128");
+  }
+  QVH_HIP(hipGetLastError());
+  if (h->timed) QVH_HIP(hipEventRecord(h->ev[2], s));
+}
+
+}  // namespace
+
+extern "C" {
+
+qvh_status qvh_ivfpq_create(uint32_t dim, int metric, uint32_t nlist, uint32_t m, int store_vectors,
+                            qvh_ivfpq** out) {
+  return guarded([&] {
+    QVH_REQUIRE(out != nullptr, "qvh_ivfpq_create: null output");
+    *out = nullptr;
+    QVH_REQUIRE(dim >= 1 && dim <= 65536, "dimension must be in [1, 65536]");
+    QVH_REQUIRE(metric >= QVH_METRIC_L2 && metric <= QVH_METRIC_COSINE, "unknown metric");
+    QVH_REQUIRE(nlist >= 1 && nlist <= (1u << 24), "nlist must be in [1, 2^24]");
+    QVH_REQUIRE(m >= 1 && dim % m == 0, "PQ: dimension must be divisible by m");
+    if (dim > 2048 || m > 128) {
+      throw Failure(QVH_EUNSUPPORTED, "IVF-PQ device path supports dim <= 2048 and m <= 128");
+    }
+    const int dev = current_device();
+    auto* h = new qvh_ivfpq;
+    h->dim = dim;
+    h->metric = metric;
+    h->nlist = nlist;
+    h->m = m;
+    h->dsub = dim / m;
+    h->mp = (m + 3) / 4 * 4;
+    h->store_vectors = store_vectors;
+    h->device = dev;
+    h->h_off.assign(nlist + 1, 0);
+    const hipError_t e = hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+      delete h;
+      throw Failure(QVH_EDEVICE, std::string("hipStreamCreate: ") + hipGetErrorString(e));
+    }
+    try {
+      h->off.reserve((nlist + 1) * sizeof(uint64_t));
+      QVH_HIP(hipMemcpy(h->off.ptr, h->h_off.data(), (nlist + 1) * sizeof(uint64_t), hipMemcpyHostToDevice));
+    } catch (...) {
+      (void)hipStreamDestroy(h->stream);
+      delete h;
+      throw;
+    }
+    *out = h;
+  });
+}
+
+void qvh_ivfpq_destroy(qvh_ivfpq* h) {
+  if (!h) return;
+  (void)hipSetDevice(h->device);
+  if (h->stream) {
+    (void)hipStreamSynchronize(h->stream);
+    (void)hipStreamDestroy(h->stream);
+  }
+  for (hipEvent_t& e : h->ev) {
+    if (e) (void)hipEventDestroy(e);
+  }
+  delete h;
+}
+
+qvh_status qvh_ivfpq_set_trained(qvh_ivfpq* h, const float* centroids, const float* codebook,
+                                 int use_precomputed) {
+  return guarded([&] {
+    QVH_REQUIRE(h && centroids && codebook, "qvh_ivfpq_set_trained: null argument");
+    std::lock_guard<std::mutex> lock(h->mu);
+    QVH_REQUIRE(!h->trained, "index is already trained");
+    QVH_HIP(hipSetDevice(h->device));
+    hipStream_t s = h->stream;
+    const uint64_t cbytes = static_cast<uint64_t>(h->nlist) * h->dim * sizeof(float);
+    const uint64_t bbytes = static_cast<uint64_t>(h->m) * 256 * h->dsub * sizeof(float);
+    h->cent.reserve(cbytes);
+    h->cent_t.reserve(cbytes);
+    h->cent_norm.reserve(h->nlist * sizeof(float));
+    h->cb.reserve(bbytes);
+    h->cbt.reserve(bbytes);
+    QVH_HIP(hipMemcpyAsync(h->cent.ptr, centroids, cbytes, hipMemcpyHostToDevice, s));
+    QVH_HIP(hipMemcpyAsync(h->cb.ptr, codebook, bbytes, hipMemcpyHostToDevice, s));
+    hipLaunchKernelGGL(centroid_prep_kernel, dim3(static_cast<unsigned>(ceil_div(h->nlist, 256))), dim3(256), 0, s,
+                       h->cent.as<float>(), h->nlist, h->dim, h->cent_t.as<float>(), h->cent_norm.as<float>());
+    hipLaunchKernelGGL(codebook_prep_kernel, dim3(static_cast<unsigned>(ceil_div(uint64_t(h->m) * 256 * h->dsub, 256))),
+                       dim3(256), 0, s, h->cb.as<float>(), h->m, h->dsub, h->cbt.as<float>());
+    h->has_pre = use_precomputed != 0 && h->metric == QVH_METRIC_L2;
+    if (h->has_pre) {
+      const uint64_t n = static_cast<uint64_t>(h->nlist) * h->m * 256;
+      h->pre.reserve(n * sizeof(float));
+      hipLaunchKernelGGL(precompute_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, s,
+                         h->cent.as<float>(), h->cb.as<float>(), h->nlist, h->dim, h->m, h->pre.as<float>());
+    }
+    QVH_HIP(hipGetLastError());
+    QVH_HIP(hipStreamSynchronize(s));
+    h->trained = true;
+  });
+}
+
+qvh_status qvh_ivfpq_precomputed(qvh_ivfpq* h, float* out) {
+  return guarded([&] {
+    QVH_REQUIRE(h && out, "qvh_ivfpq_precomputed: null argument");
+    std::lock_guard<std::mutex> lock(h->mu);
+    QVH_REQUIRE(h->has_pre, "no precomputed table (metric is not L2 or it exceeds the budget)");
+    QVH_HIP(hipSetDevice(h->device));
+    QVH_HIP(hipMemcpy(out, h->pre.ptr, static_cast<uint64_t>(h->nlist) * h->m * 256 * sizeof(float),
+                      hipMemcpyDeviceToHost));
+  });
+}
+
+qvh_status qvh_ivfpq_encode(qvh_ivfpq* h, const float* x, uint64_t n, uint32_t* assign, uint8_t* codes,
+                            float* stored_out) {
+  return guarded([&] {
+    QVH_REQUIRE(h != nullptr, "qvh_ivfpq_encode: null handle");
+    if (n == 0) return;
+    QVH_REQUIRE(x != nullptr, "qvh_ivfpq_encode: null vectors");
+    std::lock_guard<std::mutex> lock(h->mu);
+    ivf_check_trained(h);
+    QVH_HIP(hipSetDevice(h->device));
+    hipStream_t s = h->stream;
+    float* dx = static_cast<float*>(h->w_x.reserve(n * h->dim * sizeof(float)));
+    QVH_HIP(hipMemcpyAsync(dx, x, n * h->dim * sizeof(float), hipMemcpyHostToDevice, s));
+    if (h->metric == QVH_METRIC_COSINE) launch_normalize_rows(dx, n, h->dim, s);
+    ivf_encode_device(h, dx, n, s);
+    if (assign) QVH_HIP(hipMemcpyAsync(assign, h->w_assign.ptr, n * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+    if (codes) QVH_HIP(hipMemcpyAsync(codes, h->w_codes.ptr, n * h->m, hipMemcpyDeviceToHost, s));
+    if (stored_out) QVH_HIP(hipMemcpyAsync(stored_out, dx, n * h->dim * sizeof(float), hipMemcpyDeviceToHost, s));
+    QVH_HIP(hipStreamSynchronize(s));
+  });
+}
+
+qvh_status qvh_ivfpq_add(qvh_ivfpq* h, const float* x, uint64_t n, uint32_t* assign_out) {
+  return guarded([&] {
+    QVH_REQUIRE(h != nullptr, "qvh_ivfpq_add: null handle");
+    if (n == 0) return;
+    QVH_REQUIRE(x != nullptr, "qvh_ivfpq_add: null vectors");
+    std::lock_guard<std::mutex> lock(h->mu);
+    ivf_check_trained(h);
+    QVH_HIP(hipSetDevice(h->device));
+    hipStream_t s = h->stream;
+    float* dx = static_cast<float*>(h->w_x.reserve(n * h->dim * sizeof(float)));
+    QVH_HIP(hipMemcpyAsync(dx, x, n * h->dim * sizeof(float), hipMemcpyHostToDevice, s));
+    if (h->metric == QVH_METRIC_COSINE) launch_normalize_rows(dx, n, h->dim, s);
+    ivf_encode_device(h, dx, n, s);
+    std::vector<uint32_t> assign(n);
+    QVH_HIP(hipMemcpyAsync(assign.data(), h->w_assign.ptr, n * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+    QVH_HIP(hipStreamSynchronize(s));
+    // Destinations: each batch entry goes after its list's existing entries, in input order
+    // (src/ivfpq_index.cc:263-269).
+    const uint32_t nl = h->nlist;
+    std::vector<uint64_t> add(nl, 0);
+    for (uint64_t i = 0; i < n; ++i) ++add[assign[i]];
+    for (uint32_t l = 0; l < nl; ++l) {
+      QVH_REQUIRE(h->h_off[l + 1] - h->h_off[l] + add[l] <= 0xFFFFFFFFull,
+                  "too many vectors in one IVF cell (2^32 limit); use a larger nlist");
+    }
+    std::vector<uint64_t> shift(nl, 0), new_off(nl + 1, 0), cursor(nl, 0);
+    for (uint32_t l = 0; l < nl; ++l) {
+      shift[l] = l ? shift[l - 1] + add[l - 1] : 0;
+      new_off[l + 1] = new_off[l] + (h->h_off[l + 1] - h->h_off[l]) + add[l];
+      cursor[l] = new_off[l] + (h->h_off[l + 1] - h->h_off[l]);
+    }
+    std::vector<uint64_t> dest(n);
+    for (uint64_t i = 0; i < n; ++i) dest[i] = cursor[assign[i]]++;
+    const uint64_t total = h->count + n;
+    QVH_REQUIRE(total < 0xFFFFFFFFull, "IVF-PQ device path holds fewer than 2^32 vectors");
+    // padded codes and term1 of the batch
+    uint8_t* cp = static_cast<uint8_t*>(h->w_codes_p.reserve(n * h->mp));
+    hipLaunchKernelGGL(pad_codes_kernel, dim3(static_cast<unsigned>(ceil_div(n * h->mp, 256))), dim3(256), 0, s,
+                       h->w_codes.as<uint8_t>(), h->m, h->mp, n, cp);
+    float* nt1 = nullptr;
+    if (h->has_pre) {
+      nt1 = static_cast<float*>(h->w_t1.reserve(n * sizeof(float)));
+      hipLaunchKernelGGL(term1_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, s,
+                         cp, h->mp, h->w_assign.as<uint32_t>(), h->pre.as<float>(), h->m, n, nt1);
+    }
+    uint64_t* ddest = static_cast<uint64_t*>(h->w_dest.reserve(n * sizeof(uint64_t)));
+    uint64_t* dshift = static_cast<uint64_t*>(h->w_shift.reserve(nl * sizeof(uint64_t)));
+    QVH_HIP(hipMemcpyAsync(ddest, dest.data(), n * sizeof(uint64_t), hipMemcpyHostToDevice, s));
+    QVH_HIP(hipMemcpyAsync(dshift, shift.data(), nl * sizeof(uint64_t), hipMemcpyHostToDevice, s));
+    // new CSR buffers
+    DeviceBuffer ncodes, nt1buf, nvec, noff;
+    ncodes.reserve(total * h->mp);
+    if (h->has_pre) nt1buf.reserve(total * sizeof(float));
+    if (h->store_vectors) nvec.reserve(total * h->dim * sizeof(float));
+    noff.reserve((nl + 1) * sizeof(uint64_t));
+    QVH_HIP(hipMemcpyAsync(noff.ptr, new_off.data(), (nl + 1) * sizeof(uint64_t), hipMemcpyHostToDevice, s));
+    ScatterArgs sa{};
+    sa.old_off = h->off.as<uint64_t>();
+    sa.shift = dshift;
+    sa.nlist = nl;
+    sa.old_count = h->count;
+    sa.n_new = n;
+    sa.dest = ddest;
+    sa.mp = h->mp;
+    sa.dim = h->dim;
+    sa.old_codes = h->codes.as<uint8_t>();
+    sa.new_codes = cp;
+    sa.codes = ncodes.as<uint8_t>();
+    sa.old_t1 = h->t1.as<float>();
+    sa.new_t1 = nt1;
+    sa.t1 = h->has_pre ? nt1buf.as<float>() : nullptr;
+    sa.old_vec = h->vec.as<float>();
+    sa.new_vec = dx;
+    sa.vec = h->store_vectors ? nvec.as<float>() : nullptr;
+    if (h->count) {
+      hipLaunchKernelGGL(scatter_old_kernel, dim3(static_cast<unsigned>(ceil_div(h->count, 256))), dim3(256), 0, s, sa);
+    }
+    hipLaunchKernelGGL(scatter_new_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, s, sa);
+    QVH_HIP(hipGetLastError());
+    QVH_HIP(hipStreamSynchronize(s));
+    std::swap(h->codes.ptr, ncodes.ptr);
+    std::swap(h->codes.bytes, ncodes.bytes);
+    std::swap(h->t1.ptr, nt1buf.ptr);
+    std::swap(h->t1.bytes, nt1buf.bytes);
+    std::swap(h->vec.ptr, nvec.ptr);
+    std::swap(h->vec.bytes, nvec.bytes);
+    std::swap(h->off.ptr, noff.ptr);
+    std::swap(h->off.bytes, noff.bytes);
+    h->h_off = std::move(new_off);
+    h->count = total;
+    if (assign_out) std::memcpy(assign_out, assign.data(), n * sizeof(uint32_t));
+  });
+}
+
+uint64_t qvh_ivfpq_size(const qvh_ivfpq* h) { return h ? h->count : 0; }
+
+qvh_status qvh_ivfpq_list_offsets(qvh_ivfpq* h, uint64_t* offsets) {
+  return guarded([&] {
+    QVH_REQUIRE(h && offsets, "qvh_ivfpq_list_offsets: null argument");
+    std::lock_guard<std::mutex> lock(h->mu);
+    std::memcpy(offsets, h->h_off.data(), h->h_off.size() * sizeof(uint64_t));
+  });
+}
+
+qvh_status qvh_ivfpq_lists(qvh_ivfpq* h, uint8_t* codes, float* vectors) {
+  return guarded([&] {
+    QVH_REQUIRE(h != nullptr, "qvh_ivfpq_lists: null handle");
+    std::lock_guard<std::mutex> lock(h->mu);
+    QVH_HIP(hipSetDevice(h->device));
+    if (codes && h->count) {
+      std::vector<uint8_t> padded(h->count * h->mp);
+      QVH_HIP(hipMemcpy(padded.data(), h->codes.ptr, padded.size(), hipMemcpyDeviceToHost));
+      for (uint64_t i = 0; i < h->count; ++i) std::memcpy(codes + i * h->m, padded.data() + i * h->mp, h->m);
+    }
+    if (vectors && h->count) {
+      QVH_REQUIRE(h->store_vectors, "vectors are not stored (store_vectors is off)");
+      QVH_HIP(hipMemcpy(vectors, h->vec.ptr, h->count * h->dim * sizeof(float), hipMemcpyDeviceToHost));
+    }
+  });
+}
+
+qvh_status qvh_ivfpq_search(qvh_ivfpq* h, const float* queries, uint64_t nq, uint32_t k, uint32_t nprobe,
+                            uint64_t refine_factor, const uint64_t* pos_bitmap, uint64_t* out_refs,
+                            float* out_dist) {
+  return guarded([&] {
+    QVH_REQUIRE(h != nullptr, "qvh_ivfpq_search: null handle");
+    if (nq == 0 || k == 0) return;
+    QVH_REQUIRE(queries && out_refs && out_dist, "qvh_ivfpq_search: null buffer");
+    std::lock_guard<std::mutex> lock(h->mu);
+    if (!h->trained || h->count == 0) {
+      for (uint64_t i = 0; i < nq * k; ++i) {
+        out_refs[i] = QVH_EMPTY_REF;
+        out_dist[i] = __builtin_huge_valf();
+      }
+      return;
+    }
+    QVH_HIP(hipSetDevice(h->device));
+    hipStream_t s = h->stream;
+    float* dq = static_cast<float*>(h->w_q.reserve(nq * h->dim * sizeof(float)));
+    QVH_HIP(hipMemcpyAsync(dq, queries, nq * h->dim * sizeof(float), hipMemcpyHostToDevice, s));
+    const uint64_t* dbits = nullptr;
+    if (pos_bitmap) {
+      const size_t words = ceil_div(h->count, 64);
+      uint64_t* b = static_cast<uint64_t*>(h->w_bits.reserve(words * sizeof(uint64_t)));
+      QVH_HIP(hipMemcpyAsync(b, pos_bitmap, words * sizeof(uint64_t), hipMemcpyHostToDevice, s));
+      dbits = b;
+    }
+    uint64_t* drefs = static_cast<uint64_t*>(h->w_refs.reserve(nq * k * sizeof(uint64_t)));
+    float* ddist = static_cast<float*>(h->w_dist.reserve(nq * k * sizeof(float)));
+    ivf_search_impl(h, dq, nq, k, nprobe, refine_factor, dbits, drefs, ddist, s);
+    QVH_HIP(hipMemcpyAsync(out_refs, drefs, nq * k * sizeof(uint64_t), hipMemcpyDeviceToHost, s));
+    QVH_HIP(hipMemcpyAsync(out_dist, ddist, nq * k * sizeof(float), hipMemcpyDeviceToHost, s));
+    QVH_HIP(hipStreamSynchronize(s));
+  });
+}
+
+qvh_status qvh_ivfpq_search_device(qvh_ivfpq* h, const float* d_queries, uint64_t nq, uint32_t k,
+                                   uint32_t nprobe, uint64_t refine_factor, const uint64_t* d_pos_bitmap,
+                                   uint64_t* d_out_refs, float* d_out_dist, void* stream) {
+  return guarded([&] {
+    QVH_REQUIRE(h != nullptr, "qvh_ivfpq_search_device: null handle");
+    if (nq == 0 || k == 0) return;
+    QVH_REQUIRE(d_queries && d_out_refs && d_out_dist, "qvh_ivfpq_search_device: null buffer");
+    std::lock_guard<std::mutex> lock(h->mu);
+    QVH_REQUIRE(h->trained && h->count > 0, "qvh_ivfpq_search_device: index is untrained or empty");
+    QVH_HIP(hipSetDevice(h->device));
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : h->stream;
+    h->timed = h->timing;
+    ivf_search_impl(h, d_queries, nq, k, nprobe, refine_factor, d_pos_bitmap, d_out_refs, d_out_dist, s);
+  });
+}
+
+qvh_status qvh_ivfpq_set_timing(qvh_ivfpq* h, int enable) {
+  return guarded([&] {
+    QVH_REQUIRE(h != nullptr, "qvh_ivfpq_set_timing: null handle");
+    std::lock_guard<std::mutex> lock(h->mu);
+    QVH_HIP(hipSetDevice(h->device));
+    if (enable && !h->ev[0]) {
+      for (hipEvent_t& e : h->ev) QVH_HIP(hipEventCreate(&e));
+    }
+    h->timing = enable != 0;
+  });
+}
+
+qvh_status qvh_ivfpq_last_timing(qvh_ivfpq* h, float* select_ms, float* scan_ms) {
+  return guarded([&] {
+    QVH_REQUIRE(h != nullptr, "qvh_ivfpq_last_timing: null handle");
+    std::lock_guard<std::mutex> lock(h->mu);
+    QVH_REQUIRE(h->timed, "qvh_ivfpq_last_timing: the last search was not timed");
+    QVH_HIP(hipSetDevice(h->device));
+    QVH_HIP(hipEventSynchronize(h->ev[2]));
+    float a = 0, b = 0;
+    QVH_HIP(hipEventElapsedTime(&a, h->ev[0], h->ev[1]));
+    QVH_HIP(hipEventElapsedTime(&b, h->ev[1], h->ev[2]));
+    if (select_ms) *select_ms = a;
+    if (scan_ms) *scan_ms = b;
+  });
+}
+
+qvh_status qvh_ivfpq_sync(qvh_ivfpq* h) {
+  return guarded([&] {
+    QVH_REQUIRE(h != nullptr, "qvh_ivfpq_sync: null handle");
+    QVH_HIP(hipSetDevice(h->device));
+    QVH_HIP(hipStreamSynchronize(h->stream));
+  });
+}
+
+// ---- point sets for k-means assignment ------------------------------------------------------------
+
+struct qvh_points {
+  uint64_t n = 0;
+  uint32_t dim = 0;
+  int device = 0;
+  DeviceBuffer x, cent, ct, norms, out;
+  std::mutex mu;
+};
+
+qvh_status qvh_points_create(const float* x, uint64_t n, uint32_t dim, qvh_points** out) {
+  return guarded([&] {
+    QVH_REQUIRE(out != nullptr, "qvh_points_create: null output");
+    *out = nullptr;
+    QVH_REQUIRE(dim >= 1, "qvh_points_create: dim must be positive");
+    QVH_REQUIRE(x != nullptr || n == 0, "qvh_points_create: null points");
+    const int dev = current_device();
+    auto* p = new qvh_points;
+    p->n = n;
+    p->dim = dim;
+    p->device = dev;
+    try {
+      p->x.reserve(std::max<uint64_t>(n, 1) * dim * sizeof(float));
+      if (n) QVH_HIP(hipMemcpy(p->x.ptr, x, n * dim * sizeof(float), hipMemcpyHostToDevice));
+    } catch (...) {
+      delete p;
+      throw;
+    }
+    *out = p;
+  });
+}
+
+void qvh_points_destroy(qvh_points* p) { delete p; }
+
+qvh_status qvh_points_nearest(qvh_points* p, const float* centroids, uint32_t k, int max_inner_product,
+                              uint32_t* out_assign) {
+  return guarded([&] {
+    QVH_REQUIRE(p && centroids && out_assign, "qvh_points_nearest: null argument");
+    QVH_REQUIRE(k >= 1, "qvh_points_nearest: k must be positive");
+    std::lock_guard<std::mutex> lock(p->mu);
+    QVH_HIP(hipSetDevice(p->device));
+    if (p->n == 0) return;
+    const uint64_t cb = static_cast<uint64_t>(k) * p->dim * sizeof(float);
+    p->cent.reserve(cb);
+    p->ct.reserve(cb);
+    p->norms.reserve(k * sizeof(float));
+    p->out.reserve(p->n * sizeof(uint32_t));
+    QVH_HIP(hipMemcpy(p->cent.ptr, centroids, cb, hipMemcpyHostToDevice));
+    hipLaunchKernelGGL(centroid_prep_kernel, dim3(static_cast<unsigned>(ceil_div(k, 256))), dim3(256), 0, nullptr,
+                       p->cent.as<float>(), k, p->dim, p->ct.as<float>(), p->norms.as<float>());
+    NearestArgs na{};
+    na.x = p->x.as<float>();
+    na.n = p->n;
+    na.dim = p->dim;
+    na.x_stride = p->dim;
+    na.ct = p->ct.as<float>();
+    na.norms = p->norms.as<float>();
+    na.k = k;
+    na.max_ip = max_inner_product;
+    na.out32 = p->out.as<uint32_t>();
+    launch_nearest(false, na, 1, nullptr);
+    QVH_HIP(hipMemcpy(out_assign, p->out.ptr, p->n * sizeof(uint32_t), hipMemcpyDeviceToHost));
+  });
+}
+
+}  // extern "C"

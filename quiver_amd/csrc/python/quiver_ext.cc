@@ -14,6 +14,8 @@
 #include "qvh.h"
 #include "quiver/filter.h"
 #include "quiver/flat_index.h"
+#include "quiver/ivfpq_index.h"
+#include "quiver/quantizer.h"
 
 namespace py = pybind11;
 
@@ -159,4 +161,164 @@ PYBIND11_MODULE(_quiver, m) {
       .def_property_readonly("metric", [](const quiver::FlatIndex& s) {
         return std::string(quiver::to_string(s.metric()));
       });
+  py::class_<quiver::IvfPqIndex>(m, "IvfPqIndex")
+      .def(py::init([](std::size_t dim, const std::string& metric, std::size_t nlist, std::size_t pq_m,
+                       bool store_vectors, std::size_t train_iterations, std::uint64_t seed) {
+             quiver::IvfPqParams p;
+             p.dim = dim;
+             p.metric = quiver::parse_metric(metric);
+             p.nlist = nlist;
+             p.m = pq_m;
+             p.store_vectors = store_vectors;
+             p.train_iterations = train_iterations;
+             p.seed = seed;
+             return new quiver::IvfPqIndex(p);
+           }),
+           py::arg("dim"), py::arg("metric") = "l2", py::arg("nlist") = 1024, py::arg("m") = 16,
+           py::arg("store_vectors") = false, py::arg("train_iterations") = 20, py::arg("seed") = 1234)
+      .def(
+          "_train",
+          [](quiver::IvfPqIndex& self, const FloatMatrix& x, std::size_t threads) {
+            check_matrix(x, self.dim());
+            quiver::ThreadPool* pool = pool_for(threads);
+            py::gil_scoped_release release;
+            self.train(x.data(), x.shape(0), pool);
+          },
+          py::arg("vectors"), py::arg("num_threads"))
+      .def(
+          "_add",
+          [](quiver::IvfPqIndex& self, const FloatMatrix& x, const py::object& labels, std::size_t threads) {
+            check_matrix(x, self.dim());
+            LabelArray hold;
+            const std::uint64_t* lp = optional_labels(labels, x.shape(0), hold);
+            quiver::ThreadPool* pool = pool_for(threads);
+            py::gil_scoped_release release;
+            self.add(x.data(), x.shape(0), lp, pool);
+          },
+          py::arg("vectors"), py::arg("labels").none(true), py::arg("num_threads"))
+      .def(
+          "_search",
+          [](const quiver::IvfPqIndex& self, const FloatMatrix& q, std::size_t k, std::size_t nprobe,
+             std::size_t refine_factor, const py::object& allowed, std::size_t threads) {
+            check_matrix(q, self.dim());
+            std::unique_ptr<quiver::Filter> filter;
+            if (!allowed.is_none()) filter = make_filter(allowed.cast<LabelArray>());
+            const std::size_t nq = q.shape(0);
+            std::vector<std::uint64_t> labels(result_size(nq, k));
+            std::vector<float> dist(labels.size());
+            quiver::IvfPqSearchParams p;
+            p.nprobe = nprobe;
+            p.refine_factor = refine_factor;
+            p.filter = filter.get();
+            quiver::ThreadPool* pool = pool_for(threads);
+            {
+              py::gil_scoped_release release;
+              self.search_batch(q.data(), nq, k, labels.data(), dist.data(), p, pool);
+            }
+            return make_results(nq, k, std::move(labels), std::move(dist));
+          },
+          py::arg("queries"), py::arg("k"), py::arg("nprobe"), py::arg("refine_factor"),
+          py::arg("allowed").none(true), py::arg("num_threads"))
+      .def("__len__", &quiver::IvfPqIndex::size, py::call_guard<py::gil_scoped_release>())
+      .def_property_readonly("is_trained", &quiver::IvfPqIndex::is_trained)
+      .def_property_readonly("dim", &quiver::IvfPqIndex::dim)
+      .def_property_readonly("nlist", [](const quiver::IvfPqIndex& s) { return s.params().nlist; })
+      .def_property_readonly("m", [](const quiver::IvfPqIndex& s) { return s.params().m; })
+      .def_property_readonly("metric", [](const quiver::IvfPqIndex& s) {
+        return std::string(quiver::to_string(s.params().metric));
+      })
+      .def_property_readonly("memory_bytes",
+                             [](const quiver::IvfPqIndex& s) {
+                               py::gil_scoped_release release;
+                               return s.memory_bytes();
+                             })
+      .def("list_sizes", &quiver::IvfPqIndex::list_sizes, py::call_guard<py::gil_scoped_release>())
+      .def("_centroids",
+           [](const quiver::IvfPqIndex& s) {
+             const auto c = s.centroids();
+             py::array_t<float> out({s.params().nlist, s.params().dim});
+             std::memcpy(out.mutable_data(), c.data(), c.size() * sizeof(float));
+             return out;
+           })
+      .def("_codebook",
+           [](const quiver::IvfPqIndex& s) {
+             const auto c = s.codebook();
+             const std::size_t m = s.params().m;
+             py::array_t<float> out({m, std::size_t{256}, s.params().dim / m});
+             std::memcpy(out.mutable_data(), c.data(), c.size() * sizeof(float));
+             return out;
+           })
+      .def("_set_trained",
+           [](quiver::IvfPqIndex& s, const py::array_t<float, py::array::c_style>& cent,
+              const py::array_t<float, py::array::c_style>& cb) {
+             const auto& p = s.params();
+             if (static_cast<std::size_t>(cent.size()) != p.nlist * p.dim ||
+                 static_cast<std::size_t>(cb.size()) != p.m * 256 * (p.dim / p.m)) {
+               throw py::value_error("trained state has the wrong size");
+             }
+             py::gil_scoped_release release;
+             s.set_trained(cent.data(), cb.data());
+           })
+      .def("_list_offsets",
+           [](const quiver::IvfPqIndex& s) {
+             const auto v = s.list_offsets();
+             py::array_t<std::uint64_t> out(v.size());
+             std::memcpy(out.mutable_data(), v.data(), v.size() * sizeof(std::uint64_t));
+             return out;
+           })
+      .def("_list_labels",
+           [](const quiver::IvfPqIndex& s) {
+             const auto v = s.list_labels();
+             py::array_t<std::uint64_t> out(v.size());
+             std::memcpy(out.mutable_data(), v.data(), v.size() * sizeof(std::uint64_t));
+             return out;
+           })
+      .def("_list_codes",
+           [](const quiver::IvfPqIndex& s) {
+             std::vector<std::uint8_t> v;
+             {
+               py::gil_scoped_release release;
+               v = s.list_codes();
+             }
+             const std::size_t m = s.params().m;
+             py::array_t<std::uint8_t> out({v.size() / m, m});
+             std::memcpy(out.mutable_data(), v.data(), v.size());
+             return out;
+           })
+      .def("_list_vectors", [](const quiver::IvfPqIndex& s) {
+        std::vector<float> v;
+        {
+          py::gil_scoped_release release;
+          v = s.list_vectors();
+        }
+        const std::size_t d = s.params().dim;
+        py::array_t<float> out({v.size() / d, d});
+        std::memcpy(out.mutable_data(), v.data(), v.size() * sizeof(float));
+        return out;
+      });
+
+  m.def(
+      "kmeans",
+      [](const FloatMatrix& x, std::size_t k, std::size_t iterations, std::size_t max_points_per_centroid,
+         std::uint64_t seed, std::size_t threads) {
+        if (x.ndim() != 2) throw py::value_error("expected a 2-D float32 array");
+        quiver::KMeansParams kp;
+        kp.k = k;
+        kp.iterations = iterations;
+        kp.max_points_per_centroid = max_points_per_centroid;
+        kp.seed = seed;
+        std::vector<float> c;
+        const std::size_t n = x.shape(0), d = x.shape(1);
+        quiver::ThreadPool* pool = pool_for(threads);
+        {
+          py::gil_scoped_release release;
+          c = quiver::kmeans(x.data(), n, d, kp, pool);
+        }
+        py::array_t<float> out({k, d});
+        std::memcpy(out.mutable_data(), c.data(), c.size() * sizeof(float));
+        return out;
+      },
+      py::arg("vectors"), py::arg("k"), py::arg("iterations") = 25, py::arg("max_points_per_centroid") = 256,
+      py::arg("seed") = 1234, py::arg("num_threads") = 0,
+      "Lloyd's k-means (the reference's kmeans), assignment steps on the GPU.");
 }

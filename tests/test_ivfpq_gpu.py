@@ -1,0 +1,159 @@
+"""IVF-PQ on the GPU vs the oracle (the C restatement of IvfPqIndex, src/ivfpq_index.cc), same
+seeded inputs.
+
+Bit-exact: k-means centroids, PQ codebooks, cell assignments, PQ codes and list order (integer and
+byte outputs), and every returned distance (the scan re-scores its survivors in the reference's
+arithmetic). Labels: identical except inside groups of exactly equal distance at the k-th
+boundary (assert_same_topk), where the reference's order is a libstdc++ heap artifact.
+"""
+
+import numpy as np
+import pytest
+
+import quiver_amd as quiver
+from oracle.oracle import IvfPqState, rows_bitmap
+from parity import assert_same_topk
+from quiver_amd import datasets as D
+
+pytestmark = pytest.mark.gpu
+
+
+def clustered(n, dim, clusters, seed, center_seed=None):
+    crng = np.random.default_rng(1000 + clusters if center_seed is None else center_seed)
+    centers = (2.0 * crng.standard_normal((clusters, dim))).astype(np.float32)
+    rng = np.random.default_rng(seed)
+    return (centers[rng.integers(0, clusters, n)] + rng.standard_normal((n, dim))).astype(np.float32)
+
+
+def build_pair(oracle, base, metric, nlist, m, store, train_n=None, iters=10):
+    """Product index trained + filled on the GPU, and the oracle's state from the same data."""
+    print(f"case: n={base.shape[0]} dim={base.shape[1]} metric={metric} nlist={nlist} m={m} "
+          f"store={store}", flush=True)
+    tn = base.shape[0] if train_n is None else train_n
+    idx = quiver.IvfPqIndex(base.shape[1], metric, nlist=nlist, m=m, store_vectors=store,
+                            train_iterations=iters)
+    idx.train(base[:tn])
+    cent, cb, pre = oracle.ivfpq_train(base[:tn], metric, nlist, m, iters, 1234)
+    assert np.array_equal(idx.centroids.view(np.uint32), cent.view(np.uint32)), "centroids differ"
+    assert np.array_equal(idx.codebook.view(np.uint32), cb.view(np.uint32)), "codebook differs"
+    idx.add(base)
+    assign, codes, stored = oracle.ivfpq_encode(cent, cb, metric, base)
+    st = IvfPqState(metric, cent, cb, pre).set_lists(assign, codes, np.arange(base.shape[0], dtype=np.uint64),
+                                                     stored if store else None)
+    off, labels, got_codes = idx.lists()
+    assert np.array_equal(off, st.offsets), "list offsets differ"
+    assert np.array_equal(labels, st.labels), "list order differs"
+    assert np.array_equal(got_codes, st.codes), "PQ codes differ"
+    if store:
+        assert np.array_equal(idx.list_vectors().view(np.uint32), st.vectors.view(np.uint32))
+    return idx, st
+
+
+def compare_search(oracle, idx, st, queries, k, nprobe, refine=0, allowed=None):
+    got_l, got_d = idx.search(queries, k, nprobe=nprobe, refine_factor=refine, filter=allowed)
+    bm = None
+    if allowed is not None:
+        bm = rows_bitmap(np.flatnonzero(np.isin(st.labels, allowed)), st.labels.size)
+    refs, dist = oracle.ivfpq_search(st, queries, k, nprobe, refine, bm)
+    exp_l = st.ref_to_label(refs)
+    return assert_same_topk(got_l, got_d, exp_l, dist)
+
+
+def test_kmeans_matches_oracle(oracle):
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((6000, 12)).astype(np.float32)
+    assert np.array_equal(quiver.kmeans(x, 40, 8, seed=3), oracle.kmeans(x, 40, 8, seed=3))
+    dup = np.ones((1000, 2), np.float32)  # identical points: empty clusters get split
+    dup[:20, 0] = np.arange(20)
+    assert np.array_equal(quiver.kmeans(dup, 16), oracle.kmeans(dup, 16))
+    # subsampling beyond k * max_points_per_centroid
+    assert np.array_equal(quiver.kmeans(x, 8, 5, max_points_per_centroid=100, seed=7),
+                          oracle.kmeans(x, 8, 5, max_points_per_centroid=100, seed=7))
+
+
+@pytest.mark.parametrize("metric,store,refine", [("l2", False, 0), ("l2", True, 4), ("cosine", True, 4),
+                                                 ("ip", True, 8)])
+def test_ivfpq_small_matches_oracle(oracle, metric, store, refine):
+    """dim 32, 10k clustered vectors, nlist 64, m 16 (the reference's IvfPqRecall setup)."""
+    base = clustered(10_000, 32, 50, 6)
+    q = clustered(100, 32, 50, 7)
+    idx, st = build_pair(oracle, base, metric, 64, 16, store)
+    for nprobe in (1, 8, 16, 64):
+        print(compare_search(oracle, idx, st, q, 10, nprobe, refine))
+
+
+def test_ivfpq_filter_matches_oracle(oracle):
+    base = clustered(8_000, 16, 30, 8)
+    q = clustered(60, 16, 30, 9)
+    idx, st = build_pair(oracle, base, "l2", 32, 8, True)
+    rng = np.random.default_rng(1)
+    for frac in (0.5, 0.1, 0.005):
+        allowed = np.sort(rng.choice(8_000, max(1, int(8_000 * frac)), replace=False)).astype(np.uint64)
+        print(frac, compare_search(oracle, idx, st, q, 10, 32, 2, allowed))
+
+
+def test_ivfpq_without_precomputed_table(oracle):
+    """nlist * m * 256 floats above 256 MiB: per-list residual tables (src/ivfpq_index.cc:338-342)."""
+    base = clustered(8_400, 32, 40, 10)
+    q = clustered(50, 32, 40, 11)
+    idx, st = build_pair(oracle, base, "l2", 8_200, 32, False, iters=3)
+    assert st.precomputed is None
+    print(compare_search(oracle, idx, st, q, 10, 32))
+
+
+def test_ivfpq_unaligned_code_width(oracle):
+    """m = 25 (dim 100): codes are not a multiple of 4 bytes."""
+    base, q = D.unit_mix(12_000, 40)
+    idx, st = build_pair(oracle, base, "cosine", 64, 25, True, iters=6)
+    print(compare_search(oracle, idx, st, q, 10, 16, 8))
+
+
+def test_ivfpq_integer_mixture_l2(oracle):
+    """The integer-valued mixture of the 1M x 128 workload, at 60k rows: nlist 256, m 32."""
+    base, q = D.int_mix(60_000, 200)
+    idx, st = build_pair(oracle, base, "l2", 256, 32, False, iters=6)
+    for nprobe in (4, 32):
+        print(compare_search(oracle, idx, st, q, 10, nprobe))
+
+
+def test_ivfpq_incremental_adds_and_labels(oracle):
+    base = clustered(5_000, 16, 20, 12)
+    idx = quiver.IvfPqIndex(16, nlist=16, m=4, train_iterations=5)
+    idx.train(base)
+    labels = np.arange(5_000, dtype=np.uint64) * 7 + 3
+    for b in range(0, 5_000, 1_300):
+        idx.add(base[b:b + 1_300], labels=labels[b:b + 1_300])
+    assert len(idx) == 5_000
+    cent, cb = idx.centroids, idx.codebook
+    assign, codes, _ = oracle.ivfpq_encode(cent, cb, "l2", base)
+    st = IvfPqState("l2", cent, cb, oracle.ivfpq_precompute(cent, cb)).set_lists(assign, codes, labels)
+    off, lab, got_codes = idx.lists()
+    assert np.array_equal(off, st.offsets) and np.array_equal(lab, st.labels)
+    assert np.array_equal(got_codes, st.codes)
+    print(compare_search(oracle, idx, st, base[:30], 5, 16))
+
+
+def test_set_trained_uses_given_state(oracle):
+    """An index given trained state (as loading does) encodes and searches like the oracle."""
+    base = clustered(4_000, 16, 20, 13)
+    cent, cb, pre = oracle.ivfpq_train(base, "l2", 32, 8, 5, 99)
+    idx = quiver.IvfPqIndex(16, "l2", nlist=32, m=8)
+    idx.set_trained(cent, cb)
+    assert idx.is_trained
+    idx.add(base)
+    assign, codes, _ = oracle.ivfpq_encode(cent, cb, "l2", base)
+    st = IvfPqState("l2", cent, cb, pre).set_lists(assign, codes, np.arange(4_000, dtype=np.uint64))
+    print(compare_search(oracle, idx, st, base[:40], 10, 8))
+
+
+def test_untrained_and_empty():
+    idx = quiver.IvfPqIndex(8, nlist=4, m=2)
+    with pytest.raises(ValueError, match="trained"):
+        idx.add(np.zeros((1, 8)))
+    labels, dist = idx.search(np.zeros((2, 8)), k=3)
+    assert (labels == -1).all() and np.isinf(dist).all()
+    idx.train(np.random.default_rng(0).standard_normal((300, 8)).astype(np.float32))
+    with pytest.raises(ValueError, match="already trained"):
+        idx.train(np.random.default_rng(0).standard_normal((300, 8)).astype(np.float32))
+    labels, dist = idx.search(np.zeros((2, 8)), k=3)
+    assert (labels == -1).all()
