@@ -3,17 +3,24 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 
-Headline workload (one "step" = one batched search of the whole query set):
-  flat exact L2, k=10, 1,000,000 x 128 fp32 base (integer-valued 64-component mixture,
-  quiver_amd/datasets.py), 10,000 queries, batched; queries, base and outputs resident in HBM.
+Workloads (one "step" = one batched search of the whole query set; queries, index and outputs
+resident in HBM):
+  flat   exact L2, k=10, 1,000,000 x 128 fp32 base (integer-valued 64-component mixture,
+         quiver_amd/datasets.py), 10,000 queries from the same mixture.
+  ivfpq  the same base and queries in an IVF-PQ index: nlist 2048, m 32 x 8 bits, L2, residual
+         PQ trained on 100,000 rows of a seeded permutation (numpy default_rng(31)); k=10,
+         nprobe 32 (swept over 1..64 once each, untimed by the step clock).
 
-Prints ONE JSON line. `value` is queries per second of the whole batched search (query prep +
-fused MFMA scan + merge/exact re-score), timed over K steps with the device synchronized on both
-sides. `roofline` is the dominant kernel (the fused scan): algorithmic 2*n*d*nq FLOP per launch
-over its average launch time, measured with HIP events on the stream it runs on, against the
-MI355X dense FP32 matrix peak (157.3 TFLOP/s). `cpu_baseline` is the reference's own CPU path
-(its sources compiled by oracle/Makefile; the C restatement in oracle/ when that library is
-absent) timed on this host's cores over a bounded sample of the same queries.
+Prints ONE JSON line. `value` is the flat workload's queries per second (query prep + fused MFMA
+scan + merge/exact re-score), timed over K steps with the device synchronized on both sides;
+the "ivfpq" object carries the same fields for the IVF-PQ workload. `roofline` is each
+workload's dominant kernel measured with HIP events on the stream it runs on: the flat scan's
+algorithmic 2*n*d*nq FLOP per launch against the dense FP32 matrix peak (157.3 TFLOP/s), the
+IVF-PQ list scan's algorithmic code bytes (sum over queries and probed lists of len * m) against
+HBM peak (8 TB/s). `cpu_baseline` is the reference's own CPU search (its sources compiled by
+oracle/Makefile; the C restatement in oracle/ when that library is absent) timed on this host's
+cores over a bounded sample of the same queries; for IVF-PQ it loads the index built here from a
+.qvr file, so both sides search identical trained state and lists.
 """
 
 from __future__ import annotations
@@ -23,6 +30,7 @@ import ctypes as C
 import json
 import os
 import sys
+import tempfile
 import time
 
 import numpy as np
@@ -77,6 +85,12 @@ class Qvh:
         L.qvh_flat_last_timing.argtypes = [C.c_void_p, C.POINTER(C.c_float), C.POINTER(C.c_float),
                                            C.POINTER(C.c_float), C.POINTER(C.c_uint32)]
         L.qvh_flat_destroy.argtypes = [C.c_void_p]
+        L.qvh_ivfpq_search_device.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint32, C.c_uint32,
+                                              C.c_uint64, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.qvh_ivfpq_sync.argtypes = [C.c_void_p]
+        L.qvh_ivfpq_set_timing.argtypes = [C.c_void_p, C.c_int]
+        L.qvh_ivfpq_last_timing.argtypes = [C.c_void_p, C.POINTER(C.c_float), C.POINTER(C.c_float),
+                                            C.POINTER(C.c_uint64)]
         L.qvh_device_info.argtypes = [C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t,
                                       C.POINTER(C.c_int)]
 
@@ -163,6 +177,121 @@ def bench_flat(args, hip: Hip, qvh: Qvh):
     return result, base, queries
 
 
+def bench_ivfpq(args, hip: Hip, qvh: Qvh, base, queries):
+    import quiver_amd as quiver
+
+    n, dim = base.shape
+    nq, k, nlist, m, nprobe = queries.shape[0], 10, 2048, 32, 32
+    sample = np.random.default_rng(31).permutation(n)[:100_000]
+    idx = quiver.IvfPqIndex(dim, "l2", nlist=nlist, m=m)
+    t0 = time.perf_counter()
+    idx.train(base[sample])
+    train_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    idx.add(base)
+    add_s = time.perf_counter() - t0
+    h = C.c_void_p(idx._index._device_handle)
+    d_q = hip.malloc(queries.nbytes)
+    hip.h2d(d_q, queries)
+    d_refs = hip.malloc(nq * k * 8)
+    d_dist = hip.malloc(nq * k * 4)
+    qvh.check(qvh.lib.qvh_ivfpq_set_timing(h, 1), "timing")
+
+    def search(probes):
+        qvh.check(qvh.lib.qvh_ivfpq_search_device(h, d_q, nq, k, probes, 0, None, d_refs, d_dist, None),
+                  "search")
+
+    def timing():
+        a, b, nb = C.c_float(), C.c_float(), C.c_uint64()
+        qvh.check(qvh.lib.qvh_ivfpq_last_timing(h, C.byref(a), C.byref(b), C.byref(nb)), "timing")
+        return a.value, b.value, nb.value
+
+    sweep = {}
+    for p in (1, 4, 8, 16, 32, 64):
+        search(p)
+        search(p)
+        qvh.check(qvh.lib.qvh_ivfpq_sync(h), "sync")
+        sel, scan, nbytes = timing()
+        sweep[str(p)] = {"select_ms": sel, "scan_ms": scan, "code_bytes": nbytes,
+                         "scan_hbm_frac": nbytes / (scan * 1e-3) / (HBM_PEAK_GBS * 1e9)}
+
+    for _ in range(args.warmup):
+        search(nprobe)
+    qvh.check(qvh.lib.qvh_ivfpq_sync(h), "sync")
+    hip.sync()
+    stages = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        search(nprobe)
+        stages.append(timing())
+    qvh.check(qvh.lib.qvh_ivfpq_sync(h), "sync")
+    hip.sync()
+    elapsed = time.perf_counter() - t0
+
+    refs = np.empty((nq, k), np.uint64)
+    dist = np.empty((nq, k), np.float32)
+    hip.d2h(refs, d_refs)
+    hip.d2h(dist, d_dist)
+    assert (refs != np.uint64(2**64 - 1)).all() and (np.diff(dist, axis=1) >= 0).all(), "malformed results"
+    for p in (d_q, d_refs, d_dist):
+        hip.lib.hipFree(p)
+
+    st = np.array(stages, dtype=np.float64)
+    scan_ms = float(st[:, 1].mean())
+    code_bytes = int(st[0, 2])
+    achieved = code_bytes / (scan_ms * 1e-3) / 1e9
+    ms_per_step = elapsed / args.steps * 1e3
+    return idx, {
+        "value": nq / (ms_per_step * 1e-3),
+        "unit": "queries/s",
+        "ms_per_step": ms_per_step,
+        "stage_ms": {"select": float(st[:, 0].mean()), "scan": scan_ms},
+        "roofline": {"bound": "hbm", "kernel": "ivf_scan_kernel<8>", "achieved": achieved,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": load_traffic("ivf_scan_int_mix_1m_nprobe32"),
+                     "code_bytes_per_launch": code_bytes},
+        "nprobe_sweep": sweep,
+        "build": {"train_s": train_s, "add_s": add_s, "encode_vectors_per_s": n / add_s},
+        "config": {"workload": "IVF-PQ L2 k=10 nprobe=32: 1,000,000 x 128 fp32 integer-valued mixture, "
+                               "nlist 2048, m 32, trained on a 100,000-row sample; 10,000 queries batched",
+                   "n": n, "dim": dim, "nq": nq, "k": k, "nlist": nlist, "m": m, "nprobe": nprobe},
+    }
+
+
+def cpu_baseline_ivfpq(idx, queries, k, nprobe, seconds, threads):
+    """QPS of the reference CPU IVF-PQ search on the index built here (loaded from a .qvr file)."""
+    from oracle.oracle import IvfPqState, Oracle, Reference
+
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "ivfpq.qvr")
+        idx.save(path)
+        try:
+            ref = Reference()
+            kind = "reference"
+            ix = ref.ivfpq_load(path)
+            run = lambda q: ix.search(q, k, nprobe=nprobe, threads=threads)
+        except FileNotFoundError:
+            orc = Oracle()
+            kind = "port"
+            cent, cb = idx.centroids, idx.codebook
+            off, labels, codes = idx.lists()
+            st = IvfPqState("l2", cent, cb, orc.ivfpq_precompute(cent, cb))
+            st.offsets, st.labels, st.codes, st.vectors = off, labels, codes, None
+            run = lambda q: orc.ivfpq_search(st, q, k, nprobe, 0, None, threads=threads)
+        batch = 256
+        done = 0
+        t0 = time.perf_counter()
+        while done == 0 or time.perf_counter() - t0 < seconds:
+            b = done % queries.shape[0]
+            run(queries[b:b + batch])
+            done += min(batch, queries.shape[0] - b)
+        elapsed = time.perf_counter() - t0
+    return {"value": done / elapsed, "unit": "queries/s", "cores": threads, "kind": kind,
+            "sample": f"{done} queries (the 10,000-query set cycled in batches of {batch}) at nprobe {nprobe} "
+                      f"against the same 1,000,000-vector index loaded from .qvr ({elapsed:.1f} s, "
+                      f"{threads} threads, ThreadPool grain 1)"}
+
+
 def cpu_baseline_flat(base, queries, k, seconds, threads):
     """QPS of the reference CPU flat search over a bounded prefix of the query batch."""
     from oracle.oracle import Oracle, Reference
@@ -182,7 +311,7 @@ def cpu_baseline_flat(base, queries, k, seconds, threads):
     t0 = time.perf_counter()
     while done < queries.shape[0] and (time.perf_counter() - t0 < seconds or done == 0):
         run(queries[done:done + batch])
-        done += batch
+        done = min(done + batch, queries.shape[0])
     elapsed = time.perf_counter() - t0
     return {"value": done / elapsed, "unit": "queries/s", "cores": threads, "kind": kind,
             "sample": f"first {done} of {queries.shape[0]} queries against all {base.shape[0]} rows "
@@ -206,9 +335,13 @@ def main():
     hip, qvh = Hip(), Qvh()
     name, arch, cus = qvh.device()
     flat, base, queries = bench_flat(args, hip, qvh)
+    idx, ivf = bench_ivfpq(args, hip, qvh, base, queries)
     cpu = None
+    ivf["cpu_baseline"] = None
     if not args.no_cpu:
-        cpu = cpu_baseline_flat(base, queries[:4096], 10, args.cpu_seconds, args.cpu_threads)
+        cpu = cpu_baseline_flat(base, queries, 10, args.cpu_seconds, args.cpu_threads)
+        ivf["cpu_baseline"] = cpu_baseline_ivfpq(idx, queries, 10, 32, args.cpu_seconds / 3,
+                                                 args.cpu_threads)
     line = {
         "metric": METRIC,
         "value": flat["value"],
@@ -227,6 +360,7 @@ def main():
         "cpu_baseline": cpu,
         "stage_ms": flat["stage_ms"],
         "nsplit": flat["nsplit"],
+        "ivfpq": ivf,
         "device": {"name": name, "arch": arch, "compute_units": cus},
     }
     print(json.dumps(line))

@@ -77,6 +77,10 @@ void qvh_flat_destroy(qvh_flat* flat);
  * stored, i.e. normalized for cosine, for the host copy the C++ class keeps. */
 qvh_status qvh_flat_append(qvh_flat* flat, const float* rows, uint64_t n, float* stored_out);
 
+/* Appends n rows that are already in stored form (cosine rows unit-normalized), as
+ * FlatIndex::load installs the VECT section (src/flat_index.cc:155-176). */
+qvh_status qvh_flat_append_stored(qvh_flat* flat, const float* rows, uint64_t n);
+
 /* Number of stored rows. */
 uint64_t qvh_flat_size(const qvh_flat* flat);
 
@@ -135,6 +139,12 @@ qvh_status qvh_ivfpq_encode(qvh_ivfpq* ivf, const float* x, uint64_t n, uint32_t
  * place its labels. */
 qvh_status qvh_ivfpq_add(qvh_ivfpq* ivf, const float* x, uint64_t n, uint32_t* assign_out);
 
+/* Installs whole lists into an empty trained index, as IvfPqIndex::load does from the LOFF /
+ * CODE / VECT sections (src/ivfpq_index.cc:547-573): offsets [nlist + 1], codes [count][m] and,
+ * with store_vectors, vectors [count][dim], all in list order. */
+qvh_status qvh_ivfpq_set_lists(qvh_ivfpq* ivf, const uint64_t* offsets, const uint8_t* codes,
+                               const float* vectors);
+
 uint64_t qvh_ivfpq_size(const qvh_ivfpq* ivf);
 /* CSR offsets [nlist + 1] of the lists. */
 qvh_status qvh_ivfpq_list_offsets(qvh_ivfpq* ivf, uint64_t* offsets);
@@ -155,9 +165,11 @@ qvh_status qvh_ivfpq_search_device(qvh_ivfpq* ivf, const float* d_queries, uint6
                                    float* d_out_dist, void* stream);
 qvh_status qvh_ivfpq_sync(qvh_ivfpq* ivf);
 /* Measurement hook (no counterpart in the reference): HIP events around the probe selection
- * (query prep, coarse scores, top-nprobe) and the list scan of each search. */
+ * (query prep, coarse scores, top-nprobe) and the list scan of each search, and the PQ code
+ * bytes the scan had to read (sum over queries and probed lists of len * m; nullable). */
 qvh_status qvh_ivfpq_set_timing(qvh_ivfpq* ivf, int enable);
-qvh_status qvh_ivfpq_last_timing(qvh_ivfpq* ivf, float* select_ms, float* scan_ms);
+qvh_status qvh_ivfpq_last_timing(qvh_ivfpq* ivf, float* select_ms, float* scan_ms,
+                                 uint64_t* code_bytes);
 
 /* ------------------------------------------------------------------------------------------ *
  * Nearest-centroid assignment for k-means (src/product_quantizer.cc:72-77), restating

@@ -329,7 +329,12 @@ class Reference:
         L.qref_ivfpq_search.argtypes = [C.c_void_p, _f32p, _sz, _sz, _sz, _sz, C.c_void_p,
                                         C.c_int64, _sz, _u64p, _f32p]
         L.qref_ivfpq_save.argtypes = [C.c_void_p, C.c_char_p]
-        L.qref_ivfpq_load.argtypes = [C.c_char_p]
+        L.qref_flat_save.argtypes = [C.c_void_p, C.c_char_p]
+        L.qref_flat_load.argtypes = [C.c_char_p, C.c_int]
+        L.qref_flat_load.restype = C.c_void_p
+        L.qref_flat_size.argtypes = [C.c_void_p]
+        L.qref_flat_size.restype = _sz
+        L.qref_ivfpq_load.argtypes = [C.c_char_p, C.c_int]
         L.qref_ivfpq_load.restype = C.c_void_p
         L.qref_ivfpq_size.argtypes = [C.c_void_p]
         L.qref_ivfpq_size.restype = _sz
@@ -365,6 +370,21 @@ class Reference:
 
     def flat(self, dim, metric="l2"):
         return RefFlat(self, dim, metric)
+
+    def flat_load(self, path, verify_checksums=True):
+        """FlatIndex::load of the reference (src/flat_index.cc:155-176)."""
+        return RefFlat(self, 0, None, handle=self._load(self.lib.qref_flat_load, path, verify_checksums))
+
+    def ivfpq_load(self, path, verify_checksums=True):
+        """IvfPqIndex::load of the reference (src/ivfpq_index.cc:507-576)."""
+        return RefIvfPq(self, 0, None, 0, 0, 0, False, 0,
+                        handle=self._load(self.lib.qref_ivfpq_load, path, verify_checksums))
+
+    def _load(self, fn, path, verify):
+        h = fn(str(path).encode(), int(bool(verify)))
+        if not h:
+            raise ValueError(self.lib.qref_last_error().decode())
+        return h
 
     def ivfpq(self, dim, metric="l2", nlist=1024, m=16, train_iterations=20,
               store_vectors=False, seed=1234):
@@ -420,9 +440,9 @@ def _labels_arg(allowed):
 
 
 class RefFlat:
-    def __init__(self, ref: Reference, dim, metric):
+    def __init__(self, ref: Reference, dim, metric, handle=None):
         self.ref, self.dim = ref, dim
-        self.h = ref.lib.qref_flat_new(dim, metric_id(metric))
+        self.h = handle if handle else ref.lib.qref_flat_new(dim, metric_id(metric))
         if not self.h:
             raise ValueError(ref.lib.qref_last_error().decode())
 
@@ -446,12 +466,19 @@ class RefFlat:
                                                       labels, dist))
         return labels, dist
 
+    def save(self, path):
+        self.ref._check(self.ref.lib.qref_flat_save(self.h, str(path).encode()))
+
+    def __len__(self):
+        return int(self.ref.lib.qref_flat_size(self.h))
+
 
 class RefIvfPq:
-    def __init__(self, ref: Reference, dim, metric, nlist, m, iters, store_vectors, seed):
+    def __init__(self, ref: Reference, dim, metric, nlist, m, iters, store_vectors, seed,
+                 handle=None):
         self.ref, self.dim = ref, dim
-        self.h = ref.lib.qref_ivfpq_new(dim, metric_id(metric), nlist, m, iters,
-                                        int(store_vectors), C.c_uint64(seed))
+        self.h = handle if handle else ref.lib.qref_ivfpq_new(
+            dim, metric_id(metric), nlist, m, iters, int(store_vectors), C.c_uint64(seed))
         if not self.h:
             raise ValueError(ref.lib.qref_last_error().decode())
 

@@ -105,6 +105,20 @@ int qref_flat_search(void* h, const float* q, std::size_t nq, std::size_t k,
   });
 }
 
+int qref_flat_save(void* h, const char* path) {
+  return guarded([&] { static_cast<quiver::FlatIndex*>(h)->save(path); });
+}
+void* qref_flat_load(const char* path, int verify_checksums) {
+  quiver::FlatIndex* out = nullptr;
+  guarded([&] {
+    quiver::LoadOptions o;
+    o.verify_checksums = verify_checksums != 0;
+    out = new quiver::FlatIndex(quiver::FlatIndex::load(path, o));
+  });
+  return out;
+}
+std::size_t qref_flat_size(void* h) { return static_cast<quiver::FlatIndex*>(h)->size(); }
+
 // ---- IvfPqIndex -----------------------------------------------------------------------------
 void* qref_ivfpq_new(std::size_t dim, int metric, std::size_t nlist, std::size_t m,
                      std::size_t train_iterations, int store_vectors, std::uint64_t seed) {
@@ -148,9 +162,13 @@ int qref_ivfpq_search(void* h, const float* q, std::size_t nq, std::size_t k, st
 int qref_ivfpq_save(void* h, const char* path) {
   return guarded([&] { static_cast<quiver::IvfPqIndex*>(h)->save(path); });
 }
-void* qref_ivfpq_load(const char* path) {
+void* qref_ivfpq_load(const char* path, int verify_checksums) {
   quiver::IvfPqIndex* out = nullptr;
-  guarded([&] { out = new quiver::IvfPqIndex(quiver::IvfPqIndex::load(path)); });
+  guarded([&] {
+    quiver::LoadOptions o;
+    o.verify_checksums = verify_checksums != 0;
+    out = new quiver::IvfPqIndex(quiver::IvfPqIndex::load(path, o));
+  });
   return out;
 }
 std::size_t qref_ivfpq_size(void* h) { return static_cast<quiver::IvfPqIndex*>(h)->size(); }

@@ -146,6 +146,15 @@ class IvfPqIndex:
     def list_sizes(self):
         return self._index.list_sizes()
 
+    def save(self, path: str) -> None:
+        """Writes a ``.qvr`` file that the reference's ``IvfPqIndex.load`` also reads."""
+        self._index.save(str(path))
+
+    @classmethod
+    def load(cls, path: str, verify_checksums: bool = True) -> "IvfPqIndex":
+        """Reads a ``.qvr`` IVF-PQ file (ours or the reference's) onto the GPU."""
+        return cls(0, _native=_quiver.IvfPqIndex.load(str(path), verify_checksums))
+
     def __len__(self) -> int:
         return len(self._index)
 
@@ -188,6 +197,15 @@ class FlatIndex:
     def get_vector(self, row: int) -> np.ndarray:
         """Stored row ``row`` (normalized for cosine)."""
         return self._index.get_vector(int(row))
+
+    def save(self, path: str) -> None:
+        """Writes a ``.qvr`` file that the reference's ``FlatIndex.load`` also reads."""
+        self._index.save(str(path))
+
+    @classmethod
+    def load(cls, path: str, verify_checksums: bool = True) -> "FlatIndex":
+        """Reads a ``.qvr`` flat file (ours or the reference's) onto the GPU."""
+        return cls(0, _native=_quiver.FlatIndex.load(str(path), verify_checksums))
 
     def __len__(self) -> int:
         return len(self._index)

@@ -712,30 +712,40 @@ qvh_status qvh_flat_last_timing(qvh_flat* f, float* prep_ms, float* scan_ms, flo
 
 uint64_t qvh_flat_size(const qvh_flat* f) { return f ? f->n : 0; }
 
+namespace {
+
+void flat_append(qvh_flat* f, const float* rows, uint64_t n, float* stored_out, bool as_stored) {
+  QVH_REQUIRE(f != nullptr, "qvh_flat_append: null handle");
+  if (n == 0) return;
+  QVH_REQUIRE(rows != nullptr, "qvh_flat_append: null rows");
+  std::lock_guard<std::mutex> lock(f->mu);
+  QVH_REQUIRE(f->n + n <= 0xFFFFFFFFull, "FlatIndex holds at most 2^32 vectors");
+  QVH_HIP(hipSetDevice(f->device));
+  flat_grow(f, f->n + n);
+  const size_t raw_bytes = n * f->dim * sizeof(float);
+  float* stage = static_cast<float*>(f->w_stage.reserve(raw_bytes));
+  QVH_HIP(hipMemcpyAsync(stage, rows, raw_bytes, hipMemcpyHostToDevice, f->stream));
+  if (f->metric == QVH_METRIC_COSINE && !as_stored) launch_normalize_rows(stage, n, f->dim, f->stream);
+  float* dst = f->rows.as<float>() + f->n * f->dp;
+  const uint64_t total = n * f->dp;
+  hipLaunchKernelGGL(pack_rows_kernel, dim3(static_cast<unsigned>(ceil_div(total, 256))), dim3(256), 0,
+                     f->stream, stage, dst, n, f->dim, f->dp);
+  hipLaunchKernelGGL(row_norms_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0,
+                     f->stream, dst, f->norms.as<float>() + f->n, n, f->dp);
+  QVH_HIP(hipGetLastError());
+  if (stored_out) QVH_HIP(hipMemcpyAsync(stored_out, stage, raw_bytes, hipMemcpyDeviceToHost, f->stream));
+  QVH_HIP(hipStreamSynchronize(f->stream));
+  f->n += n;
+}
+
+}  // namespace
+
 qvh_status qvh_flat_append(qvh_flat* f, const float* rows, uint64_t n, float* stored_out) {
-  return guarded([&] {
-    QVH_REQUIRE(f != nullptr, "qvh_flat_append: null handle");
-    if (n == 0) return;
-    QVH_REQUIRE(rows != nullptr, "qvh_flat_append: null rows");
-    std::lock_guard<std::mutex> lock(f->mu);
-    QVH_REQUIRE(f->n + n <= 0xFFFFFFFFull, "FlatIndex holds at most 2^32 vectors");
-    QVH_HIP(hipSetDevice(f->device));
-    flat_grow(f, f->n + n);
-    const size_t raw_bytes = n * f->dim * sizeof(float);
-    float* stage = static_cast<float*>(f->w_stage.reserve(raw_bytes));
-    QVH_HIP(hipMemcpyAsync(stage, rows, raw_bytes, hipMemcpyHostToDevice, f->stream));
-    if (f->metric == QVH_METRIC_COSINE) launch_normalize_rows(stage, n, f->dim, f->stream);
-    float* dst = f->rows.as<float>() + f->n * f->dp;
-    const uint64_t total = n * f->dp;
-    hipLaunchKernelGGL(pack_rows_kernel, dim3(static_cast<unsigned>(ceil_div(total, 256))), dim3(256), 0,
-                       f->stream, stage, dst, n, f->dim, f->dp);
-    hipLaunchKernelGGL(row_norms_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0,
-                       f->stream, dst, f->norms.as<float>() + f->n, n, f->dp);
-    QVH_HIP(hipGetLastError());
-    if (stored_out) QVH_HIP(hipMemcpyAsync(stored_out, stage, raw_bytes, hipMemcpyDeviceToHost, f->stream));
-    QVH_HIP(hipStreamSynchronize(f->stream));
-    f->n += n;
-  });
+  return guarded([&] { flat_append(f, rows, n, stored_out, false); });
+}
+
+qvh_status qvh_flat_append_stored(qvh_flat* f, const float* rows, uint64_t n) {
+  return guarded([&] { flat_append(f, rows, n, nullptr, true); });
 }
 
 qvh_status qvh_flat_search(qvh_flat* f, const float* queries, uint64_t nq, uint32_t k,

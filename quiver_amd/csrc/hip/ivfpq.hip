@@ -200,6 +200,19 @@ __global__ void term1_kernel(const uint8_t* __restrict__ codes, uint32_t mp, con
   out[p] = static_cast<float>(s);
 }
 
+/// The list of every CSR position (for term1 of lists installed as a whole).
+__global__ void position_lists_kernel(const uint64_t* __restrict__ off, uint32_t nlist, uint64_t count,
+                                      uint32_t* __restrict__ out) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= count) return;
+  uint32_t lo = 0, hi = nlist;
+  while (hi - lo > 1) {
+    const uint32_t mid = (lo + hi) / 2;
+    if (off[mid] <= i) lo = mid; else hi = mid;
+  }
+  out[i] = lo;
+}
+
 /// Codes of n points from [n][m] (sub-space minor) to the padded CSR stride.
 __global__ void pad_codes_kernel(const uint8_t* __restrict__ src, uint32_t m, uint32_t mp, uint64_t n,
                                  uint8_t* __restrict__ dst) {
@@ -625,6 +638,26 @@ void launch_nearest(bool sqdiff, const NearestArgs& a, uint32_t nsub, hipStream_
 
 }  // namespace
 
+/// Measurement only: bytes of PQ codes the scan must read, sum over queries and probes of
+/// len(list) * m. One block; thread sums, then an LDS tree.
+__global__ void __launch_bounds__(256) probed_code_bytes_kernel(const uint32_t* __restrict__ probes, uint64_t entries,
+                                                                const uint64_t* __restrict__ off, uint32_t m,
+                                                                uint64_t* __restrict__ out) {
+  __shared__ uint64_t part[256];
+  uint64_t s = 0;
+  for (uint64_t i = threadIdx.x; i < entries; i += 256) {
+    const uint32_t l = probes[i];
+    s += off[l + 1] - off[l];
+  }
+  part[threadIdx.x] = s;
+  __syncthreads();
+  for (unsigned w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[0] = part[0] * m;
+}
+
 // ---- handle ---------------------------------------------------------------------------------------
 
 struct qvh_ivfpq {
@@ -641,7 +674,7 @@ struct qvh_ivfpq {
   hipStream_t stream = nullptr;
   std::mutex mu;
   DeviceBuffer w_x, w_res, w_assign, w_codes, w_codes_p, w_t1, w_dest, w_shift;
-  DeviceBuffer w_q, w_scores, w_probes, w_bits, w_refs, w_dist;
+  DeviceBuffer w_q, w_scores, w_probes, w_bits, w_refs, w_dist, w_bytes;
   bool timing = false, timed = false;
   hipEvent_t ev[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
 };
@@ -789,7 +822,12 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
     throw Failure(QVH_EUNSUPPORTED, "IVF-PQ device path supports m <= 128");
   }
   QVH_HIP(hipGetLastError());
-  if (h->timed) QVH_HIP(hipEventRecord(h->ev[2], s));
+  if (h->timed) {
+    QVH_HIP(hipEventRecord(h->ev[2], s));
+    uint64_t* bytes = static_cast<uint64_t*>(h->w_bytes.reserve(sizeof(uint64_t)));
+    hipLaunchKernelGGL(probed_code_bytes_kernel, dim3(1), dim3(256), 0, s, probes, nq * nprobe, a.off, h->m, bytes);
+    QVH_HIP(hipGetLastError());
+  }
 }
 
 }  // namespace
@@ -1009,6 +1047,62 @@ qvh_status qvh_ivfpq_add(qvh_ivfpq* h, const float* x, uint64_t n, uint32_t* ass
   });
 }
 
+qvh_status qvh_ivfpq_set_lists(qvh_ivfpq* h, const uint64_t* offsets, const uint8_t* codes,
+                               const float* vectors) {
+  return guarded([&] {
+    QVH_REQUIRE(h && offsets, "qvh_ivfpq_set_lists: null argument");
+    std::lock_guard<std::mutex> lock(h->mu);
+    ivf_check_trained(h);
+    QVH_REQUIRE(h->count == 0, "qvh_ivfpq_set_lists: the index already holds vectors");
+    const uint32_t nl = h->nlist;
+    QVH_REQUIRE(offsets[0] == 0, "list offsets must start at 0");
+    for (uint32_t l = 0; l < nl; ++l) {
+      QVH_REQUIRE(offsets[l] <= offsets[l + 1], "list offsets must not decrease");
+      QVH_REQUIRE(offsets[l + 1] - offsets[l] <= 0xFFFFFFFFull, "too many vectors in one IVF cell");
+    }
+    const uint64_t count = offsets[nl];
+    if (count == 0) return;
+    QVH_REQUIRE(count < 0xFFFFFFFFull, "IVF-PQ device path holds fewer than 2^32 vectors");
+    QVH_REQUIRE(codes != nullptr, "qvh_ivfpq_set_lists: null codes");
+    QVH_REQUIRE(!h->store_vectors || vectors != nullptr, "qvh_ivfpq_set_lists: vectors are required");
+    QVH_HIP(hipSetDevice(h->device));
+    hipStream_t s = h->stream;
+    DeviceBuffer ncodes, nt1, nvec, noff, raw, lists;
+    ncodes.reserve(count * h->mp);
+    noff.reserve((nl + 1) * sizeof(uint64_t));
+    raw.reserve(count * h->m);
+    QVH_HIP(hipMemcpyAsync(noff.ptr, offsets, (nl + 1) * sizeof(uint64_t), hipMemcpyHostToDevice, s));
+    QVH_HIP(hipMemcpyAsync(raw.ptr, codes, count * h->m, hipMemcpyHostToDevice, s));
+    hipLaunchKernelGGL(pad_codes_kernel, dim3(static_cast<unsigned>(ceil_div(count * h->mp, 256))), dim3(256), 0, s,
+                       raw.as<uint8_t>(), h->m, h->mp, count, ncodes.as<uint8_t>());
+    if (h->has_pre) {
+      lists.reserve(count * sizeof(uint32_t));
+      nt1.reserve(count * sizeof(float));
+      hipLaunchKernelGGL(position_lists_kernel, dim3(static_cast<unsigned>(ceil_div(count, 256))), dim3(256), 0, s,
+                         noff.as<uint64_t>(), nl, count, lists.as<uint32_t>());
+      hipLaunchKernelGGL(term1_kernel, dim3(static_cast<unsigned>(ceil_div(count, 256))), dim3(256), 0, s,
+                         ncodes.as<uint8_t>(), h->mp, lists.as<uint32_t>(), h->pre.as<float>(), h->m, count,
+                         nt1.as<float>());
+    }
+    if (h->store_vectors) {
+      nvec.reserve(count * h->dim * sizeof(float));
+      QVH_HIP(hipMemcpyAsync(nvec.ptr, vectors, count * h->dim * sizeof(float), hipMemcpyHostToDevice, s));
+    }
+    QVH_HIP(hipGetLastError());
+    QVH_HIP(hipStreamSynchronize(s));
+    std::swap(h->codes.ptr, ncodes.ptr);
+    std::swap(h->codes.bytes, ncodes.bytes);
+    std::swap(h->t1.ptr, nt1.ptr);
+    std::swap(h->t1.bytes, nt1.bytes);
+    std::swap(h->vec.ptr, nvec.ptr);
+    std::swap(h->vec.bytes, nvec.bytes);
+    std::swap(h->off.ptr, noff.ptr);
+    std::swap(h->off.bytes, noff.bytes);
+    h->h_off.assign(offsets, offsets + nl + 1);
+    h->count = count;
+  });
+}
+
 uint64_t qvh_ivfpq_size(const qvh_ivfpq* h) { return h ? h->count : 0; }
 
 qvh_status qvh_ivfpq_list_offsets(qvh_ivfpq* h, uint64_t* offsets) {
@@ -1099,7 +1193,7 @@ qvh_status qvh_ivfpq_set_timing(qvh_ivfpq* h, int enable) {
   });
 }
 
-qvh_status qvh_ivfpq_last_timing(qvh_ivfpq* h, float* select_ms, float* scan_ms) {
+qvh_status qvh_ivfpq_last_timing(qvh_ivfpq* h, float* select_ms, float* scan_ms, uint64_t* code_bytes) {
   return guarded([&] {
     QVH_REQUIRE(h != nullptr, "qvh_ivfpq_last_timing: null handle");
     std::lock_guard<std::mutex> lock(h->mu);
@@ -1111,6 +1205,10 @@ qvh_status qvh_ivfpq_last_timing(qvh_ivfpq* h, float* select_ms, float* scan_ms)
     QVH_HIP(hipEventElapsedTime(&b, h->ev[1], h->ev[2]));
     if (select_ms) *select_ms = a;
     if (scan_ms) *scan_ms = b;
+    if (code_bytes) {
+      QVH_HIP(hipStreamSynchronize(h->stream));
+      QVH_HIP(hipMemcpy(code_bytes, h->w_bytes.ptr, sizeof(uint64_t), hipMemcpyDeviceToHost));
+    }
   });
 }
 

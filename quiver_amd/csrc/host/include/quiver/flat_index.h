@@ -41,6 +41,12 @@ class FlatIndex {
   std::size_t dim() const noexcept { return dim_; }
   Metric metric() const noexcept { return metric_; }
 
+  /// Writes the index as a `.qvr` file readable by the reference's FlatIndex::load
+  /// (src/flat_index.cc:147-153); atomic replace of `path`.
+  void save(const std::string& path) const;
+  /// Reads a `.qvr` flat index (src/flat_index.cc:155-176) and uploads its rows as stored.
+  static FlatIndex load(const std::string& path, const LoadOptions& options = {});
+
   /// Stored vector `i` (normalized for cosine). Not synchronized with add().
   const float* vector(std::size_t i) const noexcept { return data_.data() + i * dim_; }
   Label label(std::size_t i) const noexcept { return labels_[i]; }

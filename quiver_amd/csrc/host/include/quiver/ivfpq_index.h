@@ -60,6 +60,13 @@ class IvfPqIndex {
                     float* distances, const IvfPqSearchParams& params = {},
                     ThreadPool* pool = nullptr) const;
 
+  /// Writes the index as a `.qvr` file readable by the reference's IvfPqIndex::load
+  /// (src/ivfpq_index.cc:465-505); atomic replace of `path`.
+  void save(const std::string& path) const;
+  /// Reads a `.qvr` IVF-PQ index (src/ivfpq_index.cc:507-576): the trained state goes to the
+  /// device as after train(), the CSR lists straight into the device list layout.
+  static IvfPqIndex load(const std::string& path, const LoadOptions& options = {});
+
   std::size_t size() const noexcept;
   std::size_t dim() const noexcept;
   const IvfPqParams& params() const noexcept;
@@ -83,6 +90,7 @@ class IvfPqIndex {
 
  private:
   struct Impl;
+  explicit IvfPqIndex(std::unique_ptr<Impl> impl);
   std::unique_ptr<Impl> impl_;
 };
 

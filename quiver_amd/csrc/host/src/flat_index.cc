@@ -1,12 +1,31 @@
 #include "quiver/flat_index.h"
 
 #include <algorithm>
+#include <cmath>
 #include <limits>
 #include <mutex>
 
+#include "container.h"
 #include "device_util.h"
 
 namespace quiver {
+
+namespace {
+
+constexpr std::uint32_t kMetaSection = internal::section_tag("META");
+constexpr std::uint32_t kVectorSection = internal::section_tag("VECT");
+constexpr std::uint32_t kLabelSection = internal::section_tag("LABL");
+
+/// META payload of a flat index file (src/flat_index.cc:24-29).
+struct FlatFileMeta {
+  std::uint64_t dim;
+  std::uint64_t count;
+  std::uint32_t metric;
+  std::uint32_t reserved;
+};
+static_assert(sizeof(FlatFileMeta) == 24);
+
+}  // namespace
 
 using internal::check_finite;
 using internal::qvh_check;
@@ -105,6 +124,42 @@ void FlatIndex::search_batch(const float* queries, std::size_t nq, std::size_t k
 std::size_t FlatIndex::size() const {
   std::shared_lock lock(*mu_);
   return labels_.size();
+}
+
+void FlatIndex::save(const std::string& path) const {
+  std::shared_lock lock(*mu_);
+  internal::ContainerWriter w(internal::ContainerKind::kFlat);
+  w.section_pod(kMetaSection, FlatFileMeta{dim_, labels_.size(), static_cast<std::uint32_t>(metric_), 0});
+  w.section_bytes(kVectorSection, data_.data(), data_.size() * sizeof(float));
+  w.section_bytes(kLabelSection, labels_.data(), labels_.size() * sizeof(Label));
+  w.commit(path);
+}
+
+FlatIndex FlatIndex::load(const std::string& path, const LoadOptions& options) {
+  const auto img = internal::ContainerImage::open(path, internal::ContainerKind::kFlat, options.verify_checksums);
+  const std::string bad = "corrupt index file '" + path + "': ";
+  const auto meta = img->pod<FlatFileMeta>(kMetaSection);
+  QUIVER_CHECK(meta.dim >= 1 && meta.dim <= kMaxDimension, bad + "bad dimension");
+  QUIVER_CHECK(meta.metric <= static_cast<std::uint32_t>(Metric::kCosine), bad + "unknown metric");
+  QUIVER_CHECK(meta.count <= img->file_size() / (meta.dim * sizeof(float) + sizeof(Label)), bad + "bad vector count");
+  const std::size_t dim = static_cast<std::size_t>(meta.dim), count = static_cast<std::size_t>(meta.count);
+  QUIVER_CHECK(count <= std::numeric_limits<NodeId>::max(), "FlatIndex holds at most 2^32 vectors");
+  const float* vectors = img->array<float>(kVectorSection, count * dim);
+  const Label* labels = img->array<Label>(kLabelSection, count);
+  QUIVER_CHECK(std::all_of(vectors, vectors + count * dim, [](float v) { return std::isfinite(v); }),
+               bad + "non-finite vector values");
+  FlatIndex index(dim, static_cast<Metric>(meta.metric));
+  if (count > 0) {
+    qvh_flat* h = nullptr;
+    qvh_check(qvh_flat_create(static_cast<std::uint32_t>(dim), static_cast<int>(meta.metric), &h),
+              "FlatIndex device mirror");
+    index.dev_ = std::shared_ptr<qvh_flat>(h, qvh_flat_destroy);
+    // The file holds rows as stored (already normalized for cosine): upload them unchanged.
+    qvh_check(qvh_flat_append_stored(h, vectors, count), "FlatIndex::load");
+  }
+  index.data_.assign(vectors, vectors + count * dim);
+  index.labels_.assign(labels, labels + count);
+  return index;
 }
 
 }  // namespace quiver

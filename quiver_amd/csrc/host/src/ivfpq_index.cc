@@ -1,12 +1,14 @@
 #include "quiver/ivfpq_index.h"
 
 #include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <limits>
 #include <mutex>
 #include <random>
 #include <shared_mutex>
 
+#include "container.h"
 #include "device_util.h"
 #include "quiver/quantizer.h"
 
@@ -21,6 +23,21 @@ constexpr std::size_t kMaxLists = std::size_t{1} << 24;
 constexpr std::size_t kSubCentroids = 256;
 /// The precomputed L2 term table is used when it fits this budget (src/ivfpq_index.cc:73-74).
 constexpr std::size_t kMaxPrecomputedBytes = std::size_t{256} << 20;
+
+constexpr std::uint32_t kMetaSection = internal::section_tag("META");
+constexpr std::uint32_t kCentroidSection = internal::section_tag("CENT");
+constexpr std::uint32_t kCodebookSection = internal::section_tag("PQCB");
+constexpr std::uint32_t kOffsetSection = internal::section_tag("LOFF");
+constexpr std::uint32_t kCodeSection = internal::section_tag("CODE");
+constexpr std::uint32_t kLabelSection = internal::section_tag("LABL");
+constexpr std::uint32_t kVectorSection = internal::section_tag("VECT");
+
+/// META payload of an IVF-PQ index file (src/ivfpq_index.cc:32-43).
+struct IvfPqFileMeta {
+  std::uint64_t dim, nlist, m, count, train_iterations, seed;
+  std::uint32_t metric, store_vectors, trained, reserved;
+};
+static_assert(sizeof(IvfPqFileMeta) == 64);
 
 void normalize_rows(float* v, std::size_t n, std::size_t dim) {
   if (n == 0) return;
@@ -208,6 +225,7 @@ struct IvfPqIndex::Impl {
 };
 
 IvfPqIndex::IvfPqIndex(const IvfPqParams& params) : impl_(std::make_unique<Impl>(params)) {}
+IvfPqIndex::IvfPqIndex(std::unique_ptr<Impl> impl) : impl_(std::move(impl)) {}
 IvfPqIndex::~IvfPqIndex() = default;
 IvfPqIndex::IvfPqIndex(IvfPqIndex&&) noexcept = default;
 IvfPqIndex& IvfPqIndex::operator=(IvfPqIndex&&) noexcept = default;
@@ -322,5 +340,79 @@ std::vector<float> IvfPqIndex::list_vectors() const {
 }
 
 qvh_ivfpq* IvfPqIndex::device_handle() const noexcept { return impl_->dev.get(); }
+
+void IvfPqIndex::save(const std::string& path) const {
+  std::shared_lock lock(impl_->mu);
+  const Impl& ix = *impl_;
+  const IvfPqParams& p = ix.params;
+  const IvfPqFileMeta meta{p.dim, p.nlist, p.m, ix.count, p.train_iterations, p.seed,
+                           static_cast<std::uint32_t>(p.metric), p.store_vectors ? 1u : 0u,
+                           ix.trained ? 1u : 0u, 0};
+  // Codes and vectors live on the device; bring them back in list (CSR) order.
+  std::vector<std::uint8_t> codes(ix.count * p.m);
+  std::vector<float> vectors(p.store_vectors ? ix.count * p.dim : 0);
+  if (ix.count > 0) {
+    qvh_check(qvh_ivfpq_lists(ix.dev.get(), codes.data(), p.store_vectors ? vectors.data() : nullptr),
+              "IvfPqIndex::save");
+  }
+  internal::ContainerWriter w(internal::ContainerKind::kIvfPq);
+  w.section_pod(kMetaSection, meta);
+  w.section_bytes(kCentroidSection, ix.centroids.data(), ix.centroids.size() * sizeof(float));
+  w.section_bytes(kCodebookSection, ix.codebook.data(), ix.codebook.size() * sizeof(float));
+  w.section_bytes(kOffsetSection, ix.offsets.data(), ix.offsets.size() * sizeof(std::uint64_t));
+  w.section_bytes(kCodeSection, codes.data(), codes.size());
+  w.section_bytes(kLabelSection, ix.labels.data(), ix.labels.size() * sizeof(Label));
+  if (p.store_vectors) w.section_bytes(kVectorSection, vectors.data(), vectors.size() * sizeof(float));
+  w.commit(path);
+}
+
+IvfPqIndex IvfPqIndex::load(const std::string& path, const LoadOptions& options) {
+  const auto img = internal::ContainerImage::open(path, internal::ContainerKind::kIvfPq, options.verify_checksums);
+  const std::string bad = "corrupt index file '" + path + "': ";
+  const auto meta = img->pod<IvfPqFileMeta>(kMetaSection);
+  QUIVER_CHECK(meta.dim >= 1 && meta.dim <= kMaxDimension, bad + "bad dimension");
+  QUIVER_CHECK(meta.m >= 1 && meta.m <= meta.dim && meta.dim % meta.m == 0, bad + "bad m");
+  QUIVER_CHECK(meta.nlist >= 1 && meta.nlist <= kMaxLists, bad + "bad nlist");
+  QUIVER_CHECK((meta.nlist + 1) * sizeof(std::uint64_t) <= img->file_size(), bad + "bad nlist");
+  QUIVER_CHECK(meta.metric <= static_cast<std::uint32_t>(Metric::kCosine), bad + "bad metric");
+  QUIVER_CHECK(meta.count <= img->file_size(), bad + "bad count");
+  IvfPqParams p;
+  p.dim = static_cast<std::size_t>(meta.dim);
+  p.nlist = static_cast<std::size_t>(meta.nlist);
+  p.m = static_cast<std::size_t>(meta.m);
+  p.train_iterations = static_cast<std::size_t>(meta.train_iterations);
+  p.seed = meta.seed;
+  p.metric = static_cast<Metric>(meta.metric);
+  p.store_vectors = meta.store_vectors != 0;
+  auto impl = std::make_unique<Impl>(p);
+  const std::size_t count = static_cast<std::size_t>(meta.count);
+  const std::uint64_t* offsets = img->array<std::uint64_t>(kOffsetSection, p.nlist + 1);
+  QUIVER_CHECK(offsets[0] == 0 && offsets[p.nlist] == count, bad + "bad list offsets");
+  for (std::size_t l = 0; l < p.nlist; ++l) QUIVER_CHECK(offsets[l] <= offsets[l + 1], bad + "bad list offsets");
+  const std::uint8_t* codes = img->array<std::uint8_t>(kCodeSection, count * p.m);
+  const Label* labels = img->array<Label>(kLabelSection, count);
+  const float* vectors = nullptr;
+  if (p.store_vectors) {
+    vectors = img->array<float>(kVectorSection, count * p.dim);
+    QUIVER_CHECK(std::all_of(vectors, vectors + count * p.dim, [](float v) { return std::isfinite(v); }),
+                 bad + "non-finite stored vectors");
+  }
+  if (meta.trained != 0) {
+    const std::size_t nc = p.nlist * p.dim, nb = p.m * kSubCentroids * (p.dim / p.m);
+    const float* cent = img->array<float>(kCentroidSection, nc);
+    const float* cb = img->array<float>(kCodebookSection, nb);
+    const auto finite = [](float v) { return std::isfinite(v); };
+    QUIVER_CHECK(std::all_of(cent, cent + nc, finite) && std::all_of(cb, cb + nb, finite),
+                 bad + "non-finite centroids");
+    impl->commit(std::vector<float>(cent, cent + nc), std::vector<float>(cb, cb + nb));
+    if (count > 0) qvh_check(qvh_ivfpq_set_lists(impl->dev.get(), offsets, codes, vectors), "IvfPqIndex::load");
+  } else {
+    QUIVER_CHECK(count == 0, bad + "untrained index with vectors");
+  }
+  impl->offsets.assign(offsets, offsets + p.nlist + 1);
+  impl->labels.assign(labels, labels + count);
+  impl->count = count;
+  return IvfPqIndex(std::move(impl));
+}
 
 }  // namespace quiver

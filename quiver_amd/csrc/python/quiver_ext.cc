@@ -149,6 +149,16 @@ PYBIND11_MODULE(_quiver, m) {
             return make_results(nq, k, std::move(labels), std::move(dist));
           },
           py::arg("queries"), py::arg("k"), py::arg("allowed").none(true), py::arg("num_threads"))
+      .def("save", &quiver::FlatIndex::save, py::arg("path"), py::call_guard<py::gil_scoped_release>())
+      .def_static(
+          "load",
+          [](const std::string& path, bool verify_checksums) {
+            quiver::LoadOptions o;
+            o.verify_checksums = verify_checksums;
+            py::gil_scoped_release release;
+            return quiver::FlatIndex::load(path, o);
+          },
+          py::arg("path"), py::arg("verify_checksums") = true)
       .def("__len__", &quiver::FlatIndex::size, py::call_guard<py::gil_scoped_release>())
       .def("get_vector",
            [](const quiver::FlatIndex& self, std::size_t i) {
@@ -157,6 +167,8 @@ PYBIND11_MODULE(_quiver, m) {
              std::memcpy(out.mutable_data(), self.vector(i), self.dim() * sizeof(float));
              return out;
            })
+      .def_property_readonly("_device_handle",
+                             [](const quiver::FlatIndex& s) { return reinterpret_cast<std::uintptr_t>(s.device_handle()); })
       .def_property_readonly("dim", &quiver::FlatIndex::dim)
       .def_property_readonly("metric", [](const quiver::FlatIndex& s) {
         return std::string(quiver::to_string(s.metric()));
@@ -219,8 +231,20 @@ PYBIND11_MODULE(_quiver, m) {
           },
           py::arg("queries"), py::arg("k"), py::arg("nprobe"), py::arg("refine_factor"),
           py::arg("allowed").none(true), py::arg("num_threads"))
+      .def("save", &quiver::IvfPqIndex::save, py::arg("path"), py::call_guard<py::gil_scoped_release>())
+      .def_static(
+          "load",
+          [](const std::string& path, bool verify_checksums) {
+            quiver::LoadOptions o;
+            o.verify_checksums = verify_checksums;
+            py::gil_scoped_release release;
+            return quiver::IvfPqIndex::load(path, o);
+          },
+          py::arg("path"), py::arg("verify_checksums") = true)
       .def("__len__", &quiver::IvfPqIndex::size, py::call_guard<py::gil_scoped_release>())
       .def_property_readonly("is_trained", &quiver::IvfPqIndex::is_trained)
+      .def_property_readonly("_device_handle",
+                             [](const quiver::IvfPqIndex& s) { return reinterpret_cast<std::uintptr_t>(s.device_handle()); })
       .def_property_readonly("dim", &quiver::IvfPqIndex::dim)
       .def_property_readonly("nlist", [](const quiver::IvfPqIndex& s) { return s.params().nlist; })
       .def_property_readonly("m", [](const quiver::IvfPqIndex& s) { return s.params().m; })

@@ -1,0 +1,327 @@
+"""The oracle pinned (CPU only).
+
+Three kinds of evidence, chosen so that a dropped term, a wrong sign or index, or a transposed
+operand in the C restatement (oracle/oracle.c) fails at least one of them:
+
+* golden vectors written by the COMPILED REFERENCE (tests/golden/make_golden.py): bit-identical
+  kernel outputs, normalized rows, k-means / PQ training, PQ codes, tables and ADC sums, flat
+  and IVF-PQ search outputs, trained IVF-PQ state and inverted lists;
+* known answers: the C++ standard's value for mt19937_64, the reference's own test cases
+  (tests/test_flat.cc:37-72, tests/test_quantizer.cc:70-92, tests/test_regressions.cc:101-118);
+* mathematics: float64 closed forms and brute force, exact integer arithmetic, the precomputed
+  L2 decomposition (src/ivfpq_index.cc:83-87), Lloyd's fixed point, refine-everything == exact.
+
+Label comparisons are tie-aware (parity.assert_same_topk): the reference orders exactly equal
+distances by libstdc++ heap mechanics, the oracle by (distance, id).
+"""
+
+import json
+import os
+
+import numpy as np
+import pytest
+
+from golden import inputs as G
+from oracle.oracle import IvfPqState, rows_bitmap
+from parity import assert_same_topk
+from quiver_amd import datasets as D
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+INVALID = np.uint64(2**64 - 1)
+
+
+def golden(name):
+    return np.load(os.path.join(GOLDEN, name), allow_pickle=False)
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def rows_to_labels(rows, labels=None):
+    rows = np.asarray(rows)
+    out = np.full(rows.shape, INVALID, dtype=np.uint64)
+    ok = rows != np.uint32(0xFFFFFFFF)
+    out[ok] = rows[ok].astype(np.uint64) if labels is None else labels[rows[ok].astype(np.int64)]
+    return out
+
+
+# ---- mt19937_64 ---------------------------------------------------------------------------------
+
+def test_mt19937_64_known_answer(oracle):
+    """[rand.predef]: the 10000th output of a default-constructed mt19937_64 (seed 5489)."""
+    assert int(oracle.mt64(5489, 10000)[-1]) == 9981545732273789042
+
+
+# ---- distance kernels and normalize -------------------------------------------------------------
+
+def test_kernels_match_reference_bits(oracle):
+    g = golden("kernels.npz")
+    a, b = G.kernel_pairs()
+    assert str(g["pairs_sha"]) == G.sha(a) + G.sha(b)
+    l2 = np.array([oracle.l2sqr(a[i, :i + 1], b[i, :i + 1]) for i in range(70)], np.float32)
+    dot = np.array([oracle.dot(a[i, :i + 1], b[i, :i + 1]) for i in range(70)], np.float32)
+    assert np.array_equal(bits(l2), bits(g["kern_l2"])), np.flatnonzero(bits(l2) != bits(g["kern_l2"])) + 1
+    assert np.array_equal(bits(dot), bits(g["kern_dot"])), np.flatnonzero(bits(dot) != bits(g["kern_dot"])) + 1
+
+
+def test_kernels_closed_form(oracle):
+    """Integer vectors: every partial sum is an exact float, so the result is the exact integer.
+    Real vectors: within the summation error bound of float64 truth."""
+    rng = np.random.default_rng(9)
+    for d in (1, 3, 4, 5, 8, 9, 31, 32, 33, 100, 128):
+        a = rng.integers(0, 256, d).astype(np.float32)
+        b = rng.integers(0, 256, d).astype(np.float32)
+        assert oracle.l2sqr(a, b) == float(((a.astype(np.int64) - b.astype(np.int64)) ** 2).sum())
+        assert oracle.dot(a, b) == float((a.astype(np.int64) * b.astype(np.int64)).sum())
+        x = rng.standard_normal(d).astype(np.float32)
+        y = rng.standard_normal(d).astype(np.float32)
+        bound = 2 * d * np.finfo(np.float32).eps
+        t = (x.astype(np.float64) - y) ** 2
+        assert abs(oracle.l2sqr(x, y) - t.sum()) <= bound * t.sum() + 1e-30
+        p = x.astype(np.float64) * y
+        assert abs(oracle.dot(x, y) - p.sum()) <= bound * np.abs(p).sum() + 1e-30
+
+
+def test_normalize_matches_reference_bits(oracle):
+    g = golden("kernels.npz")
+    for d in G.NORMALIZE_DIMS:
+        x = G.normalize_rows(d)
+        assert str(g[f"norm_sha_{d}"]) == G.sha(x)
+        got = oracle.normalize(x)
+        assert np.array_equal(bits(got), bits(g[f"norm_out_{d}"])), d
+
+
+def test_normalize_properties(oracle):
+    for d in G.NORMALIZE_DIMS:
+        x = G.normalize_rows(d)
+        y = oracle.normalize(x)
+        assert not y[0].any()  # the zero vector is left alone
+        # a float dot product that underflows to 0 leaves the row alone too (dispatch.cc:131)
+        assert np.array_equal(bits(y[2]), bits(x[2]))
+        norms = np.sqrt((y[[1] + list(range(3, 64))].astype(np.float64) ** 2).sum(1))
+        assert np.isfinite(norms[0]), "overflowing row must come back normalized (double path)"
+        assert np.allclose(norms, 1.0, atol=4e-6 * np.sqrt(d))
+        # direction is kept
+        cos = (x[3:].astype(np.float64) * y[3:]).sum(1) / np.linalg.norm(x[3:].astype(np.float64), axis=1)
+        assert np.allclose(cos, 1.0, atol=1e-5)
+
+
+# ---- flat search --------------------------------------------------------------------------------
+
+def _stored(oracle, base, metric):
+    return oracle.normalize(base) if metric == "cosine" else base
+
+
+@pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
+def test_flat_c1_matches_reference(oracle, metric):
+    g = golden("flat_c1.npz")
+    base, q = D.flat_small()
+    assert str(g["base_sha"]) == D.sha256(base) and str(g["query_sha"]) == D.sha256(q)
+    stored = _stored(oracle, base, metric)
+    rows, dist = oracle.flat_search(stored, q, 10, metric)
+    print(assert_same_topk(rows_to_labels(rows), dist, g[f"{metric}_labels"], g[f"{metric}_dist"]))
+    bm = rows_bitmap(G.flat_filter(base.shape[0]).astype(np.int64), base.shape[0])
+    rows, dist = oracle.flat_search(stored, q, 10, metric, row_bitmap=bm)
+    print(assert_same_topk(rows_to_labels(rows), dist, g[f"{metric}_f_labels"], g[f"{metric}_f_dist"]))
+
+
+def test_flat_fewer_than_k_matches_reference(oracle):
+    g = golden("flat_c1.npz")
+    small = G.few_rows()
+    labels = np.arange(100, 110, dtype=np.uint64)
+    rows, dist = oracle.flat_search(small, small[:3], 50)
+    got = rows_to_labels(rows, labels)
+    assert (got[:, 10:] == INVALID).all() and np.isinf(dist[:, 10:]).all()
+    assert_same_topk(got, dist, g["few_labels"], g["few_dist"])
+    bm = rows_bitmap(np.array([3, 7]), 10)
+    rows, dist = oracle.flat_search(small, small[:3], 5, row_bitmap=bm)
+    got = rows_to_labels(rows, labels)
+    assert set(got[:, :2].ravel()) <= {103, 107} and (got[:, 2:] == INVALID).all()
+    assert_same_topk(got, dist, g["few_f_labels"], g["few_f_dist"])
+
+
+def test_flat_known_answers(oracle):
+    """tests/test_flat.cc:37-52."""
+    base = np.array([[1, 0, 0, 0], [0, 2, 0, 0], [1, 1, 0, 0]], np.float32)
+    q = np.array([[3, 0.1, 0, 0]], np.float32)
+    rows, dist = oracle.flat_search(oracle.normalize(base), q, 3, "cosine")
+    assert rows[0, 0] == 0 and abs(dist[0, 0] - (1 - 3 / np.sqrt(9.01))) < 1e-5
+    rows, dist = oracle.flat_search(base, q, 3, "ip")
+    assert rows[0, 0] == 2 and abs(dist[0, 0] - (1 - 3.1)) < 1e-5
+
+
+def test_flat_brute_force_float64(oracle):
+    """Integer-valued mixture: distances are exact integers (equal to float64 truth), labels the
+    exact top-k up to equal-distance groups. N(0,1) data: within float error of float64 truth."""
+    base, q = D.int_mix(20_000, 40)
+    rows, dist = oracle.flat_search(base, q, 10)
+    d64 = ((q[:, None, :].astype(np.float64) - base[None, :, :]) ** 2).sum(-1)
+    order = np.lexsort((np.broadcast_to(np.arange(base.shape[0]), d64.shape), d64), axis=1)[:, :10]
+    assert np.array_equal(dist.astype(np.float64), np.take_along_axis(d64, order, 1))
+    assert_same_topk(rows_to_labels(rows), dist, order.astype(np.uint64), np.take_along_axis(d64, order, 1)
+                     .astype(np.float32))
+    base, q = D.flat_small()
+    rows, dist = oracle.flat_search(base[:3000], q[:20], 10)
+    d64 = ((q[:20, None, :].astype(np.float64) - base[None, :3000, :]) ** 2).sum(-1)
+    truth = np.sort(d64, 1)[:, :10]
+    assert np.allclose(dist, truth, rtol=2e-6)
+    got_true = np.take_along_axis(d64, rows.astype(np.int64), 1)
+    assert np.allclose(got_true, truth, rtol=2e-6)  # any swap is a float near-tie
+
+
+def test_argmin_first_minimum(oracle):
+    assert oracle.argmin_n(np.array([3, 1, 1, 0, 0, 2], np.float32)) == 3
+    assert oracle.argmin_n(np.zeros(9, np.float32)) == 0
+    assert oracle.argmin_n(np.array([np.inf, 5, np.inf], np.float32)) == 1
+
+
+# ---- k-means and PQ -----------------------------------------------------------------------------
+
+def test_kmeans_matches_reference_bits(oracle):
+    g = golden("kmeans.npz")
+    x, dup = G.kmeans_points()
+    assert str(g["km_sha"]) == G.sha(x) + G.sha(dup)
+    assert np.array_equal(bits(oracle.kmeans(x, 40, 8, seed=3)), bits(g["km_plain"]))
+    assert np.array_equal(bits(oracle.kmeans(dup, 16)), bits(g["km_split"]))
+    assert np.array_equal(bits(oracle.kmeans(x, 8, 5, max_points_per_centroid=100, seed=7)), bits(g["km_sub"]))
+
+
+def test_kmeans_fixed_point(oracle):
+    """Converged Lloyd's: every centroid is the mean of the points nearest to it."""
+    pts = G.clustered(3000, 8, 11)
+    cent = oracle.kmeans(pts, 30, 60, seed=2)
+    assign = oracle.nearest(pts, cent)
+    for j in range(30):
+        members = pts[assign == j].astype(np.float64)
+        assert members.shape[0] > 0
+        assert np.allclose(cent[j], members.mean(0), rtol=1e-5, atol=1e-5), j
+
+
+def test_pq_matches_reference_bits(oracle):
+    g = golden("kmeans.npz")
+    px, pq_q = G.pq_points()
+    assert str(g["pq_sha"]) == G.sha(px) + G.sha(pq_q)
+    cb = oracle.pq_train(px, 4, iterations=10, seed=5)
+    assert np.array_equal(bits(cb), bits(g["pq_codebook"]))
+    codes = oracle.pq_encode(cb, px[:500])
+    assert np.array_equal(codes, g["pq_codes"])
+    for i in range(5):
+        l2, ip = oracle.pq_tables(cb, pq_q[i])
+        assert np.array_equal(bits(l2), bits(g["pq_l2_tables"][i]))
+        assert np.array_equal(bits(ip), bits(g["pq_ip_tables"][i]))
+    adc = oracle.pq_adc(g["pq_l2_tables"][0], codes)
+    assert np.array_equal(bits(adc), bits(g["pq_adc_batch"]))
+    assert np.array_equal(bits(adc), bits(g["pq_adc_single"]))
+
+
+def test_pq_invariants(oracle):
+    """ADC equals the distance to the reconstruction (tests/test_quantizer.cc:70-92), and each
+    code is the float64 nearest codeword up to float near-ties."""
+    g = golden("kmeans.npz")
+    px, pq_q = G.pq_points()
+    cb = g["pq_codebook"].astype(np.float64)  # [m][256][dsub]
+    m, _, dsub = cb.shape
+    codes = oracle.pq_encode(g["pq_codebook"], px[:500])
+    rec = np.concatenate([cb[j][codes[:, j]] for j in range(m)], axis=1)
+    for i in range(5):
+        l2, ip = oracle.pq_tables(g["pq_codebook"], pq_q[i])
+        assert np.allclose(oracle.pq_adc(l2, codes), ((pq_q[i] - rec) ** 2).sum(1), atol=1e-3)
+        assert np.allclose(oracle.pq_adc(ip, codes), (pq_q[i] * rec).sum(1), atol=1e-3)
+    for j in range(m):
+        sub = px[:500, j * dsub:(j + 1) * dsub].astype(np.float64)
+        d = ((sub[:, None, :] - cb[j][None]) ** 2).sum(-1)
+        best = d.min(1)
+        chosen = d[np.arange(500), codes[:, j]]
+        assert np.all(chosen <= best + 1e-5 * np.maximum(best, 1.0))
+
+
+# ---- IVF-PQ ---------------------------------------------------------------------------------------
+
+def _ivf_state(oracle, base, metric, cent, cb):
+    pre = oracle.ivfpq_precompute(cent, cb) if metric == "l2" else None
+    assign, codes, stored = oracle.ivfpq_encode(cent, cb, metric, base)
+    return IvfPqState(metric, cent, cb, pre).set_lists(assign, codes, np.arange(base.shape[0], dtype=np.uint64),
+                                                       stored)
+
+
+@pytest.mark.parametrize("case", G.IVF_CASES, ids=[c[0] for c in G.IVF_CASES])
+def test_ivfpq_small_matches_reference(oracle, case):
+    name, metric, store, refine = case
+    g = golden("ivfpq_small.npz")
+    base, q = G.ivf_points()
+    assert str(g["ivf_sha"]) == G.sha(base) + G.sha(q)
+    cent, cb, pre = oracle.ivfpq_train(base, metric, G.IVF_NLIST, G.IVF_M, G.IVF_ITERS, 1234)
+    assert str(g[f"{name}_state_sha"]) == G.sha(cent) + G.sha(cb)
+    if name == "l2":
+        assert np.array_equal(bits(cent), bits(g["l2_centroids"]))
+        assert np.array_equal(bits(cb), bits(g["l2_codebook"]))
+    st = _ivf_state(oracle, base, metric, cent, cb)
+    if not store:
+        st.vectors = None
+    assert np.array_equal(st.offsets, g[f"{name}_offsets"])
+    assert np.array_equal(st.labels, g[f"{name}_order"].astype(np.uint64))
+    assert np.array_equal(st.codes, g[f"{name}_codes"])
+    for nprobe in G.IVF_NPROBES:
+        refs, dist = oracle.ivfpq_search(st, q, 10, nprobe, refine)
+        print(nprobe, assert_same_topk(st.ref_to_label(refs), dist, g[f"{name}_p{nprobe}_labels"],
+                                       g[f"{name}_p{nprobe}_dist"]))
+    if name == "l2r":
+        refs, dist = oracle.ivfpq_search(st, q[:10], 2, 32, 1 << 63)
+        assert_same_topk(st.ref_to_label(refs), dist, g["sat_labels"], g["sat_dist"])
+
+
+def test_ivfpq_refine_everything_is_exact(oracle):
+    """nprobe = nlist and k * refine_factor saturated: the exact flat answer
+    (tests/test_regressions.cc:101-118)."""
+    base, q = G.ivf_points()
+    cent, cb, _ = oracle.ivfpq_train(base, "l2", G.IVF_NLIST, G.IVF_M, G.IVF_ITERS, 1234)
+    st = _ivf_state(oracle, base, "l2", cent, cb)
+    refs, dist = oracle.ivfpq_search(st, q, 10, G.IVF_NLIST, 1 << 63)
+    rows, fdist = oracle.flat_search(base, q, 10)
+    assert_same_topk(st.ref_to_label(refs), dist, rows_to_labels(rows), fdist)
+
+
+def test_precomputed_table_decomposition(oracle):
+    """pre[l][j][c] = ||r||^2 + 2<c_l,j, r> for codeword r, so that
+    ||q - c_l - r||^2 = ||q - c_l||^2 + sum_j pre - 2 sum_j <q_j, r_j> (src/ivfpq_index.cc:83-87)."""
+    base, q = G.ivf_points()
+    cent, cb, _ = oracle.ivfpq_train(base, "l2", G.IVF_NLIST, G.IVF_M, G.IVF_ITERS, 1234)
+    pre = oracle.ivfpq_precompute(cent, cb).astype(np.float64)
+    c64, b64 = cent.astype(np.float64), cb.astype(np.float64)
+    m, _, dsub = b64.shape
+    cl = c64.reshape(G.IVF_NLIST, m, 1, dsub)
+    want = (b64[None] ** 2).sum(-1) + 2 * (cl * b64[None]).sum(-1)
+    assert np.allclose(pre, want, rtol=1e-5, atol=1e-5)
+    rng = np.random.default_rng(3)
+    for _ in range(20):
+        l, code = rng.integers(0, G.IVF_NLIST), rng.integers(0, 256, m)
+        r = np.concatenate([b64[j, code[j]] for j in range(m)])
+        lhs = ((q[0] - c64[l] - r) ** 2).sum()
+        rhs = ((q[0] - c64[l]) ** 2).sum() + pre[l, np.arange(m), code].sum() - 2 * (q[0] * r).sum()
+        assert abs(lhs - rhs) < 1e-6 * max(lhs, 1.0)
+
+
+@pytest.mark.slow
+def test_ivfpq_1m_matches_reference_hashes(oracle):
+    """The 1,000,000 x 128 integer mixture at nlist 2048, m 32: trained state, lists and the
+    first 200 searches of the compiled reference."""
+    path = os.path.join(GOLDEN, "ivfpq_1m.json")
+    if not os.path.exists(path):
+        pytest.skip("ivfpq_1m.json not generated")
+    with open(path) as f:
+        g = json.load(f)
+    base, q = D.int_mix()
+    assert D.sha256(base) == g["base_sha"] and D.sha256(q) == g["query_sha"]
+    sample = G.int_mix_sample(base.shape[0])
+    assert G.sha(sample.astype(np.int64)) == g["sample_sha"]
+    cent, cb, pre = oracle.ivfpq_train(base[sample], "l2", 2048, 32, 20, 1234)
+    assert G.sha(cent) == g["centroids_sha"] and G.sha(cb) == g["codebook_sha"]
+    st = _ivf_state(oracle, base, "l2", cent, cb)
+    st.vectors = None
+    assert G.sha(st.offsets) == g["offsets_sha"]
+    assert G.sha(st.labels) == g["labels_sha"]
+    assert G.sha(st.codes) == g["codes_sha"]
+    refs, dist = oracle.ivfpq_search(st, q[:200], 10, g["search_nprobe"])
+    exp_d = np.array(g["search_dist_bits"], dtype=np.uint32).view(np.float32)
+    print(assert_same_topk(st.ref_to_label(refs), dist, np.array(g["search_labels"]).astype(np.uint64), exp_d))
