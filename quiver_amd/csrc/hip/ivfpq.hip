@@ -358,6 +358,8 @@ struct ScanArgs {
   int refine;
   uint64_t* out_refs;
   float* out_dist;
+  uint64_t* sel;      // [nq][keep_sel] streaming scan -> finishing kernel
+  uint32_t* sel_cnt;  // [nq]
 };
 
 /// Ascending bitonic sort of s[0, n) (n a power of two) by all 256 threads.
@@ -419,6 +421,43 @@ __device__ __forceinline__ float adc_sum(const float* lut, const uint32_t (&w)[M
       const uint32_t c = (w[j >> 2] >> (8 * (j & 3))) & 0xFFu;
       s = s + lut[j * 256 + c];
     }
+  }
+  return s;
+}
+
+/// Code bytes of position pos as MPW dwords: whole 16-byte loads when the code fills all of them
+/// (FULL), else dword loads of the mp bytes and zeros after them.
+template <int MPW, bool FULL>
+__device__ __forceinline__ void load_code_padded(const uint8_t* codes, uint64_t pos, uint32_t mp, uint32_t (&w)[MPW]) {
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(codes + pos * mp);
+  if constexpr (FULL && MPW % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < MPW; i += 4) {
+      const uint4 v = *reinterpret_cast<const uint4*>(p + i);
+      w[i] = v.x;
+      w[i + 1] = v.y;
+      w[i + 2] = v.z;
+      w[i + 3] = v.w;
+    }
+  } else if constexpr (FULL && MPW == 2) {
+    const uint2 v = *reinterpret_cast<const uint2*>(p);
+    w[0] = v.x;
+    w[1] = v.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < MPW; ++i) w[i] = 4 * i < static_cast<int>(mp) ? p[i] : 0u;
+  }
+}
+
+/// sum_j table[j*256 + code_j] over all 4 * MPW table rows in order of j; rows past m hold zeros
+/// (and so do the code bytes past m), and adding +0.0 leaves the reference's sum unchanged.
+template <int MPW>
+__device__ __forceinline__ float adc_sum_rows(const float* lut, const uint32_t (&w)[MPW]) {
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4 * MPW; ++j) {
+    const uint32_t c = (w[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+    s = s + lut[j * 256 + c];
   }
   return s;
 }
@@ -625,6 +664,510 @@ __global__ void __launch_bounds__(kScanThreads) ivf_scan_kernel(ScanArgs a) {
   }
 }
 
+// ---- search: the streaming scan (approximate ADC in LDS, wave-private candidate queues) ----------
+//
+// One work-group of eight waves per query. The m x 256 table sits in LDS; the probed lists are
+// walked as one flattened sequence dealt round-robin to the 512 lanes, kStreamCodes codes per lane
+// in flight. Per-probe data (list start, probe key) lives in LDS and, while a lane stays in one
+// list, in registers, so a code costs two 16-byte loads, one 4-byte term load and m LDS lookups.
+// Candidates below the query's running threshold go to a queue private to their wave (no block
+// barrier and no atomics on the append path); a full queue is sorted inside the wave and cut to
+// keep_sel, and its keep_sel-th key tightens the threshold shared by the eight waves (each such key
+// bounds the query's final keep_sel-th key from above). At the end the eight lists are sorted
+// together and the keep_sel best go to the finishing kernel, which re-scores them exactly.
+
+constexpr int kStreamWaves = 8;
+constexpr int kStreamThreads = kStreamWaves * 64;
+constexpr uint32_t kStreamMaxProbes = 256;
+constexpr uint32_t kStreamMaxSel = 128;
+constexpr int kFinishThreads = 128;
+
+/// Ascending bitonic sort of N * 64 keys held by one wave, element e = i * 64 + lane in k[i].
+template <int N>
+__device__ __forceinline__ void wave_sort(uint64_t (&k)[N]) {
+  const int lane = threadIdx.x & 63;
+  constexpr int total = N * 64;
+#pragma unroll
+  for (int size = 2; size <= total; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      if (stride >= 64) {
+        const int is = stride / 64;
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+          const int j = i ^ is;
+          if (j > i) {
+            const bool up = ((i * 64) & size) == 0;
+            const uint64_t x = k[i], y = k[j];
+            const bool swap = (x > y) == up;
+            k[i] = swap ? y : x;
+            k[j] = swap ? x : y;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+          const uint64_t other = __shfl_xor(k[i], stride, 64);
+          const bool up = ((i * 64 + lane) & size) == 0;
+          const bool lower = (lane & stride) == 0;
+          k[i] = (lower == up) ? (other < k[i] ? other : k[i]) : (other > k[i] ? other : k[i]);
+        }
+      }
+    }
+  }
+}
+
+/// Key at sorted position e (wave-uniform) of a wave-sorted register array.
+template <int N>
+__device__ __forceinline__ uint64_t wave_key_at(const uint64_t (&k)[N], uint32_t e) {
+  uint64_t v = 0;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    if (static_cast<uint32_t>(i) == e / 64) v = k[i];
+  }
+  return __shfl(v, static_cast<int>(e % 64), 64);
+}
+
+/// Table entry (j, c) of the per-query table, in the reference's order (sum over t, then the
+/// factor -2 for L2, src/ivfpq_index.cc:315-317 and src/product_quantizer.cc:180-186).
+__device__ __forceinline__ float table_entry(const float* qv, const float* cbt, uint32_t dsub, uint32_t j,
+                                             uint32_t c, bool l2) {
+  const float* cb = cbt + static_cast<uint64_t>(j) * dsub * 256 + c;
+  const float* qj = qv + static_cast<uint64_t>(j) * dsub;
+  float v = 0.0f;
+  for (uint32_t t = 0; t < dsub; ++t) v = v + qj[t] * cb[t * 256];
+  return l2 ? v * -2.0f : v;
+}
+
+template <int MPW, bool FULL, int CAP>
+__device__ __forceinline__ void stream_scan(const ScanArgs& a) {
+  constexpr int QN = CAP / 64;     // queue keys per lane
+  constexpr int kRows = 4 * MPW;   // table rows: the m sub-spaces, then zero rows
+  constexpr int kStreamCodes = 2;  // codes per lane per round
+  extern __shared__ __attribute__((aligned(16))) unsigned char s_raw[];
+  float* s_lut = reinterpret_cast<float*>(s_raw);                                  // [kRows][256]
+  uint64_t* s_queue = reinterpret_cast<uint64_t*>(s_lut + kRows * 256);            // [waves][CAP]
+  uint32_t* s_vstart = reinterpret_cast<uint32_t*>(s_queue + kStreamWaves * CAP);  // [nprobe + 1]
+  uint32_t* s_base = s_vstart + a.nprobe + 1;  // [nprobe] list start - flattened start (mod 2^32)
+  uint32_t* s_list = s_base + a.nprobe;        // [nprobe]
+  float* s_score = reinterpret_cast<float*>(s_list + a.nprobe);  // [nprobe] probe keys
+  __shared__ uint32_t s_thr;  // ordered distance bits: an upper bound of the keep_sel-th distance
+  __shared__ uint32_t s_wcount[kStreamWaves];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const uint32_t q = blockIdx.x;
+  const float* qv = a.Q + static_cast<uint64_t>(q) * a.dim;
+  const uint32_t m = a.m;
+  const bool l2 = a.mode == kModePre;
+
+  // Per-query table (src/ivfpq_index.cc:309-318).
+  if (a.dsub == 4) {
+#pragma unroll 4
+    for (uint32_t e = tid; e < m * 256; e += kStreamThreads) {
+      const uint32_t j = e >> 8, c = e & 255u;
+      const float* cb = a.cbt + static_cast<uint64_t>(j) * 1024 + c;
+      const float* qj = qv + j * 4;
+      float v = 0.0f;
+      v = v + qj[0] * cb[0];
+      v = v + qj[1] * cb[256];
+      v = v + qj[2] * cb[512];
+      v = v + qj[3] * cb[768];
+      s_lut[e] = l2 ? v * -2.0f : v;
+    }
+  } else {
+    for (uint32_t e = tid; e < m * 256; e += kStreamThreads) s_lut[e] = table_entry(qv, a.cbt, a.dsub, e >> 8, e & 255u, l2);
+  }
+  for (uint32_t e = m * 256 + tid; e < kRows * 256; e += kStreamThreads) s_lut[e] = 0.0f;
+  // Probed lists: lengths, then flattened starts by a wave-wide scan (nprobe <= 256).
+  if (wave == 0) {
+    uint32_t len[4], lo[4];
+    uint32_t mine = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t p = lane * 4 + i;
+      len[i] = 0;
+      lo[i] = 0;
+      if (p < a.nprobe) {
+        const uint32_t l = a.probes[static_cast<uint64_t>(q) * a.nprobe + p];
+        lo[i] = static_cast<uint32_t>(a.off[l]);
+        len[i] = static_cast<uint32_t>(a.off[l + 1]) - lo[i];
+        s_list[p] = l;
+        s_score[p] = a.scores[static_cast<uint64_t>(q) * a.nlist + l];
+      }
+      mine += len[i];
+    }
+    uint32_t incl = mine;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t o = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += o;
+    }
+    uint32_t start = incl - mine;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t p = lane * 4 + i;
+      if (p < a.nprobe) {
+        s_vstart[p] = start;
+        s_base[p] = lo[i] - start;
+      }
+      start += len[i];
+    }
+    if (lane == 63) s_vstart[a.nprobe] = incl;
+    if (lane == 0) s_thr = 0xFFFFFFFFu;
+  }
+  __syncthreads();
+  const uint32_t keep_sel = a.keep_sel;
+  uint64_t* queue = s_queue + wave * CAP;
+  uint32_t cnt = 0;                   // wave-uniform queue fill
+  float thr = __builtin_huge_valf();  // candidates need dist <= thr
+  uint32_t thr_bits = 0xFFFFFFFFu;    // the same bound as ordered bits
+
+  // Cuts the wave's queue to the entries whose distance is at most the keep_sel-th smallest one
+  // (found bit by bit with wave ballots), and publishes that distance as the shared bound.
+  auto flush = [&]() {
+    uint64_t k[QN];
+    uint32_t d[QN];
+#pragma unroll
+    for (int i = 0; i < QN; ++i) {
+      const uint32_t e = i * 64 + lane;
+      k[i] = e < cnt ? queue[e] : ~0ull;
+      d[i] = static_cast<uint32_t>(k[i] >> 32);
+    }
+    if (cnt <= keep_sel) return;
+    uint32_t t = 0;
+    for (int b = 31; b >= 0; --b) {
+      const uint32_t probe = t | ((1u << b) - 1u);
+      uint32_t below = 0;
+#pragma unroll
+      for (int i = 0; i < QN; ++i) {
+        if (static_cast<uint32_t>(i * 64) < cnt) below += static_cast<uint32_t>(__popcll(__ballot(d[i] <= probe)));
+      }
+      if (below < keep_sel) t |= 1u << b;
+    }
+    // t is the keep_sel-th smallest distance (as ordered bits); keep every entry at or below it,
+    // unless ties at t would keep more than CAP / 2: then also find the position u such that the
+    // entries below t plus the ties at t with position <= u are exactly keep_sel.
+    uint32_t kept = 0, under = 0;
+#pragma unroll
+    for (int i = 0; i < QN; ++i) {
+      if (static_cast<uint32_t>(i * 64) < cnt) {
+        kept += static_cast<uint32_t>(__popcll(__ballot(d[i] <= t)));
+        under += static_cast<uint32_t>(__popcll(__ballot(d[i] < t)));
+      }
+    }
+    uint32_t u = 0xFFFFFFFFu;
+    if (kept > static_cast<uint32_t>(CAP / 2)) {
+      const uint32_t need = keep_sel - under;
+      u = 0;
+      for (int b = 31; b >= 0; --b) {
+        const uint32_t probe = u | ((1u << b) - 1u);
+        uint32_t below = 0;
+#pragma unroll
+        for (int i = 0; i < QN; ++i) {
+          if (static_cast<uint32_t>(i * 64) < cnt) {
+            below += static_cast<uint32_t>(__popcll(__ballot(d[i] == t && static_cast<uint32_t>(k[i]) <= probe)));
+          }
+        }
+        if (below < need) u |= 1u << b;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    uint32_t at = 0;
+#pragma unroll
+    for (int i = 0; i < QN; ++i) {
+      if (static_cast<uint32_t>(i * 64) < cnt) {
+        const bool keepit = k[i] != ~0ull && (d[i] < t || (d[i] == t && static_cast<uint32_t>(k[i]) <= u));
+        const uint64_t mk = __ballot(keepit);
+        const uint32_t below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mk >> 32),
+                                                         __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mk), 0u));
+        if (keepit) queue[at + below] = k[i];
+        at += static_cast<uint32_t>(__popcll(mk));
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    cnt = at;
+    // t, the keep_sel-th smallest distance among the wave's candidates, bounds the query's.
+    if (lane == 0) atomicMin(&s_thr, t);
+    if (t < thr_bits) {
+      thr_bits = t;
+      thr = ordered_to_float(t);
+    }
+  };
+  // Appends two codes' candidates (at most 128 while the queue holds at most CAP / 2), then cuts the
+  // queue once it holds more than flush_at, so the threshold follows the scan closely.
+  const uint32_t flush_at = min(static_cast<uint32_t>(CAP / 2), max(64u, 2 * keep_sel));
+  auto offer2 = [&](bool pa, float da, uint32_t posa, bool pb, float db, uint32_t posb) {
+    pa = pa && da <= thr;
+    pb = pb && db <= thr;
+    const uint64_t ma = __ballot(pa), mb = __ballot(pb);
+    if ((ma | mb) == 0) return;
+    const uint32_t ba = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(ma >> 32),
+                                                  __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(ma), 0u));
+    if (pa) queue[cnt + ba] = make_key(da, posa);
+    cnt += static_cast<uint32_t>(__popcll(ma));
+    const uint32_t bb = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mb >> 32),
+                                                  __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mb), 0u));
+    if (pb) queue[cnt + bb] = make_key(db, posb);
+    cnt += static_cast<uint32_t>(__popcll(mb));
+    if (cnt > flush_at) flush();
+  };
+
+  const uint32_t total = s_vstart[a.nprobe];
+  uint32_t p = 0;
+  uint32_t vend = s_vstart[1];
+  uint32_t base = s_base[0];
+  float score = s_score[0];
+  for (uint32_t v0 = 0; v0 < total; v0 += kStreamThreads * kStreamCodes) {
+    uint32_t pos[kStreamCodes];
+    float sc[kStreamCodes];
+    bool ok[kStreamCodes];
+#pragma unroll
+    for (int r = 0; r < kStreamCodes; ++r) {
+      const uint32_t v = v0 + r * kStreamThreads + tid;
+      ok[r] = v < total;
+      if (ok[r] && v >= vend) {
+        do {
+          ++p;
+        } while (v >= s_vstart[p + 1]);
+        vend = s_vstart[p + 1];
+        base = s_base[p];
+        score = s_score[p];
+      }
+      pos[r] = v + base;
+      sc[r] = score;
+      if (a.bitmap && ok[r]) ok[r] = (a.bitmap[pos[r] >> 6] >> (pos[r] & 63)) & 1ull;
+    }
+    uint32_t w[kStreamCodes][MPW];
+    float t1v[kStreamCodes];
+#pragma unroll
+    for (int r = 0; r < kStreamCodes; ++r) {
+      const uint32_t pr = ok[r] ? pos[r] : 0u;
+      load_code_padded<MPW, FULL>(a.codes, pr, a.mp, w[r]);
+      t1v[r] = l2 ? a.t1[pr] : 0.0f;
+    }
+    float dist[kStreamCodes];
+    bool any = false;
+#pragma unroll
+    for (int r = 0; r < kStreamCodes; ++r) {
+      const float sum = adc_sum_rows<MPW>(s_lut, w[r]);
+      const float d = l2 ? sc[r] + (t1v[r] + sum) : 1.0f - (-sc[r] + sum);  // src/ivfpq_index.cc:333-346
+      dist[r] = d == d ? d : __builtin_huge_valf();
+      any = any || (ok[r] && dist[r] <= thr);
+    }
+    if (__ballot(any) != 0) offer2(ok[0], dist[0], pos[0], ok[1], dist[1], pos[1]);
+    if (v0 == 0) {
+      // Every wave cuts its first candidates and the block shares the tightest bound.
+      flush();
+      __syncthreads();
+    }
+    const uint32_t shared_thr = *static_cast<volatile uint32_t*>(&s_thr);
+    if (shared_thr < thr_bits) {
+      thr_bits = shared_thr;
+      thr = ordered_to_float(shared_thr);
+    }
+  }
+  flush();
+  // The eight cut lists (<= CAP / 2 each) move to slots [wave * ks, wave * ks + ks) and are sorted
+  // together; the first keep_sel keys are the scan's answer.
+  uint64_t mine[QN];
+#pragma unroll
+  for (int i = 0; i < QN; ++i) {
+    const uint32_t e = i * 64 + lane;
+    mine[i] = e < cnt ? queue[e] : ~0ull;
+  }
+  if (lane == 0) s_wcount[wave] = cnt;
+  __syncthreads();
+  uint32_t most = 0, merged = 0;
+#pragma unroll
+  for (int w2 = 0; w2 < kStreamWaves; ++w2) {
+    most = max(most, s_wcount[w2]);
+    merged += s_wcount[w2];
+  }
+  const uint32_t ks = pow2_at_least(max(most, 1u));
+#pragma unroll
+  for (int i = 0; i < QN; ++i) {
+    const uint32_t e = i * 64 + lane;
+    if (e < ks) s_queue[wave * ks + e] = mine[i];
+  }
+  const uint32_t n = kStreamWaves * ks;
+  for (uint32_t size = 2; size <= n; size <<= 1) {
+    for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+      __syncthreads();
+      for (uint32_t i = tid; i < n / 2; i += kStreamThreads) {
+        const uint32_t lo = 2 * i - (i & (stride - 1));
+        const uint32_t hi = lo + stride;
+        const bool up = (lo & size) == 0;
+        const uint64_t x = s_queue[lo], y = s_queue[hi];
+        if ((x > y) == up) {
+          s_queue[lo] = y;
+          s_queue[hi] = x;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  uint32_t cnt_f = min(merged, keep_sel);
+
+  auto list_of = [&](uint32_t pos) {
+    uint32_t pl = 0;
+    while (pl + 1 < a.nprobe && !(pos - (s_base[pl] + s_vstart[pl]) < s_vstart[pl + 1] - s_vstart[pl])) ++pl;
+    return pl;
+  };
+  // Exact re-score of the approximate ranking (L2 with the precomputed table): the reference's
+  // table entry pre + qtab, summed in order of j, plus ||q - c||^2 (src/ivfpq_index.cc:334-346).
+  if (l2) {
+    if (static_cast<uint32_t>(tid) < cnt_f) {
+      const uint32_t pos = static_cast<uint32_t>(s_queue[tid]);
+      const uint32_t pl = list_of(pos);
+      const float* pre = a.pre + static_cast<uint64_t>(s_list[pl]) * m * 256;
+      uint32_t wc[MPW];
+      load_code<MPW>(a.codes, pos, a.mp, wc);
+      float sum = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4 * MPW; ++j) {
+        if (j < static_cast<int>(m)) {
+          const uint32_t c = (wc[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+          sum = sum + (pre[j * 256 + c] + s_lut[j * 256 + c]);
+        }
+      }
+      float d = s_score[pl] + sum;
+      d = d == d ? d : __builtin_huge_valf();
+      s_queue[tid] = make_key(d, pos);
+    }
+    const uint32_t n2 = pow2_at_least(max(cnt_f, 2u));
+    if (static_cast<uint32_t>(tid) >= cnt_f && static_cast<uint32_t>(tid) < n2) s_queue[tid] = ~0ull;
+    for (uint32_t size = 2; size <= n2; size <<= 1) {
+      for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+        __syncthreads();
+        for (uint32_t i = tid; i < n2 / 2; i += kStreamThreads) {
+          const uint32_t lo = 2 * i - (i & (stride - 1));
+          const uint32_t hi = lo + stride;
+          const bool up = (lo & size) == 0;
+          const uint64_t x = s_queue[lo], y = s_queue[hi];
+          if ((x > y) == up) {
+            s_queue[lo] = y;
+            s_queue[hi] = x;
+          }
+        }
+      }
+    }
+    __syncthreads();
+    cnt_f = min(cnt_f, a.keep);
+  }
+  if (a.refine) {
+    // Exact re-ranking needs the stored vectors: hand the candidates to the finishing kernel.
+    for (uint32_t i = tid; i < cnt_f; i += kStreamThreads) a.sel[static_cast<uint64_t>(q) * a.keep_sel + i] = s_queue[i];
+    if (tid == 0) a.sel_cnt[q] = cnt_f;
+    return;
+  }
+  const uint32_t nout = min(cnt_f, a.k);
+  for (uint32_t j = tid; j < a.k; j += kStreamThreads) {
+    uint64_t ref = QVH_EMPTY_REF;
+    float d = __builtin_huge_valf();
+    if (j < nout) {
+      const uint64_t key = s_queue[j];
+      const uint32_t pos = static_cast<uint32_t>(key);
+      const uint32_t pl = list_of(pos);
+      ref = (static_cast<uint64_t>(s_list[pl]) << 32) | (pos - (s_base[pl] + s_vstart[pl]));
+      d = ordered_to_float(static_cast<uint32_t>(key >> 32));
+    }
+    a.out_refs[static_cast<uint64_t>(q) * a.k + j] = ref;
+    a.out_dist[static_cast<uint64_t>(q) * a.k + j] = d;
+  }
+}
+
+// Up to 32 code bytes: held to 80 registers so that three eight-wave groups share a CU.
+template <int MPW, bool FULL, int CAP>
+__global__ void __launch_bounds__(kStreamThreads) __attribute__((amdgpu_waves_per_eu(6, 8)))
+ivf_stream_kernel(ScanArgs a) {
+  stream_scan<MPW, FULL, CAP>(a);
+}
+
+// 33 to 64 code bytes: no register cap.
+template <bool FULL, int CAP>
+__global__ void __launch_bounds__(kStreamThreads) ivf_stream_wide_kernel(ScanArgs a) {
+  stream_scan<16, FULL, CAP>(a);
+}
+
+/// Ascending bitonic sort of s[0, n) (n a power of two, n <= 2 * blockDim) by the block.
+__device__ __forceinline__ void finish_sort(uint64_t* s, uint32_t n) {
+  for (uint32_t size = 2; size <= n; size <<= 1) {
+    for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+      __syncthreads();
+      for (uint32_t i = threadIdx.x; i < n / 2; i += blockDim.x) {
+        const uint32_t lo = 2 * i - (i & (stride - 1));
+        const uint32_t hi = lo + stride;
+        const bool up = (lo & size) == 0;
+        const uint64_t x = s[lo], y = s[hi];
+        if ((x > y) == up) {
+          s[lo] = y;
+          s[hi] = x;
+        }
+      }
+    }
+  }
+  __syncthreads();
+}
+
+/// Exact re-ranking of the streaming scan's candidates with the stored vectors, and the k results
+/// of one query per block (src/ivfpq_index.cc:139-142,362-381).
+__global__ void __launch_bounds__(kFinishThreads) ivf_finish_kernel(ScanArgs a) {
+  __shared__ uint64_t s_key[kStreamMaxSel];
+  extern __shared__ __attribute__((aligned(16))) unsigned char f_raw[];
+  uint32_t* s_lo = reinterpret_cast<uint32_t*>(f_raw);  // [nprobe]
+  uint32_t* s_hi = s_lo + a.nprobe;
+  uint32_t* s_list = s_hi + a.nprobe;
+  float* s_score = reinterpret_cast<float*>(s_list + a.nprobe);
+  const uint32_t q = blockIdx.x;
+  const int tid = threadIdx.x;
+  const float* qv = a.Q + static_cast<uint64_t>(q) * a.dim;
+  for (uint32_t p = tid; p < a.nprobe; p += kFinishThreads) {
+    const uint32_t l = a.probes[static_cast<uint64_t>(q) * a.nprobe + p];
+    s_list[p] = l;
+    s_lo[p] = static_cast<uint32_t>(a.off[l]);
+    s_hi[p] = static_cast<uint32_t>(a.off[l + 1]);
+    s_score[p] = a.scores[static_cast<uint64_t>(q) * a.nlist + l];
+  }
+  uint32_t cnt = a.sel_cnt[q];
+  s_key[tid] = static_cast<uint32_t>(tid) < cnt ? a.sel[static_cast<uint64_t>(q) * a.keep_sel + tid] : ~0ull;
+  __syncthreads();
+  auto list_of = [&](uint32_t pos) {
+    uint32_t pl = 0;
+    while (pl + 1 < a.nprobe && !(s_lo[pl] <= pos && pos < s_hi[pl])) ++pl;
+    return pl;
+  };
+  if (a.refine) {
+    // Exact re-ranking with the stored vectors (src/ivfpq_index.cc:139-142,363-373).
+    __syncthreads();
+    if (static_cast<uint32_t>(tid) < cnt) {
+      const uint32_t pos = static_cast<uint32_t>(s_key[tid]);
+      const float* x = a.vec + static_cast<uint64_t>(pos) * a.dim;
+      const float d = a.mode == kModeIp ? 1.0f - exact_dot(qv, x, a.dim) : exact_l2sqr(qv, x, a.dim);
+      s_key[tid] = make_key(d, pos);
+    } else {
+      s_key[tid] = ~0ull;
+    }
+    finish_sort(s_key, pow2_at_least(max(cnt, 2u)));
+  }
+  __syncthreads();
+  const uint32_t nout = min(cnt, a.k);
+  if (static_cast<uint32_t>(tid) < a.k) {
+    uint64_t ref = QVH_EMPTY_REF;
+    float dist = __builtin_huge_valf();
+    if (static_cast<uint32_t>(tid) < nout) {
+      const uint64_t key = s_key[tid];
+      const uint32_t pos = static_cast<uint32_t>(key);
+      const uint32_t pl = list_of(pos);
+      ref = (static_cast<uint64_t>(s_list[pl]) << 32) | (pos - s_lo[pl]);
+      dist = ordered_to_float(static_cast<uint32_t>(key >> 32));
+    }
+    a.out_refs[static_cast<uint64_t>(q) * a.k + tid] = ref;
+    a.out_dist[static_cast<uint64_t>(q) * a.k + tid] = dist;
+  }
+}
+
 void launch_nearest(bool sqdiff, const NearestArgs& a, uint32_t nsub, hipStream_t s) {
   if (a.n == 0) return;
   const dim3 grid(static_cast<unsigned>(ceil_div(a.n, kNearThreads)), nsub);
@@ -674,7 +1217,7 @@ struct qvh_ivfpq {
   hipStream_t stream = nullptr;
   std::mutex mu;
   DeviceBuffer w_x, w_res, w_assign, w_codes, w_codes_p, w_t1, w_dest, w_shift;
-  DeviceBuffer w_q, w_scores, w_probes, w_bits, w_refs, w_dist, w_bytes;
+  DeviceBuffer w_q, w_scores, w_probes, w_bits, w_refs, w_dist, w_bytes, w_sel, w_selcnt;
   bool timing = false, timed = false;
   hipEvent_t ev[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
 };
@@ -798,25 +1341,62 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   }
   const uint32_t mpw = h->mp / 4;
   // Dynamic LDS above the default 64 KiB needs the kernel's limit raised first.
-  auto raise_lds = [&](const void* fn) {
-    if (lds > 64 * 1024) {
-      QVH_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+  auto raise_lds = [&](const void* fn, size_t bytes) {
+    if (bytes > 64 * 1024) {
+      QVH_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)));
     }
   };
-  if (mpw <= 2) {
-    raise_lds(reinterpret_cast<const void*>(ivf_scan_kernel<2>));
+  // The streaming scan covers the table modes with up to 256 probes, m <= 64 and a candidate set of
+  // at most 128; the rest takes the block-buffer scan below.
+  const uint32_t mpw_t = mpw <= 2 ? 2 : mpw <= 4 ? 4 : mpw <= 8 ? 8 : 16;  // the kernel's code width in dwords
+  const bool full = h->mp == 4 * mpw_t;
+  const bool small_sel = a.keep_sel <= 64 && k <= 64;
+  const size_t rows = 4 * mpw_t;
+  const size_t lds2 = rows * 256 * sizeof(float) + kStreamWaves * (small_sel ? 128 : 256) * sizeof(uint64_t) +
+                      (4 * static_cast<size_t>(nprobe) + 1) * sizeof(uint32_t);
+  if (mode != kModeResidual && nprobe <= kStreamMaxProbes && a.keep_sel >= 1 && a.keep_sel <= kStreamMaxSel &&
+      k <= kStreamMaxSel && lds2 <= 150 * 1024) {
+    a.sel = static_cast<uint64_t*>(h->w_sel.reserve(nq * a.keep_sel * sizeof(uint64_t)));
+    a.sel_cnt = static_cast<uint32_t*>(h->w_selcnt.reserve(nq * sizeof(uint32_t)));
+    auto launch2 = [&](auto kernel) {
+      const void* fn = reinterpret_cast<const void*>(kernel);
+      raise_lds(fn, lds2);
+      hipLaunchKernelGGL(kernel, grid, dim3(kStreamThreads), lds2, s, a);
+    };
+#define QVH_STREAM(MPW_)                                                                                  \
+  (full ? (small_sel ? launch2(ivf_stream_kernel<MPW_, true, 128>) : launch2(ivf_stream_kernel<MPW_, true, 256>)) \
+        : (small_sel ? launch2(ivf_stream_kernel<MPW_, false, 128>) : launch2(ivf_stream_kernel<MPW_, false, 256>)))
+    if (mpw_t == 2) {
+      QVH_STREAM(2);
+    } else if (mpw_t == 4) {
+      QVH_STREAM(4);
+    } else if (mpw_t == 8) {
+      QVH_STREAM(8);
+    } else if (full) {
+      small_sel ? launch2(ivf_stream_wide_kernel<true, 128>) : launch2(ivf_stream_wide_kernel<true, 256>);
+    } else {
+      small_sel ? launch2(ivf_stream_wide_kernel<false, 128>) : launch2(ivf_stream_wide_kernel<false, 256>);
+    }
+#undef QVH_STREAM
+    QVH_HIP(hipGetLastError());
+    if (a.refine) {
+      hipLaunchKernelGGL(ivf_finish_kernel, grid, dim3(kFinishThreads), 4 * static_cast<size_t>(nprobe) * sizeof(uint32_t),
+                         s, a);
+    }
+  } else if (mpw <= 2) {
+    raise_lds(reinterpret_cast<const void*>(ivf_scan_kernel<2>), lds);
     hipLaunchKernelGGL(ivf_scan_kernel<2>, grid, dim3(kScanThreads), lds, s, a);
   } else if (mpw <= 4) {
-    raise_lds(reinterpret_cast<const void*>(ivf_scan_kernel<4>));
+    raise_lds(reinterpret_cast<const void*>(ivf_scan_kernel<4>), lds);
     hipLaunchKernelGGL(ivf_scan_kernel<4>, grid, dim3(kScanThreads), lds, s, a);
   } else if (mpw <= 8) {
-    raise_lds(reinterpret_cast<const void*>(ivf_scan_kernel<8>));
+    raise_lds(reinterpret_cast<const void*>(ivf_scan_kernel<8>), lds);
     hipLaunchKernelGGL(ivf_scan_kernel<8>, grid, dim3(kScanThreads), lds, s, a);
   } else if (mpw <= 16) {
-    raise_lds(reinterpret_cast<const void*>(ivf_scan_kernel<16>));
+    raise_lds(reinterpret_cast<const void*>(ivf_scan_kernel<16>), lds);
     hipLaunchKernelGGL(ivf_scan_kernel<16>, grid, dim3(kScanThreads), lds, s, a);
   } else if (mpw <= 32) {
-    raise_lds(reinterpret_cast<const void*>(ivf_scan_kernel<32>));
+    raise_lds(reinterpret_cast<const void*>(ivf_scan_kernel<32>), lds);
     hipLaunchKernelGGL(ivf_scan_kernel<32>, grid, dim3(kScanThreads), lds, s, a);
   } else {
     throw Failure(QVH_EUNSUPPORTED, "IVF-PQ device path supports m <= 128");
