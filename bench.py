@@ -71,6 +71,9 @@ class Hip:
     def sync(self):
         assert self.lib.hipDeviceSynchronize() == 0
 
+    def copy_d2d(self, dst, src, nbytes: int):
+        assert self.lib.hipMemcpy(dst, src, nbytes, 3) == 0
+
 
 class Qvh:
     def __init__(self):
@@ -106,13 +109,31 @@ class Qvh:
         return name.value.decode(), arch.value.decode(), cus.value
 
 
-def load_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary, if present."""
-    path = os.path.join(ROOT, "profiles", f"{kernel}_pmc.json")
+COPY_CALIBRATION_BYTES = 256 << 20
+
+
+def load_traffic(name: str):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary profiles/<name>.md (its
+    line "traffic_bytes_per_launch: N"), if present."""
+    path = os.path.join(ROOT, "profiles", f"{name}.md")
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        return json.load(f).get("traffic_bytes_per_launch")
+        for line in f:
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip())
+    return None
+
+
+def copy_calibration(hip: Hip):
+    """One device-to-device copy of COPY_CALIBRATION_BYTES: the plain copy kernel whose
+    FETCH_SIZE / WRITE_SIZE counters scale the others to bytes."""
+    a = hip.malloc(COPY_CALIBRATION_BYTES)
+    b = hip.malloc(COPY_CALIBRATION_BYTES)
+    hip.copy_d2d(b, a, COPY_CALIBRATION_BYTES)
+    hip.sync()
+    hip.lib.hipFree(a)
+    hip.lib.hipFree(b)
 
 
 def bench_flat(args, hip: Hip, qvh: Qvh):
@@ -167,7 +188,7 @@ def bench_flat(args, hip: Hip, qvh: Qvh):
         "roofline": {"bound": "mfma", "kernel": "flat_scan_kernel<128,16>", "achieved": achieved,
                      "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / FP32_MFMA_PEAK_TFLOPS,
-                     "traffic": load_traffic("flat_scan_int_mix_1m")},
+                     "traffic": load_traffic("flat_scan_int_mix_1m_pmc")},
         "config": {"workload": "flat exact L2 k=10: 1,000,000 x 128 fp32 integer-valued mixture, "
                                "10,000 queries batched", "n": n, "dim": dim, "nq": nq, "k": k},
     }
@@ -195,15 +216,16 @@ def bench_ivfpq(args, hip: Hip, qvh: Qvh, base, queries):
     hip.h2d(d_q, queries)
     d_refs = hip.malloc(nq * k * 8)
     d_dist = hip.malloc(nq * k * 4)
-    qvh.check(qvh.lib.qvh_ivfpq_set_timing(h, 1), "timing")
+    qvh.check(qvh.lib.qvh_ivfpq_set_timing(h, 2), "timing")
 
     def search(probes):
         qvh.check(qvh.lib.qvh_ivfpq_search_device(h, d_q, nq, k, probes, 0, None, d_refs, d_dist, None),
                   "search")
 
-    def timing():
+    def timing(with_bytes=True):
         a, b, nb = C.c_float(), C.c_float(), C.c_uint64()
-        qvh.check(qvh.lib.qvh_ivfpq_last_timing(h, C.byref(a), C.byref(b), C.byref(nb)), "timing")
+        qvh.check(qvh.lib.qvh_ivfpq_last_timing(h, C.byref(a), C.byref(b), C.byref(nb) if with_bytes else None),
+                  "timing")
         return a.value, b.value, nb.value
 
     sweep = {}
@@ -215,6 +237,8 @@ def bench_ivfpq(args, hip: Hip, qvh: Qvh, base, queries):
         sweep[str(p)] = {"select_ms": sel, "scan_ms": scan, "code_bytes": nbytes,
                          "scan_hbm_frac": nbytes / (scan * 1e-3) / (HBM_PEAK_GBS * 1e9)}
 
+    # The timed steps record stage events only (level 1): the code-byte count is a separate kernel.
+    qvh.check(qvh.lib.qvh_ivfpq_set_timing(h, 1), "timing")
     for _ in range(args.warmup):
         search(nprobe)
     qvh.check(qvh.lib.qvh_ivfpq_sync(h), "sync")
@@ -223,7 +247,7 @@ def bench_ivfpq(args, hip: Hip, qvh: Qvh, base, queries):
     t0 = time.perf_counter()
     for _ in range(args.steps):
         search(nprobe)
-        stages.append(timing())
+        stages.append(timing(with_bytes=False))
     qvh.check(qvh.lib.qvh_ivfpq_sync(h), "sync")
     hip.sync()
     elapsed = time.perf_counter() - t0
@@ -238,7 +262,7 @@ def bench_ivfpq(args, hip: Hip, qvh: Qvh, base, queries):
 
     st = np.array(stages, dtype=np.float64)
     scan_ms = float(st[:, 1].mean())
-    code_bytes = int(st[0, 2])
+    code_bytes = int(sweep[str(nprobe)]["code_bytes"])
     achieved = code_bytes / (scan_ms * 1e-3) / 1e9
     ms_per_step = elapsed / args.steps * 1e3
     return idx, {
@@ -246,9 +270,9 @@ def bench_ivfpq(args, hip: Hip, qvh: Qvh, base, queries):
         "unit": "queries/s",
         "ms_per_step": ms_per_step,
         "stage_ms": {"select": float(st[:, 0].mean()), "scan": scan_ms},
-        "roofline": {"bound": "hbm", "kernel": "ivf_scan_kernel<8>", "achieved": achieved,
+        "roofline": {"bound": "hbm", "kernel": "ivf_stream_kernel<8, true, 128>", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": load_traffic("ivf_scan_int_mix_1m_nprobe32"),
+                     "traffic": load_traffic("ivf_stream_int_mix_1m_nprobe32_pmc"),
                      "code_bytes_per_launch": code_bytes},
         "nprobe_sweep": sweep,
         "build": {"train_s": train_s, "add_s": add_s, "encode_vectors_per_s": n / add_s},
@@ -326,6 +350,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help=f"first run one {COPY_CALIBRATION_BYTES >> 20} MiB device copy (for rocprofv3 --pmc scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build's search path runs on a single MI355X and "
@@ -334,6 +360,8 @@ def main():
 
     hip, qvh = Hip(), Qvh()
     name, arch, cus = qvh.device()
+    if args.copy_calibration:
+        copy_calibration(hip)
     flat, base, queries = bench_flat(args, hip, qvh)
     idx, ivf = bench_ivfpq(args, hip, qvh, base, queries)
     cpu = None

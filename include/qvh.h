@@ -164,9 +164,10 @@ qvh_status qvh_ivfpq_search_device(qvh_ivfpq* ivf, const float* d_queries, uint6
                                    const uint64_t* d_pos_bitmap, uint64_t* d_out_refs,
                                    float* d_out_dist, void* stream);
 qvh_status qvh_ivfpq_sync(qvh_ivfpq* ivf);
-/* Measurement hook (no counterpart in the reference): HIP events around the probe selection
- * (query prep, coarse scores, top-nprobe) and the list scan of each search, and the PQ code
- * bytes the scan had to read (sum over queries and probed lists of len * m; nullable). */
+/* Measurement hook (no counterpart in the reference). Level 1: HIP events around the probe
+ * selection (query prep, coarse scores, top-nprobe) and the list scan of each search. Level 2
+ * adds, after the scan, a count of the PQ code bytes the scan had to read (sum over queries and
+ * probed lists of len * m), which qvh_ivfpq_last_timing returns in code_bytes (nullable). */
 qvh_status qvh_ivfpq_set_timing(qvh_ivfpq* ivf, int enable);
 qvh_status qvh_ivfpq_last_timing(qvh_ivfpq* ivf, float* select_ms, float* scan_ms,
                                  uint64_t* code_bytes);

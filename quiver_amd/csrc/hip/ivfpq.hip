@@ -1218,7 +1218,8 @@ struct qvh_ivfpq {
   std::mutex mu;
   DeviceBuffer w_x, w_res, w_assign, w_codes, w_codes_p, w_t1, w_dest, w_shift;
   DeviceBuffer w_q, w_scores, w_probes, w_bits, w_refs, w_dist, w_bytes, w_sel, w_selcnt;
-  bool timing = false, timed = false;
+  int timing = 0;               // 0 off, 1 stage events, 2 events and probed code bytes
+  bool timed = false, timed_bytes = false;
   hipEvent_t ev[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
 };
 
@@ -1286,7 +1287,6 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
                                         " candidates is not supported on the device path yet");
   }
   QVH_REQUIRE(h->count < 0xFFFFFFFFull, "IVF-PQ device path holds fewer than 2^32 vectors");
-  h->timed = h->timing;
   if (h->timed) QVH_HIP(hipEventRecord(h->ev[0], s));
   // prepared queries
   float* dq = static_cast<float*>(h->w_q.reserve(nq * h->dim * sizeof(float)));
@@ -1402,8 +1402,8 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
     throw Failure(QVH_EUNSUPPORTED, "IVF-PQ device path supports m <= 128");
   }
   QVH_HIP(hipGetLastError());
-  if (h->timed) {
-    QVH_HIP(hipEventRecord(h->ev[2], s));
+  if (h->timed) QVH_HIP(hipEventRecord(h->ev[2], s));
+  if (h->timed_bytes) {
     uint64_t* bytes = static_cast<uint64_t*>(h->w_bytes.reserve(sizeof(uint64_t)));
     hipLaunchKernelGGL(probed_code_bytes_kernel, dim3(1), dim3(256), 0, s, probes, nq * nprobe, a.off, h->m, bytes);
     QVH_HIP(hipGetLastError());
@@ -1738,6 +1738,8 @@ qvh_status qvh_ivfpq_search(qvh_ivfpq* h, const float* queries, uint64_t nq, uin
     }
     uint64_t* drefs = static_cast<uint64_t*>(h->w_refs.reserve(nq * k * sizeof(uint64_t)));
     float* ddist = static_cast<float*>(h->w_dist.reserve(nq * k * sizeof(float)));
+    h->timed = h->timing > 0;
+    h->timed_bytes = h->timing > 1;
     ivf_search_impl(h, dq, nq, k, nprobe, refine_factor, dbits, drefs, ddist, s);
     QVH_HIP(hipMemcpyAsync(out_refs, drefs, nq * k * sizeof(uint64_t), hipMemcpyDeviceToHost, s));
     QVH_HIP(hipMemcpyAsync(out_dist, ddist, nq * k * sizeof(float), hipMemcpyDeviceToHost, s));
@@ -1756,7 +1758,8 @@ qvh_status qvh_ivfpq_search_device(qvh_ivfpq* h, const float* d_queries, uint64_
     QVH_REQUIRE(h->trained && h->count > 0, "qvh_ivfpq_search_device: index is untrained or empty");
     QVH_HIP(hipSetDevice(h->device));
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : h->stream;
-    h->timed = h->timing;
+    h->timed = h->timing > 0;
+    h->timed_bytes = h->timing > 1;
     ivf_search_impl(h, d_queries, nq, k, nprobe, refine_factor, d_pos_bitmap, d_out_refs, d_out_dist, s);
   });
 }
@@ -1766,10 +1769,11 @@ qvh_status qvh_ivfpq_set_timing(qvh_ivfpq* h, int enable) {
     QVH_REQUIRE(h != nullptr, "qvh_ivfpq_set_timing: null handle");
     std::lock_guard<std::mutex> lock(h->mu);
     QVH_HIP(hipSetDevice(h->device));
+    QVH_REQUIRE(enable >= 0 && enable <= 2, "qvh_ivfpq_set_timing: level must be 0, 1 or 2");
     if (enable && !h->ev[0]) {
       for (hipEvent_t& e : h->ev) QVH_HIP(hipEventCreate(&e));
     }
-    h->timing = enable != 0;
+    h->timing = enable;
   });
 }
 
@@ -1786,6 +1790,7 @@ qvh_status qvh_ivfpq_last_timing(qvh_ivfpq* h, float* select_ms, float* scan_ms,
     if (select_ms) *select_ms = a;
     if (scan_ms) *scan_ms = b;
     if (code_bytes) {
+      QVH_REQUIRE(h->timed_bytes, "qvh_ivfpq_last_timing: code bytes are measured at timing level 2");
       QVH_HIP(hipStreamSynchronize(h->stream));
       QVH_HIP(hipMemcpy(code_bytes, h->w_bytes.ptr, sizeof(uint64_t), hipMemcpyDeviceToHost));
     }
