@@ -20,6 +20,7 @@
 
 #include "common.hpp"
 #include "exact.hpp"
+#include "select.hpp"
 
 namespace qvh {
 void launch_normalize_rows(float* d_rows, uint64_t n, uint32_t dim, hipStream_t stream);
@@ -452,11 +453,130 @@ __global__ void fill_u32_kernel(uint32_t* p, uint64_t n, uint32_t v) {
   if (i < n) p[i] = v;
 }
 
-uint32_t padded_dim(uint32_t dim) {
-  for (uint32_t dp : {16u, 32u, 48u, 64u, 80u, 96u, 112u, 128u})
-    if (dim <= dp) return dp;
-  return 0;
+// ---- general exact search: k above the register lists, or dim above the MFMA query width -----------
+//
+// One work-group of four waves per query computes every admitted row's distance in the
+// reference's arithmetic (so no re-score is needed) and keeps the k best in wave queues cut by
+// wave_cut; the four lists are then sorted together.
+
+constexpr int kExactThreads = 256;
+constexpr int kExactWaves = kExactThreads / 64;
+constexpr uint32_t kExactMaxK = 1024;
+
+struct ExactArgs {
+  const float* X;  // [n][dp] rows as stored
+  uint32_t dp, dim;
+  uint64_t n;
+  const float* Q;  // [nq][dp] prepared queries
+  uint32_t k;
+  int l2;
+  const uint64_t* bitmap;
+  uint32_t* out_rows;
+  float* out_dist;
+};
+
+template <int CAP>
+__global__ void __launch_bounds__(kExactThreads) flat_exact_kernel(ExactArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char e_raw[];
+  uint64_t* s_queue = reinterpret_cast<uint64_t*>(e_raw);  // [waves][CAP]
+  __shared__ uint32_t s_thr;
+  __shared__ uint32_t s_wcount[kExactWaves];
+  constexpr int QN = CAP / 64;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const uint32_t q = blockIdx.x;
+  const float* qv = a.Q + static_cast<uint64_t>(q) * a.dp;
+  if (tid == 0) s_thr = 0xFFFFFFFFu;
+  __syncthreads();
+  uint64_t* queue = s_queue + wave * CAP;
+  uint32_t cnt = 0;
+  uint32_t thr_bits = 0xFFFFFFFFu;
+  float thr = __builtin_huge_valf();
+  auto cut = [&]() {
+    uint32_t t = thr_bits;
+    const uint32_t before = cnt;
+    cnt = wave_cut<CAP>(queue, cnt, a.k, &t);
+    if (before > a.k) {
+      if (lane == 0) atomicMin(&s_thr, t);
+      if (t < thr_bits) {
+        thr_bits = t;
+        thr = ordered_to_float(t);
+      }
+    }
+  };
+  for (uint64_t r0 = 0; r0 < a.n; r0 += kExactThreads) {
+    const uint64_t r = r0 + tid;
+    bool ok = r < a.n;
+    if (ok && a.bitmap) ok = (a.bitmap[r >> 6] >> (r & 63)) & 1ull;
+    const float d = ok ? exact_flat_distance(qv, a.X + r * a.dp, a.dim, a.l2 != 0) : 0.0f;
+    const bool pass = ok && d <= thr;
+    const uint64_t mk = __ballot(pass);
+    if (mk != 0) {
+      if (pass) queue[cnt + lane_rank(mk)] = make_key(d, static_cast<uint32_t>(r));
+      cnt += static_cast<uint32_t>(__popcll(mk));
+      if (cnt > static_cast<uint32_t>(CAP - 64)) cut();
+    }
+    const uint32_t shared_thr = *static_cast<volatile uint32_t*>(&s_thr);
+    if (shared_thr < thr_bits) {
+      thr_bits = shared_thr;
+      thr = ordered_to_float(shared_thr);
+    }
+  }
+  cut();
+  uint64_t mine[QN];
+#pragma unroll
+  for (int i = 0; i < QN; ++i) {
+    const uint32_t e = i * 64 + lane;
+    mine[i] = e < cnt ? queue[e] : ~0ull;
+  }
+  if (lane == 0) s_wcount[wave] = cnt;
+  __syncthreads();
+  uint32_t most = 0, merged = 0;
+#pragma unroll
+  for (int w = 0; w < kExactWaves; ++w) {
+    most = max(most, s_wcount[w]);
+    merged += s_wcount[w];
+  }
+  uint32_t ks = 1;
+  while (ks < most) ks <<= 1;
+#pragma unroll
+  for (int i = 0; i < QN; ++i) {
+    const uint32_t e = i * 64 + lane;
+    if (e < ks) s_queue[wave * ks + e] = mine[i];
+  }
+  block_sort_keys(s_queue, kExactWaves * ks);
+  const uint32_t nout = min(merged, a.k);
+  for (uint32_t j = tid; j < a.k; j += kExactThreads) {
+    const uint64_t key = j < nout ? s_queue[j] : ~0ull;
+    a.out_rows[static_cast<uint64_t>(q) * a.k + j] = j < nout ? static_cast<uint32_t>(key) : QVH_EMPTY_ROW;
+    a.out_dist[static_cast<uint64_t>(q) * a.k + j] =
+        j < nout ? ordered_to_float(static_cast<uint32_t>(key >> 32)) : __builtin_huge_valf();
+  }
 }
+
+void launch_exact(const ExactArgs& a, uint64_t nq, hipStream_t s) {
+  const uint32_t cap = a.k <= 64 ? 128 : a.k <= 128 ? 256 : a.k <= 256 ? 512 : a.k <= 512 ? 1024 : 2048;
+  const size_t lds = static_cast<size_t>(kExactWaves) * cap * sizeof(uint64_t);
+  auto go = [&](auto kernel) {
+    if (lds > 64 * 1024) {
+      QVH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  static_cast<int>(lds)));
+    }
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(nq)), dim3(kExactThreads), lds, s, a);
+  };
+  switch (cap) {
+    case 128: go(flat_exact_kernel<128>); break;
+    case 256: go(flat_exact_kernel<256>); break;
+    case 512: go(flat_exact_kernel<512>); break;
+    case 1024: go(flat_exact_kernel<1024>); break;
+    default: go(flat_exact_kernel<2048>); break;
+  }
+  QVH_HIP(hipGetLastError());
+}
+
+/// Row stride in floats: the dimension rounded up to 16 (the MFMA scan's K step).
+uint32_t padded_dim(uint32_t dim) { return (dim + 15u) / 16u * 16u; }
 
 template <int DP, int KL>
 void launch_scan_kl(bool l2, bool filter, dim3 grid, const ScanArgs& a, hipStream_t s) {
@@ -562,13 +682,35 @@ void flat_prep_queries(qvh_flat* f, const float* d_raw, uint64_t nq, hipStream_t
 
 void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t k,
                       const uint64_t* d_bitmap, uint32_t* d_rows, float* d_dist, hipStream_t s) {
-  QVH_REQUIRE(k <= 32, "flat search: k > 32 is not supported on the device path yet");
   QVH_REQUIRE(nq <= 0xFFFFFFFFull, "flat search: too many queries in one call");
-  const int kl = k <= 16 ? 16 : 32;
+  if (k > kExactMaxK) {
+    throw Failure(QVH_EUNSUPPORTED, "flat search: k > " + std::to_string(kExactMaxK) + " is not supported on the device path");
+  }
   f->timed = f->timing;
   if (f->timed) QVH_HIP(hipEventRecord(f->ev[0], s));
   flat_prep_queries(f, d_queries, nq, s);
   if (f->timed) QVH_HIP(hipEventRecord(f->ev[1], s));
+  if (k > 32 || f->dp > static_cast<uint32_t>(kMaxDp)) {
+    ExactArgs e;
+    e.X = f->rows.as<float>();
+    e.dp = f->dp;
+    e.dim = f->dim;
+    e.n = f->n;
+    e.Q = f->w_q.as<float>();
+    e.k = k;
+    e.l2 = f->metric == QVH_METRIC_L2;
+    e.bitmap = d_bitmap;
+    e.out_rows = d_rows;
+    e.out_dist = d_dist;
+    launch_exact(e, nq, s);
+    f->last_nsplit = 0;
+    if (f->timed) {
+      QVH_HIP(hipEventRecord(f->ev[2], s));
+      QVH_HIP(hipEventRecord(f->ev[3], s));
+    }
+    return;
+  }
+  const int kl = k <= 16 ? 16 : 32;
 
   int cus = 256;
   (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, f->device);
@@ -652,7 +794,6 @@ qvh_status qvh_flat_create(uint32_t dim, int metric, qvh_flat** out) {
     QVH_REQUIRE(dim >= 1 && dim <= 65536, "dimension must be in [1, 65536]");
     QVH_REQUIRE(metric >= QVH_METRIC_L2 && metric <= QVH_METRIC_COSINE, "unknown metric");
     const uint32_t dp = padded_dim(dim);
-    if (dp == 0) throw Failure(QVH_EUNSUPPORTED, "flat device path supports dim <= 128 for now");
     const int dev = current_device();
     auto* f = new qvh_flat;
     f->dim = dim;

@@ -1,0 +1,108 @@
+// Wave-level top-k selection over 64-bit keys (ordered float distance << 32 | id), shared by the
+// scans that cannot keep their candidates in registers.
+//
+// A wave appends candidates to a private LDS queue of CAP keys. A cut keeps the `keep` smallest
+// keys: the keep-th smallest distance t is found bit by bit with wave ballots (32 steps), every
+// key with distance < t is kept, and among the keys at distance t only the smallest ids that make
+// up exactly `keep` (a second 32-step search on the id bits, needed only when ties would otherwise
+// keep more than CAP / 2). The wave's keep-th distance bounds the final keep-th distance from
+// above, so candidates beyond it can be dropped as they arrive.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace qvh {
+
+__device__ __forceinline__ uint32_t lane_rank(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+}
+
+/// Cuts queue[0, cnt) (wave-uniform cnt) to its `keep` smallest keys; returns the new count and
+/// the keep-th smallest distance (ordered bits) in *bound, or leaves both alone when cnt <= keep.
+template <int CAP>
+__device__ uint32_t wave_cut(uint64_t* queue, uint32_t cnt, uint32_t keep, uint32_t* bound) {
+  constexpr int QN = CAP / 64;
+  const int lane = threadIdx.x & 63;
+  if (cnt <= keep) return cnt;
+  uint64_t k[QN];
+  uint32_t d[QN];
+#pragma unroll
+  for (int i = 0; i < QN; ++i) {
+    const uint32_t e = i * 64 + lane;
+    k[i] = e < cnt ? queue[e] : ~0ull;
+    d[i] = static_cast<uint32_t>(k[i] >> 32);
+  }
+  uint32_t t = 0;
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t probe = t | ((1u << b) - 1u);
+    uint32_t below = 0;
+#pragma unroll
+    for (int i = 0; i < QN; ++i) {
+      if (static_cast<uint32_t>(i * 64) < cnt) below += static_cast<uint32_t>(__popcll(__ballot(d[i] <= probe)));
+    }
+    if (below < keep) t |= 1u << b;
+  }
+  uint32_t kept = 0, under = 0;
+#pragma unroll
+  for (int i = 0; i < QN; ++i) {
+    if (static_cast<uint32_t>(i * 64) < cnt) {
+      kept += static_cast<uint32_t>(__popcll(__ballot(d[i] <= t)));
+      under += static_cast<uint32_t>(__popcll(__ballot(d[i] < t)));
+    }
+  }
+  uint32_t u = 0xFFFFFFFFu;
+  if (kept > static_cast<uint32_t>(CAP / 2)) {
+    const uint32_t need = keep - under;
+    u = 0;
+    for (int b = 31; b >= 0; --b) {
+      const uint32_t probe = u | ((1u << b) - 1u);
+      uint32_t below = 0;
+#pragma unroll
+      for (int i = 0; i < QN; ++i) {
+        if (static_cast<uint32_t>(i * 64) < cnt) {
+          below += static_cast<uint32_t>(__popcll(__ballot(d[i] == t && static_cast<uint32_t>(k[i]) <= probe)));
+        }
+      }
+      if (below < need) u |= 1u << b;
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  uint32_t at = 0;
+#pragma unroll
+  for (int i = 0; i < QN; ++i) {
+    if (static_cast<uint32_t>(i * 64) < cnt) {
+      const bool keepit = k[i] != ~0ull && (d[i] < t || (d[i] == t && static_cast<uint32_t>(k[i]) <= u));
+      const uint64_t mk = __ballot(keepit);
+      if (keepit) queue[at + lane_rank(mk)] = k[i];
+      at += static_cast<uint32_t>(__popcll(mk));
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  *bound = t;
+  return at;
+}
+
+/// Ascending bitonic sort of s[0, n) (n a power of two) by the whole block.
+__device__ __forceinline__ void block_sort_keys(uint64_t* s, uint32_t n) {
+  for (uint32_t size = 2; size <= n; size <<= 1) {
+    for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+      __syncthreads();
+      for (uint32_t i = threadIdx.x; i < n / 2; i += blockDim.x) {
+        const uint32_t lo = 2 * i - (i & (stride - 1));
+        const uint32_t hi = lo + stride;
+        const bool up = (lo & size) == 0;
+        const uint64_t x = s[lo], y = s[hi];
+        if ((x > y) == up) {
+          s[lo] = y;
+          s[hi] = x;
+        }
+      }
+    }
+  }
+  __syncthreads();
+}
+
+}  // namespace qvh

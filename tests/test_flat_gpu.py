@@ -87,6 +87,35 @@ def test_awkward_dimensions(oracle, dim):
         _check(oracle, base, q, 7, metric)
 
 
+@pytest.mark.parametrize("dim", [129, 200, 257, 1000])
+@pytest.mark.parametrize("metric", ["l2", "cosine"])
+def test_dimensions_above_the_mfma_width(oracle, dim, metric):
+    """dim > 128 takes the general exact kernel (distances computed in the reference's order)."""
+    rng = np.random.default_rng(dim)
+    base = rng.standard_normal((3_000, dim)).astype(np.float32)
+    q = rng.standard_normal((20, dim)).astype(np.float32)
+    print(_check(oracle, base, q, 10, metric))
+    allowed = np.sort(rng.choice(3_000, 300, replace=False)).astype(np.uint64)
+    print(_check(oracle, base, q, 7, metric, allowed))
+
+
+@pytest.mark.parametrize("k", [33, 64, 100, 300, 1024])
+@pytest.mark.parametrize("metric", ["l2", "ip"])
+def test_large_k(oracle, k, metric):
+    """k > 32 takes the general exact kernel: queue cuts at k, ties by row."""
+    base, q = D.int_mix(20_000, 30)
+    print(_check(oracle, base, q, k, metric))
+    allowed = D.allowed_ids(base.shape[0], 0.02, seed=9)
+    print(_check(oracle, base, q, k, metric, allowed))
+
+
+def test_k_above_the_device_limit_is_rejected():
+    idx = quiver.FlatIndex(8)
+    idx.add(np.random.default_rng(0).standard_normal((100, 8)).astype(np.float32))
+    with pytest.raises(ValueError, match="k > 1024"):
+        idx.search(np.zeros((1, 8), np.float32), 1025)
+
+
 @pytest.mark.parametrize("k", [1, 2, 10, 16, 17, 32])
 def test_k_values(oracle, k):
     base, q = D.flat_small()
