@@ -275,26 +275,48 @@ __global__ void scatter_new_kernel(ScatterArgs a) {
 constexpr int kCoarseQ = 8;  // queries per coarse workgroup
 
 /// Coarse scores (src/ivfpq_index.cc:285-297): L2: sum_j (q_j - c_j)^2; IP/cosine: -sum_j q_j c_j,
-/// both in order of j (centroid_table.h:65-85). Stored as the reference's probe key.
+/// both in order of j (centroid_table.h:65-85). Stored as the reference's probe key. One thread
+/// per centroid and kCoarseQ queries per work-group; the query values are block-uniform, so they
+/// come in through scalar loads and the vector unit does only the arithmetic.
+template <bool IP>
 __global__ void __launch_bounds__(256) coarse_kernel(const float* __restrict__ Q, uint32_t nq, uint32_t dim,
-                                                     const float* __restrict__ ct, uint32_t nlist, int ip,
+                                                     const float* __restrict__ ct, uint32_t nlist,
                                                      float* __restrict__ scores) {
-  extern __shared__ float s_q[];  // [kCoarseQ][dim]
   const uint32_t c = blockIdx.x * 256 + threadIdx.x;
   const uint32_t q0 = blockIdx.y * kCoarseQ;
   const uint32_t nb = min(static_cast<uint32_t>(kCoarseQ), nq - q0);
-  for (uint32_t e = threadIdx.x; e < nb * dim; e += 256) s_q[e] = Q[static_cast<uint64_t>(q0) * dim + e];
-  __syncthreads();
-  if (c >= nlist) return;
+  const float* qrow[kCoarseQ];
+#pragma unroll
+  for (int b = 0; b < kCoarseQ; ++b) qrow[b] = Q + static_cast<uint64_t>(q0 + (b < static_cast<int>(nb) ? b : 0)) * dim;
+  const uint32_t cc = c < nlist ? c : nlist - 1;
   float acc[kCoarseQ];
 #pragma unroll
   for (int b = 0; b < kCoarseQ; ++b) acc[b] = 0.0f;
-  for (uint32_t j = 0; j < dim; ++j) {
-    const float cj = ct[static_cast<uint64_t>(j) * nlist + c];
+  uint32_t j = 0;
+  for (; j + 4 <= dim; j += 4) {
+    float cj[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) cj[t] = ct[static_cast<uint64_t>(j + t) * nlist + cc];
 #pragma unroll
     for (int b = 0; b < kCoarseQ; ++b) {
-      const float qv = s_q[(b < static_cast<int>(nb) ? b : 0) * dim + j];
-      if (ip) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float qv = qrow[b][j + t];
+        if (IP) {
+          acc[b] = acc[b] + qv * cj[t];
+        } else {
+          const float d = qv - cj[t];
+          acc[b] = acc[b] + d * d;
+        }
+      }
+    }
+  }
+  for (; j < dim; ++j) {
+    const float cj = ct[static_cast<uint64_t>(j) * nlist + cc];
+#pragma unroll
+    for (int b = 0; b < kCoarseQ; ++b) {
+      const float qv = qrow[b][j];
+      if (IP) {
         acc[b] = acc[b] + qv * cj;
       } else {
         const float d = qv - cj;
@@ -302,15 +324,52 @@ __global__ void __launch_bounds__(256) coarse_kernel(const float* __restrict__ Q
       }
     }
   }
-  for (uint32_t b = 0; b < nb; ++b) scores[static_cast<uint64_t>(q0 + b) * nlist + c] = ip ? -acc[b] : acc[b];
+  if (c >= nlist) return;
+  for (uint32_t b = 0; b < nb; ++b) scores[static_cast<uint64_t>(q0 + b) * nlist + c] = IP ? -acc[b] : acc[b];
 }
 
 /// The nprobe smallest (score, list) per query, ascending (std::partial_sort of
-/// src/ivfpq_index.cc:298-300, with ties broken by the list id). One wave per query: every lane
-/// keeps the smallest key of its strided share above the last key popped.
+/// src/ivfpq_index.cc:298-300, with ties broken by the list id). One wave per query. With up to
+/// 64 * PER lists, every lane keeps its PER keys in registers; each step takes the wave minimum
+/// of the lanes' current smallest keys, and the lane that supplied it moves to its next smallest.
+template <int PER>
 __global__ void __launch_bounds__(256) probe_select_kernel(const float* __restrict__ scores, uint32_t nq,
                                                            uint32_t nlist, uint32_t nprobe,
                                                            uint32_t* __restrict__ probes) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t q = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (q >= nq) return;
+  const float* sq = scores + static_cast<uint64_t>(q) * nlist;
+  uint64_t key[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const uint32_t l = lane + 64 * i;
+    float s = l < nlist ? sq[l] : 0.0f;
+    s = s == s ? s : __builtin_huge_valf();
+    key[i] = l < nlist ? make_key(s, l) : ~0ull;
+  }
+  auto smallest = [&]() {
+    uint64_t b = key[0];
+#pragma unroll
+    for (int i = 1; i < PER; ++i) b = key[i] < b ? key[i] : b;
+    return b;
+  };
+  uint64_t cur = smallest();
+  for (uint32_t p = 0; p < nprobe; ++p) {
+    const uint64_t best = wave_min_u64(cur);
+    if (lane == 0) probes[static_cast<uint64_t>(q) * nprobe + p] = static_cast<uint32_t>(best);
+    if (cur == best) {
+#pragma unroll
+      for (int i = 0; i < PER; ++i) key[i] = key[i] == best ? ~0ull : key[i];
+      cur = smallest();
+    }
+  }
+}
+
+/// Same selection for any nlist: a lane rescans its strided share above the last key popped.
+__global__ void __launch_bounds__(256) probe_select_any_kernel(const float* __restrict__ scores, uint32_t nq,
+                                                               uint32_t nlist, uint32_t nprobe,
+                                                               uint32_t* __restrict__ probes) {
   const int lane = threadIdx.x & 63;
   const uint32_t q = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (q >= nq) return;
@@ -1296,13 +1355,26 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   float* scores = static_cast<float*>(h->w_scores.reserve(nq * h->nlist * sizeof(float)));
   {
     const dim3 grid(static_cast<unsigned>(ceil_div(h->nlist, 256)), static_cast<unsigned>(ceil_div(nq, kCoarseQ)));
-    hipLaunchKernelGGL(coarse_kernel, grid, dim3(256), kCoarseQ * h->dim * sizeof(float), s, dq,
-                       static_cast<uint32_t>(nq), h->dim, h->cent_t.as<float>(), h->nlist,
-                       h->metric != QVH_METRIC_L2 ? 1 : 0, scores);
+    if (h->metric != QVH_METRIC_L2) {
+      hipLaunchKernelGGL(coarse_kernel<true>, grid, dim3(256), 0, s, dq, static_cast<uint32_t>(nq), h->dim,
+                         h->cent_t.as<float>(), h->nlist, scores);
+    } else {
+      hipLaunchKernelGGL(coarse_kernel<false>, grid, dim3(256), 0, s, dq, static_cast<uint32_t>(nq), h->dim,
+                         h->cent_t.as<float>(), h->nlist, scores);
+    }
   }
   uint32_t* probes = static_cast<uint32_t*>(h->w_probes.reserve(nq * nprobe * sizeof(uint32_t)));
-  hipLaunchKernelGGL(probe_select_kernel, dim3(static_cast<unsigned>(ceil_div(nq, 4))), dim3(256), 0, s, scores,
-                     static_cast<uint32_t>(nq), h->nlist, nprobe, probes);
+  {
+    const dim3 grid(static_cast<unsigned>(ceil_div(nq, 4)));
+    const uint32_t nq32 = static_cast<uint32_t>(nq);
+    if (h->nlist <= 64 * 8) {
+      hipLaunchKernelGGL(probe_select_kernel<8>, grid, dim3(256), 0, s, scores, nq32, h->nlist, nprobe, probes);
+    } else if (h->nlist <= 64 * 32) {
+      hipLaunchKernelGGL(probe_select_kernel<32>, grid, dim3(256), 0, s, scores, nq32, h->nlist, nprobe, probes);
+    } else {
+      hipLaunchKernelGGL(probe_select_any_kernel, grid, dim3(256), 0, s, scores, nq32, h->nlist, nprobe, probes);
+    }
+  }
   QVH_HIP(hipGetLastError());
   if (h->timed) QVH_HIP(hipEventRecord(h->ev[1], s));
   ScanArgs a{};
