@@ -735,7 +735,10 @@ __global__ void __launch_bounds__(kScanThreads) ivf_scan_kernel(ScanArgs a) {
 // bounds the query's final keep_sel-th key from above). At the end the eight lists are sorted
 // together and the keep_sel best go to the finishing kernel, which re-scores them exactly.
 
-constexpr int kStreamWaves = 8;
+#ifndef QVH_STREAM_WAVES
+#define QVH_STREAM_WAVES 8
+#endif
+constexpr int kStreamWaves = QVH_STREAM_WAVES;
 constexpr int kStreamThreads = kStreamWaves * 64;
 constexpr uint32_t kStreamMaxProbes = 256;
 constexpr uint32_t kStreamMaxSel = 128;
@@ -954,22 +957,17 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
       thr = ordered_to_float(t);
     }
   };
-  // Appends two codes' candidates (at most 128 while the queue holds at most CAP / 2), then cuts the
-  // queue once it holds more than flush_at, so the threshold follows the scan closely.
+  // Appends one code's candidates (at most 64) at a time and cuts the queue once it holds more than
+  // flush_at <= CAP / 2; a cut leaves at most CAP / 2, so the queue never holds more than CAP.
   const uint32_t flush_at = min(static_cast<uint32_t>(CAP / 2), max(64u, 2 * keep_sel));
-  auto offer2 = [&](bool pa, float da, uint32_t posa, bool pb, float db, uint32_t posb) {
-    pa = pa && da <= thr;
-    pb = pb && db <= thr;
-    const uint64_t ma = __ballot(pa), mb = __ballot(pb);
-    if ((ma | mb) == 0) return;
-    const uint32_t ba = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(ma >> 32),
-                                                  __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(ma), 0u));
-    if (pa) queue[cnt + ba] = make_key(da, posa);
-    cnt += static_cast<uint32_t>(__popcll(ma));
-    const uint32_t bb = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mb >> 32),
-                                                  __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mb), 0u));
-    if (pb) queue[cnt + bb] = make_key(db, posb);
-    cnt += static_cast<uint32_t>(__popcll(mb));
+  auto offer = [&](bool pass, float d, uint32_t pos) {
+    pass = pass && d <= thr;
+    const uint64_t mk = __ballot(pass);
+    if (mk == 0) return;
+    const uint32_t below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mk >> 32),
+                                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mk), 0u));
+    if (pass) queue[cnt + below] = make_key(d, pos);
+    cnt += static_cast<uint32_t>(__popcll(mk));
     if (cnt > flush_at) flush();
   };
 
@@ -1015,7 +1013,10 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
       dist[r] = d == d ? d : __builtin_huge_valf();
       any = any || (ok[r] && dist[r] <= thr);
     }
-    if (__ballot(any) != 0) offer2(ok[0], dist[0], pos[0], ok[1], dist[1], pos[1]);
+    if (__ballot(any) != 0) {
+#pragma unroll
+      for (int r = 0; r < kStreamCodes; ++r) offer(ok[r], dist[r], pos[r]);
+    }
     if (v0 == 0) {
       // Every wave cuts its first candidates and the block shares the tightest bound.
       flush();
@@ -1045,12 +1046,14 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
     merged += s_wcount[w2];
   }
   const uint32_t ks = pow2_at_least(max(most, 1u));
+  constexpr uint32_t kWavesPow2 = kStreamWaves <= 8 ? 8 : 16;
 #pragma unroll
   for (int i = 0; i < QN; ++i) {
     const uint32_t e = i * 64 + lane;
     if (e < ks) s_queue[wave * ks + e] = mine[i];
   }
-  const uint32_t n = kStreamWaves * ks;
+  for (uint32_t e = kStreamWaves * ks + tid; e < kWavesPow2 * ks; e += kStreamThreads) s_queue[e] = ~0ull;
+  const uint32_t n = kWavesPow2 * ks;
   for (uint32_t size = 2; size <= n; size <<= 1) {
     for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
       __syncthreads();
@@ -1139,7 +1142,7 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
 
 // Up to 32 code bytes: held to 80 registers so that three eight-wave groups share a CU.
 template <int MPW, bool FULL, int CAP>
-__global__ void __launch_bounds__(kStreamThreads) __attribute__((amdgpu_waves_per_eu(6, 8)))
+__global__ void __launch_bounds__(kStreamThreads) __attribute__((amdgpu_waves_per_eu(6)))
 ivf_stream_kernel(ScanArgs a) {
   stream_scan<MPW, FULL, CAP>(a);
 }

@@ -157,3 +157,21 @@ def test_untrained_and_empty():
         idx.train(np.random.default_rng(0).standard_normal((300, 8)).astype(np.float32))
     labels, dist = idx.search(np.zeros((2, 8)), k=3)
     assert (labels == -1).all()
+
+
+@pytest.mark.parametrize("metric,refine", [("l2", 0), ("ip", 0), ("l2", 3)])
+def test_every_round_improves_on_the_last(oracle, metric, refine):
+    """One list whose codes come ever closer to the query in scan order: every round's candidates
+    beat all earlier ones, so every wave's queue takes a full round of appends after each cut."""
+    rng = np.random.default_rng(14)
+    dim, n = 16, 12_288
+    direction = rng.standard_normal(dim).astype(np.float32)
+    direction /= np.linalg.norm(direction)
+    t = np.linspace(60.0, 0.0, n, dtype=np.float32)
+    base = (t[:, None] * direction[None, :] + 0.01 * rng.standard_normal((n, dim))).astype(np.float32)
+    if metric == "ip":
+        base = -base  # larger <q, x> later in the list
+    q = (np.zeros((4, dim)) + 0.001 * rng.standard_normal((4, dim))).astype(np.float32)
+    q[:, 0] += 1.0
+    idx, st = build_pair(oracle, base, metric, 1, 8, refine > 0, iters=4)
+    print(compare_search(oracle, idx, st, q, 10, 1, refine))
