@@ -282,6 +282,95 @@ def bench_ivfpq(args, hip: Hip, qvh: Qvh, base, queries):
     }
 
 
+def bench_flat_filtered(args, qvh: Qvh):
+    """1,183,514 x 100 unit-norm mixture, cosine, k=10, 10,000 queries, through the host-buffer API
+    (FlatIndex.search: queries and filter from host memory), unfiltered and with allowed-id sets of
+    10% and 0.5%; the stage times come from the same handle's HIP events."""
+    import quiver_amd as quiver
+    from quiver_amd import datasets as D
+
+    base, q = D.unit_mix()
+    n, dim, k = base.shape[0], base.shape[1], 10
+    idx = quiver.FlatIndex(dim, "cosine")
+    idx.add(base)
+    h = C.c_void_p(idx._index._device_handle)
+    qvh.check(qvh.lib.qvh_flat_set_timing(h, 1), "timing")
+    out = {}
+    for name, frac in (("none", None), ("10%", 0.10), ("0.5%", 0.005)):
+        allowed = None if frac is None else D.allowed_ids(n, frac)
+        admitted = n if allowed is None else allowed.size
+        idx.search(q, k, filter=allowed)
+        times, scans = [], []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            idx.search(q, k, filter=allowed)
+            times.append(time.perf_counter() - t0)
+            p_, s_, m_, ns = C.c_float(), C.c_float(), C.c_float(), C.c_uint32()
+            qvh.check(qvh.lib.qvh_flat_last_timing(h, C.byref(p_), C.byref(s_), C.byref(m_), C.byref(ns)), "timing")
+            scans.append(s_.value)
+        scan_ms = float(np.mean(scans))
+        tflops = 2.0 * admitted * dim * q.shape[0] / (scan_ms * 1e-3) / 1e12
+        out[name] = {"qps_host_api": q.shape[0] / float(np.mean(times)), "admitted_rows": int(admitted),
+                     "scan_ms": scan_ms, "scan_tflops_admitted": tflops,
+                     "frac_of_fp32_mfma_peak": tflops / FP32_MFMA_PEAK_TFLOPS}
+    return {"config": {"workload": "flat exact cosine k=10: 1,183,514 x 100 unit-norm 256-component mixture, "
+                                   "10,000 queries, host-buffer API, allowed-id filters", "n": n, "dim": dim,
+                       "nq": int(q.shape[0]), "k": k},
+            "filters": out}
+
+
+def bench_ivfpq_cosine_refine(args, hip: Hip, qvh: Qvh):
+    """IVF-PQ cosine with exact re-ranking on the same 1,183,514 x 100 set: nlist 2048, m 25,
+    stored vectors, refine_factor 8 (80 candidates re-ranked), k=10, nprobe 16 and 64."""
+    import quiver_amd as quiver
+    from quiver_amd import datasets as D
+
+    base, q = D.unit_mix()
+    n, dim, k, nq = base.shape[0], base.shape[1], 10, q.shape[0]
+    sample = np.random.default_rng(31).permutation(n)[:100_000]
+    idx = quiver.IvfPqIndex(dim, "cosine", nlist=2048, m=25, store_vectors=True)
+    t0 = time.perf_counter()
+    idx.train(base[sample])
+    train_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    idx.add(base)
+    add_s = time.perf_counter() - t0
+    h = C.c_void_p(idx._index._device_handle)
+    d_q = hip.malloc(q.nbytes)
+    hip.h2d(d_q, q)
+    d_refs = hip.malloc(nq * k * 8)
+    d_dist = hip.malloc(nq * k * 4)
+    out = {}
+    for nprobe in (16, 64):
+        qvh.check(qvh.lib.qvh_ivfpq_set_timing(h, 2), "timing")
+        qvh.check(qvh.lib.qvh_ivfpq_search_device(h, d_q, nq, k, nprobe, 8, None, d_refs, d_dist, None), "search")
+        a, b, nb = C.c_float(), C.c_float(), C.c_uint64()
+        qvh.check(qvh.lib.qvh_ivfpq_last_timing(h, C.byref(a), C.byref(b), C.byref(nb)), "timing")
+        qvh.check(qvh.lib.qvh_ivfpq_set_timing(h, 1), "timing")
+        steps = []
+        qvh.check(qvh.lib.qvh_ivfpq_sync(h), "sync")
+        t0 = time.perf_counter()
+        for _ in range(5):
+            qvh.check(qvh.lib.qvh_ivfpq_search_device(h, d_q, nq, k, nprobe, 8, None, d_refs, d_dist, None), "search")
+            sa, sb = C.c_float(), C.c_float()
+            qvh.check(qvh.lib.qvh_ivfpq_last_timing(h, C.byref(sa), C.byref(sb), None), "timing")
+            steps.append((sa.value, sb.value))
+        qvh.check(qvh.lib.qvh_ivfpq_sync(h), "sync")
+        elapsed = time.perf_counter() - t0
+        st = np.array(steps)
+        scan_ms = float(st[:, 1].mean())
+        out[str(nprobe)] = {"qps": nq * 5 / elapsed, "select_ms": float(st[:, 0].mean()), "scan_ms": scan_ms,
+                            "code_bytes": nb.value,
+                            "scan_hbm_frac": nb.value / (scan_ms * 1e-3) / (HBM_PEAK_GBS * 1e9)}
+    for ptr in (d_q, d_refs, d_dist):
+        hip.lib.hipFree(ptr)
+    return {"config": {"workload": "IVF-PQ cosine k=10 refine_factor 8: 1,183,514 x 100 unit-norm mixture, "
+                                   "nlist 2048, m 25, stored vectors, trained on a 100,000-row sample; "
+                                   "10,000 queries", "n": n, "dim": dim, "nq": nq, "k": k, "nlist": 2048, "m": 25,
+                       "refine_factor": 8},
+            "build": {"train_s": train_s, "add_s": add_s}, "nprobe": out}
+
+
 def cpu_baseline_ivfpq(idx, queries, k, nprobe, seconds, threads):
     """QPS of the reference CPU IVF-PQ search on the index built here (loaded from a .qvr file)."""
     from oracle.oracle import IvfPqState, Oracle, Reference
@@ -350,6 +439,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the filtered cosine flat and the cosine IVF-PQ refine workloads")
     ap.add_argument("--copy-calibration", action="store_true",
                     help=f"first run one {COPY_CALIBRATION_BYTES >> 20} MiB device copy (for rocprofv3 --pmc scaling)")
     args = ap.parse_args()
@@ -364,6 +455,10 @@ def main():
         copy_calibration(hip)
     flat, base, queries = bench_flat(args, hip, qvh)
     idx, ivf = bench_ivfpq(args, hip, qvh, base, queries)
+    extra = {}
+    if not args.no_extra:
+        extra["flat_cosine_filtered"] = bench_flat_filtered(args, qvh)
+        extra["ivfpq_cosine_refine"] = bench_ivfpq_cosine_refine(args, hip, qvh)
     cpu = None
     ivf["cpu_baseline"] = None
     if not args.no_cpu:
@@ -389,6 +484,7 @@ def main():
         "stage_ms": flat["stage_ms"],
         "nsplit": flat["nsplit"],
         "ivfpq": ivf,
+        **extra,
         "device": {"name": name, "arch": arch, "compute_units": cus},
     }
     print(json.dumps(line))

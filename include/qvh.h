@@ -86,7 +86,8 @@ uint64_t qvh_flat_size(const qvh_flat* flat);
 
 /* The scan of FlatIndex::search_batch (src/flat_index.cc:84-106) for nq raw queries (normalized
  * here for cosine, as search_one does at :74-78). `row_bitmap` (nullable, ceil(size/64) words,
- * bit r of word r/64 set = row r admitted) is the Filter materialized over rows (:85).
+ * bit r of word r/64 set = row r admitted) is the Filter materialized over rows (:85); when it
+ * admits fewer than half of the rows, the scan runs over the list of admitted rows only.
  * Outputs: nq*k rows (QVH_EMPTY_ROW when fewer than k rows are admitted) and distances (+inf). */
 qvh_status qvh_flat_search(qvh_flat* flat, const float* queries, uint64_t nq, uint32_t k,
                            const uint64_t* row_bitmap, uint32_t* out_rows, float* out_dist);

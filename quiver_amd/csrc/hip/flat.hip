@@ -53,6 +53,7 @@ struct ScanArgs {
   uint32_t nsplit;
   uint32_t qblocks;
   uint64_t rows_per_split;  // multiple of kTileRows
+  const uint32_t* idx;      // admitted rows, ascending (indexed mode), or null
   float* part_d;            // [nq][2*nsplit][KL]
   uint32_t* part_r;
   uint32_t* qthr;           // [nq] shared prune threshold (ordered float bits), starts at +inf
@@ -76,8 +77,11 @@ __device__ __forceinline__ void list_insert(float (&Ld)[KL], uint32_t (&Lr)[KL],
   }
 }
 
-template <int DP, int KL, bool L2, bool FILTER>
+// MODE: 0 every row, 1 rows admitted by a bitmap (tested per tile), 2 the admitted rows listed in
+// a.idx (positions 0..n-1 index that list; candidates carry positions, the merge maps them to rows).
+template <int DP, int KL, bool L2, int MODE>
 __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
+  constexpr bool FILTER = MODE == 1;
   constexpr int H = DP / 2;                   // dims per lane half (K split in two halves)
   constexpr int STRIDE = DP + 4;              // LDS row stride in floats: conflict-free b128 reads
   constexpr int C4 = DP / 4;                  // float4 chunks per row
@@ -192,10 +196,12 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
       const int row = c / C4, col = c % C4;
       uint64_t gr = base + row;
       gr = gr < last_row ? gr : last_row;
+      if constexpr (MODE == 2) gr = a.idx[gr];
       stage[p] = *reinterpret_cast<const f32x4*>(a.X + gr * DP + 4 * col);
     }
     uint64_t gn = base + (tid & (kTileRows - 1));
     gn = gn < last_row ? gn : last_row;
+    if constexpr (MODE == 2) gn = a.idx[gn];
     stage_norm = a.xnorm[gn];
     if constexpr (FILTER) stage_bits = a.bitmap[base >> 6];
   };
@@ -344,6 +350,7 @@ struct MergeArgs {
   uint32_t nlists;          // 2 * nsplit
   const float* part_d;
   const uint32_t* part_r;
+  const uint32_t* idx;  // list positions -> rows (indexed scan), or null
   uint32_t* out_rows;
   float* out_dist;
 };
@@ -393,7 +400,7 @@ __global__ void __launch_bounds__(256) flat_merge_kernel(MergeArgs m) {
   }
   // Re-score the selected candidates exactly and rank them by (distance, row).
   const bool valid = lane < count;
-  const uint32_t row = static_cast<uint32_t>(sel);
+  const uint32_t row = valid && m.idx ? m.idx[static_cast<uint32_t>(sel)] : static_cast<uint32_t>(sel);
   float e = __builtin_huge_valf();
   if (valid) {
     e = exact_flat_distance(m.Q + static_cast<size_t>(q) * m.dp,
@@ -579,33 +586,38 @@ void launch_exact(const ExactArgs& a, uint64_t nq, hipStream_t s) {
 uint32_t padded_dim(uint32_t dim) { return (dim + 15u) / 16u * 16u; }
 
 template <int DP, int KL>
-void launch_scan_kl(bool l2, bool filter, dim3 grid, const ScanArgs& a, hipStream_t s) {
+void launch_scan_kl(bool l2, int mode, dim3 grid, const ScanArgs& a, hipStream_t s) {
   if (l2) {
-    if (filter) {
-      hipLaunchKernelGGL((flat_scan_kernel<DP, KL, true, true>), grid, dim3(kThreads), 0, s, a);
+    if (mode == 1) {
+      hipLaunchKernelGGL((flat_scan_kernel<DP, KL, true, 1>), grid, dim3(kThreads), 0, s, a);
+    } else if (mode == 2) {
+      hipLaunchKernelGGL((flat_scan_kernel<DP, KL, true, 2>), grid, dim3(kThreads), 0, s, a);
     } else {
-      hipLaunchKernelGGL((flat_scan_kernel<DP, KL, true, false>), grid, dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((flat_scan_kernel<DP, KL, true, 0>), grid, dim3(kThreads), 0, s, a);
     }
   } else {
-    if (filter) {
-      hipLaunchKernelGGL((flat_scan_kernel<DP, KL, false, true>), grid, dim3(kThreads), 0, s, a);
+    if (mode == 1) {
+      hipLaunchKernelGGL((flat_scan_kernel<DP, KL, false, 1>), grid, dim3(kThreads), 0, s, a);
+    } else if (mode == 2) {
+      hipLaunchKernelGGL((flat_scan_kernel<DP, KL, false, 2>), grid, dim3(kThreads), 0, s, a);
     } else {
-      hipLaunchKernelGGL((flat_scan_kernel<DP, KL, false, false>), grid, dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((flat_scan_kernel<DP, KL, false, 0>), grid, dim3(kThreads), 0, s, a);
     }
   }
 }
 
 template <int DP>
-void launch_scan_dp(int kl, bool l2, bool filter, dim3 grid, const ScanArgs& a, hipStream_t s) {
+void launch_scan_dp(int kl, bool l2, int mode, dim3 grid, const ScanArgs& a, hipStream_t s) {
   if (kl == 16) {
-    launch_scan_kl<DP, 16>(l2, filter, grid, a, s);
+    launch_scan_kl<DP, 16>(l2, mode, grid, a, s);
   } else {
-    launch_scan_kl<DP, 32>(l2, filter, grid, a, s);
+    launch_scan_kl<DP, 32>(l2, mode, grid, a, s);
   }
 }
 
 void launch_scan(uint32_t dp, int kl, dim3 grid, const ScanArgs& a, hipStream_t s) {
-  const bool l2 = a.l2 != 0, filter = a.bitmap != nullptr;
+  const bool l2 = a.l2 != 0;
+  const int filter = a.idx ? 2 : a.bitmap ? 1 : 0;
   switch (dp) {
     case 16: launch_scan_dp<16>(kl, l2, filter, grid, a, s); break;
     case 32: launch_scan_dp<32>(kl, l2, filter, grid, a, s); break;
@@ -630,7 +642,7 @@ struct qvh_flat {
   hipStream_t stream = nullptr;
   std::mutex mu;
   // per-call workspace (grown on demand, serialized by mu)
-  DeviceBuffer w_stage, w_q, w_qn, w_pd, w_pr, w_rows, w_dist, w_bits, w_thr;
+  DeviceBuffer w_stage, w_q, w_qn, w_pd, w_pr, w_rows, w_dist, w_bits, w_thr, w_idx;
   // optional per-stage timing of the last search: events before prep, scan, merge and after
   bool timing = false;
   bool timed = false;
@@ -680,8 +692,11 @@ void flat_prep_queries(qvh_flat* f, const float* d_raw, uint64_t nq, hipStream_t
   QVH_HIP(hipGetLastError());
 }
 
+/// d_idx (nullable, n_idx entries, ascending) lists the admitted rows for the MFMA scan; the caller
+/// passes it instead of the bitmap when few rows are admitted.
 void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t k,
-                      const uint64_t* d_bitmap, uint32_t* d_rows, float* d_dist, hipStream_t s) {
+                      const uint64_t* d_bitmap, uint32_t* d_rows, float* d_dist, hipStream_t s,
+                      const uint32_t* d_idx = nullptr, uint64_t n_idx = 0) {
   QVH_REQUIRE(nq <= 0xFFFFFFFFull, "flat search: too many queries in one call");
   if (k > kExactMaxK) {
     throw Failure(QVH_EUNSUPPORTED, "flat search: k > " + std::to_string(kExactMaxK) + " is not supported on the device path");
@@ -715,7 +730,8 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
   int cus = 256;
   (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, f->device);
   const uint32_t qblocks = static_cast<uint32_t>(ceil_div(nq, kQueriesPerBlock));
-  const uint64_t tiles = std::max<uint64_t>(1, ceil_div(f->n, kTileRows));
+  const uint64_t scan_rows = d_idx ? n_idx : f->n;
+  const uint64_t tiles = std::max<uint64_t>(1, ceil_div(scan_rows, kTileRows));
   // One workgroup per CU at a time: pick the split count (a multiple of 8 for the XCD mapping)
   // whose workgroup count best fills whole rounds of the CUs; fewer splits on ties.
   uint64_t nsplit = 1;
@@ -741,11 +757,12 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
   ScanArgs a;
   a.X = f->rows.as<float>();
   a.xnorm = f->norms.as<float>();
-  a.n = f->n;
+  a.n = scan_rows;
   a.Q = f->w_q.as<float>();
   a.qnorm = f->w_qn.as<float>();
   a.nq = static_cast<uint32_t>(nq);
-  a.bitmap = d_bitmap;
+  a.bitmap = d_idx ? nullptr : d_bitmap;
+  a.idx = d_idx;
   a.l2 = f->metric == QVH_METRIC_L2;
   a.nsplit = static_cast<uint32_t>(nsplit);
   a.qblocks = qblocks;
@@ -771,6 +788,7 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
   m.nlists = static_cast<uint32_t>(2 * nsplit);
   m.part_d = a.part_d;
   m.part_r = a.part_r;
+  m.idx = d_idx;
   m.out_rows = d_rows;
   m.out_dist = d_dist;
   const dim3 mgrid(static_cast<unsigned>(ceil_div(nq, 4)));
@@ -901,15 +919,41 @@ qvh_status qvh_flat_search(qvh_flat* f, const float* queries, uint64_t nq, uint3
     float* d_raw = static_cast<float*>(f->w_stage.reserve(qbytes));
     QVH_HIP(hipMemcpyAsync(d_raw, queries, qbytes, hipMemcpyHostToDevice, f->stream));
     const uint64_t* d_bits = nullptr;
+    const uint32_t* d_idx = nullptr;
+    std::vector<uint32_t> listed;
     if (row_bitmap) {
       const size_t words = ceil_div(std::max<uint64_t>(f->n, 1), 64);
-      uint64_t* b = static_cast<uint64_t*>(f->w_bits.reserve(words * sizeof(uint64_t)));
-      QVH_HIP(hipMemcpyAsync(b, row_bitmap, words * sizeof(uint64_t), hipMemcpyHostToDevice, f->stream));
-      d_bits = b;
+      // Few admitted rows: hand the MFMA scan the list of them, so its work follows their count.
+      uint64_t admitted = 0;
+      for (size_t w = 0; w < words; ++w) {
+        uint64_t bits = row_bitmap[w];
+        if (w + 1 == words && f->n % 64) bits &= (1ull << (f->n % 64)) - 1;
+        admitted += static_cast<uint64_t>(__builtin_popcountll(bits));
+      }
+      if (k <= 32 && f->dp <= static_cast<uint32_t>(kMaxDp) && 2 * admitted < f->n) {
+        listed.reserve(admitted);
+        for (size_t w = 0; w < words; ++w) {
+          uint64_t bits = row_bitmap[w];
+          if (w + 1 == words && f->n % 64) bits &= (1ull << (f->n % 64)) - 1;
+          while (bits) {
+            listed.push_back(static_cast<uint32_t>(w * 64 + static_cast<uint64_t>(__builtin_ctzll(bits))));
+            bits &= bits - 1;
+          }
+        }
+        uint32_t* li = static_cast<uint32_t*>(f->w_idx.reserve(std::max<size_t>(listed.size(), 1) * sizeof(uint32_t)));
+        if (!listed.empty()) {
+          QVH_HIP(hipMemcpyAsync(li, listed.data(), listed.size() * sizeof(uint32_t), hipMemcpyHostToDevice, f->stream));
+        }
+        d_idx = li;
+      } else {
+        uint64_t* b = static_cast<uint64_t*>(f->w_bits.reserve(words * sizeof(uint64_t)));
+        QVH_HIP(hipMemcpyAsync(b, row_bitmap, words * sizeof(uint64_t), hipMemcpyHostToDevice, f->stream));
+        d_bits = b;
+      }
     }
     uint32_t* d_rows = static_cast<uint32_t*>(f->w_rows.reserve(nq * k * sizeof(uint32_t)));
     float* d_dist = static_cast<float*>(f->w_dist.reserve(nq * k * sizeof(float)));
-    flat_search_impl(f, d_raw, nq, k, d_bits, d_rows, d_dist, f->stream);
+    flat_search_impl(f, d_raw, nq, k, d_bits, d_rows, d_dist, f->stream, d_idx, listed.size());
     QVH_HIP(hipMemcpyAsync(out_rows, d_rows, nq * k * sizeof(uint32_t), hipMemcpyDeviceToHost, f->stream));
     QVH_HIP(hipMemcpyAsync(out_dist, d_dist, nq * k * sizeof(float), hipMemcpyDeviceToHost, f->stream));
     QVH_HIP(hipStreamSynchronize(f->stream));

@@ -58,6 +58,16 @@ def test_flat_gaussian_10k_matches_oracle(oracle, metric, filtered):
     print(stats)
 
 
+@pytest.mark.parametrize("fraction", [0.005, 0.3, 0.49, 0.7])
+@pytest.mark.parametrize("metric", ["l2", "cosine"])
+def test_filter_densities(oracle, fraction, metric):
+    """Below half the rows admitted the scan runs over the list of admitted rows; above, over all
+    rows with the bitmap tested per tile. Both give the oracle's answer."""
+    base, q = D.unit_mix(30_000, 50)
+    allowed = D.allowed_ids(base.shape[0], fraction, seed=17)
+    print(_check(oracle, base, q, 10, metric, allowed))
+
+
 def test_cosine_rows_are_normalized_like_the_reference(oracle):
     base, _ = D.flat_small()
     idx = quiver.FlatIndex(128, "cosine")
