@@ -304,6 +304,9 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
             any = any || (!(d[r] > thr) && ((lane_bits >> (8 * (r >> 2) + (r & 3))) & 1u));
           }
         }
+        // Lanes past the last query never queue: their zero query makes every inner-product
+        // distance 1 exactly, a tie with their own list that would admit every row.
+        any = any && qvalid;
         // Slow path: append this lane's passing, admitted candidates to its queue.
         if (__builtin_amdgcn_ballot_w64(qcount > kQueueCap - 16)) flush_queue();
         if (any) {
