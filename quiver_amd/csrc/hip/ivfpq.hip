@@ -162,6 +162,16 @@ __global__ void codebook_prep_kernel(const float* __restrict__ cb, uint32_t m, u
   cbt[(static_cast<uint64_t>(j) * dsub + t) * 256 + c] = cb[e];
 }
 
+/// Codebook [m][256][dsub] -> c-major [256][m][dsub] (the per-query table of the bank-rotated scan
+/// is built from it with coalesced reads).
+__global__ void codebook_cmajor_kernel(const float* __restrict__ cb, uint32_t m, uint32_t dsub,
+                                       float* __restrict__ cbc) {
+  const uint64_t e = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= static_cast<uint64_t>(m) * 256 * dsub) return;
+  const uint32_t t = e % dsub, c = (e / dsub) % 256, j = static_cast<uint32_t>(e / (256ull * dsub));
+  cbc[(static_cast<uint64_t>(c) * m + j) * dsub + t] = cb[e];
+}
+
 /// residual[p] = x[p] - centroid[assign[p]] (src/ivfpq_index.cc:243).
 __global__ void residual_kernel(const float* __restrict__ x, const uint32_t* __restrict__ assign,
                                 const float* __restrict__ cent, uint64_t n, uint32_t dim,
@@ -335,7 +345,8 @@ __global__ void __launch_bounds__(256) coarse_kernel(const float* __restrict__ Q
 template <int PER>
 __global__ void __launch_bounds__(256) probe_select_kernel(const float* __restrict__ scores, uint32_t nq,
                                                            uint32_t nlist, uint32_t nprobe,
-                                                           uint32_t* __restrict__ probes) {
+                                                           uint32_t* __restrict__ probes,
+                                                           uint32_t* __restrict__ min_probe) {
   const int lane = threadIdx.x & 63;
   const uint32_t q = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (q >= nq) return;
@@ -355,21 +366,25 @@ __global__ void __launch_bounds__(256) probe_select_kernel(const float* __restri
     return b;
   };
   uint64_t cur = smallest();
+  uint32_t mn = 0xFFFFFFFFu;
   for (uint32_t p = 0; p < nprobe; ++p) {
     const uint64_t best = wave_min_u64(cur);
     if (lane == 0) probes[static_cast<uint64_t>(q) * nprobe + p] = static_cast<uint32_t>(best);
+    mn = min(mn, static_cast<uint32_t>(best));
     if (cur == best) {
 #pragma unroll
       for (int i = 0; i < PER; ++i) key[i] = key[i] == best ? ~0ull : key[i];
       cur = smallest();
     }
   }
+  if (min_probe && lane == 0) min_probe[q] = mn;
 }
 
 /// Same selection for any nlist: a lane rescans its strided share above the last key popped.
 __global__ void __launch_bounds__(256) probe_select_any_kernel(const float* __restrict__ scores, uint32_t nq,
                                                                uint32_t nlist, uint32_t nprobe,
-                                                               uint32_t* __restrict__ probes) {
+                                                               uint32_t* __restrict__ probes,
+                                                               uint32_t* __restrict__ min_probe) {
   const int lane = threadIdx.x & 63;
   const uint32_t q = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (q >= nq) return;
@@ -385,11 +400,14 @@ __global__ void __launch_bounds__(256) probe_select_any_kernel(const float* __re
     return best;
   };
   uint64_t cur = my_next(0, true);
+  uint32_t mn = 0xFFFFFFFFu;
   for (uint32_t p = 0; p < nprobe; ++p) {
     const uint64_t best = wave_min_u64(cur);
     if (lane == 0) probes[static_cast<uint64_t>(q) * nprobe + p] = static_cast<uint32_t>(best);
+    mn = min(mn, static_cast<uint32_t>(best));
     if (cur == best) cur = my_next(best, false);
   }
+  if (min_probe && lane == 0) min_probe[q] = mn;
 }
 
 // ---- search: the scan ---------------------------------------------------------------------------
@@ -398,6 +416,43 @@ constexpr int kScanThreads = 256;
 constexpr int kCandCap = 2048;       // LDS candidate buffer (u64 keys)
 constexpr int kScanRound = 4;        // codes per thread between buffer checks
 constexpr uint32_t kMaxKeepSel = kCandCap - kScanThreads * kScanRound;  // 1024
+
+// Scan order of the queries. Queries whose probe sets overlap read the same lists; run next to each
+// other, they find those lists in L2. Each query is keyed by the smallest list id it probes (a
+// min-hash of its probe set: two queries share it with probability equal to the Jaccard
+// similarity of their probe sets), and a counting sort over the keys gives the block -> query map.
+// The order changes only which block scans which query, never a query's result.
+
+/// order = the queries sorted by key (counting sort, LDS counts over the nlist keys; one block).
+/// Within a key the order is whatever the LDS atomics give.
+__global__ void __launch_bounds__(1024) probe_order_kernel(const uint32_t* __restrict__ key, uint32_t nq,
+                                                           uint32_t nlist, uint32_t* __restrict__ order) {
+  extern __shared__ uint32_t s_count[];  // [nlist]
+  __shared__ uint32_t s_part[1024];
+  __shared__ uint32_t s_carry;
+  const uint32_t tid = threadIdx.x;
+  for (uint32_t g = tid; g < nlist; g += 1024) s_count[g] = 0u;
+  if (tid == 0) s_carry = 0u;
+  __syncthreads();
+  for (uint32_t q = tid; q < nq; q += 1024) atomicAdd(&s_count[key[q]], 1u);
+  __syncthreads();
+  for (uint32_t b = 0; b < nlist; b += 1024) {
+    const uint32_t v = b + tid < nlist ? s_count[b + tid] : 0u;
+    s_part[tid] = v;
+    __syncthreads();
+    for (uint32_t off = 1; off < 1024; off <<= 1) {
+      const uint32_t add = tid >= off ? s_part[tid - off] : 0u;
+      __syncthreads();
+      s_part[tid] += add;
+      __syncthreads();
+    }
+    if (b + tid < nlist) s_count[b + tid] = s_carry + s_part[tid] - v;
+    __syncthreads();
+    if (tid == 1023) s_carry += s_part[1023];
+    __syncthreads();
+  }
+  for (uint32_t q = tid; q < nq; q += 1024) order[atomicAdd(&s_count[key[q]], 1u)] = q;
+}
 
 struct ScanArgs {
   uint32_t nq, k, m, mp, dsub, dim, nlist, nprobe;
@@ -410,6 +465,7 @@ struct ScanArgs {
   const float* t1;         // [count] (mode pre)
   const float* pre;        // [nlist][m][256] (mode pre)
   const float* cbt;        // [m][dsub][256]
+  const float* cbc;        // [256][m][dsub]
   const float* cent;       // [nlist][dim] (mode residual)
   const float* vec;        // [count][dim] or null
   const uint64_t* bitmap;  // admitted positions, or null
@@ -419,6 +475,7 @@ struct ScanArgs {
   float* out_dist;
   uint64_t* sel;      // [nq][keep_sel] streaming scan -> finishing kernel
   uint32_t* sel_cnt;  // [nq]
+  const uint32_t* order;  // [nq] block -> query of the streaming scan, or null
 };
 
 /// Ascending bitonic sort of s[0, n) (n a power of two) by all 256 threads.
@@ -735,14 +792,23 @@ __global__ void __launch_bounds__(kScanThreads) ivf_scan_kernel(ScanArgs a) {
 // bounds the query's final keep_sel-th key from above). At the end the eight lists are sorted
 // together and the keep_sel best go to the finishing kernel, which re-scores them exactly.
 
+// Four waves per block and four blocks per CU (the per-query table and queues take ~37 KB of LDS),
+// which leaves up to 128 registers per lane.
+#ifndef QVH_STREAM_ROT
+#define QVH_STREAM_ROT 0
+#endif
+#ifndef QVH_STREAM_WPE
+#define QVH_STREAM_WPE 4
+#endif
 #ifndef QVH_STREAM_WAVES
-#define QVH_STREAM_WAVES 8
+#define QVH_STREAM_WAVES 4
 #endif
 constexpr int kStreamWaves = QVH_STREAM_WAVES;
 constexpr int kStreamThreads = kStreamWaves * 64;
 constexpr uint32_t kStreamMaxProbes = 256;
 constexpr uint32_t kStreamMaxSel = 128;
 constexpr int kFinishThreads = 128;
+constexpr uint32_t kStreamMaxM = 64;  // code bytes of the widest streaming kernel
 
 /// Ascending bitonic sort of N * 64 keys held by one wave, element e = i * 64 + lane in k[i].
 template <int N>
@@ -801,31 +867,117 @@ __device__ __forceinline__ float table_entry(const float* qv, const float* cbt, 
   return l2 ? v * -2.0f : v;
 }
 
-template <int MPW, bool FULL, int CAP>
+// Bank-rotated table lookups (the L2 scan with the precomputed table). The table is laid out
+// [c][R] (R = 4 * MPW rows, R <= 32), so entry (j, c) sits in bank j (mod the 64 LDS banks), and
+// lane l visits the sub-spaces of its code in the order j = (l + s) mod R, s = 0..R-1: in every
+// step the lanes of a half-wave read R distinct banks whatever their codes. Plain [j][256] lookups
+// hit random banks, and their conflicts bound the scan; rotated ones run about 1.5x as many
+// lookups per clock. The sum runs in a lane-dependent order, so it is an approximation of the
+// reference's in-order sum (the scan's candidates are re-scored exactly afterwards).
+
+/// v_cndmask_b32 with a lane mask in SGPRs: mask bit set -> b, else a. An opaque instruction, so
+/// the three-stage rotation below stays three stages of selects.
+__device__ __forceinline__ uint32_t select_lanes(uint32_t a, uint32_t b, uint64_t mask) {
+  uint32_t r;
+  asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(mask));
+  return r;
+}
+
+/// Rotates this lane's code (MPW dwords) left by rot = 4 * D + b bytes: byte s of the result is
+/// byte (s + rot) mod 4*MPW. D's bits arrive as lane masks (stage k moves by k dwords), b as a
+/// register.
+template <int MPW>
+__device__ __forceinline__ void rotate_code(uint32_t (&w)[MPW], const uint64_t (&stage)[3], uint32_t b) {
+#pragma unroll
+  for (int st = 0; st < 3; ++st) {
+    constexpr int kStages = MPW >= 8 ? 3 : MPW >= 4 ? 2 : 1;
+    if (st < kStages) {
+      const int k = 1 << st;
+      uint32_t t[MPW];
+#pragma unroll
+      for (int i = 0; i < MPW; ++i) t[i] = select_lanes(w[i], w[(i + k) % MPW], stage[st]);
+#pragma unroll
+      for (int i = 0; i < MPW; ++i) w[i] = t[i];
+    }
+  }
+  uint32_t t[MPW];
+#pragma unroll
+  for (int i = 0; i < MPW; ++i) t[i] = __builtin_amdgcn_alignbyte(w[(i + 1) % MPW], w[i], b);
+#pragma unroll
+  for (int i = 0; i < MPW; ++i) w[i] = t[i];
+}
+
+/// sum_s table[c_s][(rot + s) mod R] over the rotated code (byte s = c_s), in order of s.
+template <int MPW>
+__device__ __forceinline__ float adc_sum_rotated(const float* lut, const uint32_t (&w)[MPW], uint32_t rot) {
+  constexpr int R = 4 * MPW;
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const uint32_t c = (w[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+    s = s + lut[c * R + ((rot + j) & (R - 1))];
+  }
+  return s;
+}
+
+template <int MPW, bool FULL, int CAP, bool ROT>
 __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
   constexpr int QN = CAP / 64;     // queue keys per lane
   constexpr int kRows = 4 * MPW;   // table rows: the m sub-spaces, then zero rows
-  constexpr int kStreamCodes = 2;  // codes per lane per round
+#ifndef QVH_STREAM_CODES
+#define QVH_STREAM_CODES 2
+#endif
+  constexpr int kStreamCodes = QVH_STREAM_CODES;  // codes per lane per round
   extern __shared__ __attribute__((aligned(16))) unsigned char s_raw[];
-  float* s_lut = reinterpret_cast<float*>(s_raw);                                  // [kRows][256]
-  uint64_t* s_queue = reinterpret_cast<uint64_t*>(s_lut + kRows * 256);            // [waves][CAP]
+  // The per-query table [kRows][256] (or [256][kRows]) is the block's static LDS for codes of up to
+  // 32 bytes: it starts at LDS address 0, so each lookup's address is the code byte times 4 (one
+  // SDWA shift) with the row offset in the instruction. Wider codes keep it in the dynamic segment.
+  float* s_lut;
+  unsigned char* s_dyn;
+  if constexpr (MPW <= 8) {
+    __shared__ __attribute__((aligned(16))) float s_lut_static[kRows * 256];
+    s_lut = s_lut_static;
+    s_dyn = s_raw;
+  } else {
+    s_lut = reinterpret_cast<float*>(s_raw);
+    s_dyn = s_raw + kRows * 256 * sizeof(float);
+  }
+  uint64_t* s_queue = reinterpret_cast<uint64_t*>(s_dyn);                          // [waves][CAP]
   uint32_t* s_vstart = reinterpret_cast<uint32_t*>(s_queue + kStreamWaves * CAP);  // [nprobe + 1]
   uint32_t* s_base = s_vstart + a.nprobe + 1;  // [nprobe] list start - flattened start (mod 2^32)
   uint32_t* s_list = s_base + a.nprobe;        // [nprobe]
   float* s_score = reinterpret_cast<float*>(s_list + a.nprobe);  // [nprobe] probe keys
-  __shared__ uint32_t s_thr;  // ordered distance bits: an upper bound of the keep_sel-th distance
-  __shared__ uint32_t s_wcount[kStreamWaves];
+  // Ordered distance bits: an upper bound of the keep_sel-th distance.
+  uint32_t& s_thr = *reinterpret_cast<uint32_t*>(s_score + a.nprobe);
+  uint32_t* s_wcount = reinterpret_cast<uint32_t*>(s_score + a.nprobe) + 1;  // [waves]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const uint32_t q = blockIdx.x;
+  const uint32_t q = a.order ? a.order[blockIdx.x] : blockIdx.x;
   const float* qv = a.Q + static_cast<uint64_t>(q) * a.dim;
   const uint32_t m = a.m;
   const bool l2 = a.mode == kModePre;
 
   // Per-query table (src/ivfpq_index.cc:309-318).
-  if (a.dsub == 4) {
+  if (ROT) {
+    // [c][kRows] layout from the c-major codebook: consecutive threads write consecutive entries
+    // and read consecutive codebook rows. Rows past m are zero.
+    for (uint32_t e = tid; e < 256 * kRows; e += kStreamThreads) {
+      const uint32_t c = e / kRows, j = e % kRows;
+      float v = 0.0f;
+      if (j < m) {
+        const float4 cb = *reinterpret_cast<const float4*>(a.cbc + (static_cast<uint64_t>(c) * m + j) * 4);
+        const float4 qj = *reinterpret_cast<const float4*>(qv + j * 4);
+        v = v + qj.x * cb.x;
+        v = v + qj.y * cb.y;
+        v = v + qj.z * cb.z;
+        v = v + qj.w * cb.w;
+        v = v * -2.0f;
+      }
+      s_lut[e] = v;
+    }
+  } else if (a.dsub == 4) {
 #pragma unroll 4
     for (uint32_t e = tid; e < m * 256; e += kStreamThreads) {
       const uint32_t j = e >> 8, c = e & 255u;
@@ -841,7 +993,9 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
   } else {
     for (uint32_t e = tid; e < m * 256; e += kStreamThreads) s_lut[e] = table_entry(qv, a.cbt, a.dsub, e >> 8, e & 255u, l2);
   }
-  for (uint32_t e = m * 256 + tid; e < kRows * 256; e += kStreamThreads) s_lut[e] = 0.0f;
+  if (!ROT) {
+    for (uint32_t e = m * 256 + tid; e < kRows * 256; e += kStreamThreads) s_lut[e] = 0.0f;
+  }
   // Probed lists: lengths, then flattened starts by a wave-wide scan (nprobe <= 256).
   if (wave == 0) {
     uint32_t len[4], lo[4];
@@ -976,15 +1130,19 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
   uint32_t vend = s_vstart[1];
   uint32_t base = s_base[0];
   float score = s_score[0];
-  for (uint32_t v0 = 0; v0 < total; v0 += kStreamThreads * kStreamCodes) {
-    uint32_t pos[kStreamCodes];
-    float sc[kStreamCodes];
-    bool ok[kStreamCodes];
+  // Software-pipelined: the codes (and t1 terms, and filter words) of round i + 1 are requested
+  // before round i's table lookups, so every wave keeps a round of loads in flight while it sums.
+  uint32_t npos[kStreamCodes];
+  float nsc[kStreamCodes], nt1[kStreamCodes];
+  bool nok[kStreamCodes];
+  uint32_t nw[kStreamCodes][MPW];
+  uint64_t nbits[kStreamCodes];
+  auto fetch = [&](uint32_t v0) {
 #pragma unroll
     for (int r = 0; r < kStreamCodes; ++r) {
       const uint32_t v = v0 + r * kStreamThreads + tid;
-      ok[r] = v < total;
-      if (ok[r] && v >= vend) {
+      nok[r] = v < total;
+      if (nok[r] && v >= vend) {
         do {
           ++p;
         } while (v >= s_vstart[p + 1]);
@@ -992,23 +1150,50 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
         base = s_base[p];
         score = s_score[p];
       }
-      pos[r] = v + base;
-      sc[r] = score;
-      if (a.bitmap && ok[r]) ok[r] = (a.bitmap[pos[r] >> 6] >> (pos[r] & 63)) & 1ull;
+      npos[r] = v + base;
+      nsc[r] = score;
+      const uint32_t pr = nok[r] ? npos[r] : 0u;
+      load_code_padded<MPW, FULL>(a.codes, pr, a.mp, nw[r]);
+      nt1[r] = l2 ? a.t1[pr] : 0.0f;
+      nbits[r] = a.bitmap ? a.bitmap[pr >> 6] : ~0ull;
     }
+  };
+  // Rotation of this lane's codes (bank-rotated lookups): rot = lane mod kRows.
+  const uint32_t rot = static_cast<uint32_t>(lane) & (kRows - 1);
+  uint64_t stage[3];
+#pragma unroll
+  for (int st = 0; st < 3; ++st) stage[st] = __ballot(((rot >> 2) >> st) & 1u);
+  if (total > 0) fetch(0);
+  for (uint32_t v0 = 0; v0 < total; v0 += kStreamThreads * kStreamCodes) {
+    uint32_t pos[kStreamCodes];
+    float sc[kStreamCodes], t1v[kStreamCodes];
+    bool ok[kStreamCodes];
     uint32_t w[kStreamCodes][MPW];
-    float t1v[kStreamCodes];
 #pragma unroll
     for (int r = 0; r < kStreamCodes; ++r) {
-      const uint32_t pr = ok[r] ? pos[r] : 0u;
-      load_code_padded<MPW, FULL>(a.codes, pr, a.mp, w[r]);
-      t1v[r] = l2 ? a.t1[pr] : 0.0f;
+      pos[r] = npos[r];
+      sc[r] = nsc[r];
+      t1v[r] = nt1[r];
+      ok[r] = nok[r] && ((nbits[r] >> (pos[r] & 63)) & 1ull);
+#pragma unroll
+      for (int i = 0; i < MPW; ++i) w[r][i] = nw[r][i];
     }
+    if (v0 + kStreamThreads * kStreamCodes < total) fetch(v0 + kStreamThreads * kStreamCodes);
     float dist[kStreamCodes];
     bool any = false;
+    // The rotation as seen by this round: its table columns are recomputed per round (and shared by
+    // the round's codes) rather than held in registers across the loop.
+    uint32_t rot_round = rot;
+    if constexpr (ROT) asm volatile("" : "+v"(rot_round));
 #pragma unroll
     for (int r = 0; r < kStreamCodes; ++r) {
-      const float sum = adc_sum_rows<MPW>(s_lut, w[r]);
+      float sum;
+      if constexpr (ROT) {
+        rotate_code<MPW>(w[r], stage, rot & 3u);
+        sum = adc_sum_rotated<MPW>(s_lut, w[r], rot_round);
+      } else {
+        sum = adc_sum_rows<MPW>(s_lut, w[r]);
+      }
       const float d = l2 ? sc[r] + (t1v[r] + sum) : 1.0f - (-sc[r] + sum);  // src/ivfpq_index.cc:333-346
       dist[r] = d == d ? d : __builtin_huge_valf();
       any = any || (ok[r] && dist[r] <= thr);
@@ -1072,10 +1257,18 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
   __syncthreads();
   uint32_t cnt_f = min(merged, keep_sel);
 
+  // Probe index of a position: eight probed lists tested per step (independent LDS reads).
   auto list_of = [&](uint32_t pos) {
-    uint32_t pl = 0;
-    while (pl + 1 < a.nprobe && !(pos - (s_base[pl] + s_vstart[pl]) < s_vstart[pl + 1] - s_vstart[pl])) ++pl;
-    return pl;
+    for (uint32_t b = 0; b + 1 < a.nprobe; b += 8) {
+      uint32_t hit = 0;
+#pragma unroll
+      for (uint32_t i = 0; i < 8; ++i) {
+        const uint32_t pl = b + i;
+        if (pl < a.nprobe && pos - (s_base[pl] + s_vstart[pl]) < s_vstart[pl + 1] - s_vstart[pl]) hit |= 1u << i;
+      }
+      if (hit) return b + static_cast<uint32_t>(__builtin_ctz(hit));
+    }
+    return a.nprobe - 1;
   };
   // Exact re-score of the approximate ranking (L2 with the precomputed table): the reference's
   // table entry pre + qtab, summed in order of j, plus ||q - c||^2 (src/ivfpq_index.cc:334-346).
@@ -1086,13 +1279,19 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
       const float* pre = a.pre + static_cast<uint64_t>(s_list[pl]) * m * 256;
       uint32_t wc[MPW];
       load_code<MPW>(a.codes, pos, a.mp, wc);
+      // All 4 * MPW table loads go out together (rows past m re-read row m - 1 and are not added).
+      float pv[4 * MPW];
+#pragma unroll
+      for (int j = 0; j < 4 * MPW; ++j) {
+        const int jr = FULL ? j : min(j, static_cast<int>(m) - 1);
+        const uint32_t c = (wc[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+        pv[j] = pre[jr * 256 + c];
+      }
       float sum = 0.0f;
 #pragma unroll
       for (int j = 0; j < 4 * MPW; ++j) {
-        if (j < static_cast<int>(m)) {
-          const uint32_t c = (wc[j >> 2] >> (8 * (j & 3))) & 0xFFu;
-          sum = sum + (pre[j * 256 + c] + s_lut[j * 256 + c]);
-        }
+        const uint32_t c = (wc[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+        if (FULL || j < static_cast<int>(m)) sum = sum + (pv[j] + s_lut[ROT ? c * kRows + j : j * 256 + c]);
       }
       float d = s_score[pl] + sum;
       d = d == d ? d : __builtin_huge_valf();
@@ -1140,17 +1339,17 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
   }
 }
 
-// Up to 32 code bytes: held to 80 registers so that three eight-wave groups share a CU.
-template <int MPW, bool FULL, int CAP>
-__global__ void __launch_bounds__(kStreamThreads) __attribute__((amdgpu_waves_per_eu(6)))
+// Up to 32 code bytes.
+template <int MPW, bool FULL, int CAP, bool ROT = false>
+__global__ void __launch_bounds__(kStreamThreads) __attribute__((amdgpu_waves_per_eu(QVH_STREAM_WPE)))
 ivf_stream_kernel(ScanArgs a) {
-  stream_scan<MPW, FULL, CAP>(a);
+  stream_scan<MPW, FULL, CAP, ROT>(a);
 }
 
 // 33 to 64 code bytes: no register cap.
 template <bool FULL, int CAP>
 __global__ void __launch_bounds__(kStreamThreads) ivf_stream_wide_kernel(ScanArgs a) {
-  stream_scan<16, FULL, CAP>(a);
+  stream_scan<16, FULL, CAP, false>(a);
 }
 
 /// Ascending bitonic sort of s[0, n) (n a power of two, n <= 2 * blockDim) by the block.
@@ -1196,9 +1395,16 @@ __global__ void __launch_bounds__(kFinishThreads) ivf_finish_kernel(ScanArgs a) 
   s_key[tid] = static_cast<uint32_t>(tid) < cnt ? a.sel[static_cast<uint64_t>(q) * a.keep_sel + tid] : ~0ull;
   __syncthreads();
   auto list_of = [&](uint32_t pos) {
-    uint32_t pl = 0;
-    while (pl + 1 < a.nprobe && !(s_lo[pl] <= pos && pos < s_hi[pl])) ++pl;
-    return pl;
+    for (uint32_t b = 0; b + 1 < a.nprobe; b += 8) {
+      uint32_t hit = 0;
+#pragma unroll
+      for (uint32_t i = 0; i < 8; ++i) {
+        const uint32_t pl = b + i;
+        if (pl < a.nprobe && s_lo[pl] <= pos && pos < s_hi[pl]) hit |= 1u << i;
+      }
+      if (hit) return b + static_cast<uint32_t>(__builtin_ctz(hit));
+    }
+    return a.nprobe - 1;
   };
   if (a.refine) {
     // Exact re-ranking with the stored vectors (src/ivfpq_index.cc:139-142,363-373).
@@ -1274,12 +1480,12 @@ struct qvh_ivfpq {
   bool has_pre = false;
   uint64_t count = 0;
   std::vector<uint64_t> h_off;  // host copy of the list offsets
-  DeviceBuffer cent, cent_t, cent_norm, cb, cbt, pre;
+  DeviceBuffer cent, cent_t, cent_norm, cb, cbt, cbc, pre;
   DeviceBuffer off, codes, t1, vec;
   hipStream_t stream = nullptr;
   std::mutex mu;
   DeviceBuffer w_x, w_res, w_assign, w_codes, w_codes_p, w_t1, w_dest, w_shift;
-  DeviceBuffer w_q, w_scores, w_probes, w_bits, w_refs, w_dist, w_bytes, w_sel, w_selcnt;
+  DeviceBuffer w_q, w_scores, w_probes, w_bits, w_refs, w_dist, w_bytes, w_sel, w_selcnt, w_key, w_order;
   int timing = 0;               // 0 off, 1 stage events, 2 events and probed code bytes
   bool timed = false, timed_bytes = false;
   hipEvent_t ev[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
@@ -1367,15 +1573,20 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
     }
   }
   uint32_t* probes = static_cast<uint32_t*>(h->w_probes.reserve(nq * nprobe * sizeof(uint32_t)));
+  // Block order of the streaming scan (queries grouped by their smallest probed list): for batches
+  // of up to 64k queries and up to 32k lists (the counts fit one block's LDS).
+  const bool ordered = nq > 1 && nq <= 65536 && h->nlist <= 32768;
+  uint32_t* min_probe = ordered ? static_cast<uint32_t*>(h->w_key.reserve(nq * sizeof(uint32_t))) : nullptr;
   {
     const dim3 grid(static_cast<unsigned>(ceil_div(nq, 4)));
     const uint32_t nq32 = static_cast<uint32_t>(nq);
     if (h->nlist <= 64 * 8) {
-      hipLaunchKernelGGL(probe_select_kernel<8>, grid, dim3(256), 0, s, scores, nq32, h->nlist, nprobe, probes);
+      hipLaunchKernelGGL(probe_select_kernel<8>, grid, dim3(256), 0, s, scores, nq32, h->nlist, nprobe, probes, min_probe);
     } else if (h->nlist <= 64 * 32) {
-      hipLaunchKernelGGL(probe_select_kernel<32>, grid, dim3(256), 0, s, scores, nq32, h->nlist, nprobe, probes);
+      hipLaunchKernelGGL(probe_select_kernel<32>, grid, dim3(256), 0, s, scores, nq32, h->nlist, nprobe, probes, min_probe);
     } else {
-      hipLaunchKernelGGL(probe_select_any_kernel, grid, dim3(256), 0, s, scores, nq32, h->nlist, nprobe, probes);
+      hipLaunchKernelGGL(probe_select_any_kernel, grid, dim3(256), 0, s, scores, nq32, h->nlist, nprobe, probes,
+                         min_probe);
     }
   }
   QVH_HIP(hipGetLastError());
@@ -1398,6 +1609,7 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   a.t1 = h->t1.as<float>();
   a.pre = h->pre.as<float>();
   a.cbt = h->cbt.as<float>();
+  a.cbc = h->cbc.as<float>();
   a.cent = h->cent.as<float>();
   a.vec = h->vec.as<float>();
   a.bitmap = d_bitmap;
@@ -1427,12 +1639,24 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   const bool full = h->mp == 4 * mpw_t;
   const bool small_sel = a.keep_sel <= 64 && k <= 64;
   const size_t rows = 4 * mpw_t;
-  const size_t lds2 = rows * 256 * sizeof(float) + kStreamWaves * (small_sel ? 128 : 256) * sizeof(uint64_t) +
-                      (4 * static_cast<size_t>(nprobe) + 1) * sizeof(uint32_t);
-  if (mode != kModeResidual && nprobe <= kStreamMaxProbes && a.keep_sel >= 1 && a.keep_sel <= kStreamMaxSel &&
-      k <= kStreamMaxSel && lds2 <= 150 * 1024) {
+  // LDS of the streaming kernels: the table (static LDS for codes of up to 32 bytes), the wave
+  // queues and the probed-list arrays (dynamic).
+  const size_t lds_table = rows * 256 * sizeof(float);
+  const size_t lds_total = lds_table + kStreamWaves * (small_sel ? 128 : 256) * sizeof(uint64_t) +
+                           (4 * static_cast<size_t>(nprobe) + 2 + kStreamWaves) * sizeof(uint32_t);
+  const size_t lds2 = mpw_t > 8 ? lds_total : lds_total - lds_table;
+  if (mode != kModeResidual && h->mp <= kStreamMaxM && nprobe <= kStreamMaxProbes && a.keep_sel >= 1 &&
+      a.keep_sel <= kStreamMaxSel && k <= kStreamMaxSel && lds_total <= 150 * 1024) {
     a.sel = static_cast<uint64_t*>(h->w_sel.reserve(nq * a.keep_sel * sizeof(uint64_t)));
     a.sel_cnt = static_cast<uint32_t*>(h->w_selcnt.reserve(nq * sizeof(uint32_t)));
+    if (ordered) {
+      uint32_t* order = static_cast<uint32_t*>(h->w_order.reserve(nq * sizeof(uint32_t)));
+      const size_t olds = static_cast<size_t>(h->nlist) * sizeof(uint32_t);
+      raise_lds(reinterpret_cast<const void*>(probe_order_kernel), olds);
+      hipLaunchKernelGGL(probe_order_kernel, dim3(1), dim3(1024), olds, s, min_probe, static_cast<uint32_t>(nq), h->nlist,
+                         order);
+      a.order = order;
+    }
     auto launch2 = [&](auto kernel) {
       const void* fn = reinterpret_cast<const void*>(kernel);
       raise_lds(fn, lds2);
@@ -1441,7 +1665,14 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
 #define QVH_STREAM(MPW_)                                                                                  \
   (full ? (small_sel ? launch2(ivf_stream_kernel<MPW_, true, 128>) : launch2(ivf_stream_kernel<MPW_, true, 256>)) \
         : (small_sel ? launch2(ivf_stream_kernel<MPW_, false, 128>) : launch2(ivf_stream_kernel<MPW_, false, 256>)))
-    if (mpw_t == 2) {
+    // Bank-rotated lookups: L2 with the precomputed table (re-scored exactly afterwards), four
+    // dims per sub-space, 16- or 32-byte codes.
+    const bool rot = QVH_STREAM_ROT && mode == kModePre && full && h->dsub == 4 && (mpw_t == 4 || mpw_t == 8);
+    if (rot && mpw_t == 8) {
+      small_sel ? launch2(ivf_stream_kernel<8, true, 128, true>) : launch2(ivf_stream_kernel<8, true, 256, true>);
+    } else if (rot) {
+      small_sel ? launch2(ivf_stream_kernel<4, true, 128, true>) : launch2(ivf_stream_kernel<4, true, 256, true>);
+    } else if (mpw_t == 2) {
       QVH_STREAM(2);
     } else if (mpw_t == 4) {
       QVH_STREAM(4);
@@ -1557,12 +1788,15 @@ qvh_status qvh_ivfpq_set_trained(qvh_ivfpq* h, const float* centroids, const flo
     h->cent_norm.reserve(h->nlist * sizeof(float));
     h->cb.reserve(bbytes);
     h->cbt.reserve(bbytes);
+    h->cbc.reserve(bbytes);
     QVH_HIP(hipMemcpyAsync(h->cent.ptr, centroids, cbytes, hipMemcpyHostToDevice, s));
     QVH_HIP(hipMemcpyAsync(h->cb.ptr, codebook, bbytes, hipMemcpyHostToDevice, s));
     hipLaunchKernelGGL(centroid_prep_kernel, dim3(static_cast<unsigned>(ceil_div(h->nlist, 256))), dim3(256), 0, s,
                        h->cent.as<float>(), h->nlist, h->dim, h->cent_t.as<float>(), h->cent_norm.as<float>());
     hipLaunchKernelGGL(codebook_prep_kernel, dim3(static_cast<unsigned>(ceil_div(uint64_t(h->m) * 256 * h->dsub, 256))),
                        dim3(256), 0, s, h->cb.as<float>(), h->m, h->dsub, h->cbt.as<float>());
+    hipLaunchKernelGGL(codebook_cmajor_kernel, dim3(static_cast<unsigned>(ceil_div(uint64_t(h->m) * 256 * h->dsub, 256))),
+                       dim3(256), 0, s, h->cb.as<float>(), h->m, h->dsub, h->cbc.as<float>());
     h->has_pre = use_precomputed != 0 && h->metric == QVH_METRIC_L2;
     if (h->has_pre) {
       const uint64_t n = static_cast<uint64_t>(h->nlist) * h->m * 256;

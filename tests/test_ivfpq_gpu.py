@@ -108,6 +108,17 @@ def test_ivfpq_unaligned_code_width(oracle):
     print(compare_search(oracle, idx, st, q, 10, 16, 8))
 
 
+@pytest.mark.parametrize("dim,m", [(64, 16), (128, 64), (96, 96)])
+def test_ivfpq_code_widths(oracle, dim, m):
+    """16 code bytes of four dims (the bank-rotated scan), 64 bytes of two dims, and 96 bytes of one
+    dim (past the widest streaming kernel)."""
+    base = clustered(5_000, dim, 24, 40 + m)
+    q = clustered(40, dim, 24, 41 + m)
+    idx, st = build_pair(oracle, base, "l2", 24, m, False, iters=3)
+    for nprobe in (3, 24):
+        print(compare_search(oracle, idx, st, q, 10, nprobe))
+
+
 def test_ivfpq_integer_mixture_l2(oracle):
     """The integer-valued mixture of the 1M x 128 workload, at 60k rows: nlist 256, m 32."""
     base, q = D.int_mix(60_000, 200)
