@@ -22,6 +22,7 @@
 
 #include "common.hpp"
 #include "exact.hpp"
+#include "select.hpp"
 
 namespace qvh {
 void launch_normalize_rows(float* d_rows, uint64_t n, uint32_t dim, hipStream_t stream);
@@ -366,6 +367,68 @@ __global__ void __launch_bounds__(256) probe_select_kernel(const float* __restri
     return b;
   };
   uint64_t cur = smallest();
+  if (nprobe <= 64) {
+    // Threshold T = the nprobe-th smallest of the 64 lane minima: nprobe distinct lanes hold a key
+    // <= T, so the nprobe smallest keys are all <= T. The keys <= T (usually a few dozen) are
+    // sorted in LDS; more than 128 of them falls through to the selection loop below.
+    uint64_t v = cur;
+#pragma unroll
+    for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        const uint64_t o = __shfl_xor(v, stride, 64);
+        const bool keep_min = ((lane & stride) == 0) == ((lane & size) == 0);
+        v = keep_min ? (o < v ? o : v) : (o > v ? o : v);
+      }
+    }
+    const uint64_t T = __shfl(v, static_cast<int>(nprobe) - 1, 64);
+    uint32_t n = 0;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) n += static_cast<uint32_t>(__popcll(__ballot(key[i] <= T)));
+    if (n <= 128) {
+      __shared__ uint64_t s_cand[4][128];
+      uint64_t* cand = s_cand[threadIdx.x >> 6];
+      uint32_t at = 0;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const bool pass = key[i] <= T;
+        const uint64_t mk = __ballot(pass);
+        if (pass) cand[at + lane_rank(mk)] = key[i];
+        at += static_cast<uint32_t>(__popcll(mk));
+      }
+      for (uint32_t e = at + lane; e < 128; e += 64) cand[e] = ~0ull;
+      __builtin_amdgcn_wave_barrier();
+      uint64_t x[2] = {cand[lane], cand[lane + 64]};
+#pragma unroll
+      for (int size = 2; size <= 128; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+          if (stride == 64) {
+            const uint64_t lo = x[0] < x[1] ? x[0] : x[1], hi = x[0] < x[1] ? x[1] : x[0];
+            x[0] = lo;
+            x[1] = hi;
+          } else {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const int e = lane + 64 * h;
+              const uint64_t o = __shfl_xor(x[h], stride, 64);
+              const bool keep_min = ((e & stride) == 0) == ((e & size) == 0);
+              x[h] = keep_min ? (o < x[h] ? o : x[h]) : (o > x[h] ? o : x[h]);
+            }
+          }
+        }
+      }
+      const uint32_t l = static_cast<uint32_t>(x[0]);
+      if (static_cast<uint32_t>(lane) < nprobe) probes[static_cast<uint64_t>(q) * nprobe + lane] = l;
+      if (min_probe) {
+        uint32_t mn = static_cast<uint32_t>(lane) < nprobe ? l : 0xFFFFFFFFu;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) mn = min(mn, static_cast<uint32_t>(__shfl_xor(mn, off, 64)));
+        if (lane == 0) min_probe[q] = mn;
+      }
+      return;
+    }
+  }
   uint32_t mn = 0xFFFFFFFFu;
   for (uint32_t p = 0; p < nprobe; ++p) {
     const uint64_t best = wave_min_u64(cur);
@@ -1575,7 +1638,8 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   uint32_t* probes = static_cast<uint32_t*>(h->w_probes.reserve(nq * nprobe * sizeof(uint32_t)));
   // Block order of the streaming scan (queries grouped by their smallest probed list): for batches
   // of up to 64k queries and up to 32k lists (the counts fit one block's LDS).
-  const bool ordered = nq > 1 && nq <= 65536 && h->nlist <= 32768;
+  const bool ordered = nq > 1 && nq <= 65536 && h->nlist <= 32768 && mode != kModeResidual && h->mp <= kStreamMaxM &&
+                       nprobe <= kStreamMaxProbes;
   uint32_t* min_probe = ordered ? static_cast<uint32_t*>(h->w_key.reserve(nq * sizeof(uint32_t))) : nullptr;
   {
     const dim3 grid(static_cast<unsigned>(ceil_div(nq, 4)));
@@ -1588,6 +1652,17 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
       hipLaunchKernelGGL(probe_select_any_kernel, grid, dim3(256), 0, s, scores, nq32, h->nlist, nprobe, probes,
                          min_probe);
     }
+  }
+  uint32_t* order = nullptr;
+  if (ordered) {
+    order = static_cast<uint32_t*>(h->w_order.reserve(nq * sizeof(uint32_t)));
+    const size_t olds = static_cast<size_t>(h->nlist) * sizeof(uint32_t);
+    if (olds > 64 * 1024) {
+      QVH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(probe_order_kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(olds)));
+    }
+    hipLaunchKernelGGL(probe_order_kernel, dim3(1), dim3(1024), olds, s, min_probe, static_cast<uint32_t>(nq), h->nlist,
+                       order);
   }
   QVH_HIP(hipGetLastError());
   if (h->timed) QVH_HIP(hipEventRecord(h->ev[1], s));
@@ -1649,14 +1724,7 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
       a.keep_sel <= kStreamMaxSel && k <= kStreamMaxSel && lds_total <= 150 * 1024) {
     a.sel = static_cast<uint64_t*>(h->w_sel.reserve(nq * a.keep_sel * sizeof(uint64_t)));
     a.sel_cnt = static_cast<uint32_t*>(h->w_selcnt.reserve(nq * sizeof(uint32_t)));
-    if (ordered) {
-      uint32_t* order = static_cast<uint32_t*>(h->w_order.reserve(nq * sizeof(uint32_t)));
-      const size_t olds = static_cast<size_t>(h->nlist) * sizeof(uint32_t);
-      raise_lds(reinterpret_cast<const void*>(probe_order_kernel), olds);
-      hipLaunchKernelGGL(probe_order_kernel, dim3(1), dim3(1024), olds, s, min_probe, static_cast<uint32_t>(nq), h->nlist,
-                         order);
-      a.order = order;
-    }
+    a.order = order;
     auto launch2 = [&](auto kernel) {
       const void* fn = reinterpret_cast<const void*>(kernel);
       raise_lds(fn, lds2);
