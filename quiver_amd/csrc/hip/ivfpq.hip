@@ -855,19 +855,13 @@ __global__ void __launch_bounds__(kScanThreads) ivf_scan_kernel(ScanArgs a) {
 // bounds the query's final keep_sel-th key from above). At the end the eight lists are sorted
 // together and the keep_sel best go to the finishing kernel, which re-scores them exactly.
 
-// Four waves per block and four blocks per CU (the per-query table and queues take ~37 KB of LDS),
-// which leaves up to 128 registers per lane.
 #ifndef QVH_STREAM_ROT
 #define QVH_STREAM_ROT 0
 #endif
-#ifndef QVH_STREAM_WPE
-#define QVH_STREAM_WPE 4
-#endif
-#ifndef QVH_STREAM_WAVES
-#define QVH_STREAM_WAVES 4
-#endif
-constexpr int kStreamWaves = QVH_STREAM_WAVES;
-constexpr int kStreamThreads = kStreamWaves * 64;
+// Waves per streaming block: 4 with 128-entry wave queues (four blocks of ~37 KB LDS per CU, 128
+// registers per lane), 8 with 256-entry queues (three blocks of ~49 KB per CU, 80 registers).
+template <int CAP>
+constexpr int stream_waves() { return CAP == 128 ? 4 : 8; }
 constexpr uint32_t kStreamMaxProbes = 256;
 constexpr uint32_t kStreamMaxSel = 128;
 constexpr int kFinishThreads = 128;
@@ -985,6 +979,8 @@ __device__ __forceinline__ float adc_sum_rotated(const float* lut, const uint32_
 
 template <int MPW, bool FULL, int CAP, bool ROT>
 __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
+  constexpr int kStreamWaves = stream_waves<CAP>();
+  constexpr int kStreamThreads = kStreamWaves * 64;
   constexpr int QN = CAP / 64;     // queue keys per lane
   constexpr int kRows = 4 * MPW;   // table rows: the m sub-spaces, then zero rows
 #ifndef QVH_STREAM_CODES
@@ -1404,14 +1400,14 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
 
 // Up to 32 code bytes.
 template <int MPW, bool FULL, int CAP, bool ROT = false>
-__global__ void __launch_bounds__(kStreamThreads) __attribute__((amdgpu_waves_per_eu(QVH_STREAM_WPE)))
-ivf_stream_kernel(ScanArgs a) {
+__global__ void __launch_bounds__(stream_waves<CAP>() * 64)
+__attribute__((amdgpu_waves_per_eu(stream_waves<CAP>() == 4 ? 4 : 6))) ivf_stream_kernel(ScanArgs a) {
   stream_scan<MPW, FULL, CAP, ROT>(a);
 }
 
 // 33 to 64 code bytes: no register cap.
 template <bool FULL, int CAP>
-__global__ void __launch_bounds__(kStreamThreads) ivf_stream_wide_kernel(ScanArgs a) {
+__global__ void __launch_bounds__(stream_waves<CAP>() * 64) ivf_stream_wide_kernel(ScanArgs a) {
   stream_scan<16, FULL, CAP, false>(a);
 }
 
@@ -1717,8 +1713,9 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   // LDS of the streaming kernels: the table (static LDS for codes of up to 32 bytes), the wave
   // queues and the probed-list arrays (dynamic).
   const size_t lds_table = rows * 256 * sizeof(float);
-  const size_t lds_total = lds_table + kStreamWaves * (small_sel ? 128 : 256) * sizeof(uint64_t) +
-                           (4 * static_cast<size_t>(nprobe) + 2 + kStreamWaves) * sizeof(uint32_t);
+  const uint32_t waves = small_sel ? stream_waves<128>() : stream_waves<256>();
+  const size_t lds_total = lds_table + waves * (small_sel ? 128 : 256) * sizeof(uint64_t) +
+                           (4 * static_cast<size_t>(nprobe) + 2 + waves) * sizeof(uint32_t);
   const size_t lds2 = mpw_t > 8 ? lds_total : lds_total - lds_table;
   if (mode != kModeResidual && h->mp <= kStreamMaxM && nprobe <= kStreamMaxProbes && a.keep_sel >= 1 &&
       a.keep_sel <= kStreamMaxSel && k <= kStreamMaxSel && lds_total <= 150 * 1024) {
@@ -1728,7 +1725,7 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
     auto launch2 = [&](auto kernel) {
       const void* fn = reinterpret_cast<const void*>(kernel);
       raise_lds(fn, lds2);
-      hipLaunchKernelGGL(kernel, grid, dim3(kStreamThreads), lds2, s, a);
+      hipLaunchKernelGGL(kernel, grid, dim3(waves * 64), lds2, s, a);
     };
 #define QVH_STREAM(MPW_)                                                                                  \
   (full ? (small_sel ? launch2(ivf_stream_kernel<MPW_, true, 128>) : launch2(ivf_stream_kernel<MPW_, true, 256>)) \
