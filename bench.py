@@ -270,7 +270,7 @@ def bench_ivfpq(args, hip: Hip, qvh: Qvh, base, queries):
         "unit": "queries/s",
         "ms_per_step": ms_per_step,
         "stage_ms": {"select": float(st[:, 0].mean()), "scan": scan_ms},
-        "roofline": {"bound": "hbm", "kernel": "ivf_stream_kernel<8, true, 128>", "achieved": achieved,
+        "roofline": {"bound": "hbm", "kernel": "ivf_stream_kernel<8, true, 128, false>", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": load_traffic("ivf_stream_int_mix_1m_nprobe32_pmc"),
                      "code_bytes_per_launch": code_bytes},
