@@ -54,6 +54,10 @@ const char* qvh_last_error(void);
  * device is present. */
 qvh_status qvh_init(int device);
 
+/* The HIP device index that handles use (qvh_init's choice, else 0). No counterpart in the
+ * reference: device-resident callers use it to check that their buffers live on that device. */
+qvh_status qvh_get_device(int* device);
+
 /* Writes the device name and the gfx target (e.g. "gfx950") into caller buffers. */
 qvh_status qvh_device_info(char* name, size_t name_len, char* arch, size_t arch_len,
                            int* compute_units);

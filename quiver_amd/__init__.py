@@ -8,7 +8,13 @@
 The classes keep the reference's Python API (python/quiver/__init__.py:166-251): distances are
 "smaller is closer" (squared L2 for ``"l2"``, ``1 - <q, x>`` for ``"ip"``, ``1 - cos(q, x)`` for
 ``"cosine"``); missing results (k larger than the index or filter) come back as label ``-1`` and
-distance ``inf``. The scans run as hand-written HIP kernels on the GPU (``quiver_amd/lib/libqvh.so``);
+distance ``inf``.
+
+``search`` also takes queries that already live in GPU memory, as a torch (ROCm) tensor: the
+search is then ordered on torch's current stream of that device and the labels (int64) and
+distances (float32) come back as tensors on the same device, without a round trip through host
+memory. torch must be imported before quiver_amd for this: torch ships its own HIP runtime, and
+memory of one runtime copy cannot be used by another (a ValueError says so). The scans run as hand-written HIP kernels on the GPU (``quiver_amd/lib/libqvh.so``);
 there is no CPU fallback: without a gfx950 device, adding or searching raises ``ValueError``.
 """
 
@@ -50,6 +56,81 @@ def _as_matrix(x: ArrayLike, dim: int) -> np.ndarray:
     if a.shape[1] != dim:
         raise ValueError(f"expected dimension {dim}, got {a.shape[1]}")
     return a
+
+
+def _is_device_tensor(x) -> bool:
+    """A torch tensor in GPU memory (torch-ROCm names HIP devices "cuda")."""
+    return type(x).__module__.startswith("torch") and bool(getattr(x, "is_cuda", False))
+
+
+def _hip_runtimes():
+    """Paths of the HIP runtime libraries mapped into this process."""
+    try:
+        with open("/proc/self/maps") as f:
+            return {line.split()[-1] for line in f if "libamdhip64" in line}
+    except OSError:  # pragma: no cover - non-Linux
+        return set()
+
+
+def _device_queries(queries, dim: int, k: int):
+    """Checks a device query batch the way _as_matrix and the host path check host ones."""
+    import torch
+
+    runtimes = _hip_runtimes()
+    if len(runtimes) > 1:
+        raise ValueError("torch and quiver_amd run on different HIP runtimes in this process "
+                         f"({', '.join(sorted(runtimes))}), so device tensors cannot be shared: "
+                         "import torch before quiver_amd")
+
+    q = queries
+    if q.dim() == 1:
+        q = q.reshape(1, -1)
+    if q.dim() != 2:
+        raise ValueError(f"expected a 1-D or 2-D array, got shape {tuple(queries.shape)}")
+    if q.shape[1] != dim:
+        raise ValueError(f"expected dimension {dim}, got {q.shape[1]}")
+    if k <= 0:
+        raise ValueError("k must be positive")
+    index_device = _quiver._device_index()
+    if q.device.index != index_device:
+        raise ValueError(f"queries are on {q.device}, the index on cuda:{index_device}")
+    q = q.to(torch.float32).contiguous()
+    if q.numel() and not bool(torch.isfinite(q).all()):
+        raise ValueError("vectors must be finite")
+    return q
+
+
+def _device_results(nq: int, k: int, device):
+    import torch
+
+    return (torch.full((nq, k), -1, dtype=torch.int64, device=device),
+            torch.full((nq, k), float("inf"), dtype=torch.float32, device=device))
+
+
+def _on_torch_stream(device, tensors, launch) -> None:
+    """Calls launch(stream) so that its device work runs after the work already queued on torch's
+    current stream and before the work queued there afterwards. The library reads a null stream
+    as "the handle's own stream", so torch's null stream is replaced by a side stream that joins
+    it on both ends."""
+    import torch
+
+    cur = torch.cuda.current_stream(device)
+    if cur.cuda_stream != 0:
+        launch(cur.cuda_stream)
+        return
+    side = torch.cuda.Stream(device=device)
+    side.wait_stream(cur)
+    for t in tensors:
+        if t is not None:
+            t.record_stream(side)
+    launch(side.cuda_stream)
+    cur.wait_stream(side)
+
+
+def _device_bitmap(bits: np.ndarray, device):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int64)).to(device)
 
 
 _MAX_LABEL = 2**63 - 1  # labels come back as int64, and -1 marks an empty slot
@@ -116,11 +197,47 @@ class IvfPqIndex:
 
     def search(self, queries: ArrayLike, k: int = 10, nprobe: int = 16, refine_factor: int = 0,
                filter: Optional[ArrayLike] = None, num_threads: int = 0) -> Tuple[np.ndarray, np.ndarray]:
+        if _is_device_tensor(queries):
+            return self._search_device(queries, int(k), int(nprobe), int(refine_factor), filter)
         q = _as_matrix(queries, self.dim)
         if k <= 0:
             raise ValueError("k must be positive")
         allowed = _as_labels(filter) if filter is not None else None
         return self._index._search(q, int(k), int(nprobe), int(refine_factor), allowed, num_threads)
+
+    def _search_device(self, queries, k: int, nprobe: int, refine_factor: int, filter):
+        import torch
+
+        q = _device_queries(queries, self.dim, k)
+        if refine_factor < 0:
+            raise ValueError("refine_factor must be non-negative")
+        labels, dist = _device_results(q.shape[0], k, q.device)
+        n = len(self)
+        if q.shape[0] == 0 or n == 0 or not self.is_trained:
+            return labels, dist
+        bitmap = None
+        if filter is not None:
+            bitmap = _device_bitmap(self._index._position_bitmap(_as_labels(filter)), q.device)
+        refs = torch.empty((q.shape[0], k), dtype=torch.int64, device=q.device)
+        _on_torch_stream(q.device, (q, bitmap, refs, dist), lambda stream: self._index._search_device(
+            q.data_ptr(), q.shape[0], k, max(nprobe, 1), refine_factor, 0 if bitmap is None else bitmap.data_ptr(),
+            refs.data_ptr(), dist.data_ptr(), stream))
+        offsets, table = self._label_tables(q.device, n)
+        found = refs != -1
+        pos = offsets[(refs >> 32).clamp(0, offsets.numel() - 1)] + (refs & 0xFFFFFFFF)
+        return torch.where(found, table[pos.clamp(0, n - 1)], labels), dist
+
+    def _label_tables(self, device, n: int):
+        """CSR offsets and labels on `device` (refs -> labels), rebuilt when the index grows."""
+        import torch
+
+        cached = getattr(self, "_dev_tables", None)
+        if cached is None or cached[0] != (n, device):
+            offsets = torch.from_numpy(self._index._list_offsets().view(np.int64)).to(device)
+            table = torch.from_numpy(self._index._list_labels().view(np.int64)).to(device)
+            cached = ((n, device), offsets, table)
+            self._dev_tables = cached
+        return cached[1], cached[2]
 
     def set_trained(self, centroids: ArrayLike, codebook: ArrayLike) -> None:
         """Install trained state (coarse centroids [nlist, dim], PQ codebook [m, 256, dim/m])
@@ -188,11 +305,41 @@ class FlatIndex:
 
     def search(self, queries: ArrayLike, k: int = 10, filter: Optional[ArrayLike] = None,
                num_threads: int = 0) -> Tuple[np.ndarray, np.ndarray]:
+        if _is_device_tensor(queries):
+            return self._search_device(queries, int(k), filter)
         q = _as_matrix(queries, self.dim)
         if k <= 0:
             raise ValueError("k must be positive")
         allowed = _as_labels(filter) if filter is not None else None
         return self._index._search(q, int(k), allowed, num_threads)
+
+    def _search_device(self, queries, k: int, filter):
+        import torch
+
+        q = _device_queries(queries, self.dim, k)
+        labels, dist = _device_results(q.shape[0], k, q.device)
+        n = len(self)
+        if q.shape[0] == 0 or n == 0:
+            return labels, dist
+        bitmap = None
+        if filter is not None:
+            bitmap = _device_bitmap(self._index._row_bitmap(_as_labels(filter)), q.device)
+        rows = torch.empty((q.shape[0], k), dtype=torch.int32, device=q.device)
+        _on_torch_stream(q.device, (q, bitmap, rows, dist), lambda stream: self._index._search_device(
+            q.data_ptr(), q.shape[0], k, 0 if bitmap is None else bitmap.data_ptr(), rows.data_ptr(), dist.data_ptr(),
+            stream))
+        table = self._label_table(q.device, n)
+        return torch.where(rows != -1, table[rows.clamp(0, n - 1).long()], labels), dist
+
+    def _label_table(self, device, n: int):
+        """Labels by row on `device`, rebuilt when the index grows."""
+        import torch
+
+        cached = getattr(self, "_dev_labels", None)
+        if cached is None or cached[0] != (n, device):
+            cached = ((n, device), torch.from_numpy(self._index._labels().view(np.int64)).to(device))
+            self._dev_labels = cached
+        return cached[1]
 
     def get_vector(self, row: int) -> np.ndarray:
         """Stored row ``row`` (normalized for cosine)."""

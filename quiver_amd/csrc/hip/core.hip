@@ -102,6 +102,13 @@ qvh_status qvh_init(int device) {
   });
 }
 
+qvh_status qvh_get_device(int* device) {
+  return qvh::guarded([&] {
+    QVH_REQUIRE(device != nullptr, "qvh_get_device: null argument");
+    *device = qvh::current_device();
+  });
+}
+
 qvh_status qvh_device_info(char* name, size_t name_len, char* arch, size_t arch_len,
                            int* compute_units) {
   return qvh::guarded([&] {

@@ -55,6 +55,19 @@ class FlatIndex {
   /// query batches through qvh_flat_search_device.
   qvh_flat* device_handle() const noexcept { return dev_.get(); }
 
+  /// Device-resident batch (no reference counterpart; for callers whose queries already live in
+  /// HBM): queries [nq][dim], the row bitmap of row_bitmap() or null, and outputs rows [nq][k]
+  /// (0xFFFFFFFF = empty) and distances [nq][k] are device pointers; the search is enqueued on
+  /// `stream` (a hipStream_t, null = the index's own) under the shared lock and not waited for.
+  /// Queries must be finite (the caller checks); rows map to labels through labels().
+  void search_batch_device(const float* d_queries, std::size_t nq, std::size_t k,
+                           const std::uint64_t* d_row_bitmap, std::uint32_t* d_rows,
+                           float* d_distances, void* stream = nullptr) const;
+  /// The filter as bits over rows (bit i = labels()[i] admitted), as search_batch builds it.
+  std::vector<std::uint64_t> row_bitmap(const Filter& filter) const;
+  /// Labels by row.
+  std::vector<Label> labels() const;
+
  private:
   void search_rows(const float* queries, std::size_t nq, std::size_t k, const Filter* filter,
                    ThreadPool* pool, Label* labels, float* distances) const;

@@ -88,6 +88,18 @@ class IvfPqIndex {
   /// The device handle (null before training), for device-resident query batches.
   qvh_ivfpq* device_handle() const noexcept;
 
+  /// Device-resident batch (no reference counterpart; for callers whose queries already live in
+  /// HBM): queries [nq][dim], the position bitmap of position_bitmap() or null (params.filter is
+  /// not read), and outputs refs [nq][k] ((list << 32) | offset, all ones = empty) and distances
+  /// [nq][k] are device pointers; enqueued on `stream` (a hipStream_t, null = the index's own)
+  /// under the shared lock and not waited for. Queries must be finite (the caller checks); refs
+  /// map to labels through list_offsets() and list_labels().
+  void search_batch_device(const float* d_queries, std::size_t nq, std::size_t k,
+                           const IvfPqSearchParams& params, const std::uint64_t* d_position_bitmap,
+                           std::uint64_t* d_refs, float* d_distances, void* stream = nullptr) const;
+  /// The filter as bits over CSR positions (bit p = list_labels()[p] admitted).
+  std::vector<std::uint64_t> position_bitmap(const Filter& filter) const;
+
  private:
   struct Impl;
   explicit IvfPqIndex(std::unique_ptr<Impl> impl);

@@ -121,6 +121,31 @@ void FlatIndex::search_batch(const float* queries, std::size_t nq, std::size_t k
   search_rows(queries, nq, k, filter, pool, labels, distances);
 }
 
+void FlatIndex::search_batch_device(const float* d_queries, std::size_t nq, std::size_t k,
+                                    const std::uint64_t* d_row_bitmap, std::uint32_t* d_rows,
+                                    float* d_distances, void* stream) const {
+  if (nq == 0 || k == 0) return;
+  QUIVER_CHECK(d_queries != nullptr && d_rows != nullptr && d_distances != nullptr,
+               "search_batch_device: null buffer");
+  QUIVER_CHECK(k <= 0xFFFFFFFFull, "k is too large");
+  std::shared_lock lock(*mu_);
+  QUIVER_CHECK(dev_ != nullptr && !labels_.empty(), "search_batch_device: the index is empty");
+  qvh_check(qvh_flat_search_device(dev_.get(), d_queries, nq, static_cast<std::uint32_t>(k), d_row_bitmap, d_rows,
+                                   d_distances, stream),
+            "FlatIndex::search_batch_device");
+}
+
+std::vector<std::uint64_t> FlatIndex::row_bitmap(const Filter& filter) const {
+  std::shared_lock lock(*mu_);
+  return internal::filter_bitmap(filter, labels_.size(), [&](std::size_t i) { return labels_[i]; },
+                                 ThreadPool::global());
+}
+
+std::vector<Label> FlatIndex::labels() const {
+  std::shared_lock lock(*mu_);
+  return labels_;
+}
+
 std::size_t FlatIndex::size() const {
   std::shared_lock lock(*mu_);
   return labels_.size();

@@ -269,6 +269,29 @@ void IvfPqIndex::search_batch(const float* queries, std::size_t nq, std::size_t 
   impl_->search_rows(queries, nq, k, params, pool, labels, distances);
 }
 
+void IvfPqIndex::search_batch_device(const float* d_queries, std::size_t nq, std::size_t k,
+                                     const IvfPqSearchParams& params, const std::uint64_t* d_position_bitmap,
+                                     std::uint64_t* d_refs, float* d_distances, void* stream) const {
+  if (nq == 0 || k == 0) return;
+  QUIVER_CHECK(d_queries != nullptr && d_refs != nullptr && d_distances != nullptr,
+               "search_batch_device: null buffer");
+  QUIVER_CHECK(k <= 0xFFFFFFFFull, "k is too large");
+  std::shared_lock lock(impl_->mu);
+  QUIVER_CHECK(impl_->trained && impl_->count > 0, "search_batch_device: the index is untrained or empty");
+  const std::uint32_t nprobe = static_cast<std::uint32_t>(
+      std::min<std::size_t>(std::max<std::size_t>(params.nprobe, 1), impl_->params.nlist));
+  qvh_check(qvh_ivfpq_search_device(impl_->dev.get(), d_queries, nq, static_cast<std::uint32_t>(k), nprobe,
+                                    params.refine_factor, d_position_bitmap, d_refs, d_distances,
+                                    stream),
+            "IvfPqIndex::search_batch_device");
+}
+
+std::vector<std::uint64_t> IvfPqIndex::position_bitmap(const Filter& filter) const {
+  std::shared_lock lock(impl_->mu);
+  return internal::filter_bitmap(filter, impl_->count, [&](std::size_t i) { return impl_->labels[i]; },
+                                 ThreadPool::global());
+}
+
 std::size_t IvfPqIndex::size() const noexcept {
   std::shared_lock lock(impl_->mu);
   return impl_->count;

@@ -103,6 +103,12 @@ PYBIND11_MODULE(_quiver, m) {
     }
   });
 
+  m.def("_device_index", [] {
+    int d = 0;
+    if (qvh_get_device(&d) != QVH_OK) throw quiver::Error(std::string("no device: ") + qvh_last_error());
+    return d;
+  });
+
   m.def(
       "simd_isa",
       [] {
@@ -169,6 +175,33 @@ PYBIND11_MODULE(_quiver, m) {
            })
       .def_property_readonly("_device_handle",
                              [](const quiver::FlatIndex& s) { return reinterpret_cast<std::uintptr_t>(s.device_handle()); })
+      .def(
+          "_search_device",
+          [](const quiver::FlatIndex& self, std::uintptr_t q, std::size_t nq, std::size_t k, std::uintptr_t bitmap,
+             std::uintptr_t rows, std::uintptr_t dist, std::uintptr_t stream) {
+            py::gil_scoped_release release;
+            self.search_batch_device(reinterpret_cast<const float*>(q), nq, k,
+                                     reinterpret_cast<const std::uint64_t*>(bitmap),
+                                     reinterpret_cast<std::uint32_t*>(rows), reinterpret_cast<float*>(dist),
+                                     reinterpret_cast<void*>(stream));
+          },
+          py::arg("queries"), py::arg("nq"), py::arg("k"), py::arg("bitmap"), py::arg("rows"), py::arg("distances"),
+          py::arg("stream"))
+      .def("_row_bitmap",
+           [](const quiver::FlatIndex& self, const LabelArray& allowed) {
+             const auto filter = make_filter(allowed);
+             std::vector<std::uint64_t> bits;
+             {
+               py::gil_scoped_release release;
+               bits = self.row_bitmap(*filter);
+             }
+             return py::array_t<std::uint64_t>(static_cast<py::ssize_t>(bits.size()), bits.data());
+           })
+      .def("_labels",
+           [](const quiver::FlatIndex& self) {
+             const auto l = self.labels();
+             return py::array_t<std::uint64_t>(static_cast<py::ssize_t>(l.size()), l.data());
+           })
       .def_property_readonly("dim", &quiver::FlatIndex::dim)
       .def_property_readonly("metric", [](const quiver::FlatIndex& s) {
         return std::string(quiver::to_string(s.metric()));
@@ -245,6 +278,32 @@ PYBIND11_MODULE(_quiver, m) {
       .def_property_readonly("is_trained", &quiver::IvfPqIndex::is_trained)
       .def_property_readonly("_device_handle",
                              [](const quiver::IvfPqIndex& s) { return reinterpret_cast<std::uintptr_t>(s.device_handle()); })
+      .def(
+          "_search_device",
+          [](const quiver::IvfPqIndex& self, std::uintptr_t q, std::size_t nq, std::size_t k, std::size_t nprobe,
+             std::uint64_t refine_factor, std::uintptr_t bitmap, std::uintptr_t refs, std::uintptr_t dist,
+             std::uintptr_t stream) {
+            quiver::IvfPqSearchParams p;
+            p.nprobe = nprobe;
+            p.refine_factor = refine_factor;
+            py::gil_scoped_release release;
+            self.search_batch_device(reinterpret_cast<const float*>(q), nq, k, p,
+                                     reinterpret_cast<const std::uint64_t*>(bitmap),
+                                     reinterpret_cast<std::uint64_t*>(refs), reinterpret_cast<float*>(dist),
+                                     reinterpret_cast<void*>(stream));
+          },
+          py::arg("queries"), py::arg("nq"), py::arg("k"), py::arg("nprobe"), py::arg("refine_factor"),
+          py::arg("bitmap"), py::arg("refs"), py::arg("distances"), py::arg("stream"))
+      .def("_position_bitmap",
+           [](const quiver::IvfPqIndex& self, const LabelArray& allowed) {
+             const auto filter = make_filter(allowed);
+             std::vector<std::uint64_t> bits;
+             {
+               py::gil_scoped_release release;
+               bits = self.position_bitmap(*filter);
+             }
+             return py::array_t<std::uint64_t>(static_cast<py::ssize_t>(bits.size()), bits.data());
+           })
       .def_property_readonly("dim", &quiver::IvfPqIndex::dim)
       .def_property_readonly("nlist", [](const quiver::IvfPqIndex& s) { return s.params().nlist; })
       .def_property_readonly("m", [](const quiver::IvfPqIndex& s) { return s.params().m; })

@@ -4,6 +4,15 @@ import sys
 
 import pytest
 
+# torch (when installed) is imported before any test module loads quiver_amd: torch ships its own
+# HIP runtime, and loading it after quiver_amd's would leave two runtime copies in the process,
+# whose device memory cannot be exchanged (the device-tensor tests pass torch tensors to the
+# library). Loaded first, torch's copy is the only one and the library binds to it.
+try:
+    import torch  # noqa: F401
+except ImportError:  # pragma: no cover - torch is optional
+    pass
+
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "tests"))

@@ -1,0 +1,122 @@
+"""Device-resident query batches from Python: torch (ROCm) tensors in GPU memory go straight to the
+device search (FlatIndex/IvfPqIndex.search_batch_device) and the results stay on the device.
+
+The host-buffer search is the reference here (it is checked against the oracle in
+test_flat_gpu.py / test_ivfpq_gpu.py): labels must be identical and distances bit-identical,
+since both run the same kernels on the same queries.
+"""
+
+import numpy as np
+import pytest
+
+import quiver_amd as quiver
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU visible to torch")
+    return torch.device("cuda", quiver._quiver._device_index())
+
+
+def _same(host, dev):
+    hl, hd = host
+    dl, dd = dev
+    assert dl.dtype == torch.int64 and dd.dtype == torch.float32
+    assert np.array_equal(hl, dl.cpu().numpy())
+    assert np.array_equal(hd.view(np.uint32), dd.cpu().numpy().view(np.uint32))
+
+
+def _data(n, dim, nq, seed):
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal((n, dim)).astype(np.float32),
+            rng.standard_normal((nq, dim)).astype(np.float32))
+
+
+@pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
+def test_flat_device_queries_match_host(metric):
+    dev = _gpu()
+    base, q = _data(20_000, 64, 300, 1)
+    print(f"case: flat {metric} n=20000 dim=64 nq=300", flush=True)
+    idx = quiver.FlatIndex(64, metric)
+    idx.add(base, labels=np.arange(20_000, dtype=np.uint64) * 3 + 7)
+    qd = torch.from_numpy(q).to(dev)
+    for k in (1, 10, 32, 100):
+        _same(idx.search(q, k), idx.search(qd, k))
+    allowed = np.arange(7, 60_000, 9, dtype=np.uint64)
+    _same(idx.search(q, 10, filter=allowed), idx.search(qd, 10, filter=allowed))
+    _same(idx.search(q[0], 5), idx.search(qd[0], 5))  # one query as a 1-D tensor
+
+
+def test_flat_device_edge_cases():
+    dev = _gpu()
+    idx = quiver.FlatIndex(16, "l2")
+    q = torch.zeros((3, 16), device=dev)
+    labels, dist = idx.search(q, 4)  # empty index
+    assert labels.shape == (3, 4) and bool((labels == -1).all()) and bool(torch.isinf(dist).all())
+    base, hq = _data(5, 16, 3, 2)
+    idx.add(base)
+    _same(idx.search(hq, 8), idx.search(torch.from_numpy(hq).to(dev), 8))  # fewer rows than k
+    idx.add(base + 1.0)  # the cached label table follows the index
+    _same(idx.search(hq, 8), idx.search(torch.from_numpy(hq).to(dev), 8))
+    with pytest.raises(ValueError):
+        idx.search(torch.full((2, 16), float("nan"), device=dev), 3)
+    with pytest.raises(ValueError):
+        idx.search(torch.zeros((2, 15), device=dev), 3)
+    with pytest.raises(ValueError):
+        idx.search(torch.zeros((2, 16), device=dev), 0)
+    # float64 and non-contiguous inputs are converted like host arrays are
+    q64 = torch.from_numpy(hq.astype(np.float64)).to(dev)
+    _same(idx.search(hq, 3), idx.search(q64, 3))
+    wide = torch.from_numpy(np.repeat(hq, 2, axis=1)).to(dev)[:, ::2]
+    _same(idx.search(hq, 3), idx.search(wide, 3))
+
+
+def test_flat_device_search_runs_on_the_current_stream():
+    dev = _gpu()
+    base, q = _data(50_000, 128, 256, 3)
+    idx = quiver.FlatIndex(128, "l2")
+    idx.add(base)
+    host = idx.search(q, 10)
+    s = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(s):
+        qd = torch.from_numpy(q).to(dev, non_blocking=False)
+        res = idx.search(qd, 10)
+    s.synchronize()
+    _same(host, res)
+
+
+@pytest.mark.parametrize("metric,store,refine", [("l2", False, 0), ("l2", True, 4), ("cosine", True, 8),
+                                                 ("ip", False, 0)])
+def test_ivfpq_device_queries_match_host(metric, store, refine):
+    dev = _gpu()
+    base, q = _data(12_000, 32, 200, 4)
+    print(f"case: ivfpq {metric} store={store} refine={refine}", flush=True)
+    idx = quiver.IvfPqIndex(32, metric, nlist=64, m=8, store_vectors=store, train_iterations=5)
+    idx.train(base)
+    idx.add(base, labels=np.arange(12_000, dtype=np.uint64) * 5 + 1)
+    qd = torch.from_numpy(q).to(dev)
+    for nprobe in (1, 8, 64):
+        _same(idx.search(q, 10, nprobe=nprobe, refine_factor=refine),
+              idx.search(qd, 10, nprobe=nprobe, refine_factor=refine))
+    allowed = np.arange(1, 60_000, 25, dtype=np.uint64)
+    _same(idx.search(q, 10, nprobe=16, refine_factor=refine, filter=allowed),
+          idx.search(qd, 10, nprobe=16, refine_factor=refine, filter=allowed))
+
+
+def test_ivfpq_device_untrained_and_growing():
+    dev = _gpu()
+    idx = quiver.IvfPqIndex(16, "l2", nlist=8, m=4, train_iterations=3)
+    q = torch.zeros((2, 16), device=dev)
+    labels, dist = idx.search(q, 3)  # untrained: empty results, as on the host
+    assert bool((labels == -1).all()) and bool(torch.isinf(dist).all())
+    base, hq = _data(3_000, 16, 20, 5)
+    idx.train(base)
+    idx.add(base[:1_000])
+    qd = torch.from_numpy(hq).to(dev)
+    _same(idx.search(hq, 5, nprobe=8), idx.search(qd, 5, nprobe=8))
+    idx.add(base[1_000:])  # the cached CSR tables follow the index
+    _same(idx.search(hq, 5, nprobe=8), idx.search(qd, 5, nprobe=8))
