@@ -96,6 +96,15 @@ uint64_t qvh_flat_size(const qvh_flat* flat);
 qvh_status qvh_flat_search(qvh_flat* flat, const float* queries, uint64_t nq, uint32_t k,
                            const uint64_t* row_bitmap, uint32_t* out_rows, float* out_dist);
 
+/* Exact top-k over the listed rows only: HnswIndex::search_exact's scan over the labels a
+ * selective filter admits (src/hnsw_index.cc:722-739, taken when the filter's cardinality is at
+ * most exact_scan_threshold x live nodes, src/hnsw_index.cc:755-760), on a device row store whose
+ * rows are the graph's node ids. `rows` (host, any order; repeats count once) must all be below
+ * the stored row count (else QVH_EINVAL). Outputs as qvh_flat_search. */
+qvh_status qvh_flat_search_rows(qvh_flat* flat, const float* queries, uint64_t nq, uint32_t k,
+                                const uint32_t* rows, uint64_t nrows, uint32_t* out_rows,
+                                float* out_dist);
+
 /* Same, on device-resident buffers, enqueued on `stream` (a hipStream_t; NULL = the handle's). */
 qvh_status qvh_flat_search_device(qvh_flat* flat, const float* d_queries, uint64_t nq,
                                   uint32_t k, const uint64_t* d_row_bitmap, uint32_t* d_out_rows,

@@ -963,6 +963,30 @@ qvh_status qvh_flat_search(qvh_flat* f, const float* queries, uint64_t nq, uint3
   });
 }
 
+qvh_status qvh_flat_search_rows(qvh_flat* f, const float* queries, uint64_t nq, uint32_t k,
+                                const uint32_t* rows, uint64_t nrows, uint32_t* out_rows, float* out_dist) {
+  std::vector<uint64_t> bits;
+  {
+    const qvh_status st = guarded([&] {
+      QVH_REQUIRE(f != nullptr, "qvh_flat_search_rows: null handle");
+      QVH_REQUIRE(rows != nullptr || nrows == 0, "qvh_flat_search_rows: null rows");
+      uint64_t n = 0;
+      {
+        std::lock_guard<std::mutex> lock(f->mu);
+        n = f->n;
+      }
+      // The listed rows as a row bitmap: the same admitted set as a filter over their labels.
+      bits.assign(ceil_div(std::max<uint64_t>(n, 1), 64), 0);
+      for (uint64_t i = 0; i < nrows; ++i) {
+        QVH_REQUIRE(rows[i] < n, "qvh_flat_search_rows: row " + std::to_string(rows[i]) + " is not stored");
+        bits[rows[i] >> 6] |= 1ull << (rows[i] & 63);
+      }
+    });
+    if (st != QVH_OK) return st;
+  }
+  return qvh_flat_search(f, queries, nq, k, bits.data(), out_rows, out_dist);
+}
+
 qvh_status qvh_flat_search_device(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t k,
                                   const uint64_t* d_row_bitmap, uint32_t* d_out_rows,
                                   float* d_out_dist, void* stream) {

@@ -35,6 +35,8 @@ class Qvh:
         L.qvh_flat_size.restype = C.c_uint64
         L.qvh_flat_search.argtypes = [C.c_void_p, _f32p, C.c_uint64, C.c_uint32, C.c_void_p,
                                       _u32p, _f32p]
+        L.qvh_flat_search_rows.argtypes = [C.c_void_p, _f32p, C.c_uint64, C.c_uint32, _u32p, C.c_uint64,
+                                           _u32p, _f32p]
         L.qvh_normalize.argtypes = [_f32p, C.c_uint64, C.c_uint32]
 
     def error(self) -> str:
@@ -88,3 +90,13 @@ class QvhFlat:
         self.q.check(self.q.lib.qvh_flat_search(
             self.h, queries, nq, k, None if bm is None else bm.ctypes.data_as(C.c_void_p), rows, dist))
         return rows, dist
+
+    def search_rows(self, queries, k, rows):
+        """Exact top-k over the listed rows (qvh_flat_search_rows); returns (status, rows, dist)."""
+        queries = np.ascontiguousarray(queries, dtype=np.float32)
+        listed = np.ascontiguousarray(rows, dtype=np.uint32)
+        nq = queries.shape[0]
+        out_rows = np.empty((nq, k), dtype=np.uint32)
+        dist = np.empty((nq, k), dtype=np.float32)
+        st = self.q.lib.qvh_flat_search_rows(self.h, queries, nq, k, listed, listed.size, out_rows, dist)
+        return st, out_rows, dist

@@ -203,3 +203,40 @@ def test_c_abi_rows_match_python_path(oracle):
     exp_r, exp_d = oracle.flat_search(base, q, 10, "l2")
     assert np.array_equal(rows, exp_r) and np.array_equal(dist.view(np.uint32), exp_d.view(np.uint32))
     f.close()
+
+
+@pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
+@pytest.mark.parametrize("count,k", [(1, 10), (37, 10), (600, 10), (600, 50), (20_000, 10)])
+def test_search_over_listed_rows(oracle, metric, count, k):
+    """HnswIndex::search_exact's scan over the node ids a selective filter admits
+    (src/hnsw_index.cc:722-739): exact top-k over a row list given in any order, with repeats."""
+    print(f"case: listed rows count={count} k={k} metric={metric}", flush=True)
+    base, q = D.unit_mix(30_000, 40)
+    rng = np.random.default_rng(count * 7 + k)
+    rows = rng.choice(base.shape[0], count, replace=False).astype(np.uint32)
+    listed = np.concatenate([rows, rows[: count // 3]])
+    rng.shuffle(listed)
+    f = Qvh().flat(base.shape[1], metric)
+    stored = f.append(base)
+    st, got_rows, got_d = f.search_rows(q, k, listed)
+    assert st == 0, f.q.error()
+    exp_rows, exp_d = oracle.flat_search(stored, q, k, metric, rows_bitmap(np.sort(rows), base.shape[0]))
+
+    def labels(r):
+        out = r.astype(np.int64)
+        out[r == np.uint32(0xFFFFFFFF)] = -1
+        return out
+
+    print(assert_same_topk(labels(got_rows), got_d, labels(exp_rows), exp_d, _true_dist(oracle, stored, q, metric)))
+
+
+def test_search_over_listed_rows_edges():
+    base, q = D.unit_mix(1_000, 5)
+    f = Qvh().flat(base.shape[1], "l2")
+    f.append(base)
+    st, rows, dist = f.search_rows(q, 4, np.zeros(0, np.uint32))  # nothing admitted
+    assert st == 0 and np.all(rows == np.uint32(0xFFFFFFFF)) and np.all(np.isinf(dist))
+    st, rows, dist = f.search_rows(q, 4, np.array([999, 3], np.uint32))  # fewer rows than k
+    assert st == 0 and set(rows[0][:2]) == {3, 999} and np.all(rows[:, 2:] == np.uint32(0xFFFFFFFF))
+    st, _, _ = f.search_rows(q, 4, np.array([5, 1_000], np.uint32))  # row 1000 is not stored
+    assert st == -22 and "not stored" in f.q.error()
