@@ -1290,7 +1290,7 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
     merged += s_wcount[w2];
   }
   const uint32_t ks = pow2_at_least(max(most, 1u));
-  constexpr uint32_t kWavesPow2 = kStreamWaves <= 8 ? 8 : 16;
+  constexpr uint32_t kWavesPow2 = kStreamWaves <= 4 ? 4 : kStreamWaves <= 8 ? 8 : 16;
 #pragma unroll
   for (int i = 0; i < QN; ++i) {
     const uint32_t e = i * 64 + lane;
