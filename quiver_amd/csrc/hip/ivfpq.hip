@@ -539,6 +539,14 @@ struct ScanArgs {
   uint64_t* sel;      // [nq][keep_sel] streaming scan -> finishing kernel
   uint32_t* sel_cnt;  // [nq]
   const uint32_t* order;  // [nq] block -> query of the streaming scan, or null
+  // Sliced queries of the streaming scan: blocks [0, nwhole) scan one query each; the rest scan
+  // one of `parts` slices of a query's probed codes and leave their best keep keys in part_keys;
+  // the slice that finishes last merges them (part_done counts finished slices, reset by the
+  // merging block).
+  uint32_t nwhole, parts;
+  uint64_t* part_keys;  // [nq - nwhole][parts][keep]
+  uint32_t* part_cnt;   // [nq - nwhole][parts]
+  uint32_t* part_done;  // [nq - nwhole], zero between searches
 };
 
 /// Ascending bitonic sort of s[0, n) (n a power of two) by all 256 threads.
@@ -866,6 +874,8 @@ constexpr uint32_t kStreamMaxProbes = 256;
 constexpr uint32_t kStreamMaxSel = 128;
 constexpr int kFinishThreads = 128;
 constexpr uint32_t kStreamMaxM = 64;  // code bytes of the widest streaming kernel
+// Slices per query of a batch smaller than one resident generation of blocks.
+constexpr uint64_t kMaxSlices = 4;
 
 /// Ascending bitonic sort of N * 64 keys held by one wave, element e = i * 64 + lane in k[i].
 template <int N>
@@ -1013,10 +1023,43 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const uint32_t q = a.order ? a.order[blockIdx.x] : blockIdx.x;
+  // Block -> (query slot, slice): whole queries first, then `parts` blocks per sliced query.
+  uint32_t slot = blockIdx.x, part = 0;
+  const bool split = blockIdx.x >= a.nwhole;
+  if (split) {
+    const uint32_t u = blockIdx.x - a.nwhole;
+    slot = a.nwhole + u / a.parts;
+    part = u % a.parts;
+  }
+  const uint32_t q = a.order ? a.order[slot] : slot;
   const float* qv = a.Q + static_cast<uint64_t>(q) * a.dim;
   const uint32_t m = a.m;
   const bool l2 = a.mode == kModePre;
+
+  // Wave 0 requests the probed lists' ids, bounds and scores first: their two dependent round
+  // trips then overlap the table build.
+  uint32_t pf_list[4], pf_lo[4], pf_len[4];
+  float pf_score[4];
+  if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t p = lane * 4 + i;
+      pf_list[i] = p < a.nprobe ? a.probes[static_cast<uint64_t>(q) * a.nprobe + p] : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t p = lane * 4 + i;
+      pf_lo[i] = 0;
+      pf_len[i] = 0;
+      pf_score[i] = 0.0f;
+      if (p < a.nprobe) {
+        const uint32_t l = pf_list[i];
+        pf_lo[i] = static_cast<uint32_t>(a.off[l]);
+        pf_len[i] = static_cast<uint32_t>(a.off[l + 1]) - pf_lo[i];
+        pf_score[i] = a.scores[static_cast<uint64_t>(q) * a.nlist + l];
+      }
+    }
+  }
 
   // Per-query table (src/ivfpq_index.cc:309-318).
   if (ROT) {
@@ -1037,17 +1080,30 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
       s_lut[e] = v;
     }
   } else if (a.dsub == 4) {
-#pragma unroll 4
-    for (uint32_t e = tid; e < m * 256; e += kStreamThreads) {
-      const uint32_t j = e >> 8, c = e & 255u;
-      const float* cb = a.cbt + static_cast<uint64_t>(j) * 1024 + c;
-      const float* qj = qv + j * 4;
-      float v = 0.0f;
-      v = v + qj[0] * cb[0];
-      v = v + qj[1] * cb[256];
-      v = v + qj[2] * cb[512];
-      v = v + qj[3] * cb[768];
-      s_lut[e] = l2 ? v * -2.0f : v;
+    // Four adjacent columns c4..c4+3 of row j per lane and step: 16-byte codebook loads (a wave
+    // reads 1 KB of one row contiguously) and one 16-byte LDS store per four entries; each entry is
+    // summed over t in order, as before.
+#pragma unroll 2
+    for (uint32_t g = tid; g < m * 64; g += kStreamThreads) {
+      const uint32_t j = g >> 6, c4 = (g & 63u) * 4;
+      const float* cb = a.cbt + static_cast<uint64_t>(j) * 1024 + c4;
+      const float4 q4 = *reinterpret_cast<const float4*>(qv + j * 4);
+      const float4 b0 = *reinterpret_cast<const float4*>(cb);
+      const float4 b1 = *reinterpret_cast<const float4*>(cb + 256);
+      const float4 b2 = *reinterpret_cast<const float4*>(cb + 512);
+      const float4 b3 = *reinterpret_cast<const float4*>(cb + 768);
+      float4 v;
+      v.x = (((0.0f + q4.x * b0.x) + q4.y * b1.x) + q4.z * b2.x) + q4.w * b3.x;
+      v.y = (((0.0f + q4.x * b0.y) + q4.y * b1.y) + q4.z * b2.y) + q4.w * b3.y;
+      v.z = (((0.0f + q4.x * b0.z) + q4.y * b1.z) + q4.z * b2.z) + q4.w * b3.z;
+      v.w = (((0.0f + q4.x * b0.w) + q4.y * b1.w) + q4.z * b2.w) + q4.w * b3.w;
+      if (l2) {
+        v.x = v.x * -2.0f;
+        v.y = v.y * -2.0f;
+        v.z = v.z * -2.0f;
+        v.w = v.w * -2.0f;
+      }
+      *reinterpret_cast<float4*>(s_lut + j * 256 + c4) = v;
     }
   } else {
     for (uint32_t e = tid; e < m * 256; e += kStreamThreads) s_lut[e] = table_entry(qv, a.cbt, a.dsub, e >> 8, e & 255u, l2);
@@ -1057,19 +1113,15 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
   }
   // Probed lists: lengths, then flattened starts by a wave-wide scan (nprobe <= 256).
   if (wave == 0) {
-    uint32_t len[4], lo[4];
+    const uint32_t(&len)[4] = pf_len;
+    const uint32_t(&lo)[4] = pf_lo;
     uint32_t mine = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t p = lane * 4 + i;
-      len[i] = 0;
-      lo[i] = 0;
       if (p < a.nprobe) {
-        const uint32_t l = a.probes[static_cast<uint64_t>(q) * a.nprobe + p];
-        lo[i] = static_cast<uint32_t>(a.off[l]);
-        len[i] = static_cast<uint32_t>(a.off[l + 1]) - lo[i];
-        s_list[p] = l;
-        s_score[p] = a.scores[static_cast<uint64_t>(q) * a.nlist + l];
+        s_list[p] = pf_list[i];
+        s_score[p] = pf_score[i];
       }
       mine += len[i];
     }
@@ -1184,7 +1236,10 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
     if (cnt > flush_at) flush();
   };
 
+  // This block's slice [v_lo, v_hi) of the query's flattened probed positions.
   const uint32_t total = s_vstart[a.nprobe];
+  const uint32_t v_lo = split ? static_cast<uint32_t>(static_cast<uint64_t>(total) * part / a.parts) : 0u;
+  const uint32_t v_hi = split ? static_cast<uint32_t>(static_cast<uint64_t>(total) * (part + 1) / a.parts) : total;
   uint32_t p = 0;
   uint32_t vend = s_vstart[1];
   uint32_t base = s_base[0];
@@ -1200,7 +1255,7 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
 #pragma unroll
     for (int r = 0; r < kStreamCodes; ++r) {
       const uint32_t v = v0 + r * kStreamThreads + tid;
-      nok[r] = v < total;
+      nok[r] = v < v_hi;
       if (nok[r] && v >= vend) {
         do {
           ++p;
@@ -1222,8 +1277,8 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
   uint64_t stage[3];
 #pragma unroll
   for (int st = 0; st < 3; ++st) stage[st] = __ballot(((rot >> 2) >> st) & 1u);
-  if (total > 0) fetch(0);
-  for (uint32_t v0 = 0; v0 < total; v0 += kStreamThreads * kStreamCodes) {
+  if (v_lo < v_hi) fetch(v_lo);
+  for (uint32_t v0 = v_lo; v0 < v_hi; v0 += kStreamThreads * kStreamCodes) {
     uint32_t pos[kStreamCodes];
     float sc[kStreamCodes], t1v[kStreamCodes];
     bool ok[kStreamCodes];
@@ -1237,7 +1292,7 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
 #pragma unroll
       for (int i = 0; i < MPW; ++i) w[r][i] = nw[r][i];
     }
-    if (v0 + kStreamThreads * kStreamCodes < total) fetch(v0 + kStreamThreads * kStreamCodes);
+    if (v0 + kStreamThreads * kStreamCodes < v_hi) fetch(v0 + kStreamThreads * kStreamCodes);
     float dist[kStreamCodes];
     bool any = false;
     // The rotation as seen by this round: its table columns are recomputed per round (and shared by
@@ -1261,7 +1316,7 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
 #pragma unroll
       for (int r = 0; r < kStreamCodes; ++r) offer(ok[r], dist[r], pos[r]);
     }
-    if (v0 == 0) {
+    if (v0 == v_lo) {
       // Every wave cuts its first candidates and the block shares the tightest bound.
       flush();
       __syncthreads();
@@ -1272,7 +1327,145 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
       thr = ordered_to_float(shared_thr);
     }
   }
+  // Probe index of a position: eight probed lists tested per step (independent LDS reads).
+  auto list_of = [&](uint32_t pos) {
+    for (uint32_t b = 0; b + 1 < a.nprobe; b += 8) {
+      uint32_t hit = 0;
+#pragma unroll
+      for (uint32_t i = 0; i < 8; ++i) {
+        const uint32_t pl = b + i;
+        if (pl < a.nprobe && pos - (s_base[pl] + s_vstart[pl]) < s_vstart[pl + 1] - s_vstart[pl]) hit |= 1u << i;
+      }
+      if (hit) return b + static_cast<uint32_t>(__builtin_ctz(hit));
+    }
+    return a.nprobe - 1;
+  };
+  // Exact re-score of one approximate candidate (L2 with the precomputed table): the reference's
+  // table entry pre + qtab, summed in order of j, plus ||q - c||^2 (src/ivfpq_index.cc:334-346).
+  auto rescore = [&](uint64_t key) -> uint64_t {
+    const uint32_t pos = static_cast<uint32_t>(key);
+    const uint32_t pl = list_of(pos);
+    const float* pre = a.pre + static_cast<uint64_t>(s_list[pl]) * m * 256;
+    uint32_t wc[MPW];
+    load_code<MPW>(a.codes, pos, a.mp, wc);
+    // All 4 * MPW table loads go out together (rows past m re-read row m - 1 and are not added).
+    float pv[4 * MPW];
+#pragma unroll
+    for (int j = 0; j < 4 * MPW; ++j) {
+      const int jr = FULL ? j : min(j, static_cast<int>(m) - 1);
+      const uint32_t c = (wc[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+      pv[j] = pre[jr * 256 + c];
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4 * MPW; ++j) {
+      const uint32_t c = (wc[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+      if (FULL || j < static_cast<int>(m)) sum = sum + (pv[j] + s_lut[ROT ? c * kRows + j : j * 256 + c]);
+    }
+    float d = s_score[pl] + sum;
+    d = d == d ? d : __builtin_huge_valf();
+    return make_key(d, pos);
+  };
+  // Result j of the query: the list ref and distance of `key`, or an empty slot.
+  auto emit = [&](uint32_t j, bool full_slot, uint64_t key) {
+    uint64_t ref = QVH_EMPTY_REF;
+    float d = __builtin_huge_valf();
+    if (full_slot) {
+      const uint32_t pos = static_cast<uint32_t>(key);
+      const uint32_t pl = list_of(pos);
+      ref = (static_cast<uint64_t>(s_list[pl]) << 32) | (pos - (s_base[pl] + s_vstart[pl]));
+      d = ordered_to_float(static_cast<uint32_t>(key >> 32));
+    }
+    a.out_refs[static_cast<uint64_t>(q) * a.k + j] = ref;
+    a.out_dist[static_cast<uint64_t>(q) * a.k + j] = d;
+  };
   flush();
+  if constexpr (kStreamWaves == 4) {
+    // Single-wave finish (four waves, k and keep_sel <= 64): the four cut lists (<= CAP / 2 = 64
+    // keys each) are packed in LDS, then wave 0 alone sorts, re-scores and emits them in registers,
+    // with no further block barrier.
+    const uint64_t mine = static_cast<uint32_t>(lane) < cnt ? queue[lane] : ~0ull;
+    if (lane == 0) s_wcount[wave] = cnt;
+    __syncthreads();
+    uint32_t before = 0, merged = 0;
+#pragma unroll
+    for (int w2 = 0; w2 < kStreamWaves; ++w2) {
+      const uint32_t c = s_wcount[w2];
+      if (w2 < wave) before += c;
+      merged += c;
+    }
+    if (static_cast<uint32_t>(lane) < cnt) s_queue[before + lane] = mine;
+    __syncthreads();
+    if (wave != 0) return;
+    // The `count` smallest of the `total` (<= 256) keys packed at s_queue[0, total), ascending:
+    // key i sits in lane i of the result (count <= 64).
+    auto wave_smallest = [&](uint32_t total, uint32_t count) -> uint64_t {
+      uint64_t kk[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t e = i * 64 + lane;
+        kk[i] = e < total ? s_queue[e] : ~0ull;
+      }
+      if (total <= 64) {
+        uint64_t t[1] = {kk[0]};
+        wave_sort<1>(t);
+        kk[0] = t[0];
+      } else if (total <= 128) {
+        uint64_t t[2] = {kk[0], kk[1]};
+        wave_sort<2>(t);
+        kk[0] = t[0];
+      } else {
+        wave_sort<4>(kk);
+      }
+      return static_cast<uint32_t>(lane) < count ? kk[0] : ~0ull;
+    };
+    uint32_t cnt_f = min(merged, keep_sel);
+    uint64_t key = wave_smallest(merged, cnt_f);
+    if (l2) {
+      if (static_cast<uint32_t>(lane) < cnt_f) key = rescore(key);
+      uint64_t t[1] = {key};
+      wave_sort<1>(t);
+      key = t[0];
+      cnt_f = min(cnt_f, a.keep);
+    }
+    if (split) {
+      // The slice's best keep keys go out (device-scope atomic stores, which write through the
+      // per-XCD L2); once they have completed (s_waitcnt) the slice counts itself done, and the
+      // last slice of the query merges the lists (device-scope atomic loads).
+      const uint32_t tq = slot - a.nwhole;
+      uint64_t* lists = a.part_keys + static_cast<uint64_t>(tq) * a.parts * a.keep;
+      if (static_cast<uint32_t>(lane) < cnt_f) {
+        __hip_atomic_store(&lists[static_cast<uint64_t>(part) * a.keep + lane], key, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if (lane == 0) __hip_atomic_store(&a.part_cnt[tq * a.parts + part], cnt_f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_s_waitcnt(0);
+      uint32_t done = 0;
+      if (lane == 0) done = __hip_atomic_fetch_add(&a.part_done[tq], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__shfl(done, 0, 64) != a.parts - 1) return;
+      uint32_t all = 0;
+      for (uint32_t pi = 0; pi < a.parts; ++pi) {
+        const uint32_t c = __hip_atomic_load(&a.part_cnt[tq * a.parts + pi], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (uint32_t i = lane; i < c; i += 64) {
+          s_queue[all + i] = __hip_atomic_load(&lists[static_cast<uint64_t>(pi) * a.keep + i], __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+        all += c;
+      }
+      __builtin_amdgcn_wave_barrier();
+      cnt_f = min(all, a.keep);
+      key = wave_smallest(all, cnt_f);
+      if (lane == 0) __hip_atomic_store(&a.part_done[tq], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (a.refine) {
+      // Exact re-ranking needs the stored vectors: hand the candidates to the finishing kernel.
+      if (static_cast<uint32_t>(lane) < cnt_f) a.sel[static_cast<uint64_t>(q) * a.keep_sel + lane] = key;
+      if (lane == 0) a.sel_cnt[q] = cnt_f;
+      return;
+    }
+    if (static_cast<uint32_t>(lane) < a.k) emit(lane, static_cast<uint32_t>(lane) < min(cnt_f, a.k), key);
+    return;
+  }
   // The eight cut lists (<= CAP / 2 each) move to slots [wave * ks, wave * ks + ks) and are sorted
   // together; the first keep_sel keys are the scan's answer.
   uint64_t mine[QN];
@@ -1316,46 +1509,10 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
   __syncthreads();
   uint32_t cnt_f = min(merged, keep_sel);
 
-  // Probe index of a position: eight probed lists tested per step (independent LDS reads).
-  auto list_of = [&](uint32_t pos) {
-    for (uint32_t b = 0; b + 1 < a.nprobe; b += 8) {
-      uint32_t hit = 0;
-#pragma unroll
-      for (uint32_t i = 0; i < 8; ++i) {
-        const uint32_t pl = b + i;
-        if (pl < a.nprobe && pos - (s_base[pl] + s_vstart[pl]) < s_vstart[pl + 1] - s_vstart[pl]) hit |= 1u << i;
-      }
-      if (hit) return b + static_cast<uint32_t>(__builtin_ctz(hit));
-    }
-    return a.nprobe - 1;
-  };
   // Exact re-score of the approximate ranking (L2 with the precomputed table): the reference's
   // table entry pre + qtab, summed in order of j, plus ||q - c||^2 (src/ivfpq_index.cc:334-346).
   if (l2) {
-    if (static_cast<uint32_t>(tid) < cnt_f) {
-      const uint32_t pos = static_cast<uint32_t>(s_queue[tid]);
-      const uint32_t pl = list_of(pos);
-      const float* pre = a.pre + static_cast<uint64_t>(s_list[pl]) * m * 256;
-      uint32_t wc[MPW];
-      load_code<MPW>(a.codes, pos, a.mp, wc);
-      // All 4 * MPW table loads go out together (rows past m re-read row m - 1 and are not added).
-      float pv[4 * MPW];
-#pragma unroll
-      for (int j = 0; j < 4 * MPW; ++j) {
-        const int jr = FULL ? j : min(j, static_cast<int>(m) - 1);
-        const uint32_t c = (wc[j >> 2] >> (8 * (j & 3))) & 0xFFu;
-        pv[j] = pre[jr * 256 + c];
-      }
-      float sum = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 4 * MPW; ++j) {
-        const uint32_t c = (wc[j >> 2] >> (8 * (j & 3))) & 0xFFu;
-        if (FULL || j < static_cast<int>(m)) sum = sum + (pv[j] + s_lut[ROT ? c * kRows + j : j * 256 + c]);
-      }
-      float d = s_score[pl] + sum;
-      d = d == d ? d : __builtin_huge_valf();
-      s_queue[tid] = make_key(d, pos);
-    }
+    if (static_cast<uint32_t>(tid) < cnt_f) s_queue[tid] = rescore(s_queue[tid]);
     const uint32_t n2 = pow2_at_least(max(cnt_f, 2u));
     if (static_cast<uint32_t>(tid) >= cnt_f && static_cast<uint32_t>(tid) < n2) s_queue[tid] = ~0ull;
     for (uint32_t size = 2; size <= n2; size <<= 1) {
@@ -1376,6 +1533,57 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
     __syncthreads();
     cnt_f = min(cnt_f, a.keep);
   }
+  if (split) {
+    // A slice leaves its (at most keep) best keys; the last slice of the query to finish merges
+    // the lists (the best keep keys of the union are the best keep keys of the whole scan). The
+    // lists and counts move through device-scope atomic stores and loads, which write through and
+    // read past the per-XCD L2 caches; a slice's stores have completed (s_waitcnt) before its
+    // count goes up. No device-scope fence: one would write back or drop the XCD's whole L2.
+    const uint32_t tq = slot - a.nwhole;
+    uint64_t* lists = a.part_keys + static_cast<uint64_t>(tq) * a.parts * a.keep;
+    for (uint32_t i = tid; i < cnt_f; i += kStreamThreads) {
+      __hip_atomic_store(&lists[static_cast<uint64_t>(part) * a.keep + i], s_queue[i], __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (tid == 0) __hip_atomic_store(&a.part_cnt[tq * a.parts + part], cnt_f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+      const uint32_t before = __hip_atomic_fetch_add(&a.part_done[tq], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_wcount[0] = before == a.parts - 1 ? 1u : 0u;
+    }
+    __syncthreads();
+    if (s_wcount[0] == 0) return;
+    uint32_t all = 0;
+    for (uint32_t pi = 0; pi < a.parts; ++pi) {
+      const uint32_t c = __hip_atomic_load(&a.part_cnt[tq * a.parts + pi], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (uint32_t i = tid; i < c; i += kStreamThreads) {
+        s_queue[all + i] = __hip_atomic_load(&lists[static_cast<uint64_t>(pi) * a.keep + i], __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+      }
+      all += c;
+    }
+    const uint32_t n3 = pow2_at_least(max(all, 2u));
+    for (uint32_t i = all + tid; i < n3; i += kStreamThreads) s_queue[i] = ~0ull;
+    for (uint32_t size = 2; size <= n3; size <<= 1) {
+      for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+        __syncthreads();
+        for (uint32_t i = tid; i < n3 / 2; i += kStreamThreads) {
+          const uint32_t lo = 2 * i - (i & (stride - 1));
+          const uint32_t hi = lo + stride;
+          const bool up = (lo & size) == 0;
+          const uint64_t x = s_queue[lo], y = s_queue[hi];
+          if ((x > y) == up) {
+            s_queue[lo] = y;
+            s_queue[hi] = x;
+          }
+        }
+      }
+    }
+    __syncthreads();
+    cnt_f = min(all, a.keep);
+    if (tid == 0) __hip_atomic_store(&a.part_done[tq], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next search
+  }
   if (a.refine) {
     // Exact re-ranking needs the stored vectors: hand the candidates to the finishing kernel.
     for (uint32_t i = tid; i < cnt_f; i += kStreamThreads) a.sel[static_cast<uint64_t>(q) * a.keep_sel + i] = s_queue[i];
@@ -1383,19 +1591,7 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
     return;
   }
   const uint32_t nout = min(cnt_f, a.k);
-  for (uint32_t j = tid; j < a.k; j += kStreamThreads) {
-    uint64_t ref = QVH_EMPTY_REF;
-    float d = __builtin_huge_valf();
-    if (j < nout) {
-      const uint64_t key = s_queue[j];
-      const uint32_t pos = static_cast<uint32_t>(key);
-      const uint32_t pl = list_of(pos);
-      ref = (static_cast<uint64_t>(s_list[pl]) << 32) | (pos - (s_base[pl] + s_vstart[pl]));
-      d = ordered_to_float(static_cast<uint32_t>(key >> 32));
-    }
-    a.out_refs[static_cast<uint64_t>(q) * a.k + j] = ref;
-    a.out_dist[static_cast<uint64_t>(q) * a.k + j] = d;
-  }
+  for (uint32_t j = tid; j < a.k; j += kStreamThreads) emit(j, j < nout, s_queue[j < nout ? j : 0]);
 }
 
 // Up to 32 code bytes.
@@ -1545,12 +1741,19 @@ struct qvh_ivfpq {
   std::mutex mu;
   DeviceBuffer w_x, w_res, w_assign, w_codes, w_codes_p, w_t1, w_dest, w_shift;
   DeviceBuffer w_q, w_scores, w_probes, w_bits, w_refs, w_dist, w_bytes, w_sel, w_selcnt, w_key, w_order;
+  DeviceBuffer w_pkeys, w_pcnt, w_pdone;  // sliced queries of the streaming scan
+  int cus = 0;                             // compute units of the device
   int timing = 0;               // 0 off, 1 stage events, 2 events and probed code bytes
   bool timed = false, timed_bytes = false;
   hipEvent_t ev[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
 };
 
 namespace {
+
+__global__ void zero_u32_kernel(uint32_t* p, uint64_t n) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
 
 int ivf_mode(const qvh_ivfpq* h) {
   if (h->metric != QVH_METRIC_L2) return kModeIp;
@@ -1725,7 +1928,33 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
     auto launch2 = [&](auto kernel) {
       const void* fn = reinterpret_cast<const void*>(kernel);
       raise_lds(fn, lds2);
-      hipLaunchKernelGGL(kernel, grid, dim3(waves * 64), lds2, s, a);
+      // Sliced queries: a batch smaller than one resident generation of blocks would leave CUs
+      // idle, so each of its queries is scanned in up to kMaxSlices slices (as many as fit in one
+      // generation), merged by the slice that finishes last. Larger batches scan whole queries:
+      // slicing their last generation measured no faster at 10k queries and slower at 2k.
+      int per_cu = 0;
+      QVH_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, static_cast<int>(waves * 64), lds2));
+      const uint64_t resident = static_cast<uint64_t>(std::max(per_cu, 0)) * static_cast<uint64_t>(std::max(h->cus, 0));
+      uint64_t parts = resident > nq ? std::min<uint64_t>(kMaxSlices, resident / nq) : 1;
+      uint64_t sliced = nq;
+      // The merging block holds parts * keep keys: in one wave's registers (256) or in the queues.
+      const uint64_t cap_keys = small_sel ? 256u : waves * 256u;
+      while (parts > 1 && parts * a.keep > cap_keys) --parts;
+      if (parts <= 1 || a.keep == 0) sliced = 0;
+      a.nwhole = static_cast<uint32_t>(nq - sliced);
+      a.parts = sliced ? static_cast<uint32_t>(parts) : 1u;
+      if (sliced) {
+        a.part_keys = static_cast<uint64_t*>(h->w_pkeys.reserve(sliced * parts * a.keep * sizeof(uint64_t)));
+        a.part_cnt = static_cast<uint32_t*>(h->w_pcnt.reserve(sliced * parts * sizeof(uint32_t)));
+        const size_t had = h->w_pdone.bytes;
+        a.part_done = static_cast<uint32_t*>(h->w_pdone.reserve(sliced * sizeof(uint32_t)));
+        if (h->w_pdone.bytes != had) {  // fresh counters start at zero; the merging block resets them
+          const uint64_t n = h->w_pdone.bytes / sizeof(uint32_t);
+          hipLaunchKernelGGL(zero_u32_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, s, a.part_done, n);
+        }
+      }
+      const dim3 sgrid(static_cast<unsigned>(a.nwhole + sliced * a.parts));
+      hipLaunchKernelGGL(kernel, sgrid, dim3(waves * 64), lds2, s, a);
     };
 #define QVH_STREAM(MPW_)                                                                                  \
   (full ? (small_sel ? launch2(ivf_stream_kernel<MPW_, true, 128>) : launch2(ivf_stream_kernel<MPW_, true, 256>)) \
@@ -1807,6 +2036,7 @@ qvh_status qvh_ivfpq_create(uint32_t dim, int metric, uint32_t nlist, uint32_t m
     h->mp = (m + 3) / 4 * 4;
     h->store_vectors = store_vectors;
     h->device = dev;
+    if (hipDeviceGetAttribute(&h->cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) h->cus = 0;
     h->h_off.assign(nlist + 1, 0);
     const hipError_t e = hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking);
     if (e != hipSuccess) {

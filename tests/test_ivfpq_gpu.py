@@ -82,6 +82,20 @@ def test_ivfpq_small_matches_oracle(oracle, metric, store, refine):
         print(compare_search(oracle, idx, st, q, 10, nprobe, refine))
 
 
+@pytest.mark.parametrize("metric,refine", [("l2", 0), ("l2", 8), ("ip", 0), ("cosine", 2)])
+def test_ivfpq_batch_sizes_and_slices(oracle, metric, refine):
+    """Batches below one resident generation of blocks scan each query in slices merged by the last
+    one to finish (1 query, 300); larger ones scan whole queries (6000). refine 8 keeps 80
+    candidates: the eight-wave kernel and its block merge; the others take the single-wave finish."""
+    base = clustered(10_000, 32, 50, 12)
+    idx, st = build_pair(oracle, base, metric, 64, 16, metric != "ip")
+    for nq in (1, 300, 6_000):
+        q = clustered(nq, 32, 50, 13 + nq)
+        print(nq, compare_search(oracle, idx, st, q, 10, 16, refine))
+    allowed = np.arange(0, 10_000, 3, dtype=np.uint64)
+    print("filtered", compare_search(oracle, idx, st, clustered(6_000, 32, 50, 14), 10, 16, refine, allowed))
+
+
 def test_ivfpq_filter_matches_oracle(oracle):
     base = clustered(8_000, 16, 30, 8)
     q = clustered(60, 16, 30, 9)
