@@ -16,8 +16,11 @@
  *
  * "Host" entry points take host buffers and return after the results are in host memory.
  * "_device" entry points take device pointers and enqueue on `stream` (NULL = the handle's own
- * stream) without synchronizing. Calls on one handle are serialized internally; distinct
- * handles may be used from distinct threads concurrently.
+ * stream) without synchronizing. Calls on one handle are serialized internally, and on the device
+ * too: a call on another stream first waits for the handle's earlier work, and the handle's stream
+ * then waits for it, so later calls (and qvh_*_sync) are ordered after it. Distinct handles may be
+ * used from distinct threads concurrently. Buffers the library regrows or releases are freed
+ * only after the device is idle.
  */
 #ifndef QVH_H_
 #define QVH_H_
@@ -110,7 +113,7 @@ qvh_status qvh_flat_search_device(qvh_flat* flat, const float* d_queries, uint64
                                   uint32_t k, const uint64_t* d_row_bitmap, uint32_t* d_out_rows,
                                   float* d_out_dist, void* stream);
 
-/* Synchronizes the handle's stream. */
+/* Waits for all work enqueued on the handle (its stream, which every call joins). */
 qvh_status qvh_flat_sync(qvh_flat* flat);
 
 /* Measurement hook (no counterpart in the reference): when enabled, each search records HIP

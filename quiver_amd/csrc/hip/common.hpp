@@ -89,6 +89,30 @@ struct DeviceBuffer {
   T* as() const { return static_cast<T*>(ptr); }
 };
 
+/// Enqueues `enqueue(s)` as part of a handle's timeline `own`. On another stream s, s first waits
+/// for the work already on `own`, and `own` then waits for what was enqueued on s: a handle's
+/// operations (which share its workspace) run on the device in call order whatever streams they
+/// use, and synchronizing `own` covers them all.
+template <class F>
+void on_handle_timeline(hipStream_t own, hipEvent_t& join, hipStream_t s, F&& enqueue) {
+  if (s == own) {
+    enqueue(s);
+    return;
+  }
+  if (!join) QVH_HIP(hipEventCreateWithFlags(&join, hipEventDisableTiming));
+  QVH_HIP(hipEventRecord(join, own));
+  QVH_HIP(hipStreamWaitEvent(s, join, 0));
+  try {
+    enqueue(s);
+  } catch (...) {
+    (void)hipEventRecord(join, s);
+    (void)hipStreamWaitEvent(own, join, 0);
+    throw;
+  }
+  QVH_HIP(hipEventRecord(join, s));
+  QVH_HIP(hipStreamWaitEvent(own, join, 0));
+}
+
 __host__ __device__ inline uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 
 // ---- device utilities ------------------------------------------------------------------------

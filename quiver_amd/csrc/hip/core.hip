@@ -75,7 +75,12 @@ void* device_alloc(size_t bytes) {
 }
 
 void device_free(void* p) noexcept {
-  if (p) (void)hipFree(p);
+  // Asynchronous work of any stream may still read a buffer that is regrown or released: the
+  // device finishes it first.
+  if (p) {
+    (void)hipDeviceSynchronize();
+    (void)hipFree(p);
+  }
 }
 
 void launch_normalize_rows(float* d_rows, uint64_t n, uint32_t dim, hipStream_t stream) {

@@ -650,6 +650,7 @@ struct qvh_flat {
   bool timing = false;
   bool timed = false;
   hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
+  hipEvent_t join = nullptr;  // orders calls on other streams into the handle's stream
   uint64_t last_nsplit = 0;
 };
 
@@ -840,6 +841,7 @@ void qvh_flat_destroy(qvh_flat* f) {
   for (hipEvent_t& e : f->ev) {
     if (e) (void)hipEventDestroy(e);
   }
+  if (f->join) (void)hipEventDestroy(f->join);
   delete f;
 }
 
@@ -997,7 +999,9 @@ qvh_status qvh_flat_search_device(qvh_flat* f, const float* d_queries, uint64_t 
     std::lock_guard<std::mutex> lock(f->mu);
     QVH_HIP(hipSetDevice(f->device));
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : f->stream;
-    flat_search_impl(f, d_queries, nq, k, d_row_bitmap, d_out_rows, d_out_dist, s);
+    on_handle_timeline(f->stream, f->join, s, [&](hipStream_t st) {
+      flat_search_impl(f, d_queries, nq, k, d_row_bitmap, d_out_rows, d_out_dist, st);
+    });
   });
 }
 

@@ -1746,6 +1746,7 @@ struct qvh_ivfpq {
   int timing = 0;               // 0 off, 1 stage events, 2 events and probed code bytes
   bool timed = false, timed_bytes = false;
   hipEvent_t ev[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
+  hipEvent_t join = nullptr;  // orders calls on other streams into the handle's stream
 };
 
 namespace {
@@ -2065,6 +2066,7 @@ void qvh_ivfpq_destroy(qvh_ivfpq* h) {
   for (hipEvent_t& e : h->ev) {
     if (e) (void)hipEventDestroy(e);
   }
+  if (h->join) (void)hipEventDestroy(h->join);
   delete h;
 }
 
@@ -2364,7 +2366,9 @@ qvh_status qvh_ivfpq_search_device(qvh_ivfpq* h, const float* d_queries, uint64_
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : h->stream;
     h->timed = h->timing > 0;
     h->timed_bytes = h->timing > 1;
-    ivf_search_impl(h, d_queries, nq, k, nprobe, refine_factor, d_pos_bitmap, d_out_refs, d_out_dist, s);
+    on_handle_timeline(h->stream, h->join, s, [&](hipStream_t st) {
+      ivf_search_impl(h, d_queries, nq, k, nprobe, refine_factor, d_pos_bitmap, d_out_refs, d_out_dist, st);
+    });
   });
 }
 

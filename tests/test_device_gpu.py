@@ -120,3 +120,36 @@ def test_ivfpq_device_untrained_and_growing():
     _same(idx.search(hq, 5, nprobe=8), idx.search(qd, 5, nprobe=8))
     idx.add(base[1_000:])  # the cached CSR tables follow the index
     _same(idx.search(hq, 5, nprobe=8), idx.search(qd, 5, nprobe=8))
+
+
+@pytest.mark.parametrize("kind", ["flat", "ivfpq"])
+def test_calls_on_two_streams_share_the_handle_safely(kind):
+    """Device searches of one handle on two streams, the second growing the handle's workspace,
+    then a host search: each call is ordered after the handle's earlier work on the device, so
+    every result equals the host path's."""
+    dev = _gpu()
+    base, _ = _data(30_000, 32, 1, 6)
+    rng = np.random.default_rng(7)
+    qa = rng.standard_normal((300, 32)).astype(np.float32)
+    qb = rng.standard_normal((6_000, 32)).astype(np.float32)
+    print(f"case: two streams {kind}", flush=True)
+    if kind == "flat":
+        idx = quiver.FlatIndex(32, "l2")
+        idx.add(base)
+        search = lambda q: idx.search(q, 10)  # noqa: E731
+    else:
+        idx = quiver.IvfPqIndex(32, "l2", nlist=64, m=8, train_iterations=4)
+        idx.train(base)
+        idx.add(base)
+        search = lambda q: idx.search(q, 10, nprobe=16)  # noqa: E731
+    want_a, want_b = search(qa), search(qb)
+    s1, s2 = torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(s1):
+        got_a = search(torch.from_numpy(qa).to(dev))
+    with torch.cuda.stream(s2):
+        got_b = search(torch.from_numpy(qb).to(dev))
+    again_a = search(qa)  # host call on the handle's own stream
+    torch.cuda.synchronize(dev)
+    _same(want_a, got_a)
+    _same(want_b, got_b)
+    assert np.array_equal(want_a[0], again_a[0])
