@@ -912,6 +912,35 @@ __device__ __forceinline__ void wave_sort(uint64_t (&k)[N]) {
   }
 }
 
+/// Ascending sort of a bitonic sequence of N * 64 keys held by one wave (element e = i * 64 + lane
+/// in k[i]): the last merge stage of the bitonic sort.
+template <int N>
+__device__ __forceinline__ void wave_merge(uint64_t (&k)[N]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int stride = N * 32; stride > 0; stride >>= 1) {
+    if (stride >= 64) {
+      const int is = stride / 64;
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const int j = i ^ is;
+        if (j > i) {
+          const uint64_t x = k[i], y = k[j];
+          k[i] = x < y ? x : y;
+          k[j] = x < y ? y : x;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const uint64_t other = __shfl_xor(k[i], stride, 64);
+        const bool lower = (lane & stride) == 0;
+        k[i] = lower ? (other < k[i] ? other : k[i]) : (other > k[i] ? other : k[i]);
+      }
+    }
+  }
+}
+
 /// Key at sorted position e (wave-uniform) of a wave-sorted register array.
 template <int N>
 __device__ __forceinline__ uint64_t wave_key_at(const uint64_t (&k)[N], uint32_t e) {
@@ -1379,8 +1408,11 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
     a.out_refs[static_cast<uint64_t>(q) * a.k + j] = ref;
     a.out_dist[static_cast<uint64_t>(q) * a.k + j] = d;
   };
-  flush();
+  // Eight-wave blocks skip the final cut: every wave list holds at most CAP / 2 keys here, and a key
+  // a cut would drop has keep_sel better ones in its own list. Four-wave blocks cut, which keeps
+  // wave 0's sort below at <= 4 keep_sel keys.
   if constexpr (kStreamWaves == 4) {
+    flush();
     // Single-wave finish (four waves, k and keep_sel <= 64): the four cut lists (<= CAP / 2 = 64
     // keys each) are packed in LDS, then wave 0 alone sorts, re-scores and emits them in registers,
     // with no further block barrier.
@@ -1466,47 +1498,36 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
     if (static_cast<uint32_t>(lane) < a.k) emit(lane, static_cast<uint32_t>(lane) < min(cnt_f, a.k), key);
     return;
   }
-  // The eight cut lists (<= CAP / 2 each) move to slots [wave * ks, wave * ks + ks) and are sorted
-  // together; the first keep_sel keys are the scan's answer.
-  uint64_t mine[QN];
-#pragma unroll
-  for (int i = 0; i < QN; ++i) {
-    const uint32_t e = i * 64 + lane;
-    mine[i] = e < cnt ? queue[e] : ~0ull;
-  }
+  // Eight waves (keep_sel <= 128): each wave sorts its list (<= CAP / 2 = 128 keys) in registers;
+  // three rounds of pairwise merges then keep the 128 smallest: the elementwise minimum of one
+  // sorted list and the other reversed holds the 128 smallest of both as a bitonic sequence, which
+  // a register bitonic merge orders. Wave 0's region ends with the block's 128 smallest, sorted.
+  // (Four-wave blocks returned above; this is compiled for them too but never reached.)
+  uint32_t merged = 0;
+  if constexpr (kStreamWaves == 8 && CAP == 256) {
+  uint64_t mine[2] = {static_cast<uint32_t>(lane) < cnt ? queue[lane] : ~0ull,
+                      static_cast<uint32_t>(lane) + 64 < cnt ? queue[64 + lane] : ~0ull};
+  wave_sort<2>(mine);
+  queue[lane] = mine[0];
+  queue[64 + lane] = mine[1];
   if (lane == 0) s_wcount[wave] = cnt;
   __syncthreads();
-  uint32_t most = 0, merged = 0;
 #pragma unroll
-  for (int w2 = 0; w2 < kStreamWaves; ++w2) {
-    most = max(most, s_wcount[w2]);
-    merged += s_wcount[w2];
-  }
-  const uint32_t ks = pow2_at_least(max(most, 1u));
-  constexpr uint32_t kWavesPow2 = kStreamWaves <= 4 ? 4 : kStreamWaves <= 8 ? 8 : 16;
+  for (int w2 = 0; w2 < kStreamWaves; ++w2) merged += s_wcount[w2];
 #pragma unroll
-  for (int i = 0; i < QN; ++i) {
-    const uint32_t e = i * 64 + lane;
-    if (e < ks) s_queue[wave * ks + e] = mine[i];
-  }
-  for (uint32_t e = kStreamWaves * ks + tid; e < kWavesPow2 * ks; e += kStreamThreads) s_queue[e] = ~0ull;
-  const uint32_t n = kWavesPow2 * ks;
-  for (uint32_t size = 2; size <= n; size <<= 1) {
-    for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-      __syncthreads();
-      for (uint32_t i = tid; i < n / 2; i += kStreamThreads) {
-        const uint32_t lo = 2 * i - (i & (stride - 1));
-        const uint32_t hi = lo + stride;
-        const bool up = (lo & size) == 0;
-        const uint64_t x = s_queue[lo], y = s_queue[hi];
-        if ((x > y) == up) {
-          s_queue[lo] = y;
-          s_queue[hi] = x;
-        }
-      }
+  for (int step = 1; step < kStreamWaves; step *= 2) {
+    if (wave % (2 * step) == 0) {
+      const uint64_t* other = s_queue + (wave + step) * CAP;
+      const uint64_t o0 = other[127 - lane], o1 = other[63 - lane];
+      mine[0] = o0 < mine[0] ? o0 : mine[0];
+      mine[1] = o1 < mine[1] ? o1 : mine[1];
+      wave_merge<2>(mine);
+      queue[lane] = mine[0];
+      queue[64 + lane] = mine[1];
     }
+    __syncthreads();
   }
-  __syncthreads();
+  }
   uint32_t cnt_f = min(merged, keep_sel);
 
   // Exact re-score of the approximate ranking (L2 with the precomputed table): the reference's
