@@ -737,10 +737,12 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
   const uint64_t scan_rows = d_idx ? n_idx : f->n;
   const uint64_t tiles = std::max<uint64_t>(1, ceil_div(scan_rows, kTileRows));
   // One workgroup per CU at a time: pick the split count (a multiple of 8 for the XCD mapping)
-  // whose workgroup count best fills whole rounds of the CUs; fewer splits on ties.
+  // whose workgroup count best fills whole rounds of the CUs; fewer splits on ties. A split keeps
+  // at least four tiles: with fewer rows per split the per-split top-k lists take in most rows
+  // (1.18M x 100 cosine with 0.5% of the ids allowed: 32 splits 0.47 ms, 16 splits 0.37 ms).
   uint64_t nsplit = 1;
   {
-    const uint64_t cap = std::min<uint64_t>(tiles, kMaxSplits);
+    const uint64_t cap = std::max<uint64_t>(1, std::min<uint64_t>(tiles / 4, kMaxSplits));
     double best = -1.0;
     for (uint64_t c = 1; c <= cap; c = c < 8 ? c + 1 : c + 8) {
       if (c >= 8 && c % 8) continue;
