@@ -534,6 +534,7 @@ struct ScanArgs {
   const uint64_t* bitmap;  // admitted positions, or null
   uint32_t keep, keep_sel;
   int refine;
+  int exact_all;  // block-buffer scan: exact distances of every probed vector (saturated refine)
   uint64_t* out_refs;
   float* out_dist;
   uint64_t* sel;      // [nq][keep_sel] streaming scan -> finishing kernel
@@ -666,7 +667,7 @@ __global__ void __launch_bounds__(kScanThreads) ivf_scan_kernel(ScanArgs a) {
   const uint32_t table = a.m * 256;
 
   // Per-query table (src/ivfpq_index.cc:309-318): <q_j, C_{j,c}> in order of t, times -2 for L2.
-  if (a.mode != kModeResidual) {
+  if (a.mode != kModeResidual && !a.exact_all) {
     for (uint32_t e = tid; e < table; e += kScanThreads) {
       const uint32_t j = e / 256, c = e % 256;
       const float* cb = a.cbt + static_cast<uint64_t>(j) * a.dsub * 256 + c;
@@ -715,7 +716,7 @@ __global__ void __launch_bounds__(kScanThreads) ivf_scan_kernel(ScanArgs a) {
     }
   };
 
-  if (a.mode != kModeResidual) {
+  if (a.mode != kModeResidual || a.exact_all) {
     // All probed lists as one sequence, dealt round-robin to the threads.
     const uint64_t total = s_pstart[a.nprobe];
     uint32_t p = 0;
@@ -728,6 +729,12 @@ __global__ void __launch_bounds__(kScanThreads) ivf_scan_kernel(ScanArgs a) {
           const uint32_t l = s_plist[p];
           const uint64_t pos = a.off[l] + (v - s_pstart[p]);
           if (!a.bitmap || ((a.bitmap[pos >> 6] >> (pos & 63)) & 1ull)) {
+            if (a.exact_all) {
+              // Refine over every stored vector: the re-ranking distance of the refine step.
+              const float* x = a.vec + pos * a.dim;
+              offer(a.mode == kModeIp ? 1.0f - exact_dot(qv, x, a.dim) : exact_l2sqr(qv, x, a.dim), pos);
+              continue;
+            }
             uint32_t w[MPW];
             load_code<MPW>(a.codes, pos, a.mp, w);
             const float s = adc_sum<MPW>(s_lut, w, a.m);
@@ -795,7 +802,7 @@ __global__ void __launch_bounds__(kScanThreads) ivf_scan_kernel(ScanArgs a) {
 
   // Exact re-score of the approximate ranking (L2 with the precomputed table): the reference's
   // table entry pre + qtab, summed in order of j, plus ||q - c||^2 (src/ivfpq_index.cc:334-346).
-  if (a.mode == kModePre) {
+  if (a.mode == kModePre && !a.exact_all) {
     for (uint32_t i = tid; i < cnt; i += kScanThreads) {
       const uint32_t pos = static_cast<uint32_t>(s_cand[i]);
       const uint32_t l = list_pos(pos);
@@ -1834,6 +1841,15 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   const int mode = ivf_mode(h);
   uint64_t keep_sel = keep;
   if (mode == kModePre) keep_sel = std::min<uint64_t>(count, keep + std::max<uint64_t>(16, keep / 2));
+  // Refine over every stored vector (k * refine_factor at or past the count): the ADC stage keeps
+  // every probed candidate, so the answer is the exact top-k of the probed, admitted vectors, which
+  // the block-buffer scan computes directly (src/ivfpq_index.cc:303-308,362-373).
+  bool exact_all = false;
+  if (keep_sel > kMaxKeepSel && refine && keep == count) {
+    exact_all = true;
+    keep = std::min<uint64_t>(k, count);
+    keep_sel = keep;
+  }
   if (keep_sel > kMaxKeepSel) {
     throw Failure(QVH_EUNSUPPORTED, "IVF-PQ search: k * refine_factor above " + std::to_string(kMaxKeepSel) +
                                         " candidates is not supported on the device path yet");
@@ -1911,7 +1927,8 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   a.bitmap = d_bitmap;
   a.keep = static_cast<uint32_t>(keep);
   a.keep_sel = static_cast<uint32_t>(keep_sel);
-  a.refine = refine ? 1 : 0;
+  a.refine = refine && !exact_all ? 1 : 0;
+  a.exact_all = exact_all ? 1 : 0;
   a.out_refs = d_refs;
   a.out_dist = d_dist;
   const size_t lds = kCandCap * sizeof(uint64_t) + (nprobe + 1) * sizeof(uint64_t) +
@@ -1942,7 +1959,7 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   const size_t lds_total = lds_table + waves * (small_sel ? 128 : 256) * sizeof(uint64_t) +
                            (4 * static_cast<size_t>(nprobe) + 2 + waves) * sizeof(uint32_t);
   const size_t lds2 = mpw_t > 8 ? lds_total : lds_total - lds_table;
-  if (mode != kModeResidual && h->mp <= kStreamMaxM && nprobe <= kStreamMaxProbes && a.keep_sel >= 1 &&
+  if (!exact_all && mode != kModeResidual && h->mp <= kStreamMaxM && nprobe <= kStreamMaxProbes && a.keep_sel >= 1 &&
       a.keep_sel <= kStreamMaxSel && k <= kStreamMaxSel && lds_total <= 150 * 1024) {
     a.sel = static_cast<uint64_t*>(h->w_sel.reserve(nq * a.keep_sel * sizeof(uint64_t)));
     a.sel_cnt = static_cast<uint32_t*>(h->w_selcnt.reserve(nq * sizeof(uint32_t)));

@@ -96,6 +96,24 @@ def test_ivfpq_batch_sizes_and_slices(oracle, metric, refine):
     print("filtered", compare_search(oracle, idx, st, clustered(6_000, 32, 50, 14), 10, 16, refine, allowed))
 
 
+@pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
+def test_ivfpq_saturated_refine(oracle, metric):
+    """refine_factor 2^63: k * refine_factor wraps, the reference saturates it at the stored count and
+    re-ranks every probed vector exactly (tests/test_regressions.cc:101-118); past the device path's
+    candidate buffer this runs as an exact scan of the probed lists."""
+    base = clustered(2_000, 8, 10, 21)
+    idx, st = build_pair(oracle, base, metric, 16, 4, True)
+    q = base[:50]
+    for nprobe in (4, 16):
+        for k in (2, 10):
+            print(nprobe, k, compare_search(oracle, idx, st, q, k, nprobe, 1 << 63))
+    labels, _ = idx.search(base[:1], 2, nprobe=16, refine_factor=1 << 63)
+    if metric == "l2":
+        assert labels[0, 0] == 0  # refine over everything is exact
+    allowed = np.arange(0, 2_000, 3, dtype=np.uint64)
+    print("filtered", compare_search(oracle, idx, st, q, 10, 16, 1 << 63, allowed))
+
+
 def test_ivfpq_filter_matches_oracle(oracle):
     base = clustered(8_000, 16, 30, 8)
     q = clustered(60, 16, 30, 9)
