@@ -5,6 +5,7 @@
 * ``quiver_amd/lib/libqvh.so``        - HIP kernels + the qvh C-ABI (include/qvh.h), gfx950 only
 * ``quiver_amd/lib/libquiver_amd.so`` - the C++ API (quiver::FlatIndex, ...) over the C-ABI
 * ``quiver_amd/_quiver*.so``          - the pybind11 module under quiver_amd/__init__.py
+* ``tests/cpp/test_cpp_api``          - the C++ API test program (run by tests/test_cpp_api_gpu.py)
 
 Every HIP source is compiled with -ffp-contract=off (fused multiply-adds only where the source
 writes fmaf(), as the bit-exact paths require) and without packed-FP32 instructions.
@@ -99,10 +100,20 @@ def build_python() -> str:
     return out
 
 
+def build_cpp_tests() -> str:
+    src = os.path.join(ROOT, "tests", "cpp", "test_cpp_api.cc")
+    out = os.path.join(ROOT, "tests", "cpp", "test_cpp_api")
+    _run(["g++", *CXX_FLAGS, src, f"-L{LIB}", "-lquiver_amd", "-lqvh", f"-Wl,-rpath,{LIB}",
+          "-Wl,-rpath,$ORIGIN/../../quiver_amd/lib", "-o", out + ".tmp"])
+    os.replace(out + ".tmp", out)
+    return out
+
+
 def build(jobs: int = 8) -> None:
     build_hip(jobs)
     build_host()
     build_python()
+    build_cpp_tests()
 
 
 if __name__ == "__main__":

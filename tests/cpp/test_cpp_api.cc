@@ -1,0 +1,258 @@
+// The public C++ API (quiver/flat_index.h, quiver/ivfpq_index.h) driven the way a C++ caller of the
+// reference drives it: the behaviours its tests check for the flat and IVF-PQ indexes
+// (tests/test_flat.cc, tests/test_quantizer.cc, tests/test_regressions.cc), compiled against this
+// package's headers and run on the GPU. Prints one line per case and exits non-zero on a failure.
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <filesystem>
+#include <functional>
+#include <random>
+#include <string>
+#include <unordered_set>
+#include <vector>
+
+#include "quiver/common.h"
+#include "quiver/filter.h"
+#include "quiver/flat_index.h"
+#include "quiver/ivfpq_index.h"
+
+namespace {
+
+int g_failures = 0;
+
+#define EXPECT(cond)                                                           \
+  do {                                                                         \
+    if (!(cond)) {                                                             \
+      std::printf("    expectation failed: %s (line %d)\n", #cond, __LINE__); \
+      ++g_failures;                                                            \
+    }                                                                          \
+  } while (0)
+
+template <class F>
+bool throws_error(F&& f) {
+  try {
+    f();
+  } catch (const quiver::Error&) {
+    return true;
+  }
+  return false;
+}
+
+std::vector<float> normal_vectors(std::size_t n, std::size_t dim, std::uint64_t seed) {
+  std::mt19937_64 rng(seed);
+  std::normal_distribution<float> unit(0.0f, 1.0f);
+  std::vector<float> v(n * dim);
+  for (float& x : v) x = unit(rng);
+  return v;
+}
+
+std::vector<float> blob_vectors(std::size_t n, std::size_t dim, std::size_t clusters, std::uint64_t seed) {
+  std::mt19937_64 crng(4242 + clusters), rng(seed);
+  std::normal_distribution<float> unit(0.0f, 1.0f);
+  std::vector<float> centers(clusters * dim);
+  for (float& x : centers) x = 3.0f * unit(crng);
+  std::uniform_int_distribution<std::size_t> pick(0, clusters - 1);
+  std::vector<float> v(n * dim);
+  for (std::size_t i = 0; i < n; ++i) {
+    const std::size_t c = pick(rng);
+    for (std::size_t j = 0; j < dim; ++j) v[i * dim + j] = centers[c * dim + j] + unit(rng);
+  }
+  return v;
+}
+
+// The k nearest rows by squared L2 distance in double precision.
+std::vector<std::size_t> brute_force(const std::vector<float>& base, const float* q, std::size_t dim,
+                                     std::size_t k) {
+  const std::size_t n = base.size() / dim;
+  std::vector<std::pair<double, std::size_t>> d(n);
+  for (std::size_t i = 0; i < n; ++i) {
+    double s = 0;
+    for (std::size_t j = 0; j < dim; ++j) {
+      const double t = static_cast<double>(q[j]) - base[i * dim + j];
+      s += t * t;
+    }
+    d[i] = {s, i};
+  }
+  std::partial_sort(d.begin(), d.begin() + static_cast<std::ptrdiff_t>(k), d.end());
+  std::vector<std::size_t> out(k);
+  for (std::size_t i = 0; i < k; ++i) out[i] = d[i].second;
+  return out;
+}
+
+double recall(const std::vector<std::size_t>& truth, const std::vector<quiver::Neighbor>& got) {
+  std::unordered_set<std::size_t> t(truth.begin(), truth.end());
+  std::size_t hit = 0;
+  for (const auto& nb : got) hit += t.count(static_cast<std::size_t>(nb.label));
+  return static_cast<double>(hit) / static_cast<double>(truth.size());
+}
+
+void flat_matches_brute_force() {
+  const std::size_t dim = 16, n = 2000, k = 10;
+  const auto base = normal_vectors(n, dim, 1);
+  const auto queries = normal_vectors(20, dim, 2);
+  quiver::FlatIndex index(dim);
+  index.add(base.data(), n);
+  EXPECT(index.size() == n);
+  for (std::size_t i = 0; i < 20; ++i) {
+    const auto r = index.search(queries.data() + i * dim, k);
+    EXPECT(r.size() == k);
+    const auto truth = brute_force(base, queries.data() + i * dim, dim, k);
+    for (std::size_t j = 0; j < k && j < r.size(); ++j) EXPECT(r[j].label == truth[j]);
+    EXPECT(std::is_sorted(r.begin(), r.end()));
+  }
+  // The batched call returns the same rows.
+  std::vector<quiver::Label> labels(20 * k);
+  std::vector<float> dist(20 * k);
+  index.search_batch(queries.data(), 20, k, labels.data(), dist.data());
+  for (std::size_t i = 0; i < 20; ++i) {
+    const auto r = index.search(queries.data() + i * dim, k);
+    for (std::size_t j = 0; j < k; ++j) EXPECT(labels[i * k + j] == r[j].label && dist[i * k + j] == r[j].distance);
+  }
+}
+
+void flat_cosine_and_inner_product() {
+  const std::size_t dim = 8, n = 500;
+  auto base = normal_vectors(n, dim, 3);
+  for (const auto metric : {quiver::Metric::kCosine, quiver::Metric::kInnerProduct}) {
+    quiver::FlatIndex index(dim, metric);
+    index.add(base.data(), n);
+    std::vector<float> q(base.begin() + 7 * dim, base.begin() + 8 * dim);
+    if (metric == quiver::Metric::kCosine) {
+      for (float& x : q) x *= 3.0f;  // the same direction: distance 0 to row 7
+      const auto r = index.search(q.data(), 1);
+      EXPECT(r.size() == 1 && r[0].label == 7 && std::fabs(r[0].distance) < 1e-5f);
+    } else {
+      const auto r = index.search(q.data(), 5);
+      EXPECT(r.size() == 5 && std::is_sorted(r.begin(), r.end()));
+    }
+  }
+}
+
+void flat_fewer_than_k_and_filters() {
+  const std::size_t dim = 4;
+  const auto base = normal_vectors(5, dim, 4);
+  quiver::FlatIndex index(dim);
+  const quiver::Label labels[5] = {10, 11, 12, 13, 14};
+  index.add(base.data(), 5, labels);
+  EXPECT(index.search(base.data(), 10).size() == 5);
+  const quiver::LabelSetFilter only{11, 13};
+  const auto r = index.search(base.data(), 10, &only);
+  EXPECT(r.size() == 2);
+  for (const auto& nb : r) EXPECT(nb.label == 11 || nb.label == 13);
+  std::vector<quiver::Label> out(10);
+  std::vector<float> dist(10);
+  index.search_batch(base.data(), 1, 10, out.data(), dist.data(), &only);
+  EXPECT(out[2] == quiver::kInvalidLabel && std::isinf(dist[2]));
+  const quiver::Label sentinel = quiver::kInvalidLabel;
+  EXPECT(throws_error([&] { index.add(base.data(), 1, &sentinel); }));
+  std::vector<float> bad(dim, 1.0f);
+  bad[1] = std::nanf("");
+  EXPECT(throws_error([&] { index.add(bad.data(), 1); }));
+}
+
+void flat_save_load(const std::string& dir) {
+  const std::size_t dim = 12, n = 300;
+  const auto base = normal_vectors(n, dim, 5);
+  quiver::FlatIndex index(dim, quiver::Metric::kCosine);
+  index.add(base.data(), n);
+  const std::string path = dir + "/flat.qvr";
+  index.save(path);
+  const auto loaded = quiver::FlatIndex::load(path);
+  EXPECT(loaded.size() == n && loaded.dim() == dim && loaded.metric() == quiver::Metric::kCosine);
+  for (std::size_t i = 0; i < 10; ++i) {
+    const auto a = index.search(base.data() + i * dim, 5), b = loaded.search(base.data() + i * dim, 5);
+    EXPECT(a.size() == b.size());
+    for (std::size_t j = 0; j < a.size() && j < b.size(); ++j) EXPECT(a[j].label == b[j].label && a[j].distance == b[j].distance);
+  }
+}
+
+void ivfpq_recall_save_load_and_errors(const std::string& dir) {
+  const std::size_t dim = 32, n = 6000, nq = 50, k = 10;
+  const auto base = blob_vectors(n, dim, 40, 6);
+  const auto queries = blob_vectors(nq, dim, 40, 7);
+  quiver::IvfPqParams p;
+  p.dim = dim;
+  p.nlist = 64;
+  p.m = 16;
+  p.store_vectors = true;
+  quiver::IvfPqIndex index(p);
+  EXPECT(!index.is_trained());
+  EXPECT(throws_error([&] { index.add(base.data(), n); }));  // must train first
+  index.train(base.data(), n);
+  EXPECT(index.is_trained());
+  EXPECT(throws_error([&] { index.train(base.data(), n); }));  // once only
+  index.add(base.data(), n);
+  EXPECT(index.size() == n);
+  quiver::IvfPqSearchParams sp;
+  sp.nprobe = 16;
+  sp.refine_factor = 4;
+  double total = 0;
+  for (std::size_t i = 0; i < nq; ++i) {
+    const auto r = index.search(queries.data() + i * dim, k, sp);
+    EXPECT(r.size() == k && std::is_sorted(r.begin(), r.end()));
+    total += recall(brute_force(base, queries.data() + i * dim, dim, k), r);
+  }
+  std::printf("    recall@10 (nprobe 16, refine 4): %.3f\n", total / nq);
+  EXPECT(total / nq >= 0.9);
+  // Refine over everything (k * refine_factor saturates at the count) with every list probed is exact.
+  sp.nprobe = p.nlist;
+  sp.refine_factor = std::size_t{1} << 63;
+  for (std::size_t i = 0; i < 5; ++i) {
+    const auto r = index.search(queries.data() + i * dim, 2, sp);
+    const auto truth = brute_force(base, queries.data() + i * dim, dim, 2);
+    EXPECT(r.size() == 2 && r[0].label == truth[0]);
+  }
+  // A filter admits only its labels.
+  const quiver::LabelSetFilter even = [&] {
+    quiver::LabelSetFilter f;
+    for (quiver::Label l = 0; l < n; l += 2) f.insert(l);
+    return f;
+  }();
+  sp.nprobe = 16;
+  sp.refine_factor = 0;
+  sp.filter = &even;
+  for (const auto& nb : index.search(queries.data(), k, sp)) EXPECT(nb.label % 2 == 0);
+  sp.filter = nullptr;
+  const std::string path = dir + "/ivf.qvr";
+  index.save(path);
+  const auto loaded = quiver::IvfPqIndex::load(path);
+  EXPECT(loaded.size() == n && loaded.is_trained());
+  for (std::size_t i = 0; i < 10; ++i) {
+    const auto a = index.search(queries.data() + i * dim, 5, sp), b = loaded.search(queries.data() + i * dim, 5, sp);
+    EXPECT(a.size() == b.size());
+    for (std::size_t j = 0; j < a.size() && j < b.size(); ++j) EXPECT(a[j].label == b[j].label && a[j].distance == b[j].distance);
+  }
+}
+
+}  // namespace
+
+int main() {
+  const std::string dir = (std::filesystem::temp_directory_path() / ("quiver_cpp_api_" + std::to_string(::getpid()))).string();
+  std::filesystem::create_directories(dir);
+  const std::pair<const char*, std::function<void()>> cases[] = {
+      {"flat_matches_brute_force", flat_matches_brute_force},
+      {"flat_cosine_and_inner_product", flat_cosine_and_inner_product},
+      {"flat_fewer_than_k_and_filters", flat_fewer_than_k_and_filters},
+      {"flat_save_load", [&] { flat_save_load(dir); }},
+      {"ivfpq_recall_save_load_and_errors", [&] { ivfpq_recall_save_load_and_errors(dir); }},
+  };
+  for (const auto& [name, fn] : cases) {
+    const int before = g_failures;
+    std::printf("case %s\n", name);
+    std::fflush(stdout);
+    try {
+      fn();
+    } catch (const std::exception& e) {
+      std::printf("    unexpected exception: %s\n", e.what());
+      ++g_failures;
+    }
+    std::printf("  %s\n", g_failures == before ? "ok" : "FAILED");
+    std::fflush(stdout);
+  }
+  std::filesystem::remove_all(dir);
+  std::printf("%s\n", g_failures == 0 ? "all cases passed" : "failures");
+  return g_failures == 0 ? 0 : 1;
+}
