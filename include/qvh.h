@@ -124,6 +124,11 @@ qvh_status qvh_flat_set_timing(qvh_flat* flat, int enable);
 qvh_status qvh_flat_last_timing(qvh_flat* flat, float* prep_ms, float* scan_ms, float* merge_ms,
                                 uint32_t* nsplit);
 
+/* Diagnostic (no counterpart in the reference): the number of queries of the last search with
+ * 32 < k <= 256 that the wide merge handed to the exact kernel (a split's 32-entry list ran out
+ * before the selection ended), 0 for other searches. Waits for the last search. */
+qvh_status qvh_flat_last_fallbacks(qvh_flat* flat, uint32_t* count);
+
 /* ------------------------------------------------------------------------------------------ *
  * IVF-PQ: replaces the encode step of IvfPqIndex::Impl::add (src/ivfpq_index.cc:208-271) and
  * the query path of IvfPqIndex::Impl::search_into (src/ivfpq_index.cc:275-381). Lists live on

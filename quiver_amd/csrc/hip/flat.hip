@@ -57,6 +57,7 @@ struct ScanArgs {
   float* part_d;            // [nq][2*nsplit][KL]
   uint32_t* part_r;
   uint32_t* qthr;           // [nq] shared prune threshold (ordered float bits), starts at +inf
+  int share;                // 0: every lane list keeps its own KL best (k > KL: no shared bound)
 };
 
 constexpr int kShareEvery = 4;  // tiles between exchanges of the shared per-query threshold
@@ -327,7 +328,7 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
     }
     if (wave_active && (t % kShareEvery) == kShareEvery - 1) {
       flush_queue();
-      share_threshold();
+      if (a.share) share_threshold();
     }
     if (t + 1 < ntiles) store_tile(buf ^ 1);
     __syncthreads();
@@ -429,6 +430,97 @@ __global__ void __launch_bounds__(256) flat_merge_kernel(MergeArgs m) {
   }
 }
 
+// k from 33 to kWideMaxK: the MFMA scan keeps 32 per lane list with no shared bound (each list holds
+// the 32 best of its own rows), and the merge takes the best sel_n = k + max(16, k / 2) keys over
+// all lists, re-scores them exactly and sorts them. A list all 32 of whose entries were taken may
+// have held more of the answer: that query runs on the exact kernel instead (fallback list).
+constexpr uint32_t kWideMaxK = 256;
+constexpr uint32_t kWideMaxSel = 512;
+
+__global__ void __launch_bounds__(256) flat_merge_wide_kernel(MergeArgs m, uint32_t sel_n,
+                                                              uint32_t* __restrict__ fallback,
+                                                              uint32_t* __restrict__ nfallback) {
+  constexpr int KL = 32;
+  __shared__ uint64_t s_sel[4][kWideMaxSel];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t q = blockIdx.x * 4 + wave;
+  if (q >= m.nq) return;  // whole wave; this kernel has no block barriers
+  uint64_t* sel = s_sel[wave];
+  const float* pd = m.part_d + static_cast<size_t>(q) * m.nlists * KL;
+  const uint32_t* pr = m.part_r + static_cast<size_t>(q) * m.nlists * KL;
+  uint32_t ptr[kMaxListsPerLane];
+  uint64_t head[kMaxListsPerLane];
+#pragma unroll
+  for (int u = 0; u < kMaxListsPerLane; ++u) {
+    const uint32_t li = lane + 64 * u;
+    ptr[u] = 0;
+    head[u] = li < m.nlists ? make_key(pd[li * KL], pr[li * KL]) : ~0ull;
+  }
+  uint32_t count = 0;
+  bool spent = false;  // one of this lane's lists gave all of its KL entries
+  for (uint32_t x = 0; x < sel_n; ++x) {
+    uint64_t mine = head[0];
+    int arg = 0;
+#pragma unroll
+    for (int u = 1; u < kMaxListsPerLane; ++u) {
+      if (head[u] < mine) {
+        mine = head[u];
+        arg = u;
+      }
+    }
+    const uint64_t best = wave_min_u64(mine);
+    if (static_cast<uint32_t>(best) == QVH_EMPTY_ROW) break;  // only empty slots remain
+    if (lane == 0) sel[x] = best;
+    ++count;
+    if (mine == best) {
+#pragma unroll
+      for (int u = 0; u < kMaxListsPerLane; ++u) {
+        if (u == arg) {
+          const uint32_t li = lane + 64 * u;
+          const uint32_t p = ++ptr[u];
+          if (p < KL) {
+            head[u] = make_key(pd[li * KL + p], pr[li * KL + p]);
+          } else {
+            head[u] = ~0ull;
+            spent = spent || x + 1 < sel_n;  // taken before the selection ended
+          }
+        }
+      }
+    }
+  }
+  if (__ballot(spent) != 0) {
+    if (lane == 0) fallback[atomicAdd(nfallback, 1u)] = q;
+    return;
+  }
+  __builtin_amdgcn_wave_barrier();
+  // Re-score the selected candidates exactly and rank them by (distance, row).
+  uint64_t x8[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t e = static_cast<uint32_t>(i * 64 + lane);
+    x8[i] = ~0ull;
+    if (e < count) {
+      const uint32_t pos = static_cast<uint32_t>(sel[e]);
+      const uint32_t row = m.idx ? m.idx[pos] : pos;
+      const float d = exact_flat_distance(m.Q + static_cast<size_t>(q) * m.dp, m.X + static_cast<size_t>(row) * m.dp,
+                                          m.dim, m.l2 != 0);
+      x8[i] = make_key(d, row);
+    }
+  }
+  wave_sort<8>(x8);
+  uint32_t* orow = m.out_rows + static_cast<size_t>(q) * m.k;
+  float* odist = m.out_dist + static_cast<size_t>(q) * m.k;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t e = static_cast<uint32_t>(i * 64 + lane);
+    if (e < m.k) {
+      const bool full = e < count;
+      orow[e] = full ? static_cast<uint32_t>(x8[i]) : QVH_EMPTY_ROW;
+      odist[e] = full ? ordered_to_float(static_cast<uint32_t>(x8[i] >> 32)) : __builtin_huge_valf();
+    }
+  }
+}
+
 // ---- ingest / prep kernels ------------------------------------------------------------------
 
 /// dst[r][c] = c < dim ? src[r][c] : 0 for r < n, c < dp.
@@ -483,6 +575,8 @@ struct ExactArgs {
   const uint64_t* bitmap;
   uint32_t* out_rows;
   float* out_dist;
+  const uint32_t* qlist;   // queries to run (block b runs qlist[b] while b < *qcount), or null: all
+  const uint32_t* qcount;
 };
 
 template <int CAP>
@@ -495,7 +589,11 @@ __global__ void __launch_bounds__(kExactThreads) flat_exact_kernel(ExactArgs a) 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const uint32_t q = blockIdx.x;
+  uint32_t q = blockIdx.x;
+  if (a.qlist) {
+    if (blockIdx.x >= *a.qcount) return;  // block-uniform, before any barrier
+    q = a.qlist[blockIdx.x];
+  }
   const float* qv = a.Q + static_cast<uint64_t>(q) * a.dp;
   if (tid == 0) s_thr = 0xFFFFFFFFu;
   __syncthreads();
@@ -645,13 +743,14 @@ struct qvh_flat {
   hipStream_t stream = nullptr;
   std::mutex mu;
   // per-call workspace (grown on demand, serialized by mu)
-  DeviceBuffer w_stage, w_q, w_qn, w_pd, w_pr, w_rows, w_dist, w_bits, w_thr, w_idx;
+  DeviceBuffer w_stage, w_q, w_qn, w_pd, w_pr, w_rows, w_dist, w_bits, w_thr, w_idx, w_fb;
   // optional per-stage timing of the last search: events before prep, scan, merge and after
   bool timing = false;
   bool timed = false;
   hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
   hipEvent_t join = nullptr;  // orders calls on other streams into the handle's stream
   uint64_t last_nsplit = 0;
+  bool last_wide = false;  // the last search took the wide merge (its fallback count is in w_fb)
 };
 
 namespace {
@@ -709,18 +808,25 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
   if (f->timed) QVH_HIP(hipEventRecord(f->ev[0], s));
   flat_prep_queries(f, d_queries, nq, s);
   if (f->timed) QVH_HIP(hipEventRecord(f->ev[1], s));
-  if (k > 32 || f->dp > static_cast<uint32_t>(kMaxDp)) {
-    ExactArgs e;
-    e.X = f->rows.as<float>();
-    e.dp = f->dp;
-    e.dim = f->dim;
-    e.n = f->n;
-    e.Q = f->w_q.as<float>();
-    e.k = k;
-    e.l2 = f->metric == QVH_METRIC_L2;
-    e.bitmap = d_bitmap;
-    e.out_rows = d_rows;
-    e.out_dist = d_dist;
+  // k <= 32: the MFMA scan with per-lane lists of KL = 16 or 32 and a shared bound; 32 < k <=
+  // kWideMaxK: the same scan without the shared bound and the wide merge (its rare fallback
+  // queries on the exact kernel); larger k or dim: the exact kernel.
+  const bool wide = k > 32 && k <= kWideMaxK && f->dp <= static_cast<uint32_t>(kMaxDp) && !d_idx;
+  f->last_wide = wide;
+  ExactArgs e{};
+  e.X = f->rows.as<float>();
+  e.dp = f->dp;
+  e.dim = f->dim;
+  e.n = f->n;
+  e.Q = f->w_q.as<float>();
+  e.k = k;
+  e.l2 = f->metric == QVH_METRIC_L2;
+  e.bitmap = d_bitmap;
+  e.out_rows = d_rows;
+  e.out_dist = d_dist;
+  e.qlist = nullptr;
+  e.qcount = nullptr;
+  if (!wide && (k > 32 || f->dp > static_cast<uint32_t>(kMaxDp))) {
     launch_exact(e, nq, s);
     f->last_nsplit = 0;
     if (f->timed) {
@@ -776,6 +882,7 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
   a.part_d = static_cast<float*>(f->w_pd.reserve(parts * sizeof(float)));
   a.part_r = static_cast<uint32_t*>(f->w_pr.reserve(parts * sizeof(uint32_t)));
   a.qthr = static_cast<uint32_t*>(f->w_thr.reserve(nq * sizeof(uint32_t)));
+  a.share = wide ? 0 : 1;
   hipLaunchKernelGGL(fill_u32_kernel, dim3(static_cast<unsigned>(ceil_div(nq, 256))), dim3(256), 0, s,
                      a.qthr, nq, 0xFF800000u);  // ordered bits of +inf
   launch_scan(f->dp, kl, dim3(static_cast<unsigned>(qblocks * nsplit)), a, s);
@@ -798,7 +905,17 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
   m.out_rows = d_rows;
   m.out_dist = d_dist;
   const dim3 mgrid(static_cast<unsigned>(ceil_div(nq, 4)));
-  if (kl == 16) {
+  if (wide) {
+    // fb[0] counts the fallback queries, fb[1..] lists them; the exact kernel then runs only those.
+    uint32_t* fb = static_cast<uint32_t*>(f->w_fb.reserve((nq + 1) * sizeof(uint32_t)));
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(256), 0, s, fb, 1, 0u);
+    const uint32_t sel_n = k + std::max<uint32_t>(16, k / 2);
+    hipLaunchKernelGGL(flat_merge_wide_kernel, mgrid, dim3(256), 0, s, m, sel_n, fb + 1, fb);
+    QVH_HIP(hipGetLastError());
+    e.qlist = fb + 1;
+    e.qcount = fb;
+    launch_exact(e, nq, s);
+  } else if (kl == 16) {
     hipLaunchKernelGGL(flat_merge_kernel<16>, mgrid, dim3(256), 0, s, m);
   } else {
     hipLaunchKernelGGL(flat_merge_kernel<32>, mgrid, dim3(256), 0, s, m);
@@ -856,6 +973,18 @@ qvh_status qvh_flat_set_timing(qvh_flat* f, int enable) {
       for (hipEvent_t& e : f->ev) QVH_HIP(hipEventCreate(&e));
     }
     f->timing = enable != 0;
+  });
+}
+
+qvh_status qvh_flat_last_fallbacks(qvh_flat* f, uint32_t* count) {
+  return guarded([&] {
+    QVH_REQUIRE(f != nullptr && count != nullptr, "qvh_flat_last_fallbacks: null argument");
+    std::lock_guard<std::mutex> lock(f->mu);
+    QVH_HIP(hipSetDevice(f->device));
+    *count = 0;
+    if (!f->last_wide) return;
+    QVH_HIP(hipStreamSynchronize(f->stream));
+    QVH_HIP(hipMemcpy(count, f->w_fb.ptr, sizeof(uint32_t), hipMemcpyDeviceToHost));
   });
 }
 

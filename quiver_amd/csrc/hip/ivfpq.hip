@@ -884,81 +884,6 @@ constexpr uint32_t kStreamMaxM = 64;  // code bytes of the widest streaming kern
 // Slices per query of a batch smaller than one resident generation of blocks.
 constexpr uint64_t kMaxSlices = 4;
 
-/// Ascending bitonic sort of N * 64 keys held by one wave, element e = i * 64 + lane in k[i].
-template <int N>
-__device__ __forceinline__ void wave_sort(uint64_t (&k)[N]) {
-  const int lane = threadIdx.x & 63;
-  constexpr int total = N * 64;
-#pragma unroll
-  for (int size = 2; size <= total; size <<= 1) {
-#pragma unroll
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      if (stride >= 64) {
-        const int is = stride / 64;
-#pragma unroll
-        for (int i = 0; i < N; ++i) {
-          const int j = i ^ is;
-          if (j > i) {
-            const bool up = ((i * 64) & size) == 0;
-            const uint64_t x = k[i], y = k[j];
-            const bool swap = (x > y) == up;
-            k[i] = swap ? y : x;
-            k[j] = swap ? x : y;
-          }
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < N; ++i) {
-          const uint64_t other = __shfl_xor(k[i], stride, 64);
-          const bool up = ((i * 64 + lane) & size) == 0;
-          const bool lower = (lane & stride) == 0;
-          k[i] = (lower == up) ? (other < k[i] ? other : k[i]) : (other > k[i] ? other : k[i]);
-        }
-      }
-    }
-  }
-}
-
-/// Ascending sort of a bitonic sequence of N * 64 keys held by one wave (element e = i * 64 + lane
-/// in k[i]): the last merge stage of the bitonic sort.
-template <int N>
-__device__ __forceinline__ void wave_merge(uint64_t (&k)[N]) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int stride = N * 32; stride > 0; stride >>= 1) {
-    if (stride >= 64) {
-      const int is = stride / 64;
-#pragma unroll
-      for (int i = 0; i < N; ++i) {
-        const int j = i ^ is;
-        if (j > i) {
-          const uint64_t x = k[i], y = k[j];
-          k[i] = x < y ? x : y;
-          k[j] = x < y ? y : x;
-        }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < N; ++i) {
-        const uint64_t other = __shfl_xor(k[i], stride, 64);
-        const bool lower = (lane & stride) == 0;
-        k[i] = lower ? (other < k[i] ? other : k[i]) : (other > k[i] ? other : k[i]);
-      }
-    }
-  }
-}
-
-/// Key at sorted position e (wave-uniform) of a wave-sorted register array.
-template <int N>
-__device__ __forceinline__ uint64_t wave_key_at(const uint64_t (&k)[N], uint32_t e) {
-  uint64_t v = 0;
-#pragma unroll
-  for (int i = 0; i < N; ++i) {
-    if (static_cast<uint32_t>(i) == e / 64) v = k[i];
-  }
-  return __shfl(v, static_cast<int>(e % 64), 64);
-}
-
 /// Table entry (j, c) of the per-query table, in the reference's order (sum over t, then the
 /// factor -2 for L2, src/ivfpq_index.cc:315-317 and src/product_quantizer.cc:180-186).
 __device__ __forceinline__ float table_entry(const float* qv, const float* cbt, uint32_t dsub, uint32_t j,

@@ -38,6 +38,7 @@ class Qvh:
         L.qvh_flat_search_rows.argtypes = [C.c_void_p, _f32p, C.c_uint64, C.c_uint32, _u32p, C.c_uint64,
                                            _u32p, _f32p]
         L.qvh_normalize.argtypes = [_f32p, C.c_uint64, C.c_uint32]
+        L.qvh_flat_last_fallbacks.argtypes = [C.c_void_p, C.POINTER(C.c_uint32)]
 
     def error(self) -> str:
         return self.lib.qvh_last_error().decode()
@@ -53,6 +54,12 @@ class Qvh:
 
     def flat(self, dim, metric):
         return QvhFlat(self, dim, metric)
+
+    def last_fallbacks(self, handle) -> int:
+        """Queries of the handle's last search that the wide merge sent to the exact kernel."""
+        n = C.c_uint32(0)
+        self.check(self.lib.qvh_flat_last_fallbacks(C.c_void_p(handle), C.byref(n)))
+        return n.value
 
 
 class QvhFlat:

@@ -109,14 +109,38 @@ def test_dimensions_above_the_mfma_width(oracle, dim, metric):
     print(_check(oracle, base, q, 7, metric, allowed))
 
 
-@pytest.mark.parametrize("k", [33, 64, 100, 300, 1024])
-@pytest.mark.parametrize("metric", ["l2", "ip"])
+@pytest.mark.parametrize("k", [33, 64, 100, 256, 300, 1024])
+@pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
 def test_large_k(oracle, k, metric):
-    """k > 32 takes the general exact kernel: queue cuts at k, ties by row."""
+    """33 <= k <= 256: the MFMA scan with unshared 32-entry lists and the wide merge; larger k: the
+    general exact kernel (queue cuts at k). Ties by row either way."""
     base, q = D.int_mix(20_000, 30)
     print(_check(oracle, base, q, k, metric))
     allowed = D.allowed_ids(base.shape[0], 0.02, seed=9)
     print(_check(oracle, base, q, k, metric, allowed))
+
+
+@pytest.mark.parametrize("metric", ["l2", "cosine"])
+def test_large_k_crowded_lists_fall_back_exactly(oracle, metric):
+    """200 near-copies of query 0 in consecutive rows: its 100 nearest crowd one split's 32-entry
+    lists, so the wide merge hands that query to the exact kernel while the others stay on the
+    MFMA path; every result still equals the oracle's."""
+    base, q = D.int_mix(40_000, 12)
+    base = base.copy()
+    noise = np.random.default_rng(3).integers(-1, 2, (200, base.shape[1]))
+    base[5_000:5_200] = np.clip(q[0] + noise, 0, 255)
+    stored = oracle.normalize(base) if metric == "cosine" else base
+    idx = quiver.FlatIndex(base.shape[1], metric)
+    idx.add(base)
+    for k in (100, 40):
+        print(f"case: crowded lists k={k} metric={metric}", flush=True)
+        got_l, got_d = idx.search(q, k)
+        if k == 100:  # more than the ~4 crowded lists' 4 x 32 entries can give: query 0 falls back
+            assert Qvh().last_fallbacks(idx._index._device_handle) >= 1
+        rows, dist = oracle.flat_search(stored, q, k, metric)
+        print(assert_same_topk(got_l, got_d, rows.astype(np.int64), dist, _true_dist(oracle, stored, q, metric)))
+    idx.search(q[1:], 100)
+    assert Qvh().last_fallbacks(idx._index._device_handle) == 0  # no crowded query: no fallback
 
 
 def test_k_above_the_device_limit_is_rejected():
