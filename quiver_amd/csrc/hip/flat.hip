@@ -564,6 +564,11 @@ __global__ void fill_u32_kernel(uint32_t* p, uint64_t n, uint32_t v) {
 constexpr int kExactThreads = 256;
 constexpr int kExactWaves = kExactThreads / 64;
 constexpr uint32_t kExactMaxK = 1024;
+// Batches of at most kSplitMaxQueries queries split each query's rows over up to kMaxRowSplits
+// work-groups of the exact kernel (at least kMinSplitRows rows each), then merge the sorted lists.
+constexpr uint64_t kSplitMaxQueries = 8;
+constexpr uint32_t kMaxRowSplits = 1024;
+constexpr uint64_t kMinSplitRows = 1024;
 
 struct ExactArgs {
   const float* X;  // [n][dp] rows as stored
@@ -577,6 +582,14 @@ struct ExactArgs {
   float* out_dist;
   const uint32_t* qlist;   // queries to run (block b runs qlist[b] while b < *qcount), or null: all
   const uint32_t* qcount;
+  // Row splits (nsplit > 1, a multiple of 8; qlist unused): split g scans rows
+  // [g * rows_per_split, (g + 1) * rows_per_split) and writes its k best to slot q * nsplit + g of
+  // out_rows / out_dist. Work-group b runs on XCD b % 8; it takes query (b / 8) % nq of split
+  // ((b / 8) / nq) * 8 + b % 8, so the nq work-groups of one split run together on one XCD and
+  // read its rows through the same L2.
+  uint32_t nsplit;
+  uint32_t nq;
+  uint64_t rows_per_split;
 };
 
 template <int CAP>
@@ -589,8 +602,12 @@ __global__ void __launch_bounds__(kExactThreads) flat_exact_kernel(ExactArgs a) 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  uint32_t q = blockIdx.x;
-  if (a.qlist) {
+  uint32_t q = blockIdx.x, split = 0;
+  if (a.nsplit > 1) {
+    const uint32_t j = blockIdx.x >> 3;
+    q = j % a.nq;
+    split = (j / a.nq) * 8 + (blockIdx.x & 7);
+  } else if (a.qlist) {
     if (blockIdx.x >= *a.qcount) return;  // block-uniform, before any barrier
     q = a.qlist[blockIdx.x];
   }
@@ -613,9 +630,12 @@ __global__ void __launch_bounds__(kExactThreads) flat_exact_kernel(ExactArgs a) 
       }
     }
   };
-  for (uint64_t r0 = 0; r0 < a.n; r0 += kExactThreads) {
+  const uint64_t r_begin = min(a.n, static_cast<uint64_t>(split) * a.rows_per_split);
+  const uint64_t r_end = a.nsplit > 1 ? min(a.n, r_begin + a.rows_per_split) : a.n;
+  const uint64_t slot = static_cast<uint64_t>(q) * max(a.nsplit, 1u) + split;
+  for (uint64_t r0 = r_begin; r0 < r_end; r0 += kExactThreads) {
     const uint64_t r = r0 + tid;
-    bool ok = r < a.n;
+    bool ok = r < r_end;
     if (ok && a.bitmap) ok = (a.bitmap[r >> 6] >> (r & 63)) & 1ull;
     const float d = ok ? exact_flat_distance(qv, a.X + r * a.dp, a.dim, a.l2 != 0) : 0.0f;
     const bool pass = ok && d <= thr;
@@ -657,9 +677,74 @@ __global__ void __launch_bounds__(kExactThreads) flat_exact_kernel(ExactArgs a) 
   const uint32_t nout = min(merged, a.k);
   for (uint32_t j = tid; j < a.k; j += kExactThreads) {
     const uint64_t key = j < nout ? s_queue[j] : ~0ull;
-    a.out_rows[static_cast<uint64_t>(q) * a.k + j] = j < nout ? static_cast<uint32_t>(key) : QVH_EMPTY_ROW;
-    a.out_dist[static_cast<uint64_t>(q) * a.k + j] =
-        j < nout ? ordered_to_float(static_cast<uint32_t>(key >> 32)) : __builtin_huge_valf();
+    a.out_rows[slot * a.k + j] = j < nout ? static_cast<uint32_t>(key) : QVH_EMPTY_ROW;
+    a.out_dist[slot * a.k + j] = j < nout ? ordered_to_float(static_cast<uint32_t>(key >> 32)) : __builtin_huge_valf();
+  }
+}
+
+/// The k best of a query's nsplit sorted partial lists of k exact keys each (rows past a list's
+/// count are QVH_EMPTY_ROW): one wave per query; each step takes the wave minimum of the lanes' list
+/// heads (lists lane, lane + 64, ... per lane). A list's next key is loaded one pop ahead, so a
+/// step waits on memory only when the same list wins twice in a row.
+template <int LPL>
+__global__ void __launch_bounds__(256) flat_merge_sorted_kernel(const uint32_t* __restrict__ part_r,
+                                                                const float* __restrict__ part_d, uint32_t nq,
+                                                                uint32_t nsplit, uint32_t k,
+                                                                uint32_t* __restrict__ out_rows,
+                                                                float* __restrict__ out_dist) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t q = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (q >= nq) return;  // whole wave; no block barriers
+  const uint32_t* pr = part_r + static_cast<uint64_t>(q) * nsplit * k;
+  const float* pd = part_d + static_cast<uint64_t>(q) * nsplit * k;
+  auto key_at = [&](uint32_t li, uint32_t p) {
+    const uint64_t o = static_cast<uint64_t>(li) * k + p;
+    return make_key(pd[o], pr[o]);
+  };
+  uint32_t ptr[LPL];
+  uint64_t head[LPL], next[LPL];
+#pragma unroll
+  for (int u = 0; u < LPL; ++u) {
+    const uint32_t li = lane + 64 * u;
+    ptr[u] = 0;
+    head[u] = li < nsplit ? key_at(li, 0) : ~0ull;
+    next[u] = li < nsplit && k > 1 ? key_at(li, 1) : ~0ull;
+  }
+  uint32_t* orow = out_rows + static_cast<uint64_t>(q) * k;
+  float* odist = out_dist + static_cast<uint64_t>(q) * k;
+  for (uint32_t x = 0; x < k; ++x) {
+    uint64_t mine = head[0];
+    int arg = 0;
+#pragma unroll
+    for (int u = 1; u < LPL; ++u) {
+      if (head[u] < mine) {
+        mine = head[u];
+        arg = u;
+      }
+    }
+    const uint64_t best = wave_min_u64(mine);
+    const bool empty = static_cast<uint32_t>(best) == QVH_EMPTY_ROW;
+    if (empty) {
+      for (uint32_t y = x + lane; y < k; y += 64) {
+        orow[y] = QVH_EMPTY_ROW;
+        odist[y] = __builtin_huge_valf();
+      }
+      return;
+    }
+    if (lane == 0) {
+      orow[x] = static_cast<uint32_t>(best);
+      odist[x] = ordered_to_float(static_cast<uint32_t>(best >> 32));
+    }
+    if (mine == best) {  // one lane: keys are distinct (rows differ)
+#pragma unroll
+      for (int u = 0; u < LPL; ++u) {
+        if (u == arg) {
+          const uint32_t p = ++ptr[u];
+          head[u] = next[u];
+          next[u] = p + 1 < k ? key_at(lane + 64 * u, p + 1) : ~0ull;
+        }
+      }
+    }
   }
 }
 
@@ -671,7 +756,7 @@ void launch_exact(const ExactArgs& a, uint64_t nq, hipStream_t s) {
       QVH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                                   static_cast<int>(lds)));
     }
-    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(nq)), dim3(kExactThreads), lds, s, a);
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(nq * std::max(1u, a.nsplit))), dim3(kExactThreads), lds, s, a);
   };
   switch (cap) {
     case 128: go(flat_exact_kernel<128>); break;
@@ -826,6 +911,42 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
   e.out_dist = d_dist;
   e.qlist = nullptr;
   e.qcount = nullptr;
+  int cus = 256;
+  (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, f->device);
+  if (nq <= kSplitMaxQueries && !d_idx && f->n >= 2 * kMinSplitRows) {
+    // A few queries: the MFMA scan's 256-query blocks would run mostly empty. Split each query's
+    // rows over enough exact-kernel work-groups to give every CU eight, then merge.
+    const uint64_t want = ceil_div(static_cast<uint64_t>(cus) * 8, nq);
+    uint64_t g = std::min<uint64_t>({want, kMaxRowSplits, f->n / kMinSplitRows});
+    const uint64_t rps = ceil_div(ceil_div(f->n, g), kExactThreads) * kExactThreads;
+    g = ceil_div(ceil_div(f->n, rps), 8) * 8;  // the XCD mapping takes whole groups of 8 splits
+    const size_t parts = static_cast<size_t>(nq) * g * k;
+    e.nsplit = static_cast<uint32_t>(g);
+    e.nq = static_cast<uint32_t>(nq);
+    e.rows_per_split = rps;
+    e.out_rows = static_cast<uint32_t*>(f->w_pr.reserve(parts * sizeof(uint32_t)));
+    e.out_dist = static_cast<float*>(f->w_pd.reserve(parts * sizeof(float)));
+    launch_exact(e, nq, s);
+    if (f->timed) QVH_HIP(hipEventRecord(f->ev[2], s));
+    const dim3 mgrid(static_cast<unsigned>(ceil_div(nq, 4))), mblock(256);
+    const uint32_t ns = e.nsplit;
+    if (g <= 64) {
+      hipLaunchKernelGGL(flat_merge_sorted_kernel<1>, mgrid, mblock, 0, s, e.out_rows, e.out_dist, nq, ns, k, d_rows, d_dist);
+    } else if (g <= 128) {
+      hipLaunchKernelGGL(flat_merge_sorted_kernel<2>, mgrid, mblock, 0, s, e.out_rows, e.out_dist, nq, ns, k, d_rows, d_dist);
+    } else if (g <= 256) {
+      hipLaunchKernelGGL(flat_merge_sorted_kernel<4>, mgrid, mblock, 0, s, e.out_rows, e.out_dist, nq, ns, k, d_rows, d_dist);
+    } else if (g <= 512) {
+      hipLaunchKernelGGL(flat_merge_sorted_kernel<8>, mgrid, mblock, 0, s, e.out_rows, e.out_dist, nq, ns, k, d_rows, d_dist);
+    } else {
+      hipLaunchKernelGGL(flat_merge_sorted_kernel<16>, mgrid, mblock, 0, s, e.out_rows, e.out_dist, nq, ns, k, d_rows, d_dist);
+    }
+    QVH_HIP(hipGetLastError());
+    f->last_wide = false;
+    f->last_nsplit = g;
+    if (f->timed) QVH_HIP(hipEventRecord(f->ev[3], s));
+    return;
+  }
   if (!wide && (k > 32 || f->dp > static_cast<uint32_t>(kMaxDp))) {
     launch_exact(e, nq, s);
     f->last_nsplit = 0;
@@ -837,8 +958,6 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
   }
   const int kl = k <= 16 ? 16 : 32;
 
-  int cus = 256;
-  (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, f->device);
   const uint32_t qblocks = static_cast<uint32_t>(ceil_div(nq, kQueriesPerBlock));
   const uint64_t scan_rows = d_idx ? n_idx : f->n;
   const uint64_t tiles = std::max<uint64_t>(1, ceil_div(scan_rows, kTileRows));

@@ -156,6 +156,27 @@ def test_k_values(oracle, k):
     _check(oracle, base[:4000], q[:50], k, "l2")
 
 
+@pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
+@pytest.mark.parametrize("nq,k,n", [(1, 10, 700_000), (3, 1, 50_000), (8, 100, 200_000), (2, 1024, 30_000),
+                                    (5, 10, 2_048), (1, 10, 2_047)])
+def test_small_batches_split_rows(oracle, metric, nq, k, n):
+    """Batches of at most eight queries split each query's rows over up to 1024 work-groups and
+    merge the sorted partial lists (2,047 rows: too few to split, one work-group per query)."""
+    base = D.gaussian(n, 16, seed=31)
+    q = D.gaussian(nq, 16, seed=32)
+    print(_check(oracle, base, q, k, metric))
+
+
+@pytest.mark.parametrize("fraction", [0.6, 0.95])
+def test_small_batches_split_rows_filtered_and_ties(oracle, fraction):
+    """Integer data (many exactly equal distances across splits) with a row filter above half
+    density (the bitmap is tested per row)."""
+    base, q = D.int_mix(300_000, 4)
+    allowed = D.allowed_ids(base.shape[0], fraction, seed=41)
+    print(_check(oracle, base, q, 10, "l2", allowed))
+    print(_check(oracle, base, q[:1], 50, "l2"))
+
+
 def test_integer_data_exact_ties(oracle):
     """Integer-valued mixture (config 2's distribution): distances are exact integers, ties are
     common; ties resolve to the smaller row."""
