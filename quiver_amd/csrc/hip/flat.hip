@@ -17,6 +17,7 @@
 // keeps a margin of near-tied candidates for the re-score to choose from.
 #include <algorithm>
 #include <vector>
+#include <type_traits>
 
 #include "common.hpp"
 #include "exact.hpp"
@@ -682,6 +683,309 @@ __global__ void __launch_bounds__(kExactThreads) flat_exact_kernel(ExactArgs a) 
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Few-query exact scan (at most kFewMaxQ queries, 32 <= dim <= kFewMaxDim, k <= kFewMaxK).
+//
+// Eight lanes share a row and load it coalesced: lane l of the eight (u = l & 3, h = l >> 2)
+// holds the four accumulators 8u + 4h .. 8u + 4h + 3 of the reference's AVX2 kernel and replays
+// their fused chains over the 32-element blocks in order (the 8-element blocks continue the u = 0
+// chains in lanes 0 and 4). The horizontal sum then maps onto DPP within the eight lanes:
+// quad_perm [1,0,3,2] adds s0 + s1 and s2 + s3, quad_perm [2,3,0,1] gives v = (s0+s1)+(s2+s3) for
+// l' = 0..3 (lanes 0-3) and l' = 4..7 (lanes 4-7), row_half_mirror adds the two halves into
+// lo[j] = v[j] + v[j+4], and (lo0+lo1)+(lo2+lo3) and the scalar tail finish in each lane. Every
+// row is read once for all the batch's queries, whose values stay in registers.
+
+constexpr int kFewThreads = 256;
+constexpr int kFewWaves = kFewThreads / 64;
+constexpr int kFewRowsPerStep = kFewWaves * 8;
+constexpr int kFewCap = 128;  // per (query, wave) queue
+constexpr uint32_t kFewMaxQ = 8;
+constexpr uint32_t kFewMaxK = 64;
+constexpr uint32_t kFewMaxDim = 159;  // four 32-element blocks, then up to three 8-blocks and a tail
+constexpr uint32_t kFewMaxDp = 160;
+constexpr uint32_t kFewMaxSplits = 1024;
+
+struct FewArgs {
+  const float* X;  // [n][dp]
+  uint32_t dp, dim;
+  uint64_t n;
+  const float* Q;  // [nq][dp] prepared queries
+  uint32_t nq, k;
+  const uint64_t* bitmap;
+  uint64_t rows_per_split;  // multiple of kFewRowsPerStep
+  uint32_t nsplit;
+  uint32_t* part_r;  // [nq][nsplit][k]
+  float* part_d;
+};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+/// One step's rows for one lane: the four 32-element block pieces and, when the dimension is
+/// not a multiple of 32, the 8-element block pieces and the tail.
+template <bool TAIL>
+struct FewRows {
+  float4 x[4];
+  float4 xe[TAIL ? 3 : 1];
+  float4 t_lo, t_hi;
+  uint64_t bits;
+};
+
+template <int NQ, bool L2, bool TAIL>
+__global__ void __launch_bounds__(kFewThreads) flat_few_kernel(FewArgs a) {
+  __shared__ uint64_t s_queue[NQ * kFewWaves * kFewCap];  // [query][wave][kFewCap]
+  __shared__ __attribute__((aligned(16))) float s_q[NQ * kFewMaxDp];
+  __shared__ __attribute__((aligned(16))) uint32_t s_thr[NQ < 4 ? 4 : NQ];
+  __shared__ uint32_t s_wcount[kFewWaves];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int grp = lane >> 3;  // the wave's row within a step
+  const int gl = lane & 7;
+  const int u = gl & 3, h = gl >> 2;
+  const uint32_t nb = a.dim / 32;              // 32-element blocks (1..4)
+  const uint32_t nj = (a.dim - 32 * nb) / 8;   // then 8-element blocks (0..3)
+  const uint32_t t0 = 32 * nb + 8 * nj;        // then the scalar tail [t0, dim)
+  const uint32_t nt = a.dim - t0;
+  const uint32_t nt4 = nt / 4 * 4;             // its first nt4 products are rounded separately
+
+  for (uint32_t i = tid; i < NQ * a.dp; i += kFewThreads) {
+    const uint32_t qi = i / a.dp;
+    s_q[qi * kFewMaxDp + i % a.dp] = qi < a.nq ? a.Q[static_cast<uint64_t>(qi) * a.dp + i % a.dp] : 0.0f;
+  }
+  if (tid < (NQ < 4 ? 4 : NQ)) s_thr[tid] = 0xFFFFFFFFu;
+  __syncthreads();
+  float4 qr[NQ][4];
+#pragma unroll
+  for (int qi = 0; qi < NQ; ++qi)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      qr[qi][b] = b < static_cast<int>(nb) ? *reinterpret_cast<const float4*>(s_q + qi * kFewMaxDp + 32 * b + 8 * u + 4 * h)
+                                           : make_float4(0.f, 0.f, 0.f, 0.f);
+  // In-row offsets of this lane's loads; pieces a dimension does not have re-read block 0 (in
+  // bounds, never used), so every load is issued unconditionally and stays in flight.
+  uint32_t off_b[4], off_e[3];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) off_b[b] = b < static_cast<int>(nb) ? 32 * b + 8 * u + 4 * h : 8 * u + 4 * h;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) off_e[j] = j < static_cast<int>(nj) ? 32 * nb + 8 * j + 4 * h : 4 * h;
+  const uint32_t off_t = nt > 0 ? t0 : 0;  // t0 + 8 <= dp when the tail is not empty
+
+  uint32_t cnt[NQ], thr_bits[NQ];
+  float thr[NQ];
+#pragma unroll
+  for (int qi = 0; qi < NQ; ++qi) {
+    cnt[qi] = 0;
+    thr_bits[qi] = 0xFFFFFFFFu;
+    thr[qi] = __builtin_huge_valf();
+  }
+  auto queue_of = [&](int qi) { return s_queue + (qi * kFewWaves + wave) * kFewCap; };
+  auto cut = [&](int qi) {
+    uint32_t t = thr_bits[qi];
+    const uint32_t before = cnt[qi];
+    cnt[qi] = wave_cut<kFewCap>(queue_of(qi), cnt[qi], a.k, &t);
+    if (before > a.k) {
+      if (lane == 0) atomicMin(&s_thr[qi], t);
+      if (t < thr_bits[qi]) {
+        thr_bits[qi] = t;
+        thr[qi] = ordered_to_float(t);
+      }
+    }
+  };
+
+  const uint32_t split = blockIdx.x;
+  const uint64_t r_begin = min(a.n, static_cast<uint64_t>(split) * a.rows_per_split);
+  const uint64_t r_end = min(a.n, r_begin + a.rows_per_split);
+  auto load = [&](uint64_t r0, FewRows<TAIL>& R) {
+    uint64_t r = r0 + wave * 8 + grp;
+    r = r < r_end ? r : r_begin;  // past the end: a row in range, masked out later
+    // The (conditional) bitmap load goes first, so that waiting for this step's rows never
+    // waits for the next step's row loads issued after it.
+    R.bits = a.bitmap ? a.bitmap[r >> 6] : ~0ull;
+    const float* xr = a.X + r * a.dp;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) R.x[b] = *reinterpret_cast<const float4*>(xr + off_b[b]);
+    if constexpr (TAIL) {
+#pragma unroll
+      for (int j = 0; j < 3; ++j) R.xe[j] = *reinterpret_cast<const float4*>(xr + off_e[j]);
+      R.t_lo = *reinterpret_cast<const float4*>(xr + off_t);
+      R.t_hi = *reinterpret_cast<const float4*>(xr + off_t + 4);
+    }
+  };
+  FewRows<TAIL> cur;
+  if (r_begin < r_end) load(r_begin, cur);
+  for (uint64_t r0 = r_begin; r0 < r_end; r0 += kFewRowsPerStep) {
+    FewRows<TAIL> nxt;
+    load(r0 + kFewRowsPerStep, nxt);  // the next step's rows are in flight while this one computes
+    const uint64_t r = r0 + wave * 8 + grp;
+    const bool ok = r < r_end && ((cur.bits >> (r & 63)) & 1ull);
+    uint32_t shared_thr[NQ];
+#pragma unroll
+    for (int qi = 0; qi < NQ; ++qi) shared_thr[qi] = __hip_atomic_load(&s_thr[qi], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+#pragma unroll
+    for (int qi = 0; qi < NQ; ++qi) {
+      if (shared_thr[qi] < thr_bits[qi]) {
+        thr_bits[qi] = shared_thr[qi];
+        thr[qi] = ordered_to_float(shared_thr[qi]);
+      }
+      float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+      auto step = [&](const float4& qv, const float4& xv) {
+        if constexpr (L2) {
+          const float d0 = qv.x - xv.x, d1 = qv.y - xv.y, d2 = qv.z - xv.z, d3 = qv.w - xv.w;
+          s0 = fmaf(d0, d0, s0);
+          s1 = fmaf(d1, d1, s1);
+          s2 = fmaf(d2, d2, s2);
+          s3 = fmaf(d3, d3, s3);
+        } else {
+          s0 = fmaf(qv.x, xv.x, s0);
+          s1 = fmaf(qv.y, xv.y, s1);
+          s2 = fmaf(qv.z, xv.z, s2);
+          s3 = fmaf(qv.w, xv.w, s3);
+        }
+      };
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        if (b < static_cast<int>(nb)) step(qr[qi][b], cur.x[b]);
+      }
+      if constexpr (TAIL) {
+        if (u == 0) {
+#pragma unroll
+          for (int j = 0; j < 3; ++j) {
+            if (j < static_cast<int>(nj)) {
+              step(*reinterpret_cast<const float4*>(s_q + qi * kFewMaxDp + 32 * nb + 8 * j + 4 * h), cur.xe[j]);
+            }
+          }
+        }
+      }
+      // horizontal sum, all eight lanes active
+      s0 = s0 + dpp_f<0xB1>(s0);
+      s1 = s1 + dpp_f<0xB1>(s1);
+      s2 = s2 + dpp_f<0xB1>(s2);
+      s3 = s3 + dpp_f<0xB1>(s3);
+      s0 = s0 + dpp_f<0x4E>(s0);
+      s1 = s1 + dpp_f<0x4E>(s1);
+      s2 = s2 + dpp_f<0x4E>(s2);
+      s3 = s3 + dpp_f<0x4E>(s3);
+      s0 = s0 + dpp_f<0x141>(s0);
+      s1 = s1 + dpp_f<0x141>(s1);
+      s2 = s2 + dpp_f<0x141>(s2);
+      s3 = s3 + dpp_f<0x141>(s3);
+      float sum = (s0 + s1) + (s2 + s3);
+      if constexpr (TAIL) {
+        const float xt[8] = {cur.t_lo.x, cur.t_lo.y, cur.t_lo.z, cur.t_lo.w,
+                             cur.t_hi.x, cur.t_hi.y, cur.t_hi.z, cur.t_hi.w};
+        const float* qt = s_q + qi * kFewMaxDp + t0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          if (static_cast<uint32_t>(i) < nt) {
+            if constexpr (L2) {
+              const float d = qt[i] - xt[i];
+              sum = static_cast<uint32_t>(i) < nt4 ? sum + d * d : fmaf(d, d, sum);
+            } else {
+              sum = static_cast<uint32_t>(i) < nt4 ? sum + qt[i] * xt[i] : fmaf(qt[i], xt[i], sum);
+            }
+          }
+        }
+      }
+      float dist = L2 ? sum : 1.0f - sum;
+      dist = dist == dist ? dist : __builtin_huge_valf();
+      const bool pass = ok && gl == 0 && static_cast<uint32_t>(qi) < a.nq && dist <= thr[qi];
+      const uint64_t mk = __ballot(pass);
+      if (mk != 0) {
+        if (pass) queue_of(qi)[cnt[qi] + lane_rank(mk)] = make_key(dist, static_cast<uint32_t>(r));
+        cnt[qi] += static_cast<uint32_t>(__popcll(mk));
+        if (cnt[qi] > static_cast<uint32_t>(kFewCap - 8)) cut(qi);
+      }
+    }
+    cur = nxt;
+  }
+  // Per query: the four wave lists (at most 64 keys each after the cut) sorted together.
+#pragma unroll
+  for (int qi = 0; qi < NQ; ++qi) {
+    cut(qi);
+    const uint64_t mine = static_cast<uint32_t>(lane) < cnt[qi] ? queue_of(qi)[lane] : ~0ull;
+    if (lane == 0) s_wcount[wave] = cnt[qi];
+    __syncthreads();
+    uint32_t most = 0, merged = 0;
+#pragma unroll
+    for (int w = 0; w < kFewWaves; ++w) {
+      most = max(most, s_wcount[w]);
+      merged += s_wcount[w];
+    }
+    uint32_t ks = 1;
+    while (ks < most) ks <<= 1;
+    uint64_t* base = s_queue + qi * kFewWaves * kFewCap;
+    if (static_cast<uint32_t>(lane) < ks) base[wave * ks + lane] = mine;
+    block_sort_keys(base, kFewWaves * ks);
+    if (static_cast<uint32_t>(qi) < a.nq) {
+      const uint32_t nout = min(merged, a.k);
+      const uint64_t slot = static_cast<uint64_t>(qi) * a.nsplit + split;
+      for (uint32_t j = tid; j < a.k; j += kFewThreads) {
+        const uint64_t key = j < nout ? base[j] : ~0ull;
+        a.part_r[slot * a.k + j] = j < nout ? static_cast<uint32_t>(key) : QVH_EMPTY_ROW;
+        a.part_d[slot * a.k + j] = j < nout ? ordered_to_float(static_cast<uint32_t>(key >> 32)) : __builtin_huge_valf();
+      }
+    }
+    __syncthreads();  // s_wcount is reused by the next query
+  }
+}
+
+/// The k best of a query's nsplit <= 1024 sorted partial lists of k <= 64 exact keys each, one
+/// 1024-thread work-group per query: T0 is the k-th smallest list head; every key of the k best
+/// is <= T0, and only the (at most k) lists whose heads are <= T0 hold such keys, so at most k * k
+/// real keys are gathered and sorted.
+constexpr uint32_t kSelectMergeMaxK = 64;
+constexpr uint32_t kSelectMergeLists = 1024;
+
+__global__ void __launch_bounds__(1024) flat_merge_select_kernel(const uint32_t* __restrict__ part_r,
+                                                                 const float* __restrict__ part_d,
+                                                                 uint32_t nsplit, uint32_t k,
+                                                                 uint32_t* __restrict__ out_rows,
+                                                                 float* __restrict__ out_dist) {
+  __shared__ uint64_t s_heads[kSelectMergeLists];
+  __shared__ uint64_t s_cand[kSelectMergeMaxK * kSelectMergeMaxK];
+  __shared__ uint32_t s_count;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t q = blockIdx.x;
+  const uint32_t* pr = part_r + static_cast<uint64_t>(q) * nsplit * k;
+  const float* pd = part_d + static_cast<uint64_t>(q) * nsplit * k;
+  const uint64_t o = static_cast<uint64_t>(tid) * k;
+  s_heads[tid] = tid < nsplit ? make_key(pd[o], pr[o]) : ~0ull;
+  if (tid == 0) s_count = 0;
+  block_sort_keys(s_heads, kSelectMergeLists);
+  const uint64_t t0 = s_heads[k - 1];
+  if (tid < nsplit) {
+    // this list's keys <= t0, eight at a time
+    for (uint32_t p0 = 0; p0 < k; p0 += 8) {
+      uint64_t key[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) key[i] = p0 + i < k ? make_key(pd[o + p0 + i], pr[o + p0 + i]) : ~0ull;
+      bool more = true;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const bool take = more && static_cast<uint32_t>(key[i]) != QVH_EMPTY_ROW && key[i] <= t0;
+        if (take) s_cand[atomicAdd(&s_count, 1u)] = key[i];
+        more = take;
+      }
+      if (!more) break;
+    }
+  }
+  __syncthreads();
+  const uint32_t c = s_count;
+  uint32_t n2 = 1;
+  while (n2 < c) n2 <<= 1;
+  for (uint32_t i = c + tid; i < n2; i += 1024) s_cand[i] = ~0ull;
+  block_sort_keys(s_cand, n2);
+  for (uint32_t j = tid; j < k; j += 1024) {
+    const bool real = j < c;
+    out_rows[static_cast<uint64_t>(q) * k + j] = real ? static_cast<uint32_t>(s_cand[j]) : QVH_EMPTY_ROW;
+    out_dist[static_cast<uint64_t>(q) * k + j] =
+        real ? ordered_to_float(static_cast<uint32_t>(s_cand[j] >> 32)) : __builtin_huge_valf();
+  }
+}
+
 /// The k best of a query's nsplit sorted partial lists of k exact keys each (rows past a list's
 /// count are QVH_EMPTY_ROW): one wave per query; each step takes the wave minimum of the lanes' list
 /// heads (lists lane, lane + 64, ... per lane). A list's next key is loaded one pop ahead, so a
@@ -746,6 +1050,32 @@ __global__ void __launch_bounds__(256) flat_merge_sorted_kernel(const uint32_t* 
       }
     }
   }
+}
+
+/// The k best of each query's nsplit sorted lists [nq][nsplit][k] into [nq][k].
+void launch_sorted_merge(const uint32_t* part_r, const float* part_d, uint64_t nq, uint32_t nsplit, uint32_t k,
+                         uint32_t* d_rows, float* d_dist, hipStream_t s) {
+  QVH_REQUIRE(nsplit <= 64 * 16, "flat search: too many partial lists to merge");
+  if (k <= kSelectMergeMaxK) {
+    hipLaunchKernelGGL(flat_merge_select_kernel, dim3(static_cast<unsigned>(nq)), dim3(1024), 0, s, part_r, part_d,
+                       nsplit, k, d_rows, d_dist);
+    QVH_HIP(hipGetLastError());
+    return;
+  }
+  const dim3 grid(static_cast<unsigned>(ceil_div(nq, 4))), block(256);
+  const uint32_t q32 = static_cast<uint32_t>(nq);
+  if (nsplit <= 64) {
+    hipLaunchKernelGGL(flat_merge_sorted_kernel<1>, grid, block, 0, s, part_r, part_d, q32, nsplit, k, d_rows, d_dist);
+  } else if (nsplit <= 128) {
+    hipLaunchKernelGGL(flat_merge_sorted_kernel<2>, grid, block, 0, s, part_r, part_d, q32, nsplit, k, d_rows, d_dist);
+  } else if (nsplit <= 256) {
+    hipLaunchKernelGGL(flat_merge_sorted_kernel<4>, grid, block, 0, s, part_r, part_d, q32, nsplit, k, d_rows, d_dist);
+  } else if (nsplit <= 512) {
+    hipLaunchKernelGGL(flat_merge_sorted_kernel<8>, grid, block, 0, s, part_r, part_d, q32, nsplit, k, d_rows, d_dist);
+  } else {
+    hipLaunchKernelGGL(flat_merge_sorted_kernel<16>, grid, block, 0, s, part_r, part_d, q32, nsplit, k, d_rows, d_dist);
+  }
+  QVH_HIP(hipGetLastError());
 }
 
 void launch_exact(const ExactArgs& a, uint64_t nq, hipStream_t s) {
@@ -866,17 +1196,25 @@ void flat_grow(qvh_flat* f, uint64_t need) {
 }
 
 /// Prepared queries (normalized for cosine, padded) and their norms in the handle workspace.
-void flat_prep_queries(qvh_flat* f, const float* d_raw, uint64_t nq, hipStream_t s) {
-  float* qs = static_cast<float*>(f->w_stage.reserve(nq * f->dim * sizeof(float)));
-  if (qs != d_raw) QVH_HIP(hipMemcpyAsync(qs, d_raw, nq * f->dim * sizeof(float), hipMemcpyDeviceToDevice, s));
-  if (f->metric == QVH_METRIC_COSINE) launch_normalize_rows(qs, nq, f->dim, s);
+/// Queries into w_q ([nq][dp], normalized for cosine) and, for the MFMA scan, their squared norms
+/// into w_qn.
+void flat_prep_queries(qvh_flat* f, const float* d_raw, uint64_t nq, hipStream_t s, bool norms) {
+  const float* qs = d_raw;
+  if (f->metric == QVH_METRIC_COSINE) {  // normalized in a copy
+    float* w = static_cast<float*>(f->w_stage.reserve(nq * f->dim * sizeof(float)));
+    if (w != d_raw) QVH_HIP(hipMemcpyAsync(w, d_raw, nq * f->dim * sizeof(float), hipMemcpyDeviceToDevice, s));
+    launch_normalize_rows(w, nq, f->dim, s);
+    qs = w;
+  }
   float* qp = static_cast<float*>(f->w_q.reserve(nq * f->dp * sizeof(float)));
-  float* qn = static_cast<float*>(f->w_qn.reserve(nq * sizeof(float)));
   const uint64_t total = nq * f->dp;
   hipLaunchKernelGGL(pack_rows_kernel, dim3(static_cast<unsigned>(ceil_div(total, 256))), dim3(256), 0, s,
                      qs, qp, nq, f->dim, f->dp);
-  hipLaunchKernelGGL(row_norms_kernel, dim3(static_cast<unsigned>(ceil_div(nq, 256))), dim3(256), 0, s,
-                     qp, qn, nq, f->dp);
+  if (norms) {
+    float* qn = static_cast<float*>(f->w_qn.reserve(nq * sizeof(float)));
+    hipLaunchKernelGGL(row_norms_kernel, dim3(static_cast<unsigned>(ceil_div(nq, 256))), dim3(256), 0, s,
+                       qp, qn, nq, f->dp);
+  }
   QVH_HIP(hipGetLastError());
 }
 
@@ -889,15 +1227,21 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
   if (k > kExactMaxK) {
     throw Failure(QVH_EUNSUPPORTED, "flat search: k > " + std::to_string(kExactMaxK) + " is not supported on the device path");
   }
+  // At most kFewMaxQ queries with 32 <= dim <= kFewMaxDim and k <= kFewMaxK: the few-query scan;
+  // other batches of at most kSplitMaxQueries: the exact kernel over row splits. Otherwise k <= 32:
+  // the MFMA scan with per-lane lists of KL = 16 or 32 and a shared bound; 32 < k <= kWideMaxK:
+  // the same scan without the shared bound and the wide merge (its rare fallback queries on the
+  // exact kernel); larger k or dim: the exact kernel.
+  const bool splittable = !d_idx && f->n >= 2 * kMinSplitRows;
+  const bool few = splittable && nq <= kFewMaxQ && k <= kFewMaxK && f->dim >= 32 && f->dim <= kFewMaxDim;
+  const bool split = splittable && !few && nq <= kSplitMaxQueries;
+  const bool wide = !few && !split && k > 32 && k <= kWideMaxK && f->dp <= static_cast<uint32_t>(kMaxDp) && !d_idx;
+  const bool exact_only = !few && !split && !wide && (k > 32 || f->dp > static_cast<uint32_t>(kMaxDp));
+  f->last_wide = wide;
   f->timed = f->timing;
   if (f->timed) QVH_HIP(hipEventRecord(f->ev[0], s));
-  flat_prep_queries(f, d_queries, nq, s);
+  flat_prep_queries(f, d_queries, nq, s, !(few || split || exact_only));
   if (f->timed) QVH_HIP(hipEventRecord(f->ev[1], s));
-  // k <= 32: the MFMA scan with per-lane lists of KL = 16 or 32 and a shared bound; 32 < k <=
-  // kWideMaxK: the same scan without the shared bound and the wide merge (its rare fallback
-  // queries on the exact kernel); larger k or dim: the exact kernel.
-  const bool wide = k > 32 && k <= kWideMaxK && f->dp <= static_cast<uint32_t>(kMaxDp) && !d_idx;
-  f->last_wide = wide;
   ExactArgs e{};
   e.X = f->rows.as<float>();
   e.dp = f->dp;
@@ -913,7 +1257,53 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
   e.qcount = nullptr;
   int cus = 256;
   (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, f->device);
-  if (nq <= kSplitMaxQueries && !d_idx && f->n >= 2 * kMinSplitRows) {
+  if (few) {
+    // A few queries of moderate width: the coalesced few-query kernel reads each row once for
+    // the whole batch, over enough row splits to give every CU four work-groups.
+    uint64_t g = std::min<uint64_t>({static_cast<uint64_t>(kFewMaxSplits), f->n / kMinSplitRows,
+                                     static_cast<uint64_t>(cus) * 4});
+    const uint64_t rps = ceil_div(ceil_div(f->n, g), kFewRowsPerStep) * kFewRowsPerStep;
+    g = ceil_div(f->n, rps);
+    const size_t parts = static_cast<size_t>(nq) * g * k;
+    FewArgs fa;
+    fa.X = f->rows.as<float>();
+    fa.dp = f->dp;
+    fa.dim = f->dim;
+    fa.n = f->n;
+    fa.Q = f->w_q.as<float>();
+    fa.nq = static_cast<uint32_t>(nq);
+    fa.k = k;
+    fa.bitmap = d_bitmap;
+    fa.rows_per_split = rps;
+    fa.nsplit = static_cast<uint32_t>(g);
+    fa.part_r = static_cast<uint32_t*>(f->w_pr.reserve(parts * sizeof(uint32_t)));
+    fa.part_d = static_cast<float*>(f->w_pd.reserve(parts * sizeof(float)));
+    const bool l2 = f->metric == QVH_METRIC_L2;
+    const dim3 grid(static_cast<unsigned>(g)), block(kFewThreads);
+    const bool tail = f->dim % 32 != 0;
+    auto go = [&](auto nqc) {
+      constexpr int NQ = decltype(nqc)::value;
+      auto kern = l2 ? (tail ? flat_few_kernel<NQ, true, true> : flat_few_kernel<NQ, true, false>)
+                     : (tail ? flat_few_kernel<NQ, false, true> : flat_few_kernel<NQ, false, false>);
+      hipLaunchKernelGGL(kern, grid, block, 0, s, fa);
+    };
+    if (nq <= 1) {
+      go(std::integral_constant<int, 1>{});
+    } else if (nq <= 2) {
+      go(std::integral_constant<int, 2>{});
+    } else if (nq <= 4) {
+      go(std::integral_constant<int, 4>{});
+    } else {
+      go(std::integral_constant<int, 8>{});
+    }
+    QVH_HIP(hipGetLastError());
+    if (f->timed) QVH_HIP(hipEventRecord(f->ev[2], s));
+    launch_sorted_merge(fa.part_r, fa.part_d, nq, fa.nsplit, k, d_rows, d_dist, s);
+    f->last_nsplit = g;
+    if (f->timed) QVH_HIP(hipEventRecord(f->ev[3], s));
+    return;
+  }
+  if (split) {
     // A few queries: the MFMA scan's 256-query blocks would run mostly empty. Split each query's
     // rows over enough exact-kernel work-groups to give every CU eight, then merge.
     const uint64_t want = ceil_div(static_cast<uint64_t>(cus) * 8, nq);
@@ -928,26 +1318,12 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
     e.out_dist = static_cast<float*>(f->w_pd.reserve(parts * sizeof(float)));
     launch_exact(e, nq, s);
     if (f->timed) QVH_HIP(hipEventRecord(f->ev[2], s));
-    const dim3 mgrid(static_cast<unsigned>(ceil_div(nq, 4))), mblock(256);
-    const uint32_t ns = e.nsplit;
-    if (g <= 64) {
-      hipLaunchKernelGGL(flat_merge_sorted_kernel<1>, mgrid, mblock, 0, s, e.out_rows, e.out_dist, nq, ns, k, d_rows, d_dist);
-    } else if (g <= 128) {
-      hipLaunchKernelGGL(flat_merge_sorted_kernel<2>, mgrid, mblock, 0, s, e.out_rows, e.out_dist, nq, ns, k, d_rows, d_dist);
-    } else if (g <= 256) {
-      hipLaunchKernelGGL(flat_merge_sorted_kernel<4>, mgrid, mblock, 0, s, e.out_rows, e.out_dist, nq, ns, k, d_rows, d_dist);
-    } else if (g <= 512) {
-      hipLaunchKernelGGL(flat_merge_sorted_kernel<8>, mgrid, mblock, 0, s, e.out_rows, e.out_dist, nq, ns, k, d_rows, d_dist);
-    } else {
-      hipLaunchKernelGGL(flat_merge_sorted_kernel<16>, mgrid, mblock, 0, s, e.out_rows, e.out_dist, nq, ns, k, d_rows, d_dist);
-    }
-    QVH_HIP(hipGetLastError());
-    f->last_wide = false;
+    launch_sorted_merge(e.out_rows, e.out_dist, nq, e.nsplit, k, d_rows, d_dist, s);
     f->last_nsplit = g;
     if (f->timed) QVH_HIP(hipEventRecord(f->ev[3], s));
     return;
   }
-  if (!wide && (k > 32 || f->dp > static_cast<uint32_t>(kMaxDp))) {
+  if (exact_only) {
     launch_exact(e, nq, s);
     f->last_nsplit = 0;
     if (f->timed) {

@@ -167,6 +167,19 @@ def test_small_batches_split_rows(oracle, metric, nq, k, n):
     print(_check(oracle, base, q, k, metric))
 
 
+@pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
+@pytest.mark.parametrize("dim,nq,k,n", [(32, 1, 10, 700_000), (40, 2, 64, 100_000), (47, 3, 1, 60_000),
+                                        (61, 8, 33, 120_000), (100, 5, 10, 2_048), (128, 4, 20, 150_000),
+                                        (159, 7, 64, 50_000), (96, 6, 16, 33_333)])
+def test_few_query_coalesced_scan(oracle, metric, dim, nq, k, n):
+    """At most eight queries with 32 <= dim <= 159 and k <= 64: eight lanes per row replay the
+    reference's accumulation order (32-element blocks, 8-element blocks, the rounded and fused
+    tail: dims 40, 47 and 61 take every branch) and each row is read once for the batch."""
+    base = D.gaussian(n, dim, seed=33)
+    q = D.gaussian(nq, dim, seed=34)
+    print(_check(oracle, base, q, k, metric))
+
+
 @pytest.mark.parametrize("fraction", [0.6, 0.95])
 def test_small_batches_split_rows_filtered_and_ties(oracle, fraction):
     """Integer data (many exactly equal distances across splits) with a row filter above half
