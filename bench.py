@@ -13,7 +13,8 @@ resident in HBM):
 
 Prints ONE JSON line. `value` is the flat workload's queries per second (query prep + fused MFMA
 scan + merge/exact re-score), timed over K steps with the device synchronized on both sides;
-the "ivfpq" object carries the same fields for the IVF-PQ workload. `roofline` is each
+the "ivfpq" object carries the same fields for the IVF-PQ workload, and "flat_small_batches" the
+flat search time of one and of eight of the same queries. `roofline` is each
 workload's dominant kernel measured with HIP events on the stream it runs on: the flat scan's
 algorithmic 2*n*d*nq FLOP per launch against the dense FP32 matrix peak (157.3 TFLOP/s), the
 IVF-PQ list scan's algorithmic code bytes (sum over queries and probed lists of len * m) against
@@ -192,6 +193,24 @@ def bench_flat(args, hip: Hip, qvh: Qvh):
         "config": {"workload": "flat exact L2 k=10: 1,000,000 x 128 fp32 integer-valued mixture, "
                                "10,000 queries batched", "n": n, "dim": dim, "nq": nq, "k": k},
     }
+    if not args.no_extra:
+        # Small batches (the first 1 and 8 queries; the few-query kernels): device time of one
+        # search from its stage events, and the caller's wall time of search + sync.
+        small = {}
+        for b in (1, 8):
+            dev, wall = [], []
+            for _ in range(21):
+                t = time.perf_counter()
+                qvh.check(qvh.lib.qvh_flat_search_device(h, d_q, b, k, None, d_rows, d_dist, None), "search")
+                qvh.check(qvh.lib.qvh_flat_sync(h), "sync")
+                wall.append(time.perf_counter() - t)
+                p, s, m, ns = C.c_float(), C.c_float(), C.c_float(), C.c_uint32()
+                qvh.check(qvh.lib.qvh_flat_last_timing(h, C.byref(p), C.byref(s), C.byref(m), C.byref(ns)),
+                          "timing")
+                dev.append(p.value + s.value + m.value)
+            small[f"nq{b}"] = {"device_us": float(np.median(dev[1:])) * 1e3,
+                               "wall_us": float(np.median(wall[1:])) * 1e6}
+        result["small_batches"] = small
     qvh.lib.qvh_flat_destroy(h)
     for p in (d_q, d_rows, d_dist):
         hip.lib.hipFree(p)
@@ -457,6 +476,7 @@ def main():
     idx, ivf = bench_ivfpq(args, hip, qvh, base, queries)
     extra = {}
     if not args.no_extra:
+        extra["flat_small_batches"] = flat["small_batches"]
         extra["flat_cosine_filtered"] = bench_flat_filtered(args, qvh)
         extra["ivfpq_cosine_refine"] = bench_ivfpq_cosine_refine(args, hip, qvh)
     cpu = None
