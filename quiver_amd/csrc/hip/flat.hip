@@ -699,7 +699,8 @@ constexpr int kFewThreads = 256;
 constexpr int kFewWaves = kFewThreads / 64;
 constexpr int kFewRowsPerStep = kFewWaves * 8;
 constexpr int kFewCap = 128;  // per (query, wave) queue
-constexpr uint32_t kFewMaxQ = 8;
+constexpr uint32_t kFewMaxQ = 8;       // queries per launch
+constexpr uint32_t kFewMaxBatch = 16;  // larger batches take the MFMA scan
 constexpr uint32_t kFewMaxK = 64;
 constexpr uint32_t kFewMaxDim = 159;  // four 32-element blocks, then up to three 8-blocks and a tail
 constexpr uint32_t kFewMaxDp = 160;
@@ -1227,13 +1228,14 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
   if (k > kExactMaxK) {
     throw Failure(QVH_EUNSUPPORTED, "flat search: k > " + std::to_string(kExactMaxK) + " is not supported on the device path");
   }
-  // At most kFewMaxQ queries with 32 <= dim <= kFewMaxDim and k <= kFewMaxK: the few-query scan;
+  // At most kFewMaxBatch queries with 32 <= dim <= kFewMaxDim and k <= kFewMaxK: the few-query
+  // scan, kFewMaxQ queries per launch;
   // other batches of at most kSplitMaxQueries: the exact kernel over row splits. Otherwise k <= 32:
   // the MFMA scan with per-lane lists of KL = 16 or 32 and a shared bound; 32 < k <= kWideMaxK:
   // the same scan without the shared bound and the wide merge (its rare fallback queries on the
   // exact kernel); larger k or dim: the exact kernel.
   const bool splittable = !d_idx && f->n >= 2 * kMinSplitRows;
-  const bool few = splittable && nq <= kFewMaxQ && k <= kFewMaxK && f->dim >= 32 && f->dim <= kFewMaxDim;
+  const bool few = splittable && nq <= kFewMaxBatch && k <= kFewMaxK && f->dim >= 32 && f->dim <= kFewMaxDim;
   const bool split = splittable && !few && nq <= kSplitMaxQueries;
   const bool wide = !few && !split && k > 32 && k <= kWideMaxK && f->dp <= static_cast<uint32_t>(kMaxDp) && !d_idx;
   const bool exact_only = !few && !split && !wide && (k > 32 || f->dp > static_cast<uint32_t>(kMaxDp));
@@ -1259,46 +1261,52 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
   (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, f->device);
   if (few) {
     // A few queries of moderate width: the coalesced few-query kernel reads each row once for
-    // the whole batch, over enough row splits to give every CU four work-groups.
+    // each launch of up to kFewMaxQ queries, over enough row splits to give every CU four
+    // work-groups; one merge then serves the whole batch.
     uint64_t g = std::min<uint64_t>({static_cast<uint64_t>(kFewMaxSplits), f->n / kMinSplitRows,
                                      static_cast<uint64_t>(cus) * 4});
     const uint64_t rps = ceil_div(ceil_div(f->n, g), kFewRowsPerStep) * kFewRowsPerStep;
     g = ceil_div(f->n, rps);
     const size_t parts = static_cast<size_t>(nq) * g * k;
-    FewArgs fa;
-    fa.X = f->rows.as<float>();
-    fa.dp = f->dp;
-    fa.dim = f->dim;
-    fa.n = f->n;
-    fa.Q = f->w_q.as<float>();
-    fa.nq = static_cast<uint32_t>(nq);
-    fa.k = k;
-    fa.bitmap = d_bitmap;
-    fa.rows_per_split = rps;
-    fa.nsplit = static_cast<uint32_t>(g);
-    fa.part_r = static_cast<uint32_t*>(f->w_pr.reserve(parts * sizeof(uint32_t)));
-    fa.part_d = static_cast<float*>(f->w_pd.reserve(parts * sizeof(float)));
+    uint32_t* part_r = static_cast<uint32_t*>(f->w_pr.reserve(parts * sizeof(uint32_t)));
+    float* part_d = static_cast<float*>(f->w_pd.reserve(parts * sizeof(float)));
     const bool l2 = f->metric == QVH_METRIC_L2;
     const dim3 grid(static_cast<unsigned>(g)), block(kFewThreads);
     const bool tail = f->dim % 32 != 0;
-    auto go = [&](auto nqc) {
-      constexpr int NQ = decltype(nqc)::value;
-      auto kern = l2 ? (tail ? flat_few_kernel<NQ, true, true> : flat_few_kernel<NQ, true, false>)
-                     : (tail ? flat_few_kernel<NQ, false, true> : flat_few_kernel<NQ, false, false>);
-      hipLaunchKernelGGL(kern, grid, block, 0, s, fa);
-    };
-    if (nq <= 1) {
-      go(std::integral_constant<int, 1>{});
-    } else if (nq <= 2) {
-      go(std::integral_constant<int, 2>{});
-    } else if (nq <= 4) {
-      go(std::integral_constant<int, 4>{});
-    } else {
-      go(std::integral_constant<int, 8>{});
+    for (uint64_t q0 = 0; q0 < nq; q0 += kFewMaxQ) {
+      const uint64_t nc = std::min<uint64_t>(kFewMaxQ, nq - q0);
+      FewArgs fa;
+      fa.X = f->rows.as<float>();
+      fa.dp = f->dp;
+      fa.dim = f->dim;
+      fa.n = f->n;
+      fa.Q = f->w_q.as<float>() + q0 * f->dp;
+      fa.nq = static_cast<uint32_t>(nc);
+      fa.k = k;
+      fa.bitmap = d_bitmap;
+      fa.rows_per_split = rps;
+      fa.nsplit = static_cast<uint32_t>(g);
+      fa.part_r = part_r + q0 * g * k;  // [query][split][k]
+      fa.part_d = part_d + q0 * g * k;
+      auto go = [&](auto nqc) {
+        constexpr int NQ = decltype(nqc)::value;
+        auto kern = l2 ? (tail ? flat_few_kernel<NQ, true, true> : flat_few_kernel<NQ, true, false>)
+                       : (tail ? flat_few_kernel<NQ, false, true> : flat_few_kernel<NQ, false, false>);
+        hipLaunchKernelGGL(kern, grid, block, 0, s, fa);
+      };
+      if (nc <= 1) {
+        go(std::integral_constant<int, 1>{});
+      } else if (nc <= 2) {
+        go(std::integral_constant<int, 2>{});
+      } else if (nc <= 4) {
+        go(std::integral_constant<int, 4>{});
+      } else {
+        go(std::integral_constant<int, 8>{});
+      }
+      QVH_HIP(hipGetLastError());
     }
-    QVH_HIP(hipGetLastError());
     if (f->timed) QVH_HIP(hipEventRecord(f->ev[2], s));
-    launch_sorted_merge(fa.part_r, fa.part_d, nq, fa.nsplit, k, d_rows, d_dist, s);
+    launch_sorted_merge(part_r, part_d, nq, static_cast<uint32_t>(g), k, d_rows, d_dist, s);
     f->last_nsplit = g;
     if (f->timed) QVH_HIP(hipEventRecord(f->ev[3], s));
     return;

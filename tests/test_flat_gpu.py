@@ -170,24 +170,28 @@ def test_small_batches_split_rows(oracle, metric, nq, k, n):
 @pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
 @pytest.mark.parametrize("dim,nq,k,n", [(32, 1, 10, 700_000), (40, 2, 64, 100_000), (47, 3, 1, 60_000),
                                         (61, 8, 33, 120_000), (100, 5, 10, 2_048), (128, 4, 20, 150_000),
-                                        (159, 7, 64, 50_000), (96, 6, 16, 33_333)])
+                                        (159, 7, 64, 50_000), (96, 6, 16, 33_333), (64, 13, 10, 80_000),
+                                        (128, 16, 64, 40_000)])
 def test_few_query_coalesced_scan(oracle, metric, dim, nq, k, n):
-    """At most eight queries with 32 <= dim <= 159 and k <= 64: eight lanes per row replay the
+    """At most sixteen queries with 32 <= dim <= 159 and k <= 64: eight lanes per row replay the
     reference's accumulation order (32-element blocks, 8-element blocks, the rounded and fused
-    tail: dims 40, 47 and 61 take every branch) and each row is read once for the batch."""
+    tail: dims 40, 47 and 61 take every branch); each launch reads a row once for up to eight
+    queries (13 and 16 queries: two launches, one merge)."""
     base = D.gaussian(n, dim, seed=33)
     q = D.gaussian(nq, dim, seed=34)
     print(_check(oracle, base, q, k, metric))
 
 
+@pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
 @pytest.mark.parametrize("fraction", [0.6, 0.95])
-def test_small_batches_split_rows_filtered_and_ties(oracle, fraction):
+def test_small_batches_split_rows_filtered_and_ties(oracle, fraction, metric):
     """Integer data (many exactly equal distances across splits) with a row filter above half
     density (the bitmap is tested per row)."""
-    base, q = D.int_mix(300_000, 4)
+    base, q = D.int_mix(300_000, 12)
     allowed = D.allowed_ids(base.shape[0], fraction, seed=41)
-    print(_check(oracle, base, q, 10, "l2", allowed))
-    print(_check(oracle, base, q[:1], 50, "l2"))
+    print(_check(oracle, base, q[:4], 10, metric, allowed))
+    print(_check(oracle, base, q, 10, metric, allowed))
+    print(_check(oracle, base, q[:1], 50, metric))
 
 
 def test_integer_data_exact_ties(oracle):
