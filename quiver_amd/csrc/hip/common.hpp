@@ -130,11 +130,42 @@ __device__ __forceinline__ uint64_t make_key(float d, uint32_t id) {
   return (static_cast<uint64_t>(float_to_ordered(d)) << 32) | id;
 }
 
+/// v from the lane that the DPP control CTRL selects (all rows and banks enabled).
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false));
+}
+
+/// The key of lane (lane ^ stride). Strides 1 and 2 are quad permutations, 4 is row_half_mirror
+/// (i -> 7 - i within eight lanes) then quad_perm [3,2,1,0] (i -> i ^ 3), and 8 is a rotation by
+/// 8 within the 16-lane row: all DPP moves, which stay in the VALU. Strides 16 and 32 cross rows
+/// and go through ds_bpermute.
+__device__ __forceinline__ uint64_t lane_xor_u64(uint64_t v, int stride) {
+  const uint32_t lo = static_cast<uint32_t>(v), hi = static_cast<uint32_t>(v >> 32);
+  uint32_t plo, phi;
+  if (stride == 1) {
+    plo = dpp_u32<0xB1>(lo);
+    phi = dpp_u32<0xB1>(hi);
+  } else if (stride == 2) {
+    plo = dpp_u32<0x4E>(lo);
+    phi = dpp_u32<0x4E>(hi);
+  } else if (stride == 4) {
+    plo = dpp_u32<0x1B>(dpp_u32<0x141>(lo));
+    phi = dpp_u32<0x1B>(dpp_u32<0x141>(hi));
+  } else if (stride == 8) {
+    plo = dpp_u32<0x128>(lo);
+    phi = dpp_u32<0x128>(hi);
+  } else {
+    return __shfl_xor(v, stride, 64);
+  }
+  return (static_cast<uint64_t>(phi) << 32) | plo;
+}
+
 /// Wave-wide (64 lanes) minimum of a 64-bit key.
 __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
-    const uint64_t o = __shfl_xor(v, off, 64);
+    const uint64_t o = lane_xor_u64(v, off);
     v = o < v ? o : v;
   }
   return v;

@@ -13,6 +13,8 @@
 
 #include <cstdint>
 
+#include "common.hpp"
+
 namespace qvh {
 
 /// Ascending bitonic sort of N * 64 keys held by one wave, element e = i * 64 + lane in k[i].
@@ -40,7 +42,7 @@ __device__ __forceinline__ void wave_sort(uint64_t (&k)[N]) {
       } else {
 #pragma unroll
         for (int i = 0; i < N; ++i) {
-          const uint64_t other = __shfl_xor(k[i], stride, 64);
+          const uint64_t other = lane_xor_u64(k[i], stride);
           const bool up = ((i * 64 + lane) & size) == 0;
           const bool lower = (lane & stride) == 0;
           k[i] = (lower == up) ? (other < k[i] ? other : k[i]) : (other > k[i] ? other : k[i]);
@@ -71,7 +73,7 @@ __device__ __forceinline__ void wave_merge(uint64_t (&k)[N]) {
     } else {
 #pragma unroll
       for (int i = 0; i < N; ++i) {
-        const uint64_t other = __shfl_xor(k[i], stride, 64);
+        const uint64_t other = lane_xor_u64(k[i], stride);
         const bool lower = (lane & stride) == 0;
         k[i] = lower ? (other < k[i] ? other : k[i]) : (other > k[i] ? other : k[i]);
       }
