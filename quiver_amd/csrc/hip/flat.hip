@@ -646,7 +646,9 @@ __global__ void __launch_bounds__(kExactThreads) flat_exact_kernel(ExactArgs a) 
       cnt += static_cast<uint32_t>(__popcll(mk));
       if (cnt > static_cast<uint32_t>(CAP - 64)) cut();
     }
-    const uint32_t shared_thr = *static_cast<volatile uint32_t*>(&s_thr);
+    // An atomic load at workgroup scope stays an LDS read; a volatile read of this reference
+    // became a flat load whose wait also drained the next step's loads.
+    const uint32_t shared_thr = __hip_atomic_load(&s_thr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (shared_thr < thr_bits) {
       thr_bits = shared_thr;
       thr = ordered_to_float(shared_thr);

@@ -1283,7 +1283,9 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
       flush();
       __syncthreads();
     }
-    const uint32_t shared_thr = *static_cast<volatile uint32_t*>(&s_thr);
+    // An atomic load at workgroup scope stays an LDS read; a volatile read of this reference
+    // became a flat load whose wait also drained the next step's loads.
+    const uint32_t shared_thr = __hip_atomic_load(&s_thr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (shared_thr < thr_bits) {
       thr_bits = shared_thr;
       thr = ordered_to_float(shared_thr);
