@@ -283,16 +283,20 @@ __global__ void scatter_new_kernel(ScatterArgs a) {
 
 // ---- search: coarse scores and probe selection ------------------------------------------------
 
-constexpr int kCoarseQ = 8;  // queries per coarse workgroup
+constexpr int kCoarseQ = 8;              // queries per coarse workgroup
+constexpr uint64_t kCoarseSingleMaxQ = 128;  // smaller batches: one query per workgroup
 
 /// Coarse scores (src/ivfpq_index.cc:285-297): L2: sum_j (q_j - c_j)^2; IP/cosine: -sum_j q_j c_j,
 /// both in order of j (centroid_table.h:65-85). Stored as the reference's probe key. One thread
-/// per centroid and kCoarseQ queries per work-group; the query values are block-uniform, so they
-/// come in through scalar loads and the vector unit does only the arithmetic.
-template <bool IP>
+/// per centroid and QB queries per work-group (kCoarseQ, or 1 for small batches, which would
+/// otherwise leave most CUs idle and compute padding queries); the query values are
+/// block-uniform, so they come in through scalar loads and the vector unit does only the
+/// arithmetic.
+template <bool IP, int QB>
 __global__ void __launch_bounds__(256) coarse_kernel(const float* __restrict__ Q, uint32_t nq, uint32_t dim,
                                                      const float* __restrict__ ct, uint32_t nlist,
                                                      float* __restrict__ scores) {
+  constexpr int kCoarseQ = QB;
   const uint32_t c = blockIdx.x * 256 + threadIdx.x;
   const uint32_t q0 = blockIdx.y * kCoarseQ;
   const uint32_t nb = min(static_cast<uint32_t>(kCoarseQ), nq - q0);
@@ -303,15 +307,18 @@ __global__ void __launch_bounds__(256) coarse_kernel(const float* __restrict__ Q
   float acc[kCoarseQ];
 #pragma unroll
   for (int b = 0; b < kCoarseQ; ++b) acc[b] = 0.0f;
+  // Centroid values are fetched JB at a time: with one query the sum chain is short, so more of
+  // them must be in flight to cover the load latency.
+  constexpr int JB = QB == 1 ? 16 : 4;
   uint32_t j = 0;
-  for (; j + 4 <= dim; j += 4) {
-    float cj[4];
+  for (; j + JB <= dim; j += JB) {
+    float cj[JB];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) cj[t] = ct[static_cast<uint64_t>(j + t) * nlist + cc];
+    for (int t = 0; t < JB; ++t) cj[t] = ct[static_cast<uint64_t>(j + t) * nlist + cc];
 #pragma unroll
     for (int b = 0; b < kCoarseQ; ++b) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
+      for (int t = 0; t < JB; ++t) {
         const float qv = qrow[b][j + t];
         if (IP) {
           acc[b] = acc[b] + qv * cj[t];
@@ -1791,14 +1798,14 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   // coarse scores + probes
   float* scores = static_cast<float*>(h->w_scores.reserve(nq * h->nlist * sizeof(float)));
   {
-    const dim3 grid(static_cast<unsigned>(ceil_div(h->nlist, 256)), static_cast<unsigned>(ceil_div(nq, kCoarseQ)));
-    if (h->metric != QVH_METRIC_L2) {
-      hipLaunchKernelGGL(coarse_kernel<true>, grid, dim3(256), 0, s, dq, static_cast<uint32_t>(nq), h->dim,
-                         h->cent_t.as<float>(), h->nlist, scores);
-    } else {
-      hipLaunchKernelGGL(coarse_kernel<false>, grid, dim3(256), 0, s, dq, static_cast<uint32_t>(nq), h->dim,
-                         h->cent_t.as<float>(), h->nlist, scores);
-    }
+    const bool single = nq <= kCoarseSingleMaxQ;
+    const dim3 grid(static_cast<unsigned>(ceil_div(h->nlist, 256)),
+                    static_cast<unsigned>(single ? nq : ceil_div(nq, kCoarseQ)));
+    const bool ip = h->metric != QVH_METRIC_L2;
+    auto kern = single ? (ip ? coarse_kernel<true, 1> : coarse_kernel<false, 1>)
+                       : (ip ? coarse_kernel<true, kCoarseQ> : coarse_kernel<false, kCoarseQ>);
+    hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, dq, static_cast<uint32_t>(nq), h->dim, h->cent_t.as<float>(),
+                       h->nlist, scores);
   }
   uint32_t* probes = static_cast<uint32_t*>(h->w_probes.reserve(nq * nprobe * sizeof(uint32_t)));
   // Block order of the streaming scan (queries grouped by their smallest probed list): for batches

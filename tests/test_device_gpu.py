@@ -122,7 +122,7 @@ def test_ivfpq_device_untrained_and_growing():
     _same(idx.search(hq, 5, nprobe=8), idx.search(qd, 5, nprobe=8))
 
 
-@pytest.mark.parametrize("kind", ["flat", "ivfpq"])
+@pytest.mark.parametrize("kind", ["flat", "flat_small", "ivfpq"])
 def test_calls_on_two_streams_share_the_handle_safely(kind):
     """Device searches of one handle on two streams, the second growing the handle's workspace,
     then a host search: each call is ordered after the handle's earlier work on the device, so
@@ -132,8 +132,10 @@ def test_calls_on_two_streams_share_the_handle_safely(kind):
     rng = np.random.default_rng(7)
     qa = rng.standard_normal((300, 32)).astype(np.float32)
     qb = rng.standard_normal((6_000, 32)).astype(np.float32)
+    if kind == "flat_small":  # the few-query scan: 5 queries, then 16 (two launches, more partial lists)
+        qa, qb = qa[:5], qb[:16]
     print(f"case: two streams {kind}", flush=True)
-    if kind == "flat":
+    if kind in ("flat", "flat_small"):
         idx = quiver.FlatIndex(32, "l2")
         idx.add(base)
         search = lambda q: idx.search(q, 10)  # noqa: E731
