@@ -881,11 +881,12 @@ __global__ void __launch_bounds__(kScanThreads) ivf_scan_kernel(ScanArgs a) {
 #define QVH_STREAM_ROT 0
 #endif
 // Waves per streaming block: 4 with 128-entry wave queues (four blocks of ~37 KB LDS per CU, 128
-// registers per lane), 8 with 256-entry queues (three blocks of ~49 KB per CU, 80 registers).
+// registers per lane), 8 with 256-entry queues (three blocks of ~49 KB per CU, 80 registers) or
+// with 512-entry queues for candidate sets of 129..256 (two blocks of ~66 KB per CU).
 template <int CAP>
 constexpr int stream_waves() { return CAP == 128 ? 4 : 8; }
 constexpr uint32_t kStreamMaxProbes = 256;
-constexpr uint32_t kStreamMaxSel = 128;
+constexpr uint32_t kStreamMaxSel = 256;
 constexpr int kFinishThreads = 128;
 constexpr uint32_t kStreamMaxM = 64;  // code bytes of the widest streaming kernel
 // Slices per query of a batch smaller than one resident generation of blocks.
@@ -1440,18 +1441,22 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
     if (static_cast<uint32_t>(lane) < a.k) emit(lane, static_cast<uint32_t>(lane) < min(cnt_f, a.k), key);
     return;
   }
-  // Eight waves (keep_sel <= 128): each wave sorts its list (<= CAP / 2 = 128 keys) in registers;
-  // three rounds of pairwise merges then keep the 128 smallest: the elementwise minimum of one
-  // sorted list and the other reversed holds the 128 smallest of both as a bitonic sequence, which
-  // a register bitonic merge orders. Wave 0's region ends with the block's 128 smallest, sorted.
-  // (Four-wave blocks returned above; this is compiled for them too but never reached.)
+  // Eight waves (keep_sel <= CAP / 2): each wave sorts its list (<= CAP / 2 keys, NK per lane) in
+  // registers; three rounds of pairwise merges then keep the CAP / 2 smallest: the elementwise
+  // minimum of one sorted list and the other reversed holds the CAP / 2 smallest of both as a
+  // bitonic sequence, which a register bitonic merge orders. Wave 0's region ends with the block's
+  // CAP / 2 smallest, sorted. (Four-wave blocks returned above; this is compiled for them too but
+  // never reached.)
   uint32_t merged = 0;
-  if constexpr (kStreamWaves == 8 && CAP == 256) {
-  uint64_t mine[2] = {static_cast<uint32_t>(lane) < cnt ? queue[lane] : ~0ull,
-                      static_cast<uint32_t>(lane) + 64 < cnt ? queue[64 + lane] : ~0ull};
-  wave_sort<2>(mine);
-  queue[lane] = mine[0];
-  queue[64 + lane] = mine[1];
+  if constexpr (kStreamWaves == 8 && CAP >= 256) {
+  constexpr int NK = CAP / 128;
+  constexpr int kList = CAP / 2;
+  uint64_t mine[NK];
+#pragma unroll
+  for (int i = 0; i < NK; ++i) mine[i] = static_cast<uint32_t>(i * 64 + lane) < cnt ? queue[i * 64 + lane] : ~0ull;
+  wave_sort<NK>(mine);
+#pragma unroll
+  for (int i = 0; i < NK; ++i) queue[i * 64 + lane] = mine[i];
   if (lane == 0) s_wcount[wave] = cnt;
   __syncthreads();
 #pragma unroll
@@ -1460,12 +1465,14 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
   for (int step = 1; step < kStreamWaves; step *= 2) {
     if (wave % (2 * step) == 0) {
       const uint64_t* other = s_queue + (wave + step) * CAP;
-      const uint64_t o0 = other[127 - lane], o1 = other[63 - lane];
-      mine[0] = o0 < mine[0] ? o0 : mine[0];
-      mine[1] = o1 < mine[1] ? o1 : mine[1];
-      wave_merge<2>(mine);
-      queue[lane] = mine[0];
-      queue[64 + lane] = mine[1];
+#pragma unroll
+      for (int i = 0; i < NK; ++i) {
+        const uint64_t o = other[kList - 1 - (i * 64 + lane)];
+        mine[i] = o < mine[i] ? o : mine[i];
+      }
+      wave_merge<NK>(mine);
+#pragma unroll
+      for (int i = 0; i < NK; ++i) queue[i * 64 + lane] = mine[i];
     }
     __syncthreads();
   }
@@ -1560,7 +1567,7 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
 // Up to 32 code bytes.
 template <int MPW, bool FULL, int CAP, bool ROT = false>
 __global__ void __launch_bounds__(stream_waves<CAP>() * 64)
-__attribute__((amdgpu_waves_per_eu(stream_waves<CAP>() == 4 ? 4 : 6))) ivf_stream_kernel(ScanArgs a) {
+__attribute__((amdgpu_waves_per_eu(stream_waves<CAP>() == 4 || CAP == 512 ? 4 : 6))) ivf_stream_kernel(ScanArgs a) {
   stream_scan<MPW, FULL, CAP, ROT>(a);
 }
 
@@ -1610,7 +1617,9 @@ __global__ void __launch_bounds__(kFinishThreads) ivf_finish_kernel(ScanArgs a) 
     s_score[p] = a.scores[static_cast<uint64_t>(q) * a.nlist + l];
   }
   uint32_t cnt = a.sel_cnt[q];
-  s_key[tid] = static_cast<uint32_t>(tid) < cnt ? a.sel[static_cast<uint64_t>(q) * a.keep_sel + tid] : ~0ull;
+  for (uint32_t i = tid; i < kStreamMaxSel; i += kFinishThreads) {
+    s_key[i] = i < cnt ? a.sel[static_cast<uint64_t>(q) * a.keep_sel + i] : ~0ull;
+  }
   __syncthreads();
   auto list_of = [&](uint32_t pos) {
     for (uint32_t b = 0; b + 1 < a.nprobe; b += 8) {
@@ -1627,30 +1636,28 @@ __global__ void __launch_bounds__(kFinishThreads) ivf_finish_kernel(ScanArgs a) 
   if (a.refine) {
     // Exact re-ranking with the stored vectors (src/ivfpq_index.cc:139-142,363-373).
     __syncthreads();
-    if (static_cast<uint32_t>(tid) < cnt) {
-      const uint32_t pos = static_cast<uint32_t>(s_key[tid]);
+    for (uint32_t i = tid; i < cnt; i += kFinishThreads) {
+      const uint32_t pos = static_cast<uint32_t>(s_key[i]);
       const float* x = a.vec + static_cast<uint64_t>(pos) * a.dim;
       const float d = a.mode == kModeIp ? 1.0f - exact_dot(qv, x, a.dim) : exact_l2sqr(qv, x, a.dim);
-      s_key[tid] = make_key(d, pos);
-    } else {
-      s_key[tid] = ~0ull;
+      s_key[i] = make_key(d, pos);
     }
     finish_sort(s_key, pow2_at_least(max(cnt, 2u)));
   }
   __syncthreads();
   const uint32_t nout = min(cnt, a.k);
-  if (static_cast<uint32_t>(tid) < a.k) {
+  for (uint32_t j = tid; j < a.k; j += kFinishThreads) {
     uint64_t ref = QVH_EMPTY_REF;
     float dist = __builtin_huge_valf();
-    if (static_cast<uint32_t>(tid) < nout) {
-      const uint64_t key = s_key[tid];
+    if (j < nout) {
+      const uint64_t key = s_key[j];
       const uint32_t pos = static_cast<uint32_t>(key);
       const uint32_t pl = list_of(pos);
       ref = (static_cast<uint64_t>(s_list[pl]) << 32) | (pos - s_lo[pl]);
       dist = ordered_to_float(static_cast<uint32_t>(key >> 32));
     }
-    a.out_refs[static_cast<uint64_t>(q) * a.k + tid] = ref;
-    a.out_dist[static_cast<uint64_t>(q) * a.k + tid] = dist;
+    a.out_refs[static_cast<uint64_t>(q) * a.k + j] = ref;
+    a.out_dist[static_cast<uint64_t>(q) * a.k + j] = dist;
   }
 }
 
@@ -1882,16 +1889,18 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
     }
   };
   // The streaming scan covers the table modes with up to 256 probes, m <= 64 and a candidate set of
-  // at most 128; the rest takes the block-buffer scan below.
+  // at most 256; the rest takes the block-buffer scan below.
   const uint32_t mpw_t = mpw <= 2 ? 2 : mpw <= 4 ? 4 : mpw <= 8 ? 8 : 16;  // the kernel's code width in dwords
   const bool full = h->mp == 4 * mpw_t;
   const bool small_sel = a.keep_sel <= 64 && k <= 64;
+  const bool big_sel = !small_sel && (a.keep_sel > 128 || k > 128);  // 512-entry wave queues
+  const uint32_t cap = small_sel ? 128 : big_sel ? 512 : 256;
   const size_t rows = 4 * mpw_t;
   // LDS of the streaming kernels: the table (static LDS for codes of up to 32 bytes), the wave
   // queues and the probed-list arrays (dynamic).
   const size_t lds_table = rows * 256 * sizeof(float);
   const uint32_t waves = small_sel ? stream_waves<128>() : stream_waves<256>();
-  const size_t lds_total = lds_table + waves * (small_sel ? 128 : 256) * sizeof(uint64_t) +
+  const size_t lds_total = lds_table + static_cast<size_t>(waves) * cap * sizeof(uint64_t) +
                            (4 * static_cast<size_t>(nprobe) + 2 + waves) * sizeof(uint32_t);
   const size_t lds2 = mpw_t > 8 ? lds_total : lds_total - lds_table;
   if (!exact_all && mode != kModeResidual && h->mp <= kStreamMaxM && nprobe <= kStreamMaxProbes && a.keep_sel >= 1 &&
@@ -1912,7 +1921,7 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
       uint64_t parts = resident > nq ? std::min<uint64_t>(kMaxSlices, resident / nq) : 1;
       uint64_t sliced = nq;
       // The merging block holds parts * keep keys: in one wave's registers (256) or in the queues.
-      const uint64_t cap_keys = small_sel ? 256u : waves * 256u;
+      const uint64_t cap_keys = small_sel ? 256u : static_cast<uint64_t>(waves) * cap;
       while (parts > 1 && parts * a.keep > cap_keys) --parts;
       if (parts <= 1 || a.keep == 0) sliced = 0;
       a.nwhole = static_cast<uint32_t>(nq - sliced);
@@ -1930,12 +1939,15 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
       const dim3 sgrid(static_cast<unsigned>(a.nwhole + sliced * a.parts));
       hipLaunchKernelGGL(kernel, sgrid, dim3(waves * 64), lds2, s, a);
     };
-#define QVH_STREAM(MPW_)                                                                                  \
-  (full ? (small_sel ? launch2(ivf_stream_kernel<MPW_, true, 128>) : launch2(ivf_stream_kernel<MPW_, true, 256>)) \
-        : (small_sel ? launch2(ivf_stream_kernel<MPW_, false, 128>) : launch2(ivf_stream_kernel<MPW_, false, 256>)))
+#define QVH_STREAM_CAP(KERNEL, ...)                                                    \
+  (small_sel ? launch2(KERNEL<__VA_ARGS__, 128>)                                       \
+             : big_sel ? launch2(KERNEL<__VA_ARGS__, 512>) : launch2(KERNEL<__VA_ARGS__, 256>))
+#define QVH_STREAM(MPW_) \
+  (full ? QVH_STREAM_CAP(ivf_stream_kernel, MPW_, true) : QVH_STREAM_CAP(ivf_stream_kernel, MPW_, false))
     // Bank-rotated lookups: L2 with the precomputed table (re-scored exactly afterwards), four
     // dims per sub-space, 16- or 32-byte codes.
-    const bool rot = QVH_STREAM_ROT && mode == kModePre && full && h->dsub == 4 && (mpw_t == 4 || mpw_t == 8);
+    const bool rot =
+        QVH_STREAM_ROT && mode == kModePre && full && h->dsub == 4 && (mpw_t == 4 || mpw_t == 8) && !big_sel;
     if (rot && mpw_t == 8) {
       small_sel ? launch2(ivf_stream_kernel<8, true, 128, true>) : launch2(ivf_stream_kernel<8, true, 256, true>);
     } else if (rot) {
@@ -1947,11 +1959,12 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
     } else if (mpw_t == 8) {
       QVH_STREAM(8);
     } else if (full) {
-      small_sel ? launch2(ivf_stream_wide_kernel<true, 128>) : launch2(ivf_stream_wide_kernel<true, 256>);
+      QVH_STREAM_CAP(ivf_stream_wide_kernel, true);
     } else {
-      small_sel ? launch2(ivf_stream_wide_kernel<false, 128>) : launch2(ivf_stream_wide_kernel<false, 256>);
+      QVH_STREAM_CAP(ivf_stream_wide_kernel, false);
     }
 #undef QVH_STREAM
+#undef QVH_STREAM_CAP
     QVH_HIP(hipGetLastError());
     if (a.refine) {
       hipLaunchKernelGGL(ivf_finish_kernel, grid, dim3(kFinishThreads), 4 * static_cast<size_t>(nprobe) * sizeof(uint32_t),

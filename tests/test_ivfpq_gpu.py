@@ -96,6 +96,19 @@ def test_ivfpq_batch_sizes_and_slices(oracle, metric, refine):
     print("filtered", compare_search(oracle, idx, st, clustered(6_000, 32, 50, 14), 10, 16, refine, allowed))
 
 
+@pytest.mark.parametrize("metric,k,refine", [("l2", 100, 0), ("l2", 170, 0), ("ip", 200, 0), ("cosine", 150, 0),
+                                             ("l2", 20, 8), ("cosine", 32, 8), ("l2", 65, 0), ("ip", 256, 0)])
+def test_ivfpq_large_candidate_sets(oracle, metric, k, refine):
+    """Candidate sets of 129..256 (k * refine plus the re-score margin for L2) stream through
+    512-entry wave queues: the same results as the oracle, for a batch of whole queries and a
+    sliced small batch."""
+    base = clustered(12_000, 32, 24, seed=41)
+    q = clustered(700, 32, 24, seed=42)
+    idx, st = build_pair(oracle, base, metric, 64, 8, refine > 0)
+    for qs in (q, q[:3]):
+        print(k, refine, qs.shape[0], compare_search(oracle, idx, st, qs, k, 16, refine))
+
+
 @pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
 def test_ivfpq_saturated_refine(oracle, metric):
     """refine_factor 2^63: k * refine_factor wraps, the reference saturates it at the stored count and
