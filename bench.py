@@ -276,6 +276,22 @@ def bench_ivfpq(args, hip: Hip, qvh: Qvh, base, queries):
     hip.d2h(refs, d_refs)
     hip.d2h(dist, d_dist)
     assert (refs != np.uint64(2**64 - 1)).all() and (np.diff(dist, axis=1) >= 0).all(), "malformed results"
+
+    larger_k = {}
+    if not args.no_extra:
+        # The same queries at nprobe 32 with k = 100 (150 candidates re-scored per query).
+        k2 = 100
+        d_refs2, d_dist2 = hip.malloc(nq * k2 * 8), hip.malloc(nq * k2 * 4)
+        scans = []
+        for _ in range(4):
+            qvh.check(qvh.lib.qvh_ivfpq_search_device(h, d_q, nq, k2, nprobe, 0, None, d_refs2, d_dist2, None),
+                      "search")
+            scans.append(timing(with_bytes=False))
+        qvh.check(qvh.lib.qvh_ivfpq_sync(h), "sync")
+        sel2, scan2 = (float(np.median([t[i] for t in scans[1:]])) for i in (0, 1))
+        larger_k = {"k100": {"select_ms": sel2, "scan_ms": scan2, "qps": nq / ((sel2 + scan2) * 1e-3)}}
+        for p in (d_refs2, d_dist2):
+            hip.lib.hipFree(p)
     for p in (d_q, d_refs, d_dist):
         hip.lib.hipFree(p)
 
@@ -294,6 +310,7 @@ def bench_ivfpq(args, hip: Hip, qvh: Qvh, base, queries):
                      "traffic": load_traffic("ivf_stream_int_mix_1m_nprobe32_pmc"),
                      "code_bytes_per_launch": code_bytes},
         "nprobe_sweep": sweep,
+        **larger_k,
         "build": {"train_s": train_s, "add_s": add_s, "encode_vectors_per_s": n / add_s},
         "config": {"workload": "IVF-PQ L2 k=10 nprobe=32: 1,000,000 x 128 fp32 integer-valued mixture, "
                                "nlist 2048, m 32, trained on a 100,000-row sample; 10,000 queries batched",
