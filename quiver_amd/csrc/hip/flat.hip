@@ -935,73 +935,15 @@ __global__ void __launch_bounds__(kFewThreads) flat_few_kernel(FewArgs a) {
   }
 }
 
-/// The k best of a query's nsplit <= 1024 sorted partial lists of k <= 64 exact keys each, one
-/// 1024-thread work-group per query: T0 is the k-th smallest list head; every key of the k best
-/// is <= T0, and only the (at most k) lists whose heads are <= T0 hold such keys, so at most k * k
-/// real keys are gathered and sorted.
-constexpr uint32_t kSelectMergeMaxK = 64;
-constexpr uint32_t kSelectMergeLists = 1024;
-
-__global__ void __launch_bounds__(1024) flat_merge_select_kernel(const uint32_t* __restrict__ part_r,
-                                                                 const float* __restrict__ part_d,
-                                                                 uint32_t nsplit, uint32_t k,
-                                                                 uint32_t* __restrict__ out_rows,
-                                                                 float* __restrict__ out_dist) {
-  __shared__ uint64_t s_heads[kSelectMergeLists];
-  __shared__ uint64_t s_cand[kSelectMergeMaxK * kSelectMergeMaxK];
-  __shared__ uint32_t s_count;
-  const uint32_t tid = threadIdx.x;
-  const uint32_t q = blockIdx.x;
-  const uint32_t* pr = part_r + static_cast<uint64_t>(q) * nsplit * k;
-  const float* pd = part_d + static_cast<uint64_t>(q) * nsplit * k;
-  const uint64_t o = static_cast<uint64_t>(tid) * k;
-  s_heads[tid] = tid < nsplit ? make_key(pd[o], pr[o]) : ~0ull;
-  if (tid == 0) s_count = 0;
-  block_sort_keys(s_heads, kSelectMergeLists);
-  const uint64_t t0 = s_heads[k - 1];
-  if (tid < nsplit) {
-    // this list's keys <= t0, eight at a time
-    for (uint32_t p0 = 0; p0 < k; p0 += 8) {
-      uint64_t key[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) key[i] = p0 + i < k ? make_key(pd[o + p0 + i], pr[o + p0 + i]) : ~0ull;
-      bool more = true;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const bool take = more && static_cast<uint32_t>(key[i]) != QVH_EMPTY_ROW && key[i] <= t0;
-        if (take) s_cand[atomicAdd(&s_count, 1u)] = key[i];
-        more = take;
-      }
-      if (!more) break;
-    }
-  }
-  __syncthreads();
-  const uint32_t c = s_count;
-  uint32_t n2 = 1;
-  while (n2 < c) n2 <<= 1;
-  for (uint32_t i = c + tid; i < n2; i += 1024) s_cand[i] = ~0ull;
-  block_sort_keys(s_cand, n2);
-  for (uint32_t j = tid; j < k; j += 1024) {
-    const bool real = j < c;
-    out_rows[static_cast<uint64_t>(q) * k + j] = real ? static_cast<uint32_t>(s_cand[j]) : QVH_EMPTY_ROW;
-    out_dist[static_cast<uint64_t>(q) * k + j] =
-        real ? ordered_to_float(static_cast<uint32_t>(s_cand[j] >> 32)) : __builtin_huge_valf();
-  }
-}
-
-/// The k best of a query's nsplit sorted partial lists of k exact keys each (rows past a list's
-/// count are QVH_EMPTY_ROW): one wave per query; each step takes the wave minimum of the lanes' list
-/// heads (lists lane, lane + 64, ... per lane). A list's next key is loaded one pop ahead, so a
-/// step waits on memory only when the same list wins twice in a row.
+/// The k best of query q's nsplit sorted partial lists of k exact keys each (rows past a list's
+/// count are QVH_EMPTY_ROW), by one wave: each step takes the wave minimum of the lanes' list heads
+/// (lists lane, lane + 64, ... per lane, up to 64 * LPL lists). A list's next key is loaded one pop
+/// ahead, so a step waits on memory only when the same list wins twice in a row.
 template <int LPL>
-__global__ void __launch_bounds__(256) flat_merge_sorted_kernel(const uint32_t* __restrict__ part_r,
-                                                                const float* __restrict__ part_d, uint32_t nq,
-                                                                uint32_t nsplit, uint32_t k,
-                                                                uint32_t* __restrict__ out_rows,
-                                                                float* __restrict__ out_dist) {
+__device__ void merge_sorted_lists(const uint32_t* __restrict__ part_r, const float* __restrict__ part_d, uint32_t q,
+                                   uint32_t nsplit, uint32_t k, uint32_t* __restrict__ out_rows,
+                                   float* __restrict__ out_dist) {
   const int lane = threadIdx.x & 63;
-  const uint32_t q = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (q >= nq) return;  // whole wave; no block barriers
   const uint32_t* pr = part_r + static_cast<uint64_t>(q) * nsplit * k;
   const float* pd = part_d + static_cast<uint64_t>(q) * nsplit * k;
   auto key_at = [&](uint32_t li, uint32_t p) {
@@ -1055,28 +997,108 @@ __global__ void __launch_bounds__(256) flat_merge_sorted_kernel(const uint32_t* 
   }
 }
 
-/// The k best of each query's nsplit sorted lists [nq][nsplit][k] into [nq][k].
+/// The k best of a query's nsplit <= 1024 sorted partial lists of k <= 256 exact keys each, one
+/// 1024-thread work-group per query: T0 is the k-th smallest list head; every key of the k best
+/// is <= T0, and only the (at most k) lists whose heads are <= T0 hold such keys, so at most k * k
+/// real keys are gathered and sorted. More than kSelectMergeCap of them (possible above k = 64)
+/// flag the query (overflow[q] = 1, else 0) for the sequential merge of the same lists, which
+/// gives the same k keys.
+constexpr uint32_t kSelectMergeMaxK = 256;
+constexpr uint32_t kSelectMergeLists = 1024;
+constexpr uint32_t kSelectMergeCap = 4096;
+
+__global__ void __launch_bounds__(1024) flat_merge_select_kernel(const uint32_t* __restrict__ part_r,
+                                                                 const float* __restrict__ part_d,
+                                                                 uint32_t nsplit, uint32_t k,
+                                                                 uint32_t* __restrict__ out_rows,
+                                                                 float* __restrict__ out_dist,
+                                                                 uint32_t* __restrict__ overflow) {
+  __shared__ uint64_t s_heads[kSelectMergeLists];
+  __shared__ uint64_t s_cand[kSelectMergeCap];
+  __shared__ uint32_t s_count;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t q = blockIdx.x;
+  const uint32_t* pr = part_r + static_cast<uint64_t>(q) * nsplit * k;
+  const float* pd = part_d + static_cast<uint64_t>(q) * nsplit * k;
+  const uint64_t o = static_cast<uint64_t>(tid) * k;
+  s_heads[tid] = tid < nsplit ? make_key(pd[o], pr[o]) : ~0ull;
+  if (tid == 0) s_count = 0;
+  block_sort_keys(s_heads, kSelectMergeLists);
+  const uint64_t t0 = s_heads[k - 1];
+  if (tid < nsplit) {
+    // this list's keys <= t0, eight at a time
+    for (uint32_t p0 = 0; p0 < k; p0 += 8) {
+      uint64_t key[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) key[i] = p0 + i < k ? make_key(pd[o + p0 + i], pr[o + p0 + i]) : ~0ull;
+      bool more = true;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const bool take = more && static_cast<uint32_t>(key[i]) != QVH_EMPTY_ROW && key[i] <= t0;
+        if (take) {
+          const uint32_t at = atomicAdd(&s_count, 1u);
+          if (at < kSelectMergeCap) s_cand[at] = key[i];
+        }
+        more = take;
+      }
+      if (!more) break;
+    }
+  }
+  __syncthreads();
+  const uint32_t c = s_count;
+  if (overflow && tid == 0) overflow[q] = c > kSelectMergeCap ? 1u : 0u;
+  if (c > kSelectMergeCap) return;  // block-uniform
+  uint32_t n2 = 1;
+  while (n2 < c) n2 <<= 1;
+  for (uint32_t i = c + tid; i < n2; i += 1024) s_cand[i] = ~0ull;
+  block_sort_keys(s_cand, n2);
+  for (uint32_t j = tid; j < k; j += 1024) {
+    const bool real = j < c;
+    out_rows[static_cast<uint64_t>(q) * k + j] = real ? static_cast<uint32_t>(s_cand[j]) : QVH_EMPTY_ROW;
+    out_dist[static_cast<uint64_t>(q) * k + j] =
+        real ? ordered_to_float(static_cast<uint32_t>(s_cand[j] >> 32)) : __builtin_huge_valf();
+  }
+}
+
+/// One wave per query of merge_sorted_lists (only the queries flagged in `only`, when given).
+template <int LPL>
+__global__ void __launch_bounds__(256) flat_merge_sorted_kernel(const uint32_t* __restrict__ part_r,
+                                                                const float* __restrict__ part_d, uint32_t nq,
+                                                                uint32_t nsplit, uint32_t k,
+                                                                uint32_t* __restrict__ out_rows,
+                                                                float* __restrict__ out_dist,
+                                                                const uint32_t* __restrict__ only) {
+  const uint32_t q = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (q >= nq || (only && only[q] == 0)) return;  // whole wave; no block barriers
+  merge_sorted_lists<LPL>(part_r, part_d, q, nsplit, k, out_rows, out_dist);
+}
+
+/// The k best of each query's nsplit sorted lists [nq][nsplit][k] into [nq][k]. `flags` ([nq]
+/// words) is needed for 64 < k <= kSelectMergeMaxK, where a query's selection can overflow.
 void launch_sorted_merge(const uint32_t* part_r, const float* part_d, uint64_t nq, uint32_t nsplit, uint32_t k,
-                         uint32_t* d_rows, float* d_dist, hipStream_t s) {
+                         uint32_t* d_rows, float* d_dist, uint32_t* flags, hipStream_t s) {
   QVH_REQUIRE(nsplit <= 64 * 16, "flat search: too many partial lists to merge");
+  const uint32_t* only = nullptr;
   if (k <= kSelectMergeMaxK) {
+    uint32_t* overflow = k > 64 ? flags : nullptr;
     hipLaunchKernelGGL(flat_merge_select_kernel, dim3(static_cast<unsigned>(nq)), dim3(1024), 0, s, part_r, part_d,
-                       nsplit, k, d_rows, d_dist);
+                       nsplit, k, d_rows, d_dist, overflow);
     QVH_HIP(hipGetLastError());
-    return;
+    if (!overflow) return;
+    only = overflow;  // the sequential merge takes the overflowed queries
   }
   const dim3 grid(static_cast<unsigned>(ceil_div(nq, 4))), block(256);
   const uint32_t q32 = static_cast<uint32_t>(nq);
   if (nsplit <= 64) {
-    hipLaunchKernelGGL(flat_merge_sorted_kernel<1>, grid, block, 0, s, part_r, part_d, q32, nsplit, k, d_rows, d_dist);
+    hipLaunchKernelGGL(flat_merge_sorted_kernel<1>, grid, block, 0, s, part_r, part_d, q32, nsplit, k, d_rows, d_dist, only);
   } else if (nsplit <= 128) {
-    hipLaunchKernelGGL(flat_merge_sorted_kernel<2>, grid, block, 0, s, part_r, part_d, q32, nsplit, k, d_rows, d_dist);
+    hipLaunchKernelGGL(flat_merge_sorted_kernel<2>, grid, block, 0, s, part_r, part_d, q32, nsplit, k, d_rows, d_dist, only);
   } else if (nsplit <= 256) {
-    hipLaunchKernelGGL(flat_merge_sorted_kernel<4>, grid, block, 0, s, part_r, part_d, q32, nsplit, k, d_rows, d_dist);
+    hipLaunchKernelGGL(flat_merge_sorted_kernel<4>, grid, block, 0, s, part_r, part_d, q32, nsplit, k, d_rows, d_dist, only);
   } else if (nsplit <= 512) {
-    hipLaunchKernelGGL(flat_merge_sorted_kernel<8>, grid, block, 0, s, part_r, part_d, q32, nsplit, k, d_rows, d_dist);
+    hipLaunchKernelGGL(flat_merge_sorted_kernel<8>, grid, block, 0, s, part_r, part_d, q32, nsplit, k, d_rows, d_dist, only);
   } else {
-    hipLaunchKernelGGL(flat_merge_sorted_kernel<16>, grid, block, 0, s, part_r, part_d, q32, nsplit, k, d_rows, d_dist);
+    hipLaunchKernelGGL(flat_merge_sorted_kernel<16>, grid, block, 0, s, part_r, part_d, q32, nsplit, k, d_rows, d_dist, only);
   }
   QVH_HIP(hipGetLastError());
 }
@@ -1161,7 +1183,7 @@ struct qvh_flat {
   hipStream_t stream = nullptr;
   std::mutex mu;
   // per-call workspace (grown on demand, serialized by mu)
-  DeviceBuffer w_stage, w_q, w_qn, w_pd, w_pr, w_rows, w_dist, w_bits, w_thr, w_idx, w_fb;
+  DeviceBuffer w_stage, w_q, w_qn, w_pd, w_pr, w_rows, w_dist, w_bits, w_thr, w_idx, w_fb, w_mflag;
   // optional per-stage timing of the last search: events before prep, scan, merge and after
   bool timing = false;
   bool timed = false;
@@ -1308,7 +1330,8 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
       QVH_HIP(hipGetLastError());
     }
     if (f->timed) QVH_HIP(hipEventRecord(f->ev[2], s));
-    launch_sorted_merge(part_r, part_d, nq, static_cast<uint32_t>(g), k, d_rows, d_dist, s);
+    launch_sorted_merge(part_r, part_d, nq, static_cast<uint32_t>(g), k, d_rows, d_dist,
+                        static_cast<uint32_t*>(f->w_mflag.reserve(nq * sizeof(uint32_t))), s);
     f->last_nsplit = g;
     if (f->timed) QVH_HIP(hipEventRecord(f->ev[3], s));
     return;
@@ -1328,7 +1351,8 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
     e.out_dist = static_cast<float*>(f->w_pd.reserve(parts * sizeof(float)));
     launch_exact(e, nq, s);
     if (f->timed) QVH_HIP(hipEventRecord(f->ev[2], s));
-    launch_sorted_merge(e.out_rows, e.out_dist, nq, e.nsplit, k, d_rows, d_dist, s);
+    launch_sorted_merge(e.out_rows, e.out_dist, nq, e.nsplit, k, d_rows, d_dist,
+                        static_cast<uint32_t*>(f->w_mflag.reserve(nq * sizeof(uint32_t))), s);
     f->last_nsplit = g;
     if (f->timed) QVH_HIP(hipEventRecord(f->ev[3], s));
     return;

@@ -158,10 +158,12 @@ def test_k_values(oracle, k):
 
 @pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
 @pytest.mark.parametrize("nq,k,n", [(1, 10, 700_000), (3, 1, 50_000), (8, 100, 200_000), (2, 1024, 30_000),
-                                    (5, 10, 2_048), (1, 10, 2_047)])
+                                    (5, 10, 2_048), (1, 10, 2_047), (3, 200, 500_000), (1, 256, 30_000)])
 def test_small_batches_split_rows(oracle, metric, nq, k, n):
     """Batches of at most eight queries split each query's rows over up to 1024 work-groups and
-    merge the sorted partial lists (2,047 rows: too few to split, one work-group per query)."""
+    merge the sorted partial lists (2,047 rows: too few to split, one work-group per query). k up
+    to 256 merges by selection below the k-th list head; k = 256 over 32 lists gathers more keys
+    than the buffer holds and takes the sequential merge; k = 1024 always does."""
     base = D.gaussian(n, 16, seed=31)
     q = D.gaussian(nq, 16, seed=32)
     print(_check(oracle, base, q, k, metric))
