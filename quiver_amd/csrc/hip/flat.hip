@@ -700,10 +700,10 @@ __global__ void __launch_bounds__(kExactThreads) flat_exact_kernel(ExactArgs a) 
 constexpr int kFewThreads = 256;
 constexpr int kFewWaves = kFewThreads / 64;
 constexpr int kFewRowsPerStep = kFewWaves * 8;
-constexpr int kFewCap = 128;  // per (query, wave) queue
+constexpr int kFewCap = 128;  // per (query, wave) queue for k <= 64; 256 for k <= 128
 constexpr uint32_t kFewMaxQ = 8;       // queries per launch
 constexpr uint32_t kFewMaxBatch = 16;  // larger batches take the MFMA scan
-constexpr uint32_t kFewMaxK = 64;
+constexpr uint32_t kFewMaxK = 128;     // dims that are multiples of 32; 64 for the others
 constexpr uint32_t kFewMaxDim = 159;  // four 32-element blocks, then up to three 8-blocks and a tail
 constexpr uint32_t kFewMaxDp = 160;
 constexpr uint32_t kFewMaxSplits = 1024;
@@ -736,9 +736,9 @@ struct FewRows {
   uint64_t bits;
 };
 
-template <int NQ, bool L2, bool TAIL>
+template <int NQ, bool L2, bool TAIL, int CAP = kFewCap>
 __global__ void __launch_bounds__(kFewThreads) flat_few_kernel(FewArgs a) {
-  __shared__ uint64_t s_queue[NQ * kFewWaves * kFewCap];  // [query][wave][kFewCap]
+  __shared__ uint64_t s_queue[NQ * kFewWaves * CAP];  // [query][wave][CAP]
   __shared__ __attribute__((aligned(16))) float s_q[NQ * kFewMaxDp];
   __shared__ __attribute__((aligned(16))) uint32_t s_thr[NQ < 4 ? 4 : NQ];
   __shared__ uint32_t s_wcount[kFewWaves];
@@ -784,11 +784,11 @@ __global__ void __launch_bounds__(kFewThreads) flat_few_kernel(FewArgs a) {
     thr_bits[qi] = 0xFFFFFFFFu;
     thr[qi] = __builtin_huge_valf();
   }
-  auto queue_of = [&](int qi) { return s_queue + (qi * kFewWaves + wave) * kFewCap; };
+  auto queue_of = [&](int qi) { return s_queue + (qi * kFewWaves + wave) * CAP; };
   auto cut = [&](int qi) {
     uint32_t t = thr_bits[qi];
     const uint32_t before = cnt[qi];
-    cnt[qi] = wave_cut<kFewCap>(queue_of(qi), cnt[qi], a.k, &t);
+    cnt[qi] = wave_cut<CAP>(queue_of(qi), cnt[qi], a.k, &t);
     if (before > a.k) {
       if (lane == 0) atomicMin(&s_thr[qi], t);
       if (t < thr_bits[qi]) {
@@ -899,16 +899,22 @@ __global__ void __launch_bounds__(kFewThreads) flat_few_kernel(FewArgs a) {
       if (mk != 0) {
         if (pass) queue_of(qi)[cnt[qi] + lane_rank(mk)] = make_key(dist, static_cast<uint32_t>(r));
         cnt[qi] += static_cast<uint32_t>(__popcll(mk));
-        if (cnt[qi] > static_cast<uint32_t>(kFewCap - 8)) cut(qi);
+        if (cnt[qi] > static_cast<uint32_t>(CAP - 8)) cut(qi);
       }
     }
     cur = nxt;
   }
-  // Per query: the four wave lists (at most 64 keys each after the cut) sorted together.
+  // Per query: the four wave lists (at most CAP / 2 keys each after the cut) sorted together.
+  constexpr int MK = CAP / 128;  // keys per lane
 #pragma unroll
   for (int qi = 0; qi < NQ; ++qi) {
     cut(qi);
-    const uint64_t mine = static_cast<uint32_t>(lane) < cnt[qi] ? queue_of(qi)[lane] : ~0ull;
+    uint64_t mine[MK];
+#pragma unroll
+    for (int i = 0; i < MK; ++i) {
+      const uint32_t e = i * 64 + lane;
+      mine[i] = e < cnt[qi] ? queue_of(qi)[e] : ~0ull;
+    }
     if (lane == 0) s_wcount[wave] = cnt[qi];
     __syncthreads();
     uint32_t most = 0, merged = 0;
@@ -919,8 +925,12 @@ __global__ void __launch_bounds__(kFewThreads) flat_few_kernel(FewArgs a) {
     }
     uint32_t ks = 1;
     while (ks < most) ks <<= 1;
-    uint64_t* base = s_queue + qi * kFewWaves * kFewCap;
-    if (static_cast<uint32_t>(lane) < ks) base[wave * ks + lane] = mine;
+    uint64_t* base = s_queue + qi * kFewWaves * CAP;
+#pragma unroll
+    for (int i = 0; i < MK; ++i) {
+      const uint32_t e = i * 64 + lane;
+      if (e < ks) base[wave * ks + e] = mine[i];
+    }
     block_sort_keys(base, kFewWaves * ks);
     if (static_cast<uint32_t>(qi) < a.nq) {
       const uint32_t nout = min(merged, a.k);
@@ -1259,7 +1269,8 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
   // the same scan without the shared bound and the wide merge (its rare fallback queries on the
   // exact kernel); larger k or dim: the exact kernel.
   const bool splittable = !d_idx && f->n >= 2 * kMinSplitRows;
-  const bool few = splittable && nq <= kFewMaxBatch && k <= kFewMaxK && f->dim >= 32 && f->dim <= kFewMaxDim;
+  const bool few = splittable && nq <= kFewMaxBatch && k <= (f->dim % 32 == 0 ? kFewMaxK : 64u) && f->dim >= 32 &&
+                   f->dim <= kFewMaxDim;
   const bool split = splittable && !few && nq <= kSplitMaxQueries;
   const bool wide = !few && !split && k > 32 && k <= kWideMaxK && f->dp <= static_cast<uint32_t>(kMaxDp) && !d_idx;
   const bool exact_only = !few && !split && !wide && (k > 32 || f->dp > static_cast<uint32_t>(kMaxDp));
@@ -1314,8 +1325,9 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
       fa.part_d = part_d + q0 * g * k;
       auto go = [&](auto nqc) {
         constexpr int NQ = decltype(nqc)::value;
-        auto kern = l2 ? (tail ? flat_few_kernel<NQ, true, true> : flat_few_kernel<NQ, true, false>)
-                       : (tail ? flat_few_kernel<NQ, false, true> : flat_few_kernel<NQ, false, false>);
+        auto kern = k > 64 ? (l2 ? flat_few_kernel<NQ, true, false, 256> : flat_few_kernel<NQ, false, false, 256>)
+                    : l2   ? (tail ? flat_few_kernel<NQ, true, true> : flat_few_kernel<NQ, true, false>)
+                           : (tail ? flat_few_kernel<NQ, false, true> : flat_few_kernel<NQ, false, false>);
         hipLaunchKernelGGL(kern, grid, block, 0, s, fa);
       };
       if (nc <= 1) {

@@ -124,8 +124,9 @@ def test_large_k(oracle, k, metric):
 def test_large_k_crowded_lists_fall_back_exactly(oracle, metric):
     """200 near-copies of query 0 in consecutive rows: its 100 nearest crowd one split's 32-entry
     lists, so the wide merge hands that query to the exact kernel while the others stay on the
-    MFMA path; every result still equals the oracle's."""
-    base, q = D.int_mix(40_000, 12)
+    MFMA path (40 queries: above the small-batch kernels' 16); every result still equals the
+    oracle's."""
+    base, q = D.int_mix(40_000, 40)
     base = base.copy()
     noise = np.random.default_rng(3).integers(-1, 2, (200, base.shape[1]))
     base[5_000:5_200] = np.clip(q[0] + noise, 0, 255)
@@ -173,12 +174,14 @@ def test_small_batches_split_rows(oracle, metric, nq, k, n):
 @pytest.mark.parametrize("dim,nq,k,n", [(32, 1, 10, 700_000), (40, 2, 64, 100_000), (47, 3, 1, 60_000),
                                         (61, 8, 33, 120_000), (100, 5, 10, 2_048), (128, 4, 20, 150_000),
                                         (159, 7, 64, 50_000), (96, 6, 16, 33_333), (64, 13, 10, 80_000),
-                                        (128, 16, 64, 40_000)])
+                                        (128, 16, 64, 40_000), (128, 3, 100, 200_000), (64, 8, 128, 60_000),
+                                        (100, 2, 100, 50_000)])
 def test_few_query_coalesced_scan(oracle, metric, dim, nq, k, n):
     """At most sixteen queries with 32 <= dim <= 159 and k <= 64: eight lanes per row replay the
     reference's accumulation order (32-element blocks, 8-element blocks, the rounded and fused
     tail: dims 40, 47 and 61 take every branch); each launch reads a row once for up to eight
-    queries (13 and 16 queries: two launches, one merge)."""
+    queries (13 and 16 queries: two launches, one merge). k up to 128 for dims that are multiples
+    of 32 (256-entry queues); dim 100 with k = 100 takes the split exact kernel."""
     base = D.gaussian(n, dim, seed=33)
     q = D.gaussian(nq, dim, seed=34)
     print(_check(oracle, base, q, k, metric))
