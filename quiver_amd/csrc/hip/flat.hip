@@ -686,7 +686,8 @@ __global__ void __launch_bounds__(kExactThreads) flat_exact_kernel(ExactArgs a) 
 }
 
 // ---------------------------------------------------------------------------------------------
-// Few-query exact scan (at most kFewMaxQ queries, 32 <= dim <= kFewMaxDim, k <= kFewMaxK).
+// Few-query exact scan (at most kFewMaxQ queries per launch, 32 <= dim <= kFewMaxDim, k <= 64, or
+// k <= kFewMaxK when dim is a multiple of 32).
 //
 // Eight lanes share a row and load it coalesced: lane l of the eight (u = l & 3, h = l >> 2)
 // holds the four accumulators 8u + 4h .. 8u + 4h + 3 of the reference's AVX2 kernel and replays
@@ -695,7 +696,7 @@ __global__ void __launch_bounds__(kExactThreads) flat_exact_kernel(ExactArgs a) 
 // quad_perm [1,0,3,2] adds s0 + s1 and s2 + s3, quad_perm [2,3,0,1] gives v = (s0+s1)+(s2+s3) for
 // l' = 0..3 (lanes 0-3) and l' = 4..7 (lanes 4-7), row_half_mirror adds the two halves into
 // lo[j] = v[j] + v[j+4], and (lo0+lo1)+(lo2+lo3) and the scalar tail finish in each lane. Every
-// row is read once for all the batch's queries, whose values stay in registers.
+// row is read once for all the launch's queries, whose values stay in registers.
 
 constexpr int kFewThreads = 256;
 constexpr int kFewWaves = kFewThreads / 64;
