@@ -891,7 +891,7 @@ constexpr uint32_t kStreamMaxSel = 256;
 constexpr int kFinishThreads = 128;
 constexpr uint32_t kStreamMaxM = 64;  // code bytes of the widest streaming kernel
 // Slices per query of a batch smaller than one resident generation of blocks.
-constexpr uint64_t kMaxSlices = 4;
+constexpr uint64_t kMaxSlices = 16;
 
 /// Table entry (j, c) of the per-query table, in the reference's order (sum over t, then the
 /// factor -2 for L2, src/ivfpq_index.cc:315-317 and src/product_quantizer.cc:180-186).
