@@ -3,9 +3,9 @@
  *
  * A plain-C restatement of the CPU algorithms of TheWiseGhost/quiver's data-parallel search path
  * (flat exact search, IVF-PQ train / add / search, PQ encode, k-means). Only tests/, the smoke
- * check in __graft_entry__.py and bench.py's cpu_baseline leg may load it, and only as the
- * checker (or, in the bench, as the timed CPU baseline). The product (quiver_amd) never links or
- * calls it.
+ * check in __graft_entry__.py and bench.py's cpu_baseline leg may load it, and only to check the
+ * device's results (or, in the bench, as the timed CPU baseline). The product (quiver_amd) never
+ * links or calls it.
  *
  * Every function cites the reference file:line it restates. Floating-point operations follow the
  * reference's exact order and rounding: the file is compiled with -ffp-contract=off; the AVX2
