@@ -124,9 +124,11 @@ qvh_status qvh_flat_set_timing(qvh_flat* flat, int enable);
 qvh_status qvh_flat_last_timing(qvh_flat* flat, float* prep_ms, float* scan_ms, float* merge_ms,
                                 uint32_t* nsplit);
 
-/* Diagnostic (no counterpart in the reference): the number of queries of the last search with
- * 32 < k <= 256 that the wide merge handed to the exact kernel (a split's 32-entry list ran out
- * before the selection ended), 0 for other searches. Waits for the last search. */
+/* Diagnostic (no counterpart in the reference): the number of queries of the last search on the
+ * MFMA scan that the merge handed to the exact kernel, because the re-scored selection could not be
+ * certified (the k-th exact distance was not below the last selected GEMM-form distance minus the
+ * query's rounding bound) or, for k above the shared-bound lists, a split's 32-entry list ran out
+ * before the selection ended; 0 for searches on the other kernels. Waits for the last search. */
 qvh_status qvh_flat_last_fallbacks(qvh_flat* flat, uint32_t* count);
 
 /* ------------------------------------------------------------------------------------------ *
@@ -186,6 +188,11 @@ qvh_status qvh_ivfpq_search_device(qvh_ivfpq* ivf, const float* d_queries, uint6
                                    const uint64_t* d_pos_bitmap, uint64_t* d_out_refs,
                                    float* d_out_dist, void* stream);
 qvh_status qvh_ivfpq_sync(qvh_ivfpq* ivf);
+/* Diagnostic (no counterpart in the reference): the number of queries of the last search (L2 with
+ * the precomputed table, which ranks by an approximate sum and re-scores the best) whose ranking
+ * could not be certified against the rounding bound and was recomputed with the reference's sums
+ * for every probed code; 0 for other searches. Waits for the last search. */
+qvh_status qvh_ivfpq_last_fallbacks(qvh_ivfpq* ivf, uint32_t* count);
 /* Measurement hook (no counterpart in the reference). Level 1: HIP events around the probe
  * selection (query prep, coarse scores, top-nprobe) and the list scan of each search. Level 2
  * adds, after the scan, a count of the PQ code bytes the scan had to read (sum over queries and
@@ -204,6 +211,43 @@ qvh_status qvh_points_create(const float* x, uint64_t n, uint32_t dim, qvh_point
 void qvh_points_destroy(qvh_points* points);
 qvh_status qvh_points_nearest(qvh_points* points, const float* centroids, uint32_t k,
                               int max_inner_product, uint32_t* out_assign);
+
+/* ------------------------------------------------------------------------------------------ *
+ * ProductQuantizer (include/quiver/quantizer.h:59-114, src/product_quantizer.cc:119-217) and
+ * nearest_centroid (src/product_quantizer.cc:14-27), over batches: the reference's per-vector
+ * methods are the n = 1 case. Every sum follows the reference's float order, so codes, tables,
+ * ADC sums and indices are bit-identical. Host buffers; each call returns when its outputs are
+ * written.
+ * ------------------------------------------------------------------------------------------ */
+typedef struct qvh_pq qvh_pq;
+
+/* ProductQuantizer(dim, m) + set_centroids (src/product_quantizer.cc:119-124,155-163): the
+ * codebook [m][256][dim/m] goes to the device. dim % m must be 0. */
+qvh_status qvh_pq_create(uint32_t dim, uint32_t m, const float* codebook, qvh_pq** out);
+void qvh_pq_destroy(qvh_pq* pq);
+
+/* ProductQuantizer::encode of n vectors [n][dim] (src/product_quantizer.cc:165-171): codes [n][m],
+ * per sub-space the first of the 256 codewords with the smallest in-order sum of squared
+ * differences (CentroidTable::l2 + argmin, src/internal/centroid_table.h:65-75,155-170). */
+qvh_status qvh_pq_encode(qvh_pq* pq, const float* x, uint64_t n, uint8_t* codes);
+
+/* ProductQuantizer::decode of n codes [n][m] into [n][dim] (src/product_quantizer.cc:173-178). */
+qvh_status qvh_pq_decode(qvh_pq* pq, const uint8_t* codes, uint64_t n, float* out);
+
+/* compute_l2_table (inner_product = 0) or compute_ip_table (1) of nq queries [nq][dim]
+ * (src/product_quantizer.cc:180-186): tables [nq][m][256]. */
+qvh_status qvh_pq_tables(qvh_pq* pq, const float* queries, uint64_t nq, int inner_product,
+                         float* tables);
+
+/* ProductQuantizer::adc_batch (src/product_quantizer.cc:194-217; adc is n = 1): out[i] = the sum
+ * over j of table[j * 256 + codes[i][j]], in order of j, for one table [m][256]. */
+qvh_status qvh_pq_adc(qvh_pq* pq, const float* table, const uint8_t* codes, uint64_t n, float* out);
+
+/* nearest_centroid (src/product_quantizer.cc:14-27) of n points [n][dim] against k centroids
+ * [k][dim]: the first index with the smallest simd::l2sqr distance (AVX2 order), 0 when no
+ * distance is below +infinity. */
+qvh_status qvh_nearest_centroid(const float* x, uint64_t n, const float* centroids, uint32_t k,
+                                uint32_t dim, uint32_t* out);
 
 #ifdef __cplusplus
 }

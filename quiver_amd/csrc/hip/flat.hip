@@ -153,7 +153,7 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
     const float oth_k = __shfl_xor(own_k, 32, 64), oth_h = __shfl_xor(own_h, 32, 64);
     float t = fminf(fminf(own_k, oth_k), fmaxf(own_h, oth_h));
     if (qvalid) {
-      uint32_t g;
+      uint32_t g = 0;
       if (h == 0) g = atomicMin(&a.qthr[q], float_to_ordered(t));
       g = __shfl(g, j, 64);
       t = fminf(t, ordered_to_float(g));
@@ -358,7 +358,23 @@ struct MergeArgs {
   const uint32_t* idx;  // list positions -> rows (indexed scan), or null
   uint32_t* out_rows;
   float* out_dist;
+  const float* delta;   // [nq] bound on |GEMM-form distance - exact distance| (query_norms_kernel)
+  uint32_t* fallback;   // queries the exact kernel recomputes (uncertified selections)
+  uint32_t* nfallback;  // their count
 };
+
+/// Certificate of a re-scored selection. The selection holds the `sel` best candidates by GEMM-form
+/// distance, the last of which is g_last; every other admitted row has a GEMM-form distance of at
+/// least g_last (the scan's bounds only drop rows above some list's sel-th distance, which is at
+/// least the union's). An unselected row's exact distance is then at least g_last - delta, so when
+/// the k-th smallest exact distance of the selection lies strictly below that, no unselected row can
+/// enter the top k. A selection that took every admitted row (count < sel) is complete, and with
+/// delta = 0 the two forms agree exactly, so the (distance, row) order of the selection is final.
+__device__ __forceinline__ bool selection_certified(uint32_t count, uint32_t sel, float g_last, float e_k,
+                                                    float delta) {
+  if (count < sel || delta == 0.0f) return true;
+  return static_cast<double>(e_k) < static_cast<double>(g_last) - static_cast<double>(delta);
+}
 
 template <int KL>
 __global__ void __launch_bounds__(256) flat_merge_kernel(MergeArgs m) {
@@ -417,6 +433,15 @@ __global__ void __launch_bounds__(256) flat_merge_kernel(MergeArgs m) {
     const uint64_t o = __shfl(key, y, 64);
     rank += o < key ? 1u : 0u;
   }
+  // The KL-th selected GEMM-form distance (lane KL - 1) and the k-th smallest exact distance.
+  const float g_last = ordered_to_float(static_cast<uint32_t>(__shfl(sel, KL - 1, 64) >> 32));
+  float e_k = valid && rank < m.k ? e : -__builtin_huge_valf();
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) e_k = fmaxf(e_k, __shfl_xor(e_k, off, 64));
+  if (!selection_certified(static_cast<uint32_t>(count), KL, g_last, e_k, m.delta[q])) {
+    if (lane == 0) m.fallback[atomicAdd(m.nfallback, 1u)] = q;
+    return;
+  }
   uint32_t* orow = m.out_rows + static_cast<size_t>(q) * m.k;
   float* odist = m.out_dist + static_cast<size_t>(q) * m.k;
   if (valid && rank < m.k) {
@@ -438,9 +463,7 @@ __global__ void __launch_bounds__(256) flat_merge_kernel(MergeArgs m) {
 constexpr uint32_t kWideMaxK = 256;
 constexpr uint32_t kWideMaxSel = 512;
 
-__global__ void __launch_bounds__(256) flat_merge_wide_kernel(MergeArgs m, uint32_t sel_n,
-                                                              uint32_t* __restrict__ fallback,
-                                                              uint32_t* __restrict__ nfallback) {
+__global__ void __launch_bounds__(256) flat_merge_wide_kernel(MergeArgs m, uint32_t sel_n) {
   constexpr int KL = 32;
   __shared__ uint64_t s_sel[4][kWideMaxSel];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -490,7 +513,7 @@ __global__ void __launch_bounds__(256) flat_merge_wide_kernel(MergeArgs m, uint3
     }
   }
   if (__ballot(spent) != 0) {
-    if (lane == 0) fallback[atomicAdd(nfallback, 1u)] = q;
+    if (lane == 0) m.fallback[atomicAdd(m.nfallback, 1u)] = q;
     return;
   }
   __builtin_amdgcn_wave_barrier();
@@ -509,6 +532,19 @@ __global__ void __launch_bounds__(256) flat_merge_wide_kernel(MergeArgs m, uint3
     }
   }
   wave_sort<8>(x8);
+  // Certificate: the k-th smallest exact distance (element k - 1) against the sel_n-th selected
+  // GEMM-form distance.
+  const uint32_t ek_at = m.k - 1;
+  uint64_t ek_key = x8[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) ek_key = ek_at / 64 == static_cast<uint32_t>(i) ? x8[i] : ek_key;
+  ek_key = __shfl(ek_key, static_cast<int>(ek_at % 64), 64);
+  const float e_k = ordered_to_float(static_cast<uint32_t>(ek_key >> 32));
+  const float g_last = count == sel_n ? ordered_to_float(static_cast<uint32_t>(sel[sel_n - 1] >> 32)) : 0.0f;
+  if (!selection_certified(count, sel_n, g_last, e_k, m.delta[q])) {
+    if (lane == 0) m.fallback[atomicAdd(m.nfallback, 1u)] = q;
+    return;
+  }
   uint32_t* orow = m.out_rows + static_cast<size_t>(q) * m.k;
   float* odist = m.out_dist + static_cast<size_t>(q) * m.k;
 #pragma unroll
@@ -534,21 +570,86 @@ __global__ void pack_rows_kernel(const float* __restrict__ src, float* __restric
   dst[idx] = c < dim ? src[r * dim + c] : 0.0f;
 }
 
-/// out[r] = sum of squares of row r (any order: only the GEMM-form screening uses it).
-__global__ void row_norms_kernel(const float* __restrict__ rows, float* __restrict__ out, uint64_t n,
-                                 uint32_t dp) {
-  const uint64_t r = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (r >= n) return;
-  const f32x4* p = reinterpret_cast<const f32x4*>(rows + r * dp);
+/// True when v is an integer of magnitude at most 2^24 (exactly representable, and so are its
+/// products and sums while they stay below 2^24).
+__device__ __forceinline__ bool small_integer(float v) { return v == rintf(v) && fabsf(v) <= 16777216.0f; }
+
+/// Squared norm of one padded row (fused chain over dp / 4 float4 chunks) and whether all of its
+/// values are small integers.
+__device__ __forceinline__ float padded_norm(const float* row, uint32_t dp, bool& integral) {
+  const f32x4* p = reinterpret_cast<const f32x4*>(row);
   float s = 0.0f;
+  bool ok = true;
   for (uint32_t c = 0; c < dp / 4; ++c) {
     const f32x4 v = p[c];
+    ok = ok && small_integer(v[0]) && small_integer(v[1]) && small_integer(v[2]) && small_integer(v[3]);
     s = fmaf(v[0], v[0], s);
     s = fmaf(v[1], v[1], s);
     s = fmaf(v[2], v[2], s);
     s = fmaf(v[3], v[3], s);
   }
-  out[r] = s;
+  integral = ok;
+  return s;
+}
+
+/// out[r] = sum of squares of row r (any order: only the GEMM-form screening uses it). With
+/// `meta`, also folds the rows into the store's bound data: meta[0] = largest squared norm (as
+/// float bits; non-negative floats order like their bits), meta[1] != 0 once a row holds a value
+/// that is not a small integer. One atomic per wave.
+__global__ void row_norms_kernel(const float* __restrict__ rows, float* __restrict__ out, uint64_t n,
+                                 uint32_t dp, uint32_t* __restrict__ meta) {
+  const uint64_t r = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  bool integral = true;
+  float s = 0.0f;
+  if (r < n) {
+    s = padded_norm(rows + r * dp, dp, integral);
+    out[r] = s;
+  }
+  if (meta == nullptr) return;
+  uint32_t top = __float_as_uint(s == s ? s : __builtin_huge_valf());
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) top = max(top, static_cast<uint32_t>(__shfl_xor(top, off, 64)));
+  const bool all_integral = __ballot(!integral) == 0;
+  if ((threadIdx.x & 63) == 0) {
+    atomicMax(&meta[0], top);
+    if (!all_integral) atomicOr(&meta[1], 1u);
+  }
+}
+
+/// Squared norms of the prepared queries and each query's bound on |GEMM-form distance - exact
+/// distance| over every stored row (the certificate of the MFMA scan's re-score; n = dp rounding
+/// steps on any product's path, u = 2^-24, P = ||q||, R = the largest stored ||x||):
+///   L2:            |g - e| <= (2n + 4) u (P + R)^2 (1 + O(nu))
+///   inner product: |g - e| <= (2n + 2) u (1 + P R) (1 + O(nu))
+/// from the standard bound gamma_n = nu / (1 - nu) on a sum of n rounded terms, applied to the
+/// GEMM form ||q||^2 + ||x||^2 - 2<q,x> and to the reference's sum of squared differences (or to
+/// the two dot products). delta uses the coefficient (4n + 16): a factor of two over the
+/// derivation covers the O(nu) terms, the rounding of the computed norms P and R, and a matrix
+/// unit whose accumulation rounds faithfully rather than to nearest. delta is 0 when the query
+/// and every stored row are small integers and (P + R)^2 <= 2^24: every product, partial sum and
+/// difference of either form is then an integer below 2^24, so both forms are exact.
+__global__ void query_norms_kernel(const float* __restrict__ qp, float* __restrict__ qn, uint32_t nq, uint32_t dp,
+                                   const uint32_t* __restrict__ meta, int l2, float* __restrict__ delta) {
+  const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
+  if (q >= nq) return;
+  bool integral = true;
+  const float s = padded_norm(qp + static_cast<uint64_t>(q) * dp, dp, integral);
+  qn[q] = s;
+  const double P = sqrt(static_cast<double>(s));
+  const double R = sqrt(static_cast<double>(__uint_as_float(meta[0])));
+  const double u = 1.0 / 16777216.0;
+  const double coef = (4.0 * dp + 16.0) * u;
+  double d;
+  if (integral && meta[1] == 0 && (P + R) * (P + R) * (1.0 + 1e-12) <= 16777216.0) {
+    d = 0.0;
+  } else if (l2) {
+    d = coef * (P + R) * (P + R);
+  } else {
+    d = coef * (1.0 + P * R);
+  }
+  // Rounded up to float; an overflowing or NaN bound stays non-finite and fails every check.
+  const float df = static_cast<float>(d);
+  delta[q] = static_cast<double>(df) < d ? __uint_as_float(__float_as_uint(df) + 1u) : df;
 }
 
 __global__ void fill_u32_kernel(uint32_t* p, uint64_t n, uint32_t v) {
@@ -583,6 +684,7 @@ struct ExactArgs {
   float* out_dist;
   const uint32_t* qlist;   // queries to run (block b runs qlist[b] while b < *qcount), or null: all
   const uint32_t* qcount;
+  const uint32_t* idx;     // admitted rows, ascending, at positions 0..n-1 (bitmap unused), or null
   // Row splits (nsplit > 1, a multiple of 8; qlist unused): split g scans rows
   // [g * rows_per_split, (g + 1) * rows_per_split) and writes its k best to slot q * nsplit + g of
   // out_rows / out_dist. Work-group b runs on XCD b % 8; it takes query (b / 8) % nq of split
@@ -635,9 +737,10 @@ __global__ void __launch_bounds__(kExactThreads) flat_exact_kernel(ExactArgs a) 
   const uint64_t r_end = a.nsplit > 1 ? min(a.n, r_begin + a.rows_per_split) : a.n;
   const uint64_t slot = static_cast<uint64_t>(q) * max(a.nsplit, 1u) + split;
   for (uint64_t r0 = r_begin; r0 < r_end; r0 += kExactThreads) {
-    const uint64_t r = r0 + tid;
+    uint64_t r = r0 + tid;
     bool ok = r < r_end;
-    if (ok && a.bitmap) ok = (a.bitmap[r >> 6] >> (r & 63)) & 1ull;
+    if (ok && a.idx) r = a.idx[r];
+    if (ok && a.bitmap && !a.idx) ok = (a.bitmap[r >> 6] >> (r & 63)) & 1ull;
     const float d = ok ? exact_flat_distance(qv, a.X + r * a.dp, a.dim, a.l2 != 0) : 0.0f;
     const bool pass = ok && d <= thr;
     const uint64_t mk = __ballot(pass);
@@ -1137,6 +1240,14 @@ void launch_exact(const ExactArgs& a, uint64_t nq, hipStream_t s) {
 /// Row stride in floats: the dimension rounded up to 16 (the MFMA scan's K step).
 uint32_t padded_dim(uint32_t dim) { return (dim + 15u) / 16u * 16u; }
 
+/// Per-lane list length of the MFMA scan with the shared bound for top-k: the re-score selects the
+/// KL best by GEMM-form distance, and the certificate needs some of them beyond the k-th, so KL
+/// leaves a margin of max(5, k / 2). 0: k is above that (the wide merge without a shared bound).
+int shared_list_length(uint32_t k) {
+  const uint32_t need = k + std::max(5u, k / 2);
+  return need <= 16 ? 16 : need <= 32 ? 32 : 0;
+}
+
 template <int DP, int KL>
 void launch_scan_kl(bool l2, int mode, dim3 grid, const ScanArgs& a, hipStream_t s) {
   if (l2) {
@@ -1191,17 +1302,20 @@ struct qvh_flat {
   int device = 0;
   uint64_t n = 0, cap = 0;
   DeviceBuffer rows, norms;
+  // meta[0]: largest stored squared norm (float bits), meta[1]: nonzero once a stored value is not a
+  // small integer (row_norms_kernel); the inputs of the re-score certificate's bound.
+  DeviceBuffer meta;
   hipStream_t stream = nullptr;
   std::mutex mu;
   // per-call workspace (grown on demand, serialized by mu)
-  DeviceBuffer w_stage, w_q, w_qn, w_pd, w_pr, w_rows, w_dist, w_bits, w_thr, w_idx, w_fb, w_mflag;
+  DeviceBuffer w_stage, w_q, w_qn, w_pd, w_pr, w_rows, w_dist, w_bits, w_thr, w_idx, w_fb, w_mflag, w_delta;
   // optional per-stage timing of the last search: events before prep, scan, merge and after
   bool timing = false;
   bool timed = false;
   hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
   hipEvent_t join = nullptr;  // orders calls on other streams into the handle's stream
   uint64_t last_nsplit = 0;
-  bool last_wide = false;  // the last search took the wide merge (its fallback count is in w_fb)
+  bool last_fb = false;  // the last search took the MFMA scan (its fallback count is in w_fb)
 };
 
 namespace {
@@ -1231,9 +1345,8 @@ void flat_grow(qvh_flat* f, uint64_t need) {
   f->cap = cap;
 }
 
-/// Prepared queries (normalized for cosine, padded) and their norms in the handle workspace.
 /// Queries into w_q ([nq][dp], normalized for cosine) and, for the MFMA scan, their squared norms
-/// into w_qn.
+/// into w_qn and their re-score bounds into w_delta.
 void flat_prep_queries(qvh_flat* f, const float* d_raw, uint64_t nq, hipStream_t s, bool norms) {
   const float* qs = d_raw;
   if (f->metric == QVH_METRIC_COSINE) {  // normalized in a copy
@@ -1248,8 +1361,10 @@ void flat_prep_queries(qvh_flat* f, const float* d_raw, uint64_t nq, hipStream_t
                      qs, qp, nq, f->dim, f->dp);
   if (norms) {
     float* qn = static_cast<float*>(f->w_qn.reserve(nq * sizeof(float)));
-    hipLaunchKernelGGL(row_norms_kernel, dim3(static_cast<unsigned>(ceil_div(nq, 256))), dim3(256), 0, s,
-                       qp, qn, nq, f->dp);
+    float* delta = static_cast<float*>(f->w_delta.reserve(nq * sizeof(float)));
+    hipLaunchKernelGGL(query_norms_kernel, dim3(static_cast<unsigned>(ceil_div(nq, 256))), dim3(256), 0, s,
+                       qp, qn, static_cast<uint32_t>(nq), f->dp, f->meta.as<uint32_t>(),
+                       f->metric == QVH_METRIC_L2 ? 1 : 0, delta);
   }
   QVH_HIP(hipGetLastError());
 }
@@ -1273,9 +1388,10 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
   const bool few = splittable && nq <= kFewMaxBatch && k <= (f->dim % 32 == 0 ? kFewMaxK : 64u) && f->dim >= 32 &&
                    f->dim <= kFewMaxDim;
   const bool split = splittable && !few && nq <= kSplitMaxQueries;
-  const bool wide = !few && !split && k > 32 && k <= kWideMaxK && f->dp <= static_cast<uint32_t>(kMaxDp) && !d_idx;
-  const bool exact_only = !few && !split && !wide && (k > 32 || f->dp > static_cast<uint32_t>(kMaxDp));
-  f->last_wide = wide;
+  const bool wide = !few && !split && shared_list_length(k) == 0 && k <= kWideMaxK &&
+                    f->dp <= static_cast<uint32_t>(kMaxDp) && !d_idx;
+  const bool exact_only = !few && !split && !wide && (shared_list_length(k) == 0 || f->dp > static_cast<uint32_t>(kMaxDp));
+  f->last_fb = !few && !split && !exact_only;
   f->timed = f->timing;
   if (f->timed) QVH_HIP(hipEventRecord(f->ev[0], s));
   flat_prep_queries(f, d_queries, nq, s, !(few || split || exact_only));
@@ -1379,7 +1495,7 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
     }
     return;
   }
-  const int kl = k <= 16 ? 16 : 32;
+  const int kl = wide ? 32 : shared_list_length(k);
 
   const uint32_t qblocks = static_cast<uint32_t>(ceil_div(nq, kQueriesPerBlock));
   const uint64_t scan_rows = d_idx ? n_idx : f->n;
@@ -1446,23 +1562,31 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
   m.idx = d_idx;
   m.out_rows = d_rows;
   m.out_dist = d_dist;
+  m.delta = f->w_delta.as<float>();
+  // fb[0] counts the queries whose selection the merge could not certify (or, in the wide merge,
+  // whose list ran out), fb[1..] lists them; the exact kernel then recomputes only those.
+  uint32_t* fb = static_cast<uint32_t*>(f->w_fb.reserve((nq + 1) * sizeof(uint32_t)));
+  hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(256), 0, s, fb, 1, 0u);
+  m.fallback = fb + 1;
+  m.nfallback = fb;
   const dim3 mgrid(static_cast<unsigned>(ceil_div(nq, 4)));
   if (wide) {
-    // fb[0] counts the fallback queries, fb[1..] lists them; the exact kernel then runs only those.
-    uint32_t* fb = static_cast<uint32_t*>(f->w_fb.reserve((nq + 1) * sizeof(uint32_t)));
-    hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(256), 0, s, fb, 1, 0u);
     const uint32_t sel_n = k + std::max<uint32_t>(16, k / 2);
-    hipLaunchKernelGGL(flat_merge_wide_kernel, mgrid, dim3(256), 0, s, m, sel_n, fb + 1, fb);
-    QVH_HIP(hipGetLastError());
-    e.qlist = fb + 1;
-    e.qcount = fb;
-    launch_exact(e, nq, s);
+    hipLaunchKernelGGL(flat_merge_wide_kernel, mgrid, dim3(256), 0, s, m, sel_n);
   } else if (kl == 16) {
     hipLaunchKernelGGL(flat_merge_kernel<16>, mgrid, dim3(256), 0, s, m);
   } else {
     hipLaunchKernelGGL(flat_merge_kernel<32>, mgrid, dim3(256), 0, s, m);
   }
   QVH_HIP(hipGetLastError());
+  e.qlist = fb + 1;
+  e.qcount = fb;
+  if (d_idx) {  // positions of the listed rows, as the scan saw them
+    e.idx = d_idx;
+    e.n = n_idx;
+    e.bitmap = nullptr;
+  }
+  launch_exact(e, nq, s);
   if (f->timed) QVH_HIP(hipEventRecord(f->ev[3], s));
 }
 
@@ -1487,6 +1611,15 @@ qvh_status qvh_flat_create(uint32_t dim, int metric, qvh_flat** out) {
     if (e != hipSuccess) {
       delete f;
       throw Failure(QVH_EDEVICE, std::string("hipStreamCreate: ") + hipGetErrorString(e));
+    }
+    try {
+      f->meta.reserve(2 * sizeof(uint32_t));
+      hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, f->stream, f->meta.as<uint32_t>(), 2, 0u);
+      QVH_HIP(hipGetLastError());
+      QVH_HIP(hipStreamSynchronize(f->stream));
+    } catch (...) {
+      qvh_flat_destroy(f);
+      throw;
     }
     *out = f;
   });
@@ -1524,7 +1657,7 @@ qvh_status qvh_flat_last_fallbacks(qvh_flat* f, uint32_t* count) {
     std::lock_guard<std::mutex> lock(f->mu);
     QVH_HIP(hipSetDevice(f->device));
     *count = 0;
-    if (!f->last_wide) return;
+    if (!f->last_fb) return;
     QVH_HIP(hipStreamSynchronize(f->stream));
     QVH_HIP(hipMemcpy(count, f->w_fb.ptr, sizeof(uint32_t), hipMemcpyDeviceToHost));
   });
@@ -1568,7 +1701,7 @@ void flat_append(qvh_flat* f, const float* rows, uint64_t n, float* stored_out, 
   hipLaunchKernelGGL(pack_rows_kernel, dim3(static_cast<unsigned>(ceil_div(total, 256))), dim3(256), 0,
                      f->stream, stage, dst, n, f->dim, f->dp);
   hipLaunchKernelGGL(row_norms_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0,
-                     f->stream, dst, f->norms.as<float>() + f->n, n, f->dp);
+                     f->stream, dst, f->norms.as<float>() + f->n, n, f->dp, f->meta.as<uint32_t>());
   QVH_HIP(hipGetLastError());
   if (stored_out) QVH_HIP(hipMemcpyAsync(stored_out, stage, raw_bytes, hipMemcpyDeviceToHost, f->stream));
   QVH_HIP(hipStreamSynchronize(f->stream));
@@ -1608,7 +1741,7 @@ qvh_status qvh_flat_search(qvh_flat* f, const float* queries, uint64_t nq, uint3
         if (w + 1 == words && f->n % 64) bits &= (1ull << (f->n % 64)) - 1;
         admitted += static_cast<uint64_t>(__builtin_popcountll(bits));
       }
-      if (k <= 32 && f->dp <= static_cast<uint32_t>(kMaxDp) && 2 * admitted < f->n) {
+      if (shared_list_length(k) != 0 && f->dp <= static_cast<uint32_t>(kMaxDp) && 2 * admitted < f->n) {
         listed.reserve(admitted);
         for (size_t w = 0; w < words; ++w) {
           uint64_t bits = row_bitmap[w];

@@ -199,6 +199,33 @@ __global__ void precompute_kernel(const float* __restrict__ cent, const float* _
   pre[e] = v;
 }
 
+/// pmax[l] = sum_j max_c |pre[l][j][c]|, summed in double and rounded up: with |score_l| and the
+/// query's table bound, it bounds the magnitudes of every term of an L2 ADC sum over list l. One
+/// block per list, one thread per sub-space.
+__global__ void __launch_bounds__(256) pre_bound_kernel(const float* __restrict__ pre, uint32_t m,
+                                                        float* __restrict__ pmax) {
+  __shared__ double part[256];
+  const uint32_t l = blockIdx.x;
+  double mx = 0.0;
+  for (uint32_t j = threadIdx.x; j < m; j += 256) {
+    const float* row = pre + (static_cast<uint64_t>(l) * m + j) * 256;
+    float r = 0.0f;
+    for (uint32_t c = 0; c < 256; ++c) r = fmaxf(r, fabsf(row[c]));
+    mx += static_cast<double>(r);
+  }
+  part[threadIdx.x] = mx;
+  __syncthreads();
+  for (uint32_t w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const double v = part[0] * (1.0 + 1e-12);
+    const float f = static_cast<float>(v);
+    pmax[l] = static_cast<double>(f) < v ? __uint_as_float(__float_as_uint(f) + 1u) : f;
+  }
+}
+
 /// term1[p] = sum_j pre[assign[p]][j][code_j], accumulated in double and rounded once.
 __global__ void term1_kernel(const uint8_t* __restrict__ codes, uint32_t mp, const uint32_t* __restrict__ assign,
                              const float* __restrict__ pre, uint32_t m, uint64_t n, float* __restrict__ out) {
@@ -554,9 +581,28 @@ struct ScanArgs {
   // merging block).
   uint32_t nwhole, parts;
   uint64_t* part_keys;  // [nq - nwhole][parts][keep]
-  uint32_t* part_cnt;   // [nq - nwhole][parts]
+  uint32_t* part_cnt;   // [nq - nwhole][parts]; bit 31 set: that slice's selection is uncertified
   uint32_t* part_done;  // [nq - nwhole], zero between searches
+  // Mode pre: the approximate ranking's certificate (adc_bound_kernel) and the queries it could not
+  // certify, which the block-buffer scan then recomputes with exact sums (exact_pre).
+  const float* delta;   // [nq]
+  uint32_t* fallback;   // [nq]
+  uint32_t* nfallback;
+  int exact_pre;        // block-buffer scan: the reference's sum for every code, no re-score
+  const uint32_t* qlist;   // block-buffer scan over listed queries (block b runs qlist[b] while
+  const uint32_t* qcount;  // b < *qcount), or null: block b runs query b
 };
+
+/// Certificate of an approximate selection (mode pre). The scan kept the keep_sel best candidates by
+/// approximate score, the last at a_last, so every other admitted code scores at least a_last, and
+/// its exact sum at least a_last - delta. When the keep-th smallest exact sum of the selection lies
+/// strictly below that, no unselected code can enter the best keep. A selection that kept every
+/// admitted code (count < keep_sel) is complete.
+__device__ __forceinline__ bool adc_selection_certified(uint32_t count, uint32_t keep_sel, float a_last, float r_keep,
+                                                        float delta) {
+  if (count < keep_sel) return true;
+  return static_cast<double>(r_keep) < static_cast<double>(a_last) - static_cast<double>(delta);
+}
 
 /// Ascending bitonic sort of s[0, n) (n a power of two) by all 256 threads.
 __device__ void block_sort_u64(uint64_t* s, uint32_t n) {
@@ -658,8 +704,9 @@ __device__ __forceinline__ float adc_sum_rows(const float* lut, const uint32_t (
   return s;
 }
 
+/// The block-buffer scan of query q by one block of kScanThreads threads.
 template <int MPW>
-__global__ void __launch_bounds__(kScanThreads) ivf_scan_kernel(ScanArgs a) {
+__device__ void ivf_scan_query(const ScanArgs& a, const uint32_t q) {
   extern __shared__ __attribute__((aligned(16))) unsigned char s_raw[];
   uint64_t* s_cand = reinterpret_cast<uint64_t*>(s_raw);                       // [kCandCap]
   uint64_t* s_pstart = s_cand + kCandCap;                                      // [nprobe + 1] flattened starts
@@ -669,7 +716,6 @@ __global__ void __launch_bounds__(kScanThreads) ivf_scan_kernel(ScanArgs a) {
   __shared__ uint64_t s_thr;
 
   const int tid = threadIdx.x;
-  const uint32_t q = blockIdx.x;
   const float* qv = a.Q + static_cast<uint64_t>(q) * a.dim;
   const float* qscore = a.scores + static_cast<uint64_t>(q) * a.nlist;
   const uint32_t table = a.m * 256;
@@ -745,13 +791,25 @@ __global__ void __launch_bounds__(kScanThreads) ivf_scan_kernel(ScanArgs a) {
             }
             uint32_t w[MPW];
             load_code<MPW>(a.codes, pos, a.mp, w);
-            const float s = adc_sum<MPW>(s_lut, w, a.m);
             const float score = qscore[l];
             float dist;
             if (a.mode == kModeIp) {
-              dist = 1.0f - (-score + s);  // base = <q, c> (src/ivfpq_index.cc:333,346)
+              dist = 1.0f - (-score + adc_sum<MPW>(s_lut, w, a.m));  // base = <q, c> (src/ivfpq_index.cc:333,346)
+            } else if (a.exact_pre) {
+              // The reference's sum: table entry pre + qtab in order of j, plus ||q - c||^2
+              // (src/ivfpq_index.cc:334-346).
+              const float* pre = a.pre + static_cast<uint64_t>(l) * table;
+              float se = 0.0f;
+#pragma unroll
+              for (int j = 0; j < 4 * MPW; ++j) {
+                if (j < static_cast<int>(a.m)) {
+                  const uint32_t c = (w[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+                  se = se + (pre[j * 256 + c] + s_lut[j * 256 + c]);
+                }
+              }
+              dist = score + se;
             } else {
-              dist = score + (a.t1[pos] + s);
+              dist = score + (a.t1[pos] + adc_sum<MPW>(s_lut, w, a.m));
             }
             offer(dist, pos);
           }
@@ -810,7 +868,10 @@ __global__ void __launch_bounds__(kScanThreads) ivf_scan_kernel(ScanArgs a) {
 
   // Exact re-score of the approximate ranking (L2 with the precomputed table): the reference's
   // table entry pre + qtab, summed in order of j, plus ||q - c||^2 (src/ivfpq_index.cc:334-346).
-  if (a.mode == kModePre && !a.exact_all) {
+  if (a.mode == kModePre && !a.exact_all && !a.exact_pre) {
+    const uint32_t selected = cnt;
+    const uint64_t last = s_cand[cnt > 0 ? cnt - 1 : 0];
+    __syncthreads();
     for (uint32_t i = tid; i < cnt; i += kScanThreads) {
       const uint32_t pos = static_cast<uint32_t>(s_cand[i]);
       const uint32_t l = list_pos(pos);
@@ -834,6 +895,12 @@ __global__ void __launch_bounds__(kScanThreads) ivf_scan_kernel(ScanArgs a) {
     for (uint32_t i = cnt + tid; i < n2; i += kScanThreads) s_cand[i] = ~0ull;
     block_sort_u64(s_cand, n2);
     cnt = min(cnt, a.keep);
+    const uint64_t kth = s_cand[cnt > 0 ? cnt - 1 : 0];
+    const bool certified =
+        adc_selection_certified(selected, keep_sel, ordered_to_float(static_cast<uint32_t>(last >> 32)),
+                                ordered_to_float(static_cast<uint32_t>(kth >> 32)), a.delta[q]);
+    // An uncertified query is recomputed afterwards by this kernel with exact sums (exact_pre).
+    if (!certified && tid == 0) a.fallback[atomicAdd(a.nfallback, 1u)] = q;
   }
 
   // Exact re-ranking with the stored vectors (src/ivfpq_index.cc:139-142,363-373).
@@ -863,6 +930,20 @@ __global__ void __launch_bounds__(kScanThreads) ivf_scan_kernel(ScanArgs a) {
     }
     a.out_refs[static_cast<uint64_t>(q) * a.k + j] = ref;
     a.out_dist[static_cast<uint64_t>(q) * a.k + j] = dist;
+  }
+}
+
+/// Block b scans query b; with a query list, the blocks take the listed queries in turn.
+template <int MPW>
+__global__ void __launch_bounds__(kScanThreads) ivf_scan_kernel(ScanArgs a) {
+  if (!a.qlist) {
+    ivf_scan_query<MPW>(a, blockIdx.x);
+    return;
+  }
+  const uint32_t n = *a.qcount;
+  for (uint32_t b = blockIdx.x; b < n; b += gridDim.x) {
+    ivf_scan_query<MPW>(a, a.qlist[b]);
+    __syncthreads();  // the next query reuses the block's LDS
   }
 }
 
@@ -902,6 +983,48 @@ __device__ __forceinline__ float table_entry(const float* qv, const float* cbt, 
   float v = 0.0f;
   for (uint32_t t = 0; t < dsub; ++t) v = v + qj[t] * cb[t * 256];
   return l2 ? v * -2.0f : v;
+}
+
+/// delta[q] bounds |approximate - exact| for every code the query's L2 scan with the precomputed
+/// table can meet. The scan sums a = score + (t1 + sum_j qtab[j][c_j]) (t1 = sum_j pre[l][j][c_j]
+/// in double, rounded once), the reference r = score + sum_j (pre[l][j][c_j] + qtab[j][c_j]), both
+/// in order of j. With B = |score_l|, P = sum_j |pre|, T = sum_j |qtab| over the code's terms, the
+/// standard bound gamma_m on a sum of m rounded terms gives |a - V| <= (m + 2) u T + 3 u P + u B and
+/// |r - V| <= (m + 2) u (P + T) + u B for the exact value V, so |a - r| <= (2m + 5) u (B + P + T)
+/// up to O(u^2). delta takes (2m + 16) u (max over probed lists of |score_l| + pmax[l], plus
+/// T_q = sum_j max_c |qtab[j][c]|), u = 2^-24. One wave per query; the table entries are computed
+/// with the scan's own arithmetic.
+__global__ void __launch_bounds__(256) adc_bound_kernel(const float* __restrict__ Q, uint32_t nq, uint32_t dim,
+                                                        uint32_t m, uint32_t dsub, const float* __restrict__ cbt,
+                                                        const float* __restrict__ scores, uint32_t nlist,
+                                                        const uint32_t* __restrict__ probes, uint32_t nprobe,
+                                                        const float* __restrict__ pmax, float* __restrict__ delta) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t q = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (q >= nq) return;  // whole wave
+  const float* qv = Q + static_cast<uint64_t>(q) * dim;
+  double tsum = 0.0;
+  for (uint32_t j = 0; j < m; ++j) {
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mx = fmaxf(mx, fabsf(table_entry(qv, cbt, dsub, j, lane + 64 * i, true)));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    tsum += static_cast<double>(mx);
+  }
+  float bp = 0.0f;
+  for (uint32_t p = lane; p < nprobe; p += 64) {
+    const uint32_t l = probes[static_cast<uint64_t>(q) * nprobe + p];
+    bp = fmaxf(bp, fabsf(scores[static_cast<uint64_t>(q) * nlist + l]) + pmax[l]);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) bp = fmaxf(bp, __shfl_xor(bp, off, 64));
+  if (lane != 0) return;
+  // (1 + 2^-20) covers the float rounding of |score| + pmax; a NaN or overflowing bound stays
+  // non-finite and certifies nothing.
+  const double d = (2.0 * m + 16.0) / 16777216.0 * ((static_cast<double>(bp) + tsum) * (1.0 + 1.0 / 1048576.0));
+  const float df = static_cast<float>(d);
+  delta[q] = static_cast<double>(df) < d ? __uint_as_float(__float_as_uint(df) + 1u) : df;
 }
 
 // Bank-rotated table lookups (the L2 scan with the precomputed table). The table is laid out
@@ -1397,31 +1520,44 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
     };
     uint32_t cnt_f = min(merged, keep_sel);
     uint64_t key = wave_smallest(merged, cnt_f);
+    bool certified = true;
     if (l2) {
+      const uint64_t last = __shfl(key, static_cast<int>(cnt_f > 0 ? cnt_f - 1 : 0), 64);
       if (static_cast<uint32_t>(lane) < cnt_f) key = rescore(key);
       uint64_t t[1] = {key};
       wave_sort<1>(t);
       key = t[0];
       cnt_f = min(cnt_f, a.keep);
+      const uint64_t kth = __shfl(key, static_cast<int>(cnt_f > 0 ? cnt_f - 1 : 0), 64);
+      certified = adc_selection_certified(merged, keep_sel, ordered_to_float(static_cast<uint32_t>(last >> 32)),
+                                          ordered_to_float(static_cast<uint32_t>(kth >> 32)), a.delta[q]);
     }
     if (split) {
-      // The slice's best keep keys go out (device-scope atomic stores, which write through the
-      // per-XCD L2); once they have completed (s_waitcnt) the slice counts itself done, and the
-      // last slice of the query merges the lists (device-scope atomic loads).
+      // The slice's best keep keys and its count (bit 31: uncertified) go out as agent-scope atomic
+      // stores; every lane then releases them at agent scope before lane 0 counts the slice done,
+      // and the last slice of the query acquires at agent scope before it reads the lists.
       const uint32_t tq = slot - a.nwhole;
       uint64_t* lists = a.part_keys + static_cast<uint64_t>(tq) * a.parts * a.keep;
       if (static_cast<uint32_t>(lane) < cnt_f) {
         __hip_atomic_store(&lists[static_cast<uint64_t>(part) * a.keep + lane], key, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
       }
-      if (lane == 0) __hip_atomic_store(&a.part_cnt[tq * a.parts + part], cnt_f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __builtin_amdgcn_s_waitcnt(0);
+      if (lane == 0) {
+        __hip_atomic_store(&a.part_cnt[tq * a.parts + part], cnt_f | (certified ? 0u : 0x80000000u), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      __builtin_amdgcn_wave_barrier();
       uint32_t done = 0;
-      if (lane == 0) done = __hip_atomic_fetch_add(&a.part_done[tq], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (lane == 0) done = __hip_atomic_fetch_add(&a.part_done[tq], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
       if (__shfl(done, 0, 64) != a.parts - 1) return;
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
       uint32_t all = 0;
+      certified = true;
       for (uint32_t pi = 0; pi < a.parts; ++pi) {
-        const uint32_t c = __hip_atomic_load(&a.part_cnt[tq * a.parts + pi], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t cw = __hip_atomic_load(&a.part_cnt[tq * a.parts + pi], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t c = cw & 0x7FFFFFFFu;
+        certified = certified && (cw >> 31) == 0;
         for (uint32_t i = lane; i < c; i += 64) {
           s_queue[all + i] = __hip_atomic_load(&lists[static_cast<uint64_t>(pi) * a.keep + i], __ATOMIC_RELAXED,
                                                __HIP_MEMORY_SCOPE_AGENT);
@@ -1433,6 +1569,9 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
       key = wave_smallest(all, cnt_f);
       if (lane == 0) __hip_atomic_store(&a.part_done[tq], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    // An uncertified query is recomputed by the block-buffer scan with exact sums, which runs after
+    // this kernel (and the finishing kernel) and overwrites its results.
+    if (!certified && lane == 0) a.fallback[atomicAdd(a.nfallback, 1u)] = q;
     if (a.refine) {
       // Exact re-ranking needs the stored vectors: hand the candidates to the finishing kernel.
       if (static_cast<uint32_t>(lane) < cnt_f) a.sel[static_cast<uint64_t>(q) * a.keep_sel + lane] = key;
@@ -1479,10 +1618,13 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
   }
   }
   uint32_t cnt_f = min(merged, keep_sel);
+  bool certified = true;
 
   // Exact re-score of the approximate ranking (L2 with the precomputed table): the reference's
   // table entry pre + qtab, summed in order of j, plus ||q - c||^2 (src/ivfpq_index.cc:334-346).
   if (l2) {
+    const uint64_t last = s_queue[cnt_f > 0 ? cnt_f - 1 : 0];
+    __syncthreads();
     if (static_cast<uint32_t>(tid) < cnt_f) s_queue[tid] = rescore(s_queue[tid]);
     const uint32_t n2 = pow2_at_least(max(cnt_f, 2u));
     if (static_cast<uint32_t>(tid) >= cnt_f && static_cast<uint32_t>(tid) < n2) s_queue[tid] = ~0ull;
@@ -1503,31 +1645,41 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
     }
     __syncthreads();
     cnt_f = min(cnt_f, a.keep);
+    const uint64_t kth = s_queue[cnt_f > 0 ? cnt_f - 1 : 0];
+    certified = adc_selection_certified(merged, keep_sel, ordered_to_float(static_cast<uint32_t>(last >> 32)),
+                                        ordered_to_float(static_cast<uint32_t>(kth >> 32)), a.delta[q]);
   }
   if (split) {
     // A slice leaves its (at most keep) best keys; the last slice of the query to finish merges
     // the lists (the best keep keys of the union are the best keep keys of the whole scan). The
-    // lists and counts move through device-scope atomic stores and loads, which write through and
-    // read past the per-XCD L2 caches; a slice's stores have completed (s_waitcnt) before its
-    // count goes up. No device-scope fence: one would write back or drop the XCD's whole L2.
+    // lists and counts (bit 31: uncertified) go out as agent-scope atomic stores, every thread
+    // releases them at agent scope before the barrier after which thread 0 counts the slice done,
+    // and the merging slice acquires at agent scope before it reads them.
     const uint32_t tq = slot - a.nwhole;
     uint64_t* lists = a.part_keys + static_cast<uint64_t>(tq) * a.parts * a.keep;
     for (uint32_t i = tid; i < cnt_f; i += kStreamThreads) {
       __hip_atomic_store(&lists[static_cast<uint64_t>(part) * a.keep + i], s_queue[i], __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (tid == 0) __hip_atomic_store(&a.part_cnt[tq * a.parts + part], cnt_f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);
+    if (tid == 0) {
+      __hip_atomic_store(&a.part_cnt[tq * a.parts + part], cnt_f | (certified ? 0u : 0x80000000u), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     __syncthreads();
     if (tid == 0) {
-      const uint32_t before = __hip_atomic_fetch_add(&a.part_done[tq], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t before = __hip_atomic_fetch_add(&a.part_done[tq], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
       s_wcount[0] = before == a.parts - 1 ? 1u : 0u;
     }
     __syncthreads();
     if (s_wcount[0] == 0) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     uint32_t all = 0;
+    certified = true;
     for (uint32_t pi = 0; pi < a.parts; ++pi) {
-      const uint32_t c = __hip_atomic_load(&a.part_cnt[tq * a.parts + pi], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t cw = __hip_atomic_load(&a.part_cnt[tq * a.parts + pi], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t c = cw & 0x7FFFFFFFu;
+      certified = certified && (cw >> 31) == 0;
       for (uint32_t i = tid; i < c; i += kStreamThreads) {
         s_queue[all + i] = __hip_atomic_load(&lists[static_cast<uint64_t>(pi) * a.keep + i], __ATOMIC_RELAXED,
                                              __HIP_MEMORY_SCOPE_AGENT);
@@ -1555,6 +1707,9 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
     cnt_f = min(all, a.keep);
     if (tid == 0) __hip_atomic_store(&a.part_done[tq], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next search
   }
+  // An uncertified query is recomputed by the block-buffer scan with exact sums, which runs after
+  // this kernel (and the finishing kernel) and overwrites its results.
+  if (!certified && tid == 0) a.fallback[atomicAdd(a.nfallback, 1u)] = q;
   if (a.refine) {
     // Exact re-ranking needs the stored vectors: hand the candidates to the finishing kernel.
     for (uint32_t i = tid; i < cnt_f; i += kStreamThreads) a.sel[static_cast<uint64_t>(q) * a.keep_sel + i] = s_queue[i];
@@ -1675,6 +1830,35 @@ void launch_nearest(bool sqdiff, const NearestArgs& a, uint32_t nsub, hipStream_
 
 }  // namespace
 
+namespace qvh {
+
+/// PQ codes [n][m] of n rows [n][dim] (ProductQuantizer::encode, src/product_quantizer.cc:165-171):
+/// per sub-space the first nearest of the 256 codewords by the in-order sum of squared differences,
+/// against the per-sub-space transposed codebook [m][dsub][256].
+void launch_pq_encode(const float* d_x, uint64_t n, uint32_t dim, uint32_t m, const float* d_cbt, uint8_t* d_codes,
+                      hipStream_t s) {
+  NearestArgs pa{};
+  pa.x = d_x;
+  pa.n = n;
+  pa.dim = dim / m;  // per sub-space
+  pa.x_stride = dim;
+  pa.x_off = 0;
+  pa.ct = d_cbt;
+  pa.k = 256;
+  pa.out8 = d_codes;
+  pa.out_stride = m;
+  launch_nearest(true, pa, m, s);
+}
+
+/// Codebook [m][256][dsub] -> per sub-space transposed [m][dsub][256].
+void launch_codebook_transpose(const float* d_cb, uint32_t m, uint32_t dsub, float* d_cbt, hipStream_t s) {
+  hipLaunchKernelGGL(codebook_prep_kernel, dim3(static_cast<unsigned>(ceil_div(uint64_t(m) * 256 * dsub, 256))),
+                     dim3(256), 0, s, d_cb, m, dsub, d_cbt);
+  QVH_HIP(hipGetLastError());
+}
+
+}  // namespace qvh
+
 /// Measurement only: bytes of PQ codes the scan must read, sum over queries and probes of
 /// len(list) * m. One block; thread sums, then an LDS tree.
 __global__ void __launch_bounds__(256) probed_code_bytes_kernel(const uint32_t* __restrict__ probes, uint64_t entries,
@@ -1708,11 +1892,14 @@ struct qvh_ivfpq {
   std::vector<uint64_t> h_off;  // host copy of the list offsets
   DeviceBuffer cent, cent_t, cent_norm, cb, cbt, cbc, pre;
   DeviceBuffer off, codes, t1, vec;
+  DeviceBuffer pmax;  // [nlist] sum_j max_c |pre[l][j][c]| (the L2 ranking's certificate)
   hipStream_t stream = nullptr;
   std::mutex mu;
   DeviceBuffer w_x, w_res, w_assign, w_codes, w_codes_p, w_t1, w_dest, w_shift;
   DeviceBuffer w_q, w_scores, w_probes, w_bits, w_refs, w_dist, w_bytes, w_sel, w_selcnt, w_key, w_order;
   DeviceBuffer w_pkeys, w_pcnt, w_pdone;  // sliced queries of the streaming scan
+  DeviceBuffer w_delta, w_fb;             // certificate bounds; uncertified queries (count, list)
+  bool last_certified = false;            // the last search ranked approximately (w_fb holds its count)
   int cus = 0;                             // compute units of the device
   int timing = 0;               // 0 off, 1 stage events, 2 events and probed code bytes
   bool timed = false, timed_bytes = false;
@@ -1844,9 +2031,27 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
     hipLaunchKernelGGL(probe_order_kernel, dim3(1), dim3(1024), olds, s, min_probe, static_cast<uint32_t>(nq), h->nlist,
                        order);
   }
+  // L2 with the precomputed table ranks candidates by an approximate sum and re-scores the best:
+  // each query's bound on the rounding difference certifies the ranking (adc_bound_kernel), and the
+  // queries it does not certify are listed in fb for an exact rescan.
+  const bool certify = mode == kModePre && !exact_all && keep > 0;
+  float* delta = nullptr;
+  uint32_t* fb = nullptr;
+  if (certify) {
+    delta = static_cast<float*>(h->w_delta.reserve(nq * sizeof(float)));
+    hipLaunchKernelGGL(adc_bound_kernel, dim3(static_cast<unsigned>(ceil_div(nq, 4))), dim3(256), 0, s, dq,
+                       static_cast<uint32_t>(nq), h->dim, h->m, h->dsub, h->cbt.as<float>(), scores, h->nlist, probes,
+                       nprobe, h->pmax.as<float>(), delta);
+    fb = static_cast<uint32_t*>(h->w_fb.reserve((nq + 1) * sizeof(uint32_t)));
+    hipLaunchKernelGGL(zero_u32_kernel, dim3(1), dim3(64), 0, s, fb, 1);
+  }
+  h->last_certified = certify;
   QVH_HIP(hipGetLastError());
   if (h->timed) QVH_HIP(hipEventRecord(h->ev[1], s));
   ScanArgs a{};
+  a.delta = delta;
+  a.fallback = fb ? fb + 1 : nullptr;
+  a.nfallback = fb;
   a.nq = static_cast<uint32_t>(nq);
   a.k = k;
   a.m = h->m;
@@ -1878,11 +2083,34 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
                      ((nprobe + 1) & ~1u) * sizeof(uint32_t) + static_cast<size_t>(h->m) * 256 * sizeof(float);
   QVH_REQUIRE(lds <= 150 * 1024, "IVF-PQ search: m and nprobe too large for the on-chip tables");
   const dim3 grid(static_cast<unsigned>(nq));
+  const uint32_t mpw = h->mp / 4;
+  // The block-buffer scan (every table mode, any candidate count up to kMaxKeepSel).
+  auto launch_block_scan = [&](const ScanArgs& args, dim3 g) {
+    auto go = [&](auto kernel) {
+      const void* fn = reinterpret_cast<const void*>(kernel);
+      if (lds > 64 * 1024) {
+        QVH_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+      }
+      hipLaunchKernelGGL(kernel, g, dim3(kScanThreads), lds, s, args);
+    };
+    if (mpw <= 2) {
+      go(ivf_scan_kernel<2>);
+    } else if (mpw <= 4) {
+      go(ivf_scan_kernel<4>);
+    } else if (mpw <= 8) {
+      go(ivf_scan_kernel<8>);
+    } else if (mpw <= 16) {
+      go(ivf_scan_kernel<16>);
+    } else if (mpw <= 32) {
+      go(ivf_scan_kernel<32>);
+    } else {
+      throw Failure(QVH_EUNSUPPORTED, "IVF-PQ device path supports m <= 128");
+    }
+  };
   if (keep == 0) {
     // nothing stored: every slot is empty
     a.keep_sel = 0;
   }
-  const uint32_t mpw = h->mp / 4;
   // Dynamic LDS above the default 64 KiB needs the kernel's limit raised first.
   auto raise_lds = [&](const void* fn, size_t bytes) {
     if (bytes > 64 * 1024) {
@@ -1971,25 +2199,21 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
       hipLaunchKernelGGL(ivf_finish_kernel, grid, dim3(kFinishThreads), 4 * static_cast<size_t>(nprobe) * sizeof(uint32_t),
                          s, a);
     }
-  } else if (mpw <= 2) {
-    raise_lds(reinterpret_cast<const void*>(ivf_scan_kernel<2>), lds);
-    hipLaunchKernelGGL(ivf_scan_kernel<2>, grid, dim3(kScanThreads), lds, s, a);
-  } else if (mpw <= 4) {
-    raise_lds(reinterpret_cast<const void*>(ivf_scan_kernel<4>), lds);
-    hipLaunchKernelGGL(ivf_scan_kernel<4>, grid, dim3(kScanThreads), lds, s, a);
-  } else if (mpw <= 8) {
-    raise_lds(reinterpret_cast<const void*>(ivf_scan_kernel<8>), lds);
-    hipLaunchKernelGGL(ivf_scan_kernel<8>, grid, dim3(kScanThreads), lds, s, a);
-  } else if (mpw <= 16) {
-    raise_lds(reinterpret_cast<const void*>(ivf_scan_kernel<16>), lds);
-    hipLaunchKernelGGL(ivf_scan_kernel<16>, grid, dim3(kScanThreads), lds, s, a);
-  } else if (mpw <= 32) {
-    raise_lds(reinterpret_cast<const void*>(ivf_scan_kernel<32>), lds);
-    hipLaunchKernelGGL(ivf_scan_kernel<32>, grid, dim3(kScanThreads), lds, s, a);
   } else {
-    throw Failure(QVH_EUNSUPPORTED, "IVF-PQ device path supports m <= 128");
+    launch_block_scan(a, grid);
   }
   QVH_HIP(hipGetLastError());
+  if (certify) {
+    // Exact rescan of the uncertified queries (normally none): the block-buffer scan with the
+    // reference's sum for every code, over the listed queries, after every kernel above.
+    ScanArgs fa = a;
+    fa.exact_pre = 1;
+    fa.keep_sel = fa.keep;
+    fa.qlist = fb + 1;
+    fa.qcount = fb;
+    launch_block_scan(fa, dim3(static_cast<unsigned>(std::min<uint64_t>(nq, 2 * static_cast<uint64_t>(std::max(h->cus, 1))))));
+    QVH_HIP(hipGetLastError());
+  }
   if (h->timed) QVH_HIP(hipEventRecord(h->ev[2], s));
   if (h->timed_bytes) {
     uint64_t* bytes = static_cast<uint64_t*>(h->w_bytes.reserve(sizeof(uint64_t)));
@@ -2087,6 +2311,9 @@ qvh_status qvh_ivfpq_set_trained(qvh_ivfpq* h, const float* centroids, const flo
       h->pre.reserve(n * sizeof(float));
       hipLaunchKernelGGL(precompute_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, s,
                          h->cent.as<float>(), h->cb.as<float>(), h->nlist, h->dim, h->m, h->pre.as<float>());
+      h->pmax.reserve(h->nlist * sizeof(float));
+      hipLaunchKernelGGL(pre_bound_kernel, dim3(h->nlist), dim3(256), 0, s, h->pre.as<float>(), h->m,
+                         h->pmax.as<float>());
     }
     QVH_HIP(hipGetLastError());
     QVH_HIP(hipStreamSynchronize(s));
@@ -2389,6 +2616,18 @@ qvh_status qvh_ivfpq_last_timing(qvh_ivfpq* h, float* select_ms, float* scan_ms,
       QVH_HIP(hipStreamSynchronize(h->stream));
       QVH_HIP(hipMemcpy(code_bytes, h->w_bytes.ptr, sizeof(uint64_t), hipMemcpyDeviceToHost));
     }
+  });
+}
+
+qvh_status qvh_ivfpq_last_fallbacks(qvh_ivfpq* h, uint32_t* count) {
+  return guarded([&] {
+    QVH_REQUIRE(h != nullptr && count != nullptr, "qvh_ivfpq_last_fallbacks: null argument");
+    std::lock_guard<std::mutex> lock(h->mu);
+    QVH_HIP(hipSetDevice(h->device));
+    *count = 0;
+    if (!h->last_certified) return;
+    QVH_HIP(hipStreamSynchronize(h->stream));
+    QVH_HIP(hipMemcpy(count, h->w_fb.ptr, sizeof(uint32_t), hipMemcpyDeviceToHost));
   });
 }
 

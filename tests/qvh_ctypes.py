@@ -39,6 +39,26 @@ class Qvh:
                                            _u32p, _f32p]
         L.qvh_normalize.argtypes = [_f32p, C.c_uint64, C.c_uint32]
         L.qvh_flat_last_fallbacks.argtypes = [C.c_void_p, C.POINTER(C.c_uint32)]
+        L.qvh_ivfpq_last_fallbacks.argtypes = [C.c_void_p, C.POINTER(C.c_uint32)]
+        _u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
+        L.qvh_pq_create.argtypes = [C.c_uint32, C.c_uint32, _f32p, C.POINTER(C.c_void_p)]
+        L.qvh_pq_destroy.argtypes = [C.c_void_p]
+        L.qvh_pq_encode.argtypes = [C.c_void_p, _f32p, C.c_uint64, _u8p]
+        L.qvh_pq_decode.argtypes = [C.c_void_p, _u8p, C.c_uint64, _f32p]
+        L.qvh_pq_tables.argtypes = [C.c_void_p, _f32p, C.c_uint64, C.c_int, _f32p]
+        L.qvh_pq_adc.argtypes = [C.c_void_p, _f32p, _u8p, C.c_uint64, _f32p]
+        L.qvh_nearest_centroid.argtypes = [_f32p, C.c_uint64, _f32p, C.c_uint32, C.c_uint32, _u32p]
+
+    def pq(self, dim, m, codebook):
+        return QvhPq(self, dim, m, codebook)
+
+    def nearest_centroid(self, x, cent):
+        """qvh_nearest_centroid of each row of x against the rows of cent."""
+        x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+        cent = np.ascontiguousarray(cent, dtype=np.float32)
+        out = np.empty(x.shape[0], dtype=np.uint32)
+        self.check(self.lib.qvh_nearest_centroid(x, x.shape[0], cent, cent.shape[0], x.shape[1], out))
+        return out
 
     def error(self) -> str:
         return self.lib.qvh_last_error().decode()
@@ -56,9 +76,15 @@ class Qvh:
         return QvhFlat(self, dim, metric)
 
     def last_fallbacks(self, handle) -> int:
-        """Queries of the handle's last search that the wide merge sent to the exact kernel."""
+        """Queries of the flat handle's last MFMA-scan search that the merge sent to the exact kernel."""
         n = C.c_uint32(0)
         self.check(self.lib.qvh_flat_last_fallbacks(C.c_void_p(handle), C.byref(n)))
+        return n.value
+
+    def ivf_last_fallbacks(self, handle) -> int:
+        """Queries of the IVF-PQ handle's last search whose approximate ranking was recomputed exactly."""
+        n = C.c_uint32(0)
+        self.check(self.lib.qvh_ivfpq_last_fallbacks(C.c_void_p(handle), C.byref(n)))
         return n.value
 
 
@@ -107,3 +133,46 @@ class QvhFlat:
         dist = np.empty((nq, k), dtype=np.float32)
         st = self.q.lib.qvh_flat_search_rows(self.h, queries, nq, k, listed, listed.size, out_rows, dist)
         return st, out_rows, dist
+
+
+class QvhPq:
+    """A qvh_pq handle: ProductQuantizer with an installed codebook [m][256][dim/m]."""
+
+    def __init__(self, q: Qvh, dim, m, codebook):
+        self.q, self.dim, self.m = q, dim, m
+        h = C.c_void_p()
+        q.check(q.lib.qvh_pq_create(dim, m, np.ascontiguousarray(codebook, dtype=np.float32), C.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self.q.lib.qvh_pq_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def encode(self, x):
+        x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+        codes = np.empty((x.shape[0], self.m), dtype=np.uint8)
+        self.q.check(self.q.lib.qvh_pq_encode(self.h, x, x.shape[0], codes))
+        return codes
+
+    def decode(self, codes):
+        codes = np.ascontiguousarray(np.atleast_2d(codes), dtype=np.uint8)
+        out = np.empty((codes.shape[0], self.dim), dtype=np.float32)
+        self.q.check(self.q.lib.qvh_pq_decode(self.h, codes, codes.shape[0], out))
+        return out
+
+    def tables(self, queries, inner_product=False):
+        queries = np.ascontiguousarray(np.atleast_2d(queries), dtype=np.float32)
+        out = np.empty((queries.shape[0], self.m, 256), dtype=np.float32)
+        self.q.check(self.q.lib.qvh_pq_tables(self.h, queries, queries.shape[0], int(inner_product), out))
+        return out
+
+    def adc(self, table, codes):
+        codes = np.ascontiguousarray(np.atleast_2d(codes), dtype=np.uint8)
+        out = np.empty(codes.shape[0], dtype=np.float32)
+        self.q.check(self.q.lib.qvh_pq_adc(self.h, np.ascontiguousarray(table, dtype=np.float32), codes,
+                                           codes.shape[0], out))
+        return out

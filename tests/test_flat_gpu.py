@@ -307,3 +307,41 @@ def test_search_over_listed_rows_edges():
     assert st == 0 and set(rows[0][:2]) == {3, 999} and np.all(rows[:, 2:] == np.uint32(0xFFFFFFFF))
     st, _, _ = f.search_rows(q, 4, np.array([5, 1_000], np.uint32))  # row 1000 is not stored
     assert st == -22 and "not stored" in f.q.error()
+
+
+@pytest.mark.parametrize("metric", ["l2", "ip"])
+def test_near_ties_within_rounding_fall_back_exactly(oracle, metric):
+    """Rows q0 + P(v) for 40 permutations P of one vector v all lie at the same true distance from
+    query 0, so their GEMM-form and exact distances differ only by rounding: the merge cannot
+    certify query 0's selection (its k-th exact distance is not below the 16th GEMM-form distance
+    minus the rounding bound) and hands it to the exact kernel. The other queries are certified.
+    Every result equals the oracle's (src/flat_index.cc:84-97)."""
+    rng = np.random.default_rng(23)
+    dim = 64
+    base = (4.0 * rng.standard_normal((60_000, dim))).astype(np.float32)
+    q = (4.0 * rng.standard_normal((40, dim))).astype(np.float32)
+    v = (0.7 * rng.standard_normal(dim)).astype(np.float32)
+    for i in range(40):
+        base[1_000 + 97 * i] = q[0] + v[rng.permutation(dim)]
+    idx = quiver.FlatIndex(dim, metric)
+    idx.add(base)
+    got_l, got_d = idx.search(q, 10)
+    fallbacks = Qvh().last_fallbacks(idx._index._device_handle)
+    rows, dist = oracle.flat_search(base, q, 10, metric)
+    print("fallbacks", fallbacks,
+          assert_same_topk(got_l, got_d, rows.astype(np.int64), dist, _true_dist(oracle, base, q, metric)))
+    if metric == "l2":
+        assert 1 <= fallbacks <= 3, fallbacks  # query 0 (and nothing like the others)
+
+
+def test_integer_rows_certify_exactly(oracle):
+    """Small-integer rows and queries whose (||q|| + max ||x||)^2 stays below 2^24: both distance forms
+    are exact, the rounding bound is 0 and no query falls back, at the size of the 1M workload's
+    batches (10,000 queries over 60,000 rows)."""
+    base, q = D.int_mix(60_000, 10_000)
+    idx = quiver.FlatIndex(128)
+    idx.add(base)
+    got_l, got_d = idx.search(q, 10)
+    assert Qvh().last_fallbacks(idx._index._device_handle) == 0
+    rows, dist = oracle.flat_search(base, q[:500], 10)
+    print(assert_same_topk(got_l[:500], got_d[:500], rows.astype(np.int64), dist, _true_dist(oracle, base, q, "l2")))

@@ -14,6 +14,7 @@ import quiver_amd as quiver
 from oracle.oracle import IvfPqState, rows_bitmap
 from parity import assert_same_topk
 from quiver_amd import datasets as D
+from qvh_ctypes import Qvh
 
 pytestmark = pytest.mark.gpu
 
@@ -231,3 +232,22 @@ def test_every_round_improves_on_the_last(oracle, metric, refine):
     q[:, 0] += 1.0
     idx, st = build_pair(oracle, base, metric, 1, 8, refine > 0, iters=4)
     print(compare_search(oracle, idx, st, q, 10, 1, refine))
+
+
+@pytest.mark.parametrize("refine", [0, 3])
+def test_uncertified_ranking_is_rescanned_exactly(oracle, refine):
+    """L2 with the precomputed table ranks by base + (term1 + sum qtab) and re-scores the best
+    keep + margin with the reference's sum base + sum (pre + qtab) (src/ivfpq_index.cc:334-346).
+    A hundred copies of one vector next to query 0 share a list and a code, more than the selection
+    holds (keep + max(16, keep / 2): 26 for k = 10, 46 with refine 3), so the approximate and exact
+    sums of the whole selection differ only by rounding: the keep-th exact sum is not below the
+    last approximate one minus the rounding bound, the ranking is not certified, and query 0 is
+    rescanned with exact sums (in a batch of whole queries and alone, as a sliced query). Every
+    result equals the oracle's."""
+    base = clustered(10_000, 32, 50, 61)
+    q = clustered(300, 32, 50, 62)
+    base[:100] = q[0] + np.float32(0.01)
+    idx, st = build_pair(oracle, base, "l2", 64, 16, refine > 0)
+    for qs in (q, q[:1]):
+        print(qs.shape[0], compare_search(oracle, idx, st, qs, 10, 8, refine))
+        assert Qvh().ivf_last_fallbacks(idx._index._device_handle) >= 1
