@@ -241,6 +241,21 @@ size_t orc_argmin_n(const float* v, size_t n) {
   return 0;
 }
 
+/* nearest_centroid (src/product_quantizer.cc:14-27): the first c whose l2sqr distance (the active
+ * AVX2 kernel) is strictly below the best so far, starting from +inf; 0 when none is. */
+size_t orc_nearest_centroid(const float* x, const float* centroids, size_t k, size_t dim) {
+  size_t best = 0;
+  float best_d = INFINITY;
+  for (size_t c = 0; c < k; ++c) {
+    const float d = orc_l2sqr_avx2(x, centroids + c * dim, dim);
+    if (d < best_d) {
+      best_d = d;
+      best = c;
+    }
+  }
+  return best;
+}
+
 /* centroid_table.h:94-144: dots accumulate x_j * c_j in order of j (unfused), then
  * d = ||c||^2 - 2*dot (or -dot for max inner product); the first strictly smaller d wins. A point
  * whose every d is NaN keeps index 0 (the caller's zero-initialized slot). */
@@ -655,44 +670,6 @@ void orc_ivfpq_encode(const float* centroids, const float* codebook, size_t nlis
 }
 
 static int ivf_ip(int metric) { return metric != ORC_L2; } /* src/ivfpq_index.cc:109 */
-
-void orc_ivfpq_probes(const orc_ivfpq* ix, const float* queries, size_t nq, size_t nprobe,
-                      int nthreads, uint32_t* out_lists, float* out_scores) {
-  const size_t d = ix->dim, nlist = ix->nlist;
-  float* ct = transpose(ix->centroids, nlist, d);
-  const int nt = nthreads_or_max(nthreads);
-#pragma omp parallel num_threads(nt)
-  {
-    float* buf = (float*)malloc(sizeof(float) * nlist);
-    float* qbuf = (float*)malloc(sizeof(float) * d);
-    cand* probes = (cand*)malloc(sizeof(cand) * nlist);
-#pragma omp for schedule(dynamic, 1)
-    for (size_t qi = 0; qi < nq; ++qi) {
-      const float* q = queries + qi * d;
-      if (ix->metric == ORC_COSINE) {
-        memcpy(qbuf, q, sizeof(float) * d);
-        normalize_one(qbuf, d);
-        q = qbuf;
-      }
-      if (ivf_ip(ix->metric)) {
-        ct_dot_t(q, ct, nlist, d, buf);
-        for (size_t l = 0; l < nlist; ++l) probes[l] = (cand){-buf[l], l};
-      } else {
-        ct_l2_t(q, ct, nlist, d, buf);
-        for (size_t l = 0; l < nlist; ++l) probes[l] = (cand){buf[l], l};
-      }
-      qsort(probes, nlist, sizeof(cand), cand_cmp);
-      for (size_t p = 0; p < nprobe; ++p) {
-        out_lists[qi * nprobe + p] = (uint32_t)probes[p].id;
-        out_scores[qi * nprobe + p] = probes[p].d;
-      }
-    }
-    free(probes);
-    free(qbuf);
-    free(buf);
-  }
-  free(ct);
-}
 
 int orc_ivfpq_search(const orc_ivfpq* ix, const float* queries, size_t nq, size_t k,
                      size_t nprobe_req, size_t refine_factor, const uint64_t* pos_bitmap,

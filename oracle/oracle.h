@@ -57,6 +57,8 @@ void orc_normalize(float* v, size_t n, size_t dim);
 void orc_ct_l2(const float* x, const float* cent, size_t k, size_t dim, float* out);
 void orc_ct_dot(const float* x, const float* cent, size_t k, size_t dim, float* out);
 size_t orc_argmin_n(const float* v, size_t n);
+/* nearest_centroid, src/product_quantizer.cc:14-27 */
+size_t orc_nearest_centroid(const float* x, const float* centroids, size_t k, size_t dim);
 void orc_nearest_batch(const float* x, size_t n, const float* cent, size_t k, size_t dim,
                        int max_inner_product, uint32_t* out, int nthreads);
 
@@ -119,9 +121,6 @@ int orc_ivfpq_search(const orc_ivfpq* ix, const float* queries, size_t nq, size_
                      int nthreads, uint64_t* out_refs, float* out_dist);
 /* Per-query coarse scores (L2: ||q-c||^2 sequential; IP/cosine: -<q,c>) and the first nprobe
  * lists by (score, list). For checking the device's probe selection. */
-void orc_ivfpq_probes(const orc_ivfpq* ix, const float* queries, size_t nq, size_t nprobe,
-                      int nthreads, uint32_t* out_lists, float* out_scores);
-
 #ifdef __cplusplus
 }
 #endif

@@ -81,6 +81,8 @@ class Oracle:
         L.orc_ct_dot.argtypes = [_f32p, _f32p, _sz, _sz, _f32p]
         L.orc_argmin_n.argtypes = [_f32p, _sz]
         L.orc_argmin_n.restype = _sz
+        L.orc_nearest_centroid.argtypes = [_f32p, _f32p, _sz, _sz]
+        L.orc_nearest_centroid.restype = _sz
         L.orc_nearest_batch.argtypes = [_f32p, _sz, _f32p, _sz, _sz, C.c_int, _u32p, C.c_int]
         L.orc_flat_search.argtypes = [_f32p, _sz, _sz, C.c_int, _f32p, _sz, _sz, C.c_void_p,
                                       C.c_int, _u32p, _f32p]
@@ -97,7 +99,6 @@ class Oracle:
                                        _u32p, _u8p, C.c_void_p]
         L.orc_ivfpq_search.argtypes = [C.c_void_p, _f32p, _sz, _sz, _sz, _sz, C.c_void_p,
                                        C.c_int, _u64p, _f32p]
-        L.orc_ivfpq_probes.argtypes = [C.c_void_p, _f32p, _sz, _sz, C.c_int, _u32p, _f32p]
 
     # -- engine / kernels --
     def mt64(self, seed: int, count: int) -> np.ndarray:
@@ -122,6 +123,12 @@ class Oracle:
     def argmin_n(self, v) -> int:
         v = _f32(v)
         return int(self.lib.orc_argmin_n(v, v.size))
+
+    def nearest_centroid(self, x, cent) -> np.ndarray:
+        """nearest_centroid (src/product_quantizer.cc:14-27) of each row of x."""
+        x, cent = _f32(np.atleast_2d(x)), _f32(cent)
+        return np.array([self.lib.orc_nearest_centroid(x[i], cent, cent.shape[0], x.shape[1])
+                         for i in range(x.shape[0])], dtype=np.uint32)
 
     def nearest(self, x, cent, max_inner_product=False, threads=0) -> np.ndarray:
         x, cent = _f32(x), _f32(cent)
@@ -251,15 +258,6 @@ class Oracle:
                                   threads, refs, dist)
         return refs, dist
 
-    def ivfpq_probes(self, ix: "IvfPqState", queries, nprobe, threads=0):
-        queries = _f32(queries)
-        nq = queries.shape[0]
-        lists = np.empty((nq, nprobe), dtype=np.uint32)
-        scores = np.empty((nq, nprobe), dtype=np.float32)
-        s = self._ivf_struct(ix)
-        self.lib.orc_ivfpq_probes(C.byref(s), queries, nq, nprobe, threads, lists, scores)
-        return lists, scores
-
 
 class IvfPqState:
     """Trained IVF-PQ state plus CSR inverted lists (the layout of the reference's LOFF / CODE /
@@ -338,6 +336,9 @@ class Reference:
         L.qref_ivfpq_load.restype = C.c_void_p
         L.qref_ivfpq_size.argtypes = [C.c_void_p]
         L.qref_ivfpq_size.restype = _sz
+        L.qref_ivfpq_memory_bytes.argtypes = [C.c_void_p]
+        L.qref_ivfpq_memory_bytes.restype = _sz
+        L.qref_ivfpq_list_sizes.argtypes = [C.c_void_p, C.c_void_p]
         L.qref_kmeans.argtypes = [_f32p, _sz, _sz, _sz, _sz, _sz, C.c_uint64, _sz, _f32p]
         L.qref_nearest_centroid.argtypes = [_f32p, _f32p, _sz, _sz]
         L.qref_nearest_centroid.restype = _sz
@@ -396,6 +397,11 @@ class Reference:
         self._check(self.lib.qref_kmeans(x, x.shape[0], x.shape[1], k, iterations,
                                          max_points_per_centroid, C.c_uint64(seed), threads, out))
         return out
+
+    def nearest_centroid(self, x, cent) -> np.ndarray:
+        x, cent = _f32(np.atleast_2d(x)), _f32(cent)
+        return np.array([self.lib.qref_nearest_centroid(np.ascontiguousarray(x[i]), cent, cent.shape[0], x.shape[1])
+                         for i in range(x.shape[0])], dtype=np.uint32)
 
     def pq_train(self, x, m, iterations=25, seed=1234, threads=0):
         x = _f32(x)
@@ -511,3 +517,12 @@ class RefIvfPq:
 
     def __len__(self):
         return int(self.ref.lib.qref_ivfpq_size(self.h))
+
+    @property
+    def memory_bytes(self) -> int:
+        return int(self.ref.lib.qref_ivfpq_memory_bytes(self.h))
+
+    def list_sizes(self, nlist: int) -> np.ndarray:
+        out = np.zeros(nlist, dtype=np.uint64)
+        self.ref.lib.qref_ivfpq_list_sizes(self.h, out.ctypes.data_as(C.c_void_p))
+        return out

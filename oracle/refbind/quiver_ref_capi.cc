@@ -172,6 +172,12 @@ void* qref_ivfpq_load(const char* path, int verify_checksums) {
   return out;
 }
 std::size_t qref_ivfpq_size(void* h) { return static_cast<quiver::IvfPqIndex*>(h)->size(); }
+std::size_t qref_ivfpq_memory_bytes(void* h) { return static_cast<quiver::IvfPqIndex*>(h)->memory_bytes(); }
+// out[nlist]: the list sizes.
+void qref_ivfpq_list_sizes(void* h, std::uint64_t* out) {
+  const auto sizes = static_cast<quiver::IvfPqIndex*>(h)->list_sizes();
+  for (std::size_t l = 0; l < sizes.size(); ++l) out[l] = sizes[l];
+}
 
 // ---- k-means / PQ ---------------------------------------------------------------------------
 int qref_kmeans(const float* x, std::size_t n, std::size_t dim, std::size_t k,

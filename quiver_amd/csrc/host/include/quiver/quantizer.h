@@ -1,16 +1,24 @@
-// k-means with the reference's interface (include/quiver/quantizer.h:47-58). The control flow
-// (subsample, random initialization, double-precision centroid sums, empty-cluster splitting)
-// runs on the host with the reference's random engine; every assignment step is one call of the
-// device's exact nearest-centroid kernel (qvh_points_nearest), so the centroids come out
-// bit-identical to the reference's.
+// k-means, nearest_centroid and the product quantizer, with the reference's interface
+// (include/quiver/quantizer.h:47-114).
+//
+// k-means runs its control flow (subsample, random initialization, double-precision centroid sums,
+// empty-cluster splitting) on the host with the reference's random engine; every assignment step is
+// one call of the device's exact nearest-centroid kernel (qvh_points_nearest), so the centroids
+// come out bit-identical to the reference's. nearest_centroid and every ProductQuantizer operation
+// run on the device (qvh_nearest_centroid, qvh_pq_*), batched: the reference's per-vector methods
+// are batches of one, and the *_batch methods (no reference counterpart) take many vectors per
+// device call.
 #pragma once
 
 #include <cstddef>
 #include <cstdint>
+#include <memory>
 #include <vector>
 
 #include "quiver/common.h"
 #include "quiver/thread_pool.h"
+
+struct qvh_pq;
 
 namespace quiver {
 
@@ -25,5 +33,75 @@ struct KMeansParams {
 /// Lloyd's k-means. Returns k x dim row-major centroids. Requires n >= k.
 std::vector<float> kmeans(const float* vectors, std::size_t n, std::size_t dim,
                           const KMeansParams& params, ThreadPool* pool = nullptr);
+
+/// Index of the centroid nearest to `x` (squared L2; the first of equal ones; 0 when no distance
+/// is finite). A device failure here terminates the process: the reference's version cannot fail.
+std::size_t nearest_centroid(const float* x, const float* centroids, std::size_t k,
+                             std::size_t dim) noexcept;
+
+/// The same for n row-major points (no reference counterpart): out[i] for point i.
+void nearest_centroid_batch(const float* x, std::size_t n, const float* centroids, std::size_t k,
+                            std::size_t dim, std::uint32_t* out);
+
+/// PQ: the vector is split into `m` sub-vectors, each replaced by the id of its nearest of 256
+/// sub-centroids, so a vector costs `m` bytes; distances to a query use asymmetric distance
+/// computation over an m x 256 table. The codebook lives on the device once trained or set; copies
+/// share it. The noexcept methods terminate the process on a device failure (the reference's CPU
+/// versions cannot fail); the *_batch methods throw quiver::Error instead.
+class ProductQuantizer {
+ public:
+  static constexpr std::size_t kSubCentroids = 256;
+
+  ProductQuantizer();
+  /// `dim` must be divisible by `m`.
+  ProductQuantizer(std::size_t dim, std::size_t m);
+  ~ProductQuantizer();
+  ProductQuantizer(const ProductQuantizer&);
+  ProductQuantizer& operator=(const ProductQuantizer&);
+  ProductQuantizer(ProductQuantizer&&) noexcept;
+  ProductQuantizer& operator=(ProductQuantizer&&) noexcept;
+
+  void train(const float* vectors, std::size_t n, ThreadPool* pool = nullptr,
+             std::size_t iterations = 25, std::uint64_t seed = 1234);
+  bool trained() const noexcept { return !centroids_.empty(); }
+
+  std::size_t dim() const noexcept { return dim_; }
+  std::size_t m() const noexcept { return m_; }
+  std::size_t dsub() const noexcept { return dsub_; }
+  std::size_t code_size() const noexcept { return m_; }
+
+  void encode(const float* vector, std::uint8_t* code) const noexcept;
+  void decode(const std::uint8_t* code, float* vector) const noexcept;
+
+  /// table[j * 256 + c] = ||q_j - centroid_{j,c}||^2
+  void compute_l2_table(const float* query, float* table) const noexcept;
+  /// table[j * 256 + c] = <q_j, centroid_{j,c}>
+  void compute_ip_table(const float* query, float* table) const noexcept;
+
+  /// Sum of table entries selected by `code`, in order of the sub-spaces.
+  float adc(const float* table, const std::uint8_t* code) const noexcept;
+  /// ADC for `n` contiguous codes.
+  void adc_batch(const float* table, const std::uint8_t* codes, std::size_t n,
+                 float* out) const noexcept;
+
+  /// Batched forms (no reference counterpart): codes [n][m], vectors [n][dim], tables
+  /// [nq][m][256] (L2 or inner product).
+  void encode_batch(const float* vectors, std::size_t n, std::uint8_t* codes) const;
+  void decode_batch(const std::uint8_t* codes, std::size_t n, float* vectors) const;
+  void compute_tables(const float* queries, std::size_t nq, bool inner_product, float* tables) const;
+
+  /// m x 256 x dsub sub-centroids.
+  const std::vector<float>& centroids() const noexcept { return centroids_; }
+  void set_centroids(std::vector<float> centroids);
+
+ private:
+  qvh_pq* device() const;
+
+  std::size_t dim_ = 0;
+  std::size_t m_ = 0;
+  std::size_t dsub_ = 0;
+  std::vector<float> centroids_;
+  std::shared_ptr<qvh_pq> dev_;  // the codebook on the device; immutable, shared by copies
+};
 
 }  // namespace quiver

@@ -4,13 +4,11 @@
 // inline, and the first exception thrown by a chunk is rethrown to the caller.
 #pragma once
 
-#include <condition_variable>
 #include <cstddef>
-#include <cstdint>
-#include <exception>
 #include <functional>
+#include <memory>
 #include <mutex>
-#include <thread>
+#include <semaphore>
 #include <vector>
 
 namespace quiver {
@@ -25,7 +23,7 @@ class ThreadPool {
   ThreadPool(const ThreadPool&) = delete;
   ThreadPool& operator=(const ThreadPool&) = delete;
 
-  std::size_t num_threads() const noexcept { return threads_.size() + 1; }
+  std::size_t num_threads() const noexcept { return helpers_.size() + 1; }
 
   /// Runs fn over [0, n) in chunks of at most `grain` items and blocks until all finish.
   void parallel_for(std::size_t n, std::size_t grain, const RangeFn& fn);
@@ -34,19 +32,15 @@ class ThreadPool {
   static ThreadPool& global();
 
  private:
-  struct Task;
-  void worker();
-  static void drain(Task& task) noexcept;
+  struct Loop;    // the shared state of one parallel_for call
+  struct Helper;  // a helper thread and the semaphore that hands it a loop
 
-  std::vector<std::thread> threads_;
-  std::mutex submit_;            // one parallel_for at a time per pool
-  std::mutex mu_;
-  std::condition_variable wake_;
-  std::condition_variable idle_;
-  Task* task_ = nullptr;
-  std::uint64_t epoch_ = 0;
-  std::size_t busy_ = 0;
-  bool stopping_ = false;
+  void serve(Helper& helper);
+  void stop_helpers() noexcept;
+
+  std::vector<std::unique_ptr<Helper>> helpers_;
+  std::mutex calls_;                    // one parallel_for at a time per pool
+  std::binary_semaphore finished_{0};  // released by the last helper to leave a loop
 };
 
 }  // namespace quiver

@@ -1,25 +1,42 @@
+#include <algorithm>
+#include <iterator>
+
 #include "quiver/common.h"
 
 namespace quiver {
 
+namespace {
+
+struct MetricAlias {
+  std::string_view name;
+  Metric metric;
+};
+
+// Every spelling parse_metric accepts (include/quiver/common.h:35-36 of the reference lists
+// them); the first spelling of each metric is its canonical name, which to_string returns.
+constexpr MetricAlias kAliases[] = {
+    {"l2", Metric::kL2},          {"euclidean", Metric::kL2},         {"ip", Metric::kInnerProduct},
+    {"inner_product", Metric::kInnerProduct}, {"dot", Metric::kInnerProduct},
+    {"cosine", Metric::kCosine},  {"cos", Metric::kCosine},           {"angular", Metric::kCosine},
+};
+
+}  // namespace
+
 std::string_view to_string(Metric metric) noexcept {
-  switch (metric) {
-    case Metric::kL2: return "l2";
-    case Metric::kInnerProduct: return "ip";
-    case Metric::kCosine: return "cosine";
-  }
-  return "unknown";
+  const auto* hit = std::find_if(std::begin(kAliases), std::end(kAliases),
+                                 [metric](const MetricAlias& a) { return a.metric == metric; });
+  return hit == std::end(kAliases) ? std::string_view("unknown") : hit->name;
 }
 
 Metric parse_metric(std::string_view name) {
-  if (name == "l2" || name == "euclidean") return Metric::kL2;
-  if (name == "ip" || name == "inner_product" || name == "dot") return Metric::kInnerProduct;
-  if (name == "cosine" || name == "cos" || name == "angular") return Metric::kCosine;
-  throw Error("unknown metric '" + std::string(name) + "' (expected l2, ip, or cosine)");
+  const auto* hit = std::find_if(std::begin(kAliases), std::end(kAliases),
+                                 [name](const MetricAlias& a) { return a.name == name; });
+  // The message is part of the API: the Python layer surfaces it as the ValueError text.
+  QUIVER_CHECK(hit != std::end(kAliases),
+               "unknown metric '" + std::string(name) + "' (expected l2, ip, or cosine)");
+  return hit->metric;
 }
 
-namespace detail {
-void throw_error(const std::string& message) { throw Error(message); }
-}  // namespace detail
+[[noreturn]] void detail::throw_error(const std::string& message) { throw Error(message); }
 
 }  // namespace quiver

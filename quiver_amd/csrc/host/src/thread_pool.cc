@@ -2,44 +2,80 @@
 
 #include <algorithm>
 #include <atomic>
+#include <exception>
+#include <thread>
 
 namespace quiver {
+
 namespace {
-// Set while this thread executes a chunk of some pool: nested loops then run inline.
-thread_local bool t_in_chunk = false;
+// Depth of loops this thread is running chunks of (any pool): a parallel_for issued from inside a
+// chunk runs inline rather than waiting for helpers that may all be busy with the outer loop.
+thread_local int t_loop_depth = 0;
 }  // namespace
 
-struct ThreadPool::Task {
-  const RangeFn* fn = nullptr;
-  std::size_t n = 0, grain = 1;
+// One parallel_for: chunks are claimed from an atomic cursor by the caller and every helper; the
+// first exception wins, and once one is recorded no new chunk starts.
+struct ThreadPool::Loop {
+  const RangeFn& fn;
+  const std::size_t n, grain;
   std::atomic<std::size_t> cursor{0};
+  std::atomic<std::size_t> helpers_inside{0};
   std::atomic<bool> failed{false};
-  std::mutex err_mu;
+  std::once_flag error_once;
   std::exception_ptr error;
+
+  Loop(const RangeFn& f, std::size_t count, std::size_t g) : fn(f), n(count), grain(g) {}
+
+  void claim_chunks() noexcept {
+    ++t_loop_depth;
+    for (;;) {
+      if (failed.load(std::memory_order_relaxed)) break;
+      const std::size_t begin = cursor.fetch_add(grain, std::memory_order_relaxed);
+      if (begin >= n) break;
+      try {
+        fn(begin, std::min(n, begin + grain));
+      } catch (...) {
+        std::call_once(error_once, [&] { error = std::current_exception(); });
+        failed.store(true, std::memory_order_relaxed);
+      }
+    }
+    --t_loop_depth;
+  }
+};
+
+// A helper sleeps on its own semaphore; the caller of parallel_for stores the loop (or null, to
+// stop it) and releases the semaphore, which orders that store before the helper reads it.
+struct ThreadPool::Helper {
+  std::binary_semaphore wake{0};
+  Loop* loop = nullptr;
+  std::thread thread;
 };
 
 ThreadPool::ThreadPool(std::size_t num_threads) {
-  if (num_threads == 0) num_threads = std::max<std::size_t>(1, std::thread::hardware_concurrency());
+  const std::size_t total = num_threads != 0 ? num_threads : std::max(1u, std::thread::hardware_concurrency());
   try {
-    for (std::size_t i = 1; i < num_threads; ++i) threads_.emplace_back([this] { worker(); });
-  } catch (...) {
-    {
-      std::lock_guard<std::mutex> lock(mu_);
-      stopping_ = true;
+    while (helpers_.size() + 1 < total) {
+      auto h = std::make_unique<Helper>();
+      Helper& ref = *h;
+      helpers_.push_back(std::move(h));
+      ref.thread = std::thread([this, &ref] { serve(ref); });
     }
-    wake_.notify_all();
-    for (auto& t : threads_) t.join();
+  } catch (...) {
+    stop_helpers();
     throw;
   }
 }
 
-ThreadPool::~ThreadPool() {
-  {
-    std::lock_guard<std::mutex> lock(mu_);
-    stopping_ = true;
+ThreadPool::~ThreadPool() { stop_helpers(); }
+
+void ThreadPool::stop_helpers() noexcept {
+  for (auto& h : helpers_) {
+    if (!h->thread.joinable()) continue;
+    h->loop = nullptr;
+    h->wake.release();
+    h->thread.join();
   }
-  wake_.notify_all();
-  for (auto& t : threads_) t.join();
+  helpers_.clear();
 }
 
 ThreadPool& ThreadPool::global() {
@@ -47,64 +83,34 @@ ThreadPool& ThreadPool::global() {
   return pool;
 }
 
-void ThreadPool::drain(Task& task) noexcept {
-  const bool outer = t_in_chunk;
-  t_in_chunk = true;
-  while (!task.failed.load(std::memory_order_relaxed)) {
-    const std::size_t b = task.cursor.fetch_add(task.grain, std::memory_order_relaxed);
-    if (b >= task.n) break;
-    try {
-      (*task.fn)(b, std::min(task.n, b + task.grain));
-    } catch (...) {
-      std::lock_guard<std::mutex> lock(task.err_mu);
-      if (!task.error) task.error = std::current_exception();
-      task.failed.store(true, std::memory_order_relaxed);
-    }
-  }
-  t_in_chunk = outer;
-}
-
-void ThreadPool::worker() {
-  std::uint64_t seen = 0;
-  std::unique_lock<std::mutex> lock(mu_);
+void ThreadPool::serve(Helper& helper) {
   for (;;) {
-    wake_.wait(lock, [&] { return stopping_ || epoch_ != seen; });
-    if (stopping_) return;
-    seen = epoch_;
-    Task* task = task_;
-    lock.unlock();
-    drain(*task);
-    lock.lock();
-    if (--busy_ == 0) idle_.notify_one();
+    helper.wake.acquire();
+    Loop* loop = helper.loop;
+    if (loop == nullptr) return;
+    loop->claim_chunks();
+    // The last helper out wakes the caller; nothing of the loop is touched after this count.
+    if (loop->helpers_inside.fetch_sub(1, std::memory_order_acq_rel) == 1) finished_.release();
   }
 }
 
 void ThreadPool::parallel_for(std::size_t n, std::size_t grain, const RangeFn& fn) {
   if (n == 0) return;
   grain = std::max<std::size_t>(grain, 1);
-  if (threads_.empty() || n <= grain || t_in_chunk) {
+  if (helpers_.empty() || n <= grain || t_loop_depth > 0) {
     fn(0, n);
     return;
   }
-  std::lock_guard<std::mutex> submit(submit_);
-  Task task;
-  task.fn = &fn;
-  task.n = n;
-  task.grain = grain;
-  {
-    std::lock_guard<std::mutex> lock(mu_);
-    task_ = &task;
-    busy_ = threads_.size();
-    ++epoch_;
+  std::lock_guard<std::mutex> one_at_a_time(calls_);
+  Loop loop(fn, n, grain);
+  loop.helpers_inside.store(helpers_.size(), std::memory_order_relaxed);
+  for (auto& h : helpers_) {
+    h->loop = &loop;
+    h->wake.release();
   }
-  wake_.notify_all();
-  drain(task);
-  {
-    std::unique_lock<std::mutex> lock(mu_);
-    idle_.wait(lock, [&] { return busy_ == 0; });
-    task_ = nullptr;
-  }
-  if (task.error) std::rethrow_exception(task.error);
+  loop.claim_chunks();
+  finished_.acquire();  // every helper has left the loop
+  if (loop.error) std::rethrow_exception(loop.error);
 }
 
 }  // namespace quiver

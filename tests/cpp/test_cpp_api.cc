@@ -1,7 +1,8 @@
-// The public C++ API (quiver/flat_index.h, quiver/ivfpq_index.h) driven the way a C++ caller of the
-// reference drives it: the behaviours its tests check for the flat and IVF-PQ indexes
-// (tests/test_flat.cc, tests/test_quantizer.cc, tests/test_regressions.cc), compiled against this
-// package's headers and run on the GPU. Prints one line per case and exits non-zero on a failure.
+// The public C++ API (quiver/flat_index.h, quiver/ivfpq_index.h, quiver/quantizer.h) driven the way
+// a C++ caller of the reference drives it: the behaviours its tests check for the flat and IVF-PQ
+// indexes, k-means, nearest_centroid and the product quantizer (tests/test_flat.cc,
+// tests/test_quantizer.cc, tests/test_regressions.cc), compiled against this package's headers and
+// run on the GPU. Prints one line per case and exits non-zero on a failure.
 
 #include <algorithm>
 #include <cmath>
@@ -18,6 +19,7 @@
 #include "quiver/filter.h"
 #include "quiver/flat_index.h"
 #include "quiver/ivfpq_index.h"
+#include "quiver/quantizer.h"
 
 namespace {
 
@@ -227,6 +229,154 @@ void ivfpq_recall_save_load_and_errors(const std::string& dir) {
   }
 }
 
+double l2_double(const float* a, const float* b, std::size_t dim) {
+  double s = 0;
+  for (std::size_t j = 0; j < dim; ++j) {
+    const double t = static_cast<double>(a[j]) - b[j];
+    s += t * t;
+  }
+  return s;
+}
+
+double dot_double(const float* a, const float* b, std::size_t dim) {
+  double s = 0;
+  for (std::size_t j = 0; j < dim; ++j) s += static_cast<double>(a[j]) * b[j];
+  return s;
+}
+
+// tests/test_quantizer.cc:20-37: three well separated clusters; nearest_centroid finds each centre's
+// centroid within 0.05.
+void kmeans_recovers_separated_clusters() {
+  const std::size_t dim = 4, per = 200, k = 3;
+  const float centers[3][4] = {{0, 0, 0, 0}, {10, 10, 0, 0}, {0, 0, 10, 10}};
+  const auto noise = normal_vectors(per * k, dim, 1);
+  std::vector<float> data;
+  for (std::size_t c = 0; c < k; ++c)
+    for (std::size_t i = 0; i < per; ++i)
+      for (std::size_t j = 0; j < dim; ++j) data.push_back(centers[c][j] + 0.1f * noise[(c * per + i) * dim + j]);
+  quiver::KMeansParams kp;
+  kp.k = k;
+  const auto cent = quiver::kmeans(data.data(), per * k, dim, kp);
+  for (const auto& c : centers) {
+    const std::size_t nearest = quiver::nearest_centroid(c, cent.data(), k, dim);
+    EXPECT(nearest < k && l2_double(c, cent.data() + nearest * dim, dim) < 0.05);
+  }
+  // The first of equal centroids wins; no finite distance: index 0.
+  const std::vector<float> twins = {5, 5, 1, 1, 1, 1};
+  const float origin[2] = {1, 1};
+  EXPECT(quiver::nearest_centroid(origin, twins.data(), 3, 2) == 1);
+  const std::vector<float> huge = {3e38f, 3e38f, -3e38f, -3e38f};
+  EXPECT(quiver::nearest_centroid(origin, huge.data(), 2, 2) == 0);
+}
+
+// tests/test_quantizer.cc:39-48: identical points force empty clusters; no NaN comes out.
+void kmeans_handles_duplicate_points() {
+  std::vector<float> data(1000 * 2, 1.0f);
+  for (std::size_t i = 0; i < 20; ++i) data[i * 2] = static_cast<float>(i);
+  quiver::KMeansParams kp;
+  kp.k = 16;
+  for (float x : quiver::kmeans(data.data(), 1000, 2, kp)) EXPECT(std::isfinite(x));
+}
+
+// tests/test_quantizer.cc:50-68: more sub-quantizers reconstruct better.
+void pq_reconstruction_beats_coarser_codes() {
+  const std::size_t dim = 32, n = 4000;
+  const auto data = blob_vectors(n, dim, 10, 3);
+  double prev = 1e30;
+  for (std::size_t m : {4u, 8u, 16u}) {
+    quiver::ProductQuantizer pq(dim, m);
+    pq.train(data.data(), n);
+    EXPECT(pq.trained() && pq.code_size() == m && pq.dsub() == dim / m);
+    std::vector<std::uint8_t> codes(n * m);
+    std::vector<float> back(n * dim);
+    pq.encode_batch(data.data(), n, codes.data());
+    pq.decode_batch(codes.data(), n, back.data());
+    std::vector<std::uint8_t> one(m);
+    std::vector<float> rec(dim);
+    for (std::size_t i = 0; i < n; i += 397) {  // the per-vector calls agree with the batch
+      pq.encode(data.data() + i * dim, one.data());
+      EXPECT(std::equal(one.begin(), one.end(), codes.begin() + static_cast<std::ptrdiff_t>(i * m)));
+      pq.decode(one.data(), rec.data());
+      EXPECT(std::equal(rec.begin(), rec.end(), back.begin() + static_cast<std::ptrdiff_t>(i * dim)));
+    }
+    double err = 0;
+    for (std::size_t i = 0; i < n * dim; ++i) err += (data[i] - back[i]) * static_cast<double>(data[i] - back[i]);
+    err /= static_cast<double>(n * dim);
+    std::printf("    m=%zu reconstruction mse %.4f\n", m, err);
+    EXPECT(err < prev);
+    prev = err;
+  }
+  EXPECT(prev < 0.3);
+}
+
+// tests/test_quantizer.cc:70-92: ADC over the L2 table is the distance to the reconstruction, and
+// over the IP table the inner product with it; adc_batch equals adc.
+void pq_adc_equals_distance_to_reconstruction() {
+  const std::size_t dim = 16, n = 1000, m = 4;
+  const auto data = normal_vectors(n, dim, 4);
+  quiver::ProductQuantizer pq(dim, m);
+  pq.train(data.data(), n);
+  const auto q = normal_vectors(1, dim, 5);
+  std::vector<float> l2t(m * 256), ipt(m * 256);
+  pq.compute_l2_table(q.data(), l2t.data());
+  pq.compute_ip_table(q.data(), ipt.data());
+  std::vector<std::uint8_t> codes(7 * m);
+  for (std::size_t i = 0; i < 7; ++i) pq.encode(data.data() + i * dim, codes.data() + i * m);
+  std::vector<float> batch(7);
+  pq.adc_batch(l2t.data(), codes.data(), 7, batch.data());
+  for (std::size_t i = 0; i < 7; ++i) {
+    std::vector<float> rec(dim);
+    pq.decode(codes.data() + i * m, rec.data());
+    const float a = pq.adc(l2t.data(), codes.data() + i * m);
+    EXPECT(std::fabs(a - l2_double(q.data(), rec.data(), dim)) < 1e-3);
+    EXPECT(batch[i] == a);
+    EXPECT(std::fabs(pq.adc(ipt.data(), codes.data() + i * m) - dot_double(q.data(), rec.data(), dim)) < 1e-3);
+  }
+  // A copy shares the trained codebook; set_centroids installs one directly.
+  const quiver::ProductQuantizer copy = pq;
+  quiver::ProductQuantizer other(dim, m);
+  other.set_centroids(pq.centroids());
+  std::vector<std::uint8_t> c1(m), c2(m);
+  copy.encode(data.data() + 3 * dim, c1.data());
+  other.encode(data.data() + 3 * dim, c2.data());
+  EXPECT(std::equal(c1.begin(), c1.end(), codes.begin() + 3 * static_cast<std::ptrdiff_t>(m)) && c1 == c2);
+}
+
+// tests/test_quantizer.cc:94-99
+void pq_rejects_bad_shapes() {
+  EXPECT(throws_error([] { quiver::ProductQuantizer(10, 3); }));
+  quiver::ProductQuantizer pq(8, 2);
+  const auto few = normal_vectors(100, 8, 1);
+  EXPECT(throws_error([&] { pq.train(few.data(), 100); }));
+  EXPECT(throws_error([&] { pq.set_centroids(std::vector<float>(7)); }));
+  EXPECT(throws_error([&] { quiver::ProductQuantizer().train(few.data(), 100); }));
+}
+
+// IvfPqIndex::list_sizes / memory_bytes (src/ivfpq_index.cc:446-463): the sizes add up to size(),
+// and the byte count follows the reference's accounting.
+void ivfpq_list_sizes_and_memory_bytes() {
+  const std::size_t dim = 16, n = 3000;
+  const auto base = blob_vectors(n, dim, 20, 8);
+  for (const bool store : {false, true}) {
+    quiver::IvfPqParams p;
+    p.dim = dim;
+    p.nlist = 32;
+    p.m = 8;
+    p.store_vectors = store;
+    quiver::IvfPqIndex index(p);
+    EXPECT(index.list_sizes().size() == p.nlist);
+    index.train(base.data(), n);
+    index.add(base.data(), n);
+    const auto sizes = index.list_sizes();
+    std::size_t total = 0;
+    for (std::size_t s : sizes) total += s;
+    EXPECT(total == n);
+    const std::size_t expect = (p.nlist * dim + p.m * 256 * (dim / p.m) + p.nlist * p.m * 256) * sizeof(float) +
+                               n * p.m + n * sizeof(quiver::Label) + (store ? n * dim * sizeof(float) : 0);
+    EXPECT(index.memory_bytes() == expect);
+  }
+}
+
 }  // namespace
 
 int main() {
@@ -238,6 +388,12 @@ int main() {
       {"flat_fewer_than_k_and_filters", flat_fewer_than_k_and_filters},
       {"flat_save_load", [&] { flat_save_load(dir); }},
       {"ivfpq_recall_save_load_and_errors", [&] { ivfpq_recall_save_load_and_errors(dir); }},
+      {"kmeans_recovers_separated_clusters", kmeans_recovers_separated_clusters},
+      {"kmeans_handles_duplicate_points", kmeans_handles_duplicate_points},
+      {"pq_reconstruction_beats_coarser_codes", pq_reconstruction_beats_coarser_codes},
+      {"pq_adc_equals_distance_to_reconstruction", pq_adc_equals_distance_to_reconstruction},
+      {"pq_rejects_bad_shapes", pq_rejects_bad_shapes},
+      {"ivfpq_list_sizes_and_memory_bytes", ivfpq_list_sizes_and_memory_bytes},
   };
   for (const auto& [name, fn] : cases) {
     const int before = g_failures;

@@ -77,3 +77,26 @@ def few_rows():
 def int_mix_sample(n: int):
     """Training rows of the 1M-row IVF-PQ workload: the first 100,000 of a seeded permutation."""
     return np.random.default_rng(31).permutation(n)[:100_000]
+
+
+def nearest_centroid_cases():
+    """(points, centroids) pairs for nearest_centroid: dims that take every branch of the AVX2
+    reduction (32-element blocks, 8-element blocks, the tail), duplicated centroids (the first of
+    equal distances wins), and centroids so large that some or all distances overflow to +inf."""
+    rng = np.random.default_rng(61)
+    cases = []
+    for n, k, dim in ((200, 50, 37), (100, 300, 128), (150, 40, 3), (80, 64, 70)):
+        cases.append((rng.standard_normal((n, dim)).astype(np.float32),
+                      rng.standard_normal((k, dim)).astype(np.float32)))
+    rows = rng.standard_normal((20, 16)).astype(np.float32)
+    twins = np.repeat(rows, 2, axis=0)
+    cases.append(((rows + 1e-3 * rng.standard_normal(rows.shape)).astype(np.float32), twins))
+    big = rng.standard_normal((12, 8)).astype(np.float32)
+    big[:6] *= np.float32(3e37)
+    pts = rng.standard_normal((10, 8)).astype(np.float32)
+    pts[0] = np.float32(3e37)
+    cases.append((pts, big))
+    allbig = np.full((5, 8), np.float32(3e38))
+    allbig[::2] *= -1
+    cases.append((np.zeros((3, 8), np.float32), allbig))
+    return cases

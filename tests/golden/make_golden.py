@@ -8,6 +8,7 @@ inputs where they are small, and the reference's outputs.
 
     python tests/golden/make_golden.py            # small fixtures (seconds)
     python tests/golden/make_golden.py --full     # + the 1M-row IVF-PQ workload hashes (minutes)
+    python tests/golden/make_golden.py --only nearest   # one fixture
 
 Fixtures:
   kernels.npz     l2sqr / dot for dims 1..70, normalize bits (incl. zero and overflow rows)
@@ -18,6 +19,8 @@ Fixtures:
   ivfpq_small.npz IVF-PQ train + add + search (n=4000, dim 32, nlist 32, m 8): centroids,
                   codebook, CSR lists, search outputs at nprobe 1/8/32, L2 (+refine), cosine
                   (+refine), inner product, and the refine-saturation case
+  nearest.npz     nearest_centroid over seeded points and centroids (AVX2 tail branches,
+                  duplicated centroids, overflowing distances)
   ivfpq_1m.json   (--full) SHA-256 of the trained state and lists of the 1,000,000 x 128 integer
                   mixture at nlist 2048, m 32 (trained on default_rng(31)'s first 100,000 rows),
                   and search outputs of the first 200 queries at nprobe 32
@@ -42,7 +45,8 @@ from oracle.oracle import Reference  # noqa: E402
 from quiver_amd import datasets as D  # noqa: E402
 from tests.golden.inputs import (IVF_CASES, IVF_ITERS, IVF_M, IVF_NLIST, IVF_NPROBES,  # noqa: E402
                                  NORMALIZE_DIMS, few_rows, flat_filter, int_mix_sample, ivf_points,
-                                 kernel_pairs, kmeans_points, normalize_rows, pq_points, sha)
+                                 kernel_pairs, kmeans_points, nearest_centroid_cases, normalize_rows,
+                                 pq_points, sha)
 
 
 def kernels(ref: Reference):
@@ -93,6 +97,14 @@ def kmeans_pq(ref: Reference):
     return out
 
 
+def nearest(ref: Reference):
+    out = {}
+    for i, (x, cent) in enumerate(nearest_centroid_cases()):
+        out[f"case{i}_sha"] = np.array(sha(x) + sha(cent))
+        out[f"case{i}_out"] = ref.nearest_centroid(x, cent)
+    return out
+
+
 def ivfpq_small(ref: Reference, tmp: str):
     base, q = ivf_points()
     out = dict(ivf_sha=np.array(sha(base) + sha(q)))
@@ -139,9 +151,14 @@ def ivfpq_1m(ref: Reference, tmp: str):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--full", action="store_true")
+    ap.add_argument("--only", choices=["nearest"], help="write only this fixture")
     args = ap.parse_args()
     ref = Reference()
     print("reference SIMD path:", ref.simd_isa)
+    if args.only == "nearest":
+        np.savez_compressed(os.path.join(HERE, "nearest.npz"), **nearest(ref))
+        return
+    np.savez_compressed(os.path.join(HERE, "nearest.npz"), **nearest(ref))
     np.savez_compressed(os.path.join(HERE, "kernels.npz"), **kernels(ref))
     np.savez_compressed(os.path.join(HERE, "flat_c1.npz"), **flat_c1(ref))
     np.savez_compressed(os.path.join(HERE, "kmeans.npz"), **kmeans_pq(ref))

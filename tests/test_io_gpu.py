@@ -72,6 +72,9 @@ def test_ivfpq_reference_file_round_trip(tmp_path, reference, metric, store, ref
 
     ours = quiver.IvfPqIndex.load(theirs)
     assert ours.is_trained and len(ours) == 6_000
+    # IvfPqIndex::list_sizes / memory_bytes (src/ivfpq_index.cc:446-463) equal the reference's
+    assert np.array_equal(np.asarray(ours.list_sizes(), dtype=np.uint64), ref.list_sizes(32))
+    assert ours.memory_bytes == ref.memory_bytes
     for nprobe in (1, 8, 32):
         exp_l, exp_d = ref.search(q, 10, nprobe=nprobe, refine_factor=refine)
         got_l, got_d = ours.search(q, 10, nprobe=nprobe, refine_factor=refine)
@@ -95,6 +98,8 @@ def test_ivfpq_saved_here_loads_in_reference(tmp_path, reference):
     ours.save(path)
     ref = reference.ivfpq_load(path)
     assert len(ref) == 5_000
+    assert np.array_equal(np.asarray(ours.list_sizes(), dtype=np.uint64), ref.list_sizes(16))
+    assert ours.memory_bytes == ref.memory_bytes
     for nprobe, refine in ((4, 0), (16, 3)):
         exp_l, exp_d = ref.search(q, 10, nprobe=nprobe, refine_factor=refine)
         got_l, got_d = ours.search(q, 10, nprobe=nprobe, refine_factor=refine)

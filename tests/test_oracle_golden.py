@@ -178,6 +178,34 @@ def test_argmin_first_minimum(oracle):
 
 # ---- k-means and PQ -----------------------------------------------------------------------------
 
+def test_nearest_centroid_matches_reference(oracle):
+    """nearest_centroid (src/product_quantizer.cc:14-27) against the compiled reference's outputs:
+    AVX2 tail branches, first-of-equal on duplicated centroids, overflowing distances (index 0
+    when none is finite)."""
+    g = golden("nearest.npz")
+    for i, (x, cent) in enumerate(G.nearest_centroid_cases()):
+        assert str(g[f"case{i}_sha"]) == G.sha(x) + G.sha(cent)
+        assert np.array_equal(oracle.nearest_centroid(x, cent), g[f"case{i}_out"]), i
+
+
+def test_nearest_centroid_brute_force(oracle):
+    """Against float64 brute force wherever the two nearest centroids are further apart than the
+    float rounding of the distances; a dropped term or a swapped operand moves the answer."""
+    rng = np.random.default_rng(62)
+    for dim in (1, 5, 16, 40, 77, 128):
+        x = rng.standard_normal((60, dim)).astype(np.float32)
+        cent = rng.standard_normal((90, dim)).astype(np.float32)
+        got = oracle.nearest_centroid(x, cent)
+        d = ((x[:, None, :].astype(np.float64) - cent[None].astype(np.float64)) ** 2).sum(-1)
+        part = np.sort(d, axis=1)
+        clear = part[:, 1] - part[:, 0] > 1e-5 * (1 + part[:, 0])
+        assert clear.sum() > 50
+        assert np.array_equal(got[clear], d.argmin(axis=1)[clear].astype(np.uint32)), dim
+    twins = np.repeat(rng.standard_normal((4, 3)).astype(np.float32), 3, axis=0)
+    assert list(oracle.nearest_centroid(twins[::3], twins)) == [0, 3, 6, 9]
+    assert oracle.nearest_centroid(np.zeros(2, np.float32), np.full((3, 2), 3e38, np.float32))[0] == 0
+
+
 def test_kmeans_matches_reference_bits(oracle):
     g = golden("kmeans.npz")
     x, dup = G.kmeans_points()
