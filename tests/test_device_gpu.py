@@ -1,15 +1,19 @@
 """Device-resident query batches from Python: torch (ROCm) tensors in GPU memory go straight to the
-device search (FlatIndex/IvfPqIndex.search_batch_device) and the results stay on the device.
+device search (FlatIndex/IvfPqIndex.search_batch_device) and the results stay on the device. The
+reference's bindings take host arrays only (python/quiver_ext.cc:24-25); its search_batch
+(src/flat_index.cc:126-140, src/ivfpq_index.cc:421-437) defines the answer.
 
-The host-buffer search is the reference here (it is checked against the oracle in
-test_flat_gpu.py / test_ivfpq_gpu.py): labels must be identical and distances bit-identical,
-since both run the same kernels on the same queries.
+The main cases check the device-tensor results against the oracle directly: distances bit-identical,
+labels identical up to equal-distance groups at the k-th boundary. The edge cases (empty index,
+conversions, streams) compare with the host-buffer path, itself checked against the oracle.
 """
 
 import numpy as np
 import pytest
 
 import quiver_amd as quiver
+from oracle.oracle import IvfPqState, rows_bitmap
+from parity import assert_same_topk
 
 pytestmark = pytest.mark.gpu
 
@@ -36,19 +40,45 @@ def _data(n, dim, nq, seed):
             rng.standard_normal((nq, dim)).astype(np.float32))
 
 
+def _oracle_match(dev_result, exp_labels, exp_dist):
+    """Device-tensor results against the oracle's labels (uint64, all ones = empty) and distances."""
+    dl, dd = dev_result
+    assert dl.dtype == torch.int64 and dd.dtype == torch.float32
+    return assert_same_topk(dl.cpu().numpy(), dd.cpu().numpy(), exp_labels, exp_dist)
+
+
+def _flat_expected(oracle, stored, q, k, metric, labels, allowed=None):
+    bm = None
+    if allowed is not None:
+        bm = rows_bitmap(np.flatnonzero(np.isin(labels, allowed)), labels.size)
+    rows, dist = oracle.flat_search(stored, q, k, metric, bm)
+    exp = np.full(rows.shape, np.uint64(2**64 - 1), dtype=np.uint64)
+    ok = rows != np.uint32(0xFFFFFFFF)
+    exp[ok] = labels[rows[ok].astype(np.int64)]
+    return exp, dist
+
+
 @pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
-def test_flat_device_queries_match_host(metric):
+def test_flat_device_queries_match_oracle(oracle, metric):
     dev = _gpu()
     base, q = _data(20_000, 64, 300, 1)
     print(f"case: flat {metric} n=20000 dim=64 nq=300", flush=True)
+    labels = np.arange(20_000, dtype=np.uint64) * 3 + 7
     idx = quiver.FlatIndex(64, metric)
-    idx.add(base, labels=np.arange(20_000, dtype=np.uint64) * 3 + 7)
+    idx.add(base, labels=labels)
+    stored = oracle.normalize(base) if metric == "cosine" else base
     qd = torch.from_numpy(q).to(dev)
-    for k in (1, 10, 32, 100):
-        _same(idx.search(q, k), idx.search(qd, k))
+    for k in (1, 10, 32, 100):  # MFMA scan with KL 16 and 32, the wide merge
+        print(k, _oracle_match(idx.search(qd, k), *_flat_expected(oracle, stored, q, k, metric, labels)))
     allowed = np.arange(7, 60_000, 9, dtype=np.uint64)
-    _same(idx.search(q, 10, filter=allowed), idx.search(qd, 10, filter=allowed))
-    _same(idx.search(q[0], 5), idx.search(qd[0], 5))  # one query as a 1-D tensor
+    print(_oracle_match(idx.search(qd, 10, filter=allowed),
+                        *_flat_expected(oracle, stored, q, 10, metric, labels, allowed)))
+    for nq in (1, 5):  # the few-query scan (a 1-D tensor is one query)
+        one = idx.search(qd[0], 5) if nq == 1 else idx.search(qd[:nq], 5)
+        exp_l, exp_d = _flat_expected(oracle, stored, q[:nq], 5, metric, labels)
+        if nq == 1:
+            one = (one[0].reshape(1, -1), one[1].reshape(1, -1))
+        print(nq, _oracle_match(one, exp_l, exp_d))
 
 
 def test_flat_device_edge_cases():
@@ -91,20 +121,30 @@ def test_flat_device_search_runs_on_the_current_stream():
 
 @pytest.mark.parametrize("metric,store,refine", [("l2", False, 0), ("l2", True, 4), ("cosine", True, 8),
                                                  ("ip", False, 0)])
-def test_ivfpq_device_queries_match_host(metric, store, refine):
+def test_ivfpq_device_queries_match_oracle(oracle, metric, store, refine):
     dev = _gpu()
     base, q = _data(12_000, 32, 200, 4)
     print(f"case: ivfpq {metric} store={store} refine={refine}", flush=True)
+    labels = np.arange(12_000, dtype=np.uint64) * 5 + 1
     idx = quiver.IvfPqIndex(32, metric, nlist=64, m=8, store_vectors=store, train_iterations=5)
     idx.train(base)
-    idx.add(base, labels=np.arange(12_000, dtype=np.uint64) * 5 + 1)
+    cent, cb, pre = oracle.ivfpq_train(base, metric, 64, 8, 5, 1234)
+    assert np.array_equal(idx.centroids.view(np.uint32), cent.view(np.uint32))
+    assert np.array_equal(idx.codebook.view(np.uint32), cb.view(np.uint32))
+    idx.add(base, labels=labels)
+    assign, codes, stored = oracle.ivfpq_encode(cent, cb, metric, base)
+    st = IvfPqState(metric, cent, cb, pre).set_lists(assign, codes, labels, stored if store else None)
     qd = torch.from_numpy(q).to(dev)
+
+    def check(nprobe, allowed=None):
+        bm = None if allowed is None else rows_bitmap(np.flatnonzero(np.isin(st.labels, allowed)), st.labels.size)
+        refs, dist = oracle.ivfpq_search(st, q, 10, nprobe, refine, bm)
+        got = idx.search(qd, 10, nprobe=nprobe, refine_factor=refine, filter=allowed)
+        print(nprobe, allowed is not None, _oracle_match(got, st.ref_to_label(refs), dist))
+
     for nprobe in (1, 8, 64):
-        _same(idx.search(q, 10, nprobe=nprobe, refine_factor=refine),
-              idx.search(qd, 10, nprobe=nprobe, refine_factor=refine))
-    allowed = np.arange(1, 60_000, 25, dtype=np.uint64)
-    _same(idx.search(q, 10, nprobe=16, refine_factor=refine, filter=allowed),
-          idx.search(qd, 10, nprobe=16, refine_factor=refine, filter=allowed))
+        check(nprobe)
+    check(16, np.arange(1, 60_000, 25, dtype=np.uint64))
 
 
 def test_ivfpq_device_untrained_and_growing():
