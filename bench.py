@@ -18,10 +18,13 @@ flat search time of one and of eight of the same queries. `roofline` is each
 workload's dominant kernel measured with HIP events on the stream it runs on: the flat scan's
 algorithmic 2*n*d*nq FLOP per launch against the dense FP32 matrix peak (157.3 TFLOP/s), the
 IVF-PQ list scan's algorithmic code bytes (sum over queries and probed lists of len * m) against
-HBM peak (8 TB/s). `cpu_baseline` is the reference's own CPU search (its sources compiled by
-oracle/Makefile; the C restatement in oracle/ when that library is absent) timed on this host's
-cores over a bounded sample of the same queries; for IVF-PQ it loads the index built here from a
-.qvr file, so both sides search identical trained state and lists.
+HBM peak (8 TB/s). `host_api` is the reference's own way of timing (bench/ann_bench.cc:351-357,
+378): search_batch through the C++ classes with host buffers in and out, best of 3, which adds the
+PCIe transfers. `cpu_baseline` is the reference's own CPU search (its sources compiled by
+oracle/Makefile; the C restatement in oracle/ when that library is absent) timed on every CPU this
+process may use (`host`: hardware_concurrency, affinity, cgroup quota) and on one thread, over a
+bounded sample of the same queries; for IVF-PQ it loads the index built here from a .qvr file, so
+both sides search identical trained state and lists.
 """
 
 from __future__ import annotations
@@ -110,6 +113,24 @@ class Qvh:
         return name.value.decode(), arch.value.decode(), cus.value
 
 
+def host_cores():
+    """CPUs this process may use: the affinity mask, bounded by a cgroup v2 CPU quota if one is set
+    (cpu.max), next to std::thread::hardware_concurrency() (os.cpu_count()), which is what the
+    reference's ThreadPool(0) sizes itself to."""
+    visible = os.cpu_count() or 1
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else visible
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, period = f.read().split()[:2]
+            if q != "max":
+                quota = float(q) / float(period)
+    except (OSError, ValueError):
+        pass
+    usable = affinity if quota is None else max(1, min(affinity, int(quota)))
+    return {"hardware_concurrency": visible, "affinity": affinity, "cgroup_cpus": quota, "usable": usable}
+
+
 COPY_CALIBRATION_BYTES = 256 << 20
 
 
@@ -193,6 +214,17 @@ def bench_flat(args, hip: Hip, qvh: Qvh):
         "config": {"workload": "flat exact L2 k=10: 1,000,000 x 128 fp32 integer-valued mixture, "
                                "10,000 queries batched", "n": n, "dim": dim, "nq": nq, "k": k},
     }
+    # The reference's timing (bench/ann_bench.cc:351-357,378): FlatIndex::search_batch from host
+    # buffers to host buffers, best of 3 after a warm-up, through the C++ class (Python binding).
+    import quiver_amd as quiver
+
+    host_index = quiver.FlatIndex(dim, "l2")
+    host_index.add(base)
+    host_index.search(queries, k)
+    best = min(_timed(lambda: host_index.search(queries, k)) for _ in range(3))
+    result["host_api"] = {"qps": nq / best, "ms": best * 1e3,
+                          "note": "FlatIndex::search_batch, host numpy buffers in and out (PCIe included)"}
+    del host_index
     if not args.no_extra:
         # Small batches (the first 1 and 8 queries; the few-query kernels): device time of one
         # search from its stage events, and the caller's wall time of search + sync.
@@ -215,6 +247,12 @@ def bench_flat(args, hip: Hip, qvh: Qvh):
     for p in (d_q, d_rows, d_dist):
         hip.lib.hipFree(p)
     return result, base, queries
+
+
+def _timed(fn) -> float:
+    t = time.perf_counter()
+    fn()
+    return time.perf_counter() - t
 
 
 def bench_ivfpq(args, hip: Hip, qvh: Qvh, base, queries):
@@ -277,8 +315,29 @@ def bench_ivfpq(args, hip: Hip, qvh: Qvh, base, queries):
     hip.d2h(dist, d_dist)
     assert (refs != np.uint64(2**64 - 1)).all() and (np.diff(dist, axis=1) >= 0).all(), "malformed results"
 
+    # Host buffers in and out through IvfPqIndex::search_batch (bench/ann_bench.cc:351-357,378).
+    idx.search(queries, k, nprobe=nprobe)
+    best = min(_timed(lambda: idx.search(queries, k, nprobe=nprobe)) for _ in range(3))
+    host_api = {"qps": nq / best, "ms": best * 1e3,
+                "note": "IvfPqIndex::search_batch, host numpy buffers in and out (PCIe included)"}
     larger_k = {}
     if not args.no_extra:
+        # Small batches (sliced queries): device time of the select and scan stages, and the
+        # caller's wall time of search + sync.
+        small = {}
+        for b in (1, 100):
+            dev, wall = [], []
+            for _ in range(21):
+                t = time.perf_counter()
+                qvh.check(qvh.lib.qvh_ivfpq_search_device(h, d_q, b, k, nprobe, 0, None, d_refs, d_dist, None),
+                          "search")
+                qvh.check(qvh.lib.qvh_ivfpq_sync(h), "sync")
+                wall.append(time.perf_counter() - t)
+                sel_, scan_, _ = timing(with_bytes=False)
+                dev.append(sel_ + scan_)
+            small[f"nq{b}"] = {"device_us": float(np.median(dev[1:])) * 1e3,
+                               "wall_us": float(np.median(wall[1:])) * 1e6}
+        larger_k["small_batches"] = small
         # The same queries at nprobe 32 with k = 100 (150 candidates re-scored per query).
         k2 = 100
         d_refs2, d_dist2 = hip.malloc(nq * k2 * 8), hip.malloc(nq * k2 * 4)
@@ -289,7 +348,7 @@ def bench_ivfpq(args, hip: Hip, qvh: Qvh, base, queries):
             scans.append(timing(with_bytes=False))
         qvh.check(qvh.lib.qvh_ivfpq_sync(h), "sync")
         sel2, scan2 = (float(np.median([t[i] for t in scans[1:]])) for i in (0, 1))
-        larger_k = {"k100": {"select_ms": sel2, "scan_ms": scan2, "qps": nq / ((sel2 + scan2) * 1e-3)}}
+        larger_k["k100"] = {"select_ms": sel2, "scan_ms": scan2, "qps": nq / ((sel2 + scan2) * 1e-3)}
         for p in (d_refs2, d_dist2):
             hip.lib.hipFree(p)
     for p in (d_q, d_refs, d_dist):
@@ -305,6 +364,7 @@ def bench_ivfpq(args, hip: Hip, qvh: Qvh, base, queries):
         "unit": "queries/s",
         "ms_per_step": ms_per_step,
         "stage_ms": {"select": float(st[:, 0].mean()), "scan": scan_ms},
+        "host_api": host_api,
         "roofline": {"bound": "hbm", "kernel": "ivf_stream_kernel<8, true, 128, false>", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": load_traffic("ivf_stream_int_mix_1m_nprobe32_pmc"),
@@ -438,7 +498,7 @@ def cpu_baseline_ivfpq(idx, queries, k, nprobe, seconds, threads):
     return {"value": done / elapsed, "unit": "queries/s", "cores": threads, "kind": kind,
             "sample": f"{done} queries (the 10,000-query set cycled in batches of {batch}) at nprobe {nprobe} "
                       f"against the same 1,000,000-vector index loaded from .qvr ({elapsed:.1f} s, "
-                      f"{threads} threads, ThreadPool grain 1)"}
+                      f"ThreadPool({threads}), grain 1)"}
 
 
 def cpu_baseline_flat(base, queries, k, seconds, threads):
@@ -464,7 +524,14 @@ def cpu_baseline_flat(base, queries, k, seconds, threads):
     elapsed = time.perf_counter() - t0
     return {"value": done / elapsed, "unit": "queries/s", "cores": threads, "kind": kind,
             "sample": f"first {done} of {queries.shape[0]} queries against all {base.shape[0]} rows "
-                      f"({elapsed:.1f} s, {threads} threads, ThreadPool grain 1)"}
+                      f"({elapsed:.1f} s, ThreadPool({threads}), grain 1)"}
+
+
+def with_one_thread(full, one):
+    """The multithreaded baseline with the one-thread run beside it (the reference reports both)."""
+    out = dict(full)
+    out["one_thread"] = {"value": one["value"], "sample": one["sample"]}
+    return out
 
 
 def main():
@@ -473,7 +540,8 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="CPU baseline threads (default: every CPU the process may use, cgroup quota included)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the filtered cosine flat and the cosine IVF-PQ refine workloads")
@@ -498,10 +566,15 @@ def main():
         extra["ivfpq_cosine_refine"] = bench_ivfpq_cosine_refine(args, hip, qvh)
     cpu = None
     ivf["cpu_baseline"] = None
+    cores = host_cores()
     if not args.no_cpu:
-        cpu = cpu_baseline_flat(base, queries, 10, args.cpu_seconds, args.cpu_threads)
-        ivf["cpu_baseline"] = cpu_baseline_ivfpq(idx, queries, 10, 32, args.cpu_seconds / 3,
-                                                 args.cpu_threads)
+        threads = args.cpu_threads or cores["usable"]
+        cpu = with_one_thread(cpu_baseline_flat(base, queries, 10, args.cpu_seconds, threads),
+                              cpu_baseline_flat(base, queries, 10, args.cpu_seconds / 3, 1))
+        cpu["host"] = cores
+        ivf["cpu_baseline"] = with_one_thread(
+            cpu_baseline_ivfpq(idx, queries, 10, 32, args.cpu_seconds / 3, threads),
+            cpu_baseline_ivfpq(idx, queries, 10, 32, args.cpu_seconds / 3, 1))
     line = {
         "metric": METRIC,
         "value": flat["value"],
@@ -519,6 +592,7 @@ def main():
         "roofline": flat["roofline"],
         "cpu_baseline": cpu,
         "stage_ms": flat["stage_ms"],
+        "host_api": flat["host_api"],
         "nsplit": flat["nsplit"],
         "ivfpq": ivf,
         **extra,

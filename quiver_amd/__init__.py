@@ -48,14 +48,16 @@ ArrayLike = Union[np.ndarray, Iterable]
 
 
 def _as_matrix(x: ArrayLike, dim: int) -> np.ndarray:
-    a = np.ascontiguousarray(x, dtype=np.float32)
+    """Vectors as a C-contiguous float32 [n, dim] matrix; a single vector may be 1-D. The messages
+    are the reference's (python/quiver/__init__.py:28-36)."""
+    a = np.asarray(x, dtype=np.float32)
     if a.ndim == 1:
-        a = a.reshape(1, -1)
-    if a.ndim != 2:
+        a = a[np.newaxis, :]
+    elif a.ndim != 2:
         raise ValueError(f"expected a 1-D or 2-D array, got shape {a.shape}")
     if a.shape[1] != dim:
         raise ValueError(f"expected dimension {dim}, got {a.shape[1]}")
-    return a
+    return np.ascontiguousarray(a)
 
 
 def _is_device_tensor(x) -> bool:
@@ -136,33 +138,46 @@ def _device_bitmap(bits: np.ndarray, device):
 _MAX_LABEL = 2**63 - 1  # labels come back as int64, and -1 marks an empty slot
 
 
+def _check_label(v) -> None:
+    """One label: an integer (bool excluded) in [0, 2**63)."""
+    if isinstance(v, bool) or not isinstance(v, (int, np.integer)):
+        raise TypeError("labels must be integers")
+    if v < 0:
+        raise ValueError("labels must be non-negative")
+    if v > _MAX_LABEL:
+        raise ValueError("labels must be below 2**63")
+
+
+def _label_array(labels) -> np.ndarray:
+    if isinstance(labels, np.ndarray) and labels.dtype != object:
+        flat = labels.ravel()
+        if flat.size == 0:
+            return flat.astype(np.uint64)
+        if not np.issubdtype(flat.dtype, np.integer):
+            raise TypeError("labels must be integers")
+        if flat.min() < 0:
+            raise ValueError("labels must be non-negative")
+        if flat.max() > _MAX_LABEL:
+            raise ValueError("labels must be below 2**63")
+        return flat.astype(np.uint64)
+    # Python objects are checked one by one as ints: numpy would read [0, 2**63] as float64.
+    if isinstance(labels, np.ndarray):
+        items = labels.ravel().tolist()
+    elif isinstance(labels, (int, np.integer)):
+        items = [labels]
+    else:
+        items = list(labels)
+    for v in items:
+        _check_label(v)
+    return np.fromiter((int(v) for v in items), dtype=np.uint64, count=len(items))
+
+
 def _as_labels(labels: Optional[ArrayLike], n: Optional[int] = None) -> Optional[np.ndarray]:
-    """Validate labels: integers in [0, 2**63). Accepts arrays, lists, sets, and iterators."""
+    """Labels as uint64: integers in [0, 2**63) from an array, a list, a set or an iterator, with
+    the reference's messages (python/quiver/__init__.py:42-72); n, when given, is the count."""
     if labels is None:
         return None
-    if isinstance(labels, np.ndarray):
-        a = labels.reshape(-1)
-        if a.dtype == object:
-            return _as_labels(a.tolist(), n)
-        if a.size and not np.issubdtype(a.dtype, np.integer):
-            raise TypeError("labels must be integers")
-        if a.size:
-            if np.issubdtype(a.dtype, np.signedinteger) and a.min() < 0:
-                raise ValueError("labels must be non-negative")
-            if a.max() > _MAX_LABEL:
-                raise ValueError("labels must be below 2**63")
-        a = np.ascontiguousarray(a, dtype=np.uint64)
-    else:
-        # Check as Python ints before numpy sees them: numpy would turn [0, 2**63] into float64.
-        items = [labels] if isinstance(labels, (int, np.integer)) else list(labels)
-        for v in items:
-            if isinstance(v, bool) or not isinstance(v, (int, np.integer)):
-                raise TypeError("labels must be integers")
-            if v < 0:
-                raise ValueError("labels must be non-negative")
-            if v > _MAX_LABEL:
-                raise ValueError("labels must be below 2**63")
-        a = np.array([int(v) for v in items], dtype=np.uint64)
+    a = _label_array(labels)
     if n is not None and a.shape[0] != n:
         raise ValueError(f"got {a.shape[0]} labels for {n} vectors")
     return a

@@ -1113,10 +1113,12 @@ __device__ void merge_sorted_lists(const uint32_t* __restrict__ part_r, const fl
 
 /// The k best of a query's nsplit <= 1024 sorted partial lists of k <= 256 exact keys each, one
 /// 1024-thread work-group per query: T0 is the k-th smallest list head; every key of the k best
-/// is <= T0, and only the (at most k) lists whose heads are <= T0 hold such keys, so at most k * k
-/// real keys are gathered and sorted. More than kSelectMergeCap of them (possible above k = 64)
-/// flag the query (overflow[q] = 1, else 0) for the sequential merge of the same lists, which
-/// gives the same k keys.
+/// is <= T0. The heads are distinct keys (a row lives in one split), so at most k lists have a
+/// head <= T0, and only they hold such keys: at most k * k real keys are gathered and sorted. With
+/// fewer lists than k, T0 is the padding key and every real key is gathered, nsplit * k < k * k of
+/// them. So for k <= 64 the kSelectMergeCap = 4096 buffer always suffices; above, a query that
+/// gathers more is flagged (overflow[q] = 1, else 0) for the sequential merge of the same lists,
+/// which gives the same k keys.
 constexpr uint32_t kSelectMergeMaxK = 256;
 constexpr uint32_t kSelectMergeLists = 1024;
 constexpr uint32_t kSelectMergeCap = 4096;

@@ -596,11 +596,11 @@ struct ScanArgs {
 /// Certificate of an approximate selection (mode pre). The scan kept the keep_sel best candidates by
 /// approximate score, the last at a_last, so every other admitted code scores at least a_last, and
 /// its exact sum at least a_last - delta. When the keep-th smallest exact sum of the selection lies
-/// strictly below that, no unselected code can enter the best keep. A selection that kept every
-/// admitted code (count < keep_sel) is complete.
-__device__ __forceinline__ bool adc_selection_certified(uint32_t count, uint32_t keep_sel, float a_last, float r_keep,
-                                                        float delta) {
-  if (count < keep_sel) return true;
+/// strictly below that, no unselected code can enter the best keep. A complete selection (no queue
+/// cut or compaction ever dropped a candidate, and the selection holds all that were kept) holds
+/// every admitted code and needs no check.
+__device__ __forceinline__ bool adc_selection_certified(bool complete, float a_last, float r_keep, float delta) {
+  if (complete) return true;
   return static_cast<double>(r_keep) < static_cast<double>(a_last) - static_cast<double>(delta);
 }
 
@@ -714,6 +714,7 @@ __device__ void ivf_scan_query(const ScanArgs& a, const uint32_t q) {
   float* s_lut = reinterpret_cast<float*>(s_plist + ((a.nprobe + 1) & ~1u));  // [m][256]
   __shared__ uint32_t s_count;
   __shared__ uint64_t s_thr;
+  __shared__ uint32_t s_dropped;  // a compaction dropped candidates
 
   const int tid = threadIdx.x;
   const float* qv = a.Q + static_cast<uint64_t>(q) * a.dim;
@@ -743,6 +744,7 @@ __device__ void ivf_scan_query(const ScanArgs& a, const uint32_t q) {
     s_pstart[a.nprobe] = acc;
     s_count = 0;
     s_thr = ~0ull;
+    s_dropped = 0;
   }
   __syncthreads();
 
@@ -756,6 +758,7 @@ __device__ void ivf_scan_query(const ScanArgs& a, const uint32_t q) {
     block_sort_u64(s_cand, n2);
     if (tid == 0) {
       const uint32_t kept = min(cnt, keep_sel);
+      if (cnt > keep_sel) s_dropped = 1;
       s_count = kept;
       if (kept == keep_sel && kept > 0) s_thr = min(s_thr, s_cand[kept - 1]);
     }
@@ -897,7 +900,7 @@ __device__ void ivf_scan_query(const ScanArgs& a, const uint32_t q) {
     cnt = min(cnt, a.keep);
     const uint64_t kth = s_cand[cnt > 0 ? cnt - 1 : 0];
     const bool certified =
-        adc_selection_certified(selected, keep_sel, ordered_to_float(static_cast<uint32_t>(last >> 32)),
+        adc_selection_certified(s_dropped == 0 && selected <= keep_sel, ordered_to_float(static_cast<uint32_t>(last >> 32)),
                                 ordered_to_float(static_cast<uint32_t>(kth >> 32)), a.delta[q]);
     // An uncertified query is recomputed afterwards by this kernel with exact sums (exact_pre).
     if (!certified && tid == 0) a.fallback[atomicAdd(a.nfallback, 1u)] = q;
@@ -992,10 +995,12 @@ __device__ __forceinline__ float table_entry(const float* qv, const float* cbt, 
 /// standard bound gamma_m on a sum of m rounded terms gives |a - V| <= (m + 2) u T + 3 u P + u B and
 /// |r - V| <= (m + 2) u (P + T) + u B for the exact value V, so |a - r| <= (2m + 5) u (B + P + T)
 /// up to O(u^2). delta takes (2m + 16) u (max over probed lists of |score_l| + pmax[l], plus
-/// T_q = sum_j max_c |qtab[j][c]|), u = 2^-24. One wave per query; the table entries are computed
-/// with the scan's own arithmetic.
+/// T_q), u = 2^-24, where T_q = 2 (1 + 2^-20) sum_j ||q_j|| cmax[j] bounds sum_j |qtab[j][c_j]|
+/// for every code: qtab[j][c] = -2 <q_j, C_jc> is a sum of dsub rounded products, so by
+/// Cauchy-Schwarz its magnitude is at most 2 (1 + dsub u) ||q_j|| ||C_jc||, and cmax[j] is the
+/// largest ||C_jc||. One wave per query.
 __global__ void __launch_bounds__(256) adc_bound_kernel(const float* __restrict__ Q, uint32_t nq, uint32_t dim,
-                                                        uint32_t m, uint32_t dsub, const float* __restrict__ cbt,
+                                                        uint32_t m, uint32_t dsub, const float* __restrict__ cmax,
                                                         const float* __restrict__ scores, uint32_t nlist,
                                                         const uint32_t* __restrict__ probes, uint32_t nprobe,
                                                         const float* __restrict__ pmax, float* __restrict__ delta) {
@@ -1004,14 +1009,16 @@ __global__ void __launch_bounds__(256) adc_bound_kernel(const float* __restrict_
   if (q >= nq) return;  // whole wave
   const float* qv = Q + static_cast<uint64_t>(q) * dim;
   double tsum = 0.0;
-  for (uint32_t j = 0; j < m; ++j) {
-    float mx = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) mx = fmaxf(mx, fabsf(table_entry(qv, cbt, dsub, j, lane + 64 * i, true)));
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-    tsum += static_cast<double>(mx);
+  for (uint32_t j = lane; j < m; j += 64) {
+    double norm2 = 0.0;
+    for (uint32_t t = 0; t < dsub; ++t) {
+      const double v = qv[static_cast<uint64_t>(j) * dsub + t];
+      norm2 += v * v;
+    }
+    tsum += sqrt(norm2) * static_cast<double>(cmax[j]);
   }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) tsum += __shfl_xor(tsum, off, 64);
   float bp = 0.0f;
   for (uint32_t p = lane; p < nprobe; p += 64) {
     const uint32_t l = probes[static_cast<uint64_t>(q) * nprobe + p];
@@ -1020,11 +1027,29 @@ __global__ void __launch_bounds__(256) adc_bound_kernel(const float* __restrict_
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) bp = fmaxf(bp, __shfl_xor(bp, off, 64));
   if (lane != 0) return;
-  // (1 + 2^-20) covers the float rounding of |score| + pmax; a NaN or overflowing bound stays
-  // non-finite and certifies nothing.
-  const double d = (2.0 * m + 16.0) / 16777216.0 * ((static_cast<double>(bp) + tsum) * (1.0 + 1.0 / 1048576.0));
+  // (1 + 2^-20) covers the float rounding of |score| + pmax, the double sums and dsub u; a NaN or
+  // overflowing bound stays non-finite and certifies nothing.
+  const double tq = 2.0 * tsum;
+  const double d = (2.0 * m + 16.0) / 16777216.0 * ((static_cast<double>(bp) + tq) * (1.0 + 1.0 / 1048576.0));
   const float df = static_cast<float>(d);
   delta[q] = static_cast<double>(df) < d ? __uint_as_float(__float_as_uint(df) + 1u) : df;
+}
+
+/// cmax[j] = max_c ||codebook[j][c]||, computed in double and rounded up. One thread per sub-space.
+__global__ void codeword_norm_kernel(const float* __restrict__ cb, uint32_t m, uint32_t dsub,
+                                     float* __restrict__ cmax) {
+  const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= m) return;
+  double best = 0.0;
+  for (uint32_t c = 0; c < 256; ++c) {
+    const float* w = cb + (static_cast<uint64_t>(j) * 256 + c) * dsub;
+    double s = 0.0;
+    for (uint32_t t = 0; t < dsub; ++t) s += static_cast<double>(w[t]) * static_cast<double>(w[t]);
+    best = fmax(best, sqrt(s));
+  }
+  const double v = best * (1.0 + 1e-12);
+  const float f = static_cast<float>(v);
+  cmax[j] = static_cast<double>(f) < v ? __uint_as_float(__float_as_uint(f) + 1u) : f;
 }
 
 // Bank-rotated table lookups (the L2 scan with the precomputed table). The table is laid out
@@ -1529,7 +1554,9 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
       key = t[0];
       cnt_f = min(cnt_f, a.keep);
       const uint64_t kth = __shfl(key, static_cast<int>(cnt_f > 0 ? cnt_f - 1 : 0), 64);
-      certified = adc_selection_certified(merged, keep_sel, ordered_to_float(static_cast<uint32_t>(last >> 32)),
+      // No wave ever cut its queue (s_thr untouched) and the selection took every kept key.
+      const bool complete = merged <= keep_sel && s_thr == 0xFFFFFFFFu;
+      certified = adc_selection_certified(complete, ordered_to_float(static_cast<uint32_t>(last >> 32)),
                                           ordered_to_float(static_cast<uint32_t>(kth >> 32)), a.delta[q]);
     }
     if (split) {
@@ -1646,7 +1673,8 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
     __syncthreads();
     cnt_f = min(cnt_f, a.keep);
     const uint64_t kth = s_queue[cnt_f > 0 ? cnt_f - 1 : 0];
-    certified = adc_selection_certified(merged, keep_sel, ordered_to_float(static_cast<uint32_t>(last >> 32)),
+    const bool complete = merged <= keep_sel && s_thr == 0xFFFFFFFFu;
+    certified = adc_selection_certified(complete, ordered_to_float(static_cast<uint32_t>(last >> 32)),
                                         ordered_to_float(static_cast<uint32_t>(kth >> 32)), a.delta[q]);
   }
   if (split) {
@@ -1893,6 +1921,7 @@ struct qvh_ivfpq {
   DeviceBuffer cent, cent_t, cent_norm, cb, cbt, cbc, pre;
   DeviceBuffer off, codes, t1, vec;
   DeviceBuffer pmax;  // [nlist] sum_j max_c |pre[l][j][c]| (the L2 ranking's certificate)
+  DeviceBuffer cmax;  // [m] largest codeword norm per sub-space (the same)
   hipStream_t stream = nullptr;
   std::mutex mu;
   DeviceBuffer w_x, w_res, w_assign, w_codes, w_codes_p, w_t1, w_dest, w_shift;
@@ -2040,7 +2069,7 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   if (certify) {
     delta = static_cast<float*>(h->w_delta.reserve(nq * sizeof(float)));
     hipLaunchKernelGGL(adc_bound_kernel, dim3(static_cast<unsigned>(ceil_div(nq, 4))), dim3(256), 0, s, dq,
-                       static_cast<uint32_t>(nq), h->dim, h->m, h->dsub, h->cbt.as<float>(), scores, h->nlist, probes,
+                       static_cast<uint32_t>(nq), h->dim, h->m, h->dsub, h->cmax.as<float>(), scores, h->nlist, probes,
                        nprobe, h->pmax.as<float>(), delta);
     fb = static_cast<uint32_t*>(h->w_fb.reserve((nq + 1) * sizeof(uint32_t)));
     hipLaunchKernelGGL(zero_u32_kernel, dim3(1), dim3(64), 0, s, fb, 1);
@@ -2203,6 +2232,8 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
     launch_block_scan(a, grid);
   }
   QVH_HIP(hipGetLastError());
+  // The scan stage ends here; the rescan of uncertified queries (normally an empty launch) follows.
+  if (h->timed) QVH_HIP(hipEventRecord(h->ev[2], s));
   if (certify) {
     // Exact rescan of the uncertified queries (normally none): the block-buffer scan with the
     // reference's sum for every code, over the listed queries, after every kernel above.
@@ -2214,7 +2245,6 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
     launch_block_scan(fa, dim3(static_cast<unsigned>(std::min<uint64_t>(nq, 2 * static_cast<uint64_t>(std::max(h->cus, 1))))));
     QVH_HIP(hipGetLastError());
   }
-  if (h->timed) QVH_HIP(hipEventRecord(h->ev[2], s));
   if (h->timed_bytes) {
     uint64_t* bytes = static_cast<uint64_t*>(h->w_bytes.reserve(sizeof(uint64_t)));
     hipLaunchKernelGGL(probed_code_bytes_kernel, dim3(1), dim3(256), 0, s, probes, nq * nprobe, a.off, h->m, bytes);
@@ -2314,6 +2344,9 @@ qvh_status qvh_ivfpq_set_trained(qvh_ivfpq* h, const float* centroids, const flo
       h->pmax.reserve(h->nlist * sizeof(float));
       hipLaunchKernelGGL(pre_bound_kernel, dim3(h->nlist), dim3(256), 0, s, h->pre.as<float>(), h->m,
                          h->pmax.as<float>());
+      h->cmax.reserve(h->m * sizeof(float));
+      hipLaunchKernelGGL(codeword_norm_kernel, dim3(static_cast<unsigned>(ceil_div(h->m, 64))), dim3(64), 0, s,
+                         h->cb.as<float>(), h->m, h->dsub, h->cmax.as<float>());
     }
     QVH_HIP(hipGetLastError());
     QVH_HIP(hipStreamSynchronize(s));

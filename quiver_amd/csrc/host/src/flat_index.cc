@@ -77,6 +77,7 @@ void FlatIndex::search_rows(const float* queries, std::size_t nq, std::size_t k,
     std::fill(out_dist, out_dist + nq * k, std::numeric_limits<float>::infinity());
     return;
   }
+  QUIVER_CHECK(k <= 0xFFFFFFFFull, "k is too large");
   ThreadPool& tp = pool ? *pool : ThreadPool::global();
   std::vector<std::uint64_t> bitmap;
   if (filter != nullptr) {

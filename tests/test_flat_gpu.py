@@ -345,3 +345,15 @@ def test_integer_rows_certify_exactly(oracle):
     assert Qvh().last_fallbacks(idx._index._device_handle) == 0
     rows, dist = oracle.flat_search(base, q[:500], 10)
     print(assert_same_topk(got_l[:500], got_d[:500], rows.astype(np.int64), dist, _true_dist(oracle, base, q, "l2")))
+
+
+@pytest.mark.parametrize("dim", [16, 64])
+@pytest.mark.parametrize("k", [63, 64])
+def test_few_splits_large_k_merge_by_selection(oracle, dim, k):
+    """Small batches over 3,000 rows split into fewer lists than k (the exact kernel's 8 splits for
+    dim 16, the few-query kernel's 2 for dim 64): the selection merge then gathers every real key
+    of every list, nsplit * k < k * k <= 4096, and needs no overflow path for k <= 64."""
+    base = D.gaussian(3_000, dim, seed=35)
+    q = D.gaussian(3, dim, seed=36)
+    for metric in ("l2", "ip"):
+        print(_check(oracle, base, q, k, metric))
