@@ -113,6 +113,18 @@ qvh_status qvh_flat_search_device(qvh_flat* flat, const float* d_queries, uint64
                                   uint32_t k, const uint64_t* d_row_bitmap, uint32_t* d_out_rows,
                                   float* d_out_dist, void* stream);
 
+/* qvh_flat_search_device without any allocation: no counterpart in the reference; for callers that
+ * cannot allocate device memory during a search (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Same arguments, kernels and results as qvh_flat_search_device;
+ * the workspace (prepared queries, norms, bounds, partial lists, counters) comes from a fixed
+ * 64 MiB array in device memory that each GPU the library runs on holds until the process ends. A
+ * search that needs more (many queries, or few queries with a large k) fails with QVH_EINVAL
+ * before anything is enqueued. All calls on one GPU share that GPU's array: calls that overlap on
+ * one GPU (on any handles or streams) race; each call clears what must start at zero itself. */
+qvh_status qvh_flat_search_device_noalloc(qvh_flat* flat, const float* d_queries, uint64_t nq,
+                                          uint32_t k, const uint64_t* d_row_bitmap,
+                                          uint32_t* d_out_rows, float* d_out_dist, void* stream);
+
 /* Waits for all work enqueued on the handle (its stream, which every call joins). */
 qvh_status qvh_flat_sync(qvh_flat* flat);
 

@@ -1317,7 +1317,8 @@ struct qvh_flat {
   hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
   hipEvent_t join = nullptr;  // orders calls on other streams into the handle's stream
   uint64_t last_nsplit = 0;
-  bool last_fb = false;  // the last search took the MFMA scan (its fallback count is in w_fb)
+  bool last_fb = false;               // the last search took the MFMA scan
+  uint32_t* last_fb_count = nullptr;  // where its fallback count went (device memory)
 };
 
 namespace {
@@ -1347,63 +1348,178 @@ void flat_grow(qvh_flat* f, uint64_t need) {
   f->cap = cap;
 }
 
-/// Queries into w_q ([nq][dp], normalized for cosine) and, for the MFMA scan, their squared norms
-/// into w_qn and their re-score bounds into w_delta.
-void flat_prep_queries(qvh_flat* f, const float* d_raw, uint64_t nq, hipStream_t s, bool norms) {
-  const float* qs = d_raw;
-  if (f->metric == QVH_METRIC_COSINE) {  // normalized in a copy
-    float* w = static_cast<float*>(f->w_stage.reserve(nq * f->dim * sizeof(float)));
-    if (w != d_raw) QVH_HIP(hipMemcpyAsync(w, d_raw, nq * f->dim * sizeof(float), hipMemcpyDeviceToDevice, s));
-    launch_normalize_rows(w, nq, f->dim, s);
-    qs = w;
-  }
-  float* qp = static_cast<float*>(f->w_q.reserve(nq * f->dp * sizeof(float)));
-  const uint64_t total = nq * f->dp;
-  hipLaunchKernelGGL(pack_rows_kernel, dim3(static_cast<unsigned>(ceil_div(total, 256))), dim3(256), 0, s,
-                     qs, qp, nq, f->dim, f->dp);
-  if (norms) {
-    float* qn = static_cast<float*>(f->w_qn.reserve(nq * sizeof(float)));
-    float* delta = static_cast<float*>(f->w_delta.reserve(nq * sizeof(float)));
-    hipLaunchKernelGGL(query_norms_kernel, dim3(static_cast<unsigned>(ceil_div(nq, 256))), dim3(256), 0, s,
-                       qp, qn, static_cast<uint32_t>(nq), f->dp, f->meta.as<uint32_t>(),
-                       f->metric == QVH_METRIC_L2 ? 1 : 0, delta);
-  }
-  QVH_HIP(hipGetLastError());
-}
+/// One search's path, launch geometry and workspace, decided on the host before anything is
+/// launched, so a caller with a fixed workspace can be refused up front.
+struct FlatPlan {
+  enum Path { kFew, kSplit, kExactOnly, kMfma } path = kMfma;
+  bool wide = false;
+  int kl = 16;
+  uint64_t g = 0, rps = 0;                       // few / split: row splits and rows per split
+  uint64_t nsplit = 1, rows_per_split = 0;       // MFMA scan
+  uint32_t qblocks = 0;
+  uint64_t scan_rows = 0;
+  // Bytes of each workspace buffer (0 = unused).
+  size_t stage = 0, q = 0, qn = 0, delta = 0, pd = 0, pr = 0, thr = 0, fb = 0, mflag = 0;
 
-/// d_idx (nullable, n_idx entries, ascending) lists the admitted rows for the MFMA scan; the caller
-/// passes it instead of the bitmap when few rows are admitted.
-void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t k,
-                      const uint64_t* d_bitmap, uint32_t* d_rows, float* d_dist, hipStream_t s,
-                      const uint32_t* d_idx = nullptr, uint64_t n_idx = 0) {
+  static size_t aligned(size_t b) { return (b + 255) / 256 * 256; }
+  size_t total() const {
+    return aligned(stage) + aligned(q) + aligned(qn) + aligned(delta) + aligned(pd) + aligned(pr) + aligned(thr) +
+           aligned(fb) + aligned(mflag);
+  }
+};
+
+/// The workspace of one search, on the handle's buffers or carved from a caller-fixed region.
+struct FlatBuffers {
+  float* stage = nullptr;
+  float* q = nullptr;
+  float* qn = nullptr;
+  float* delta = nullptr;
+  float* pd = nullptr;
+  uint32_t* pr = nullptr;
+  uint32_t* thr = nullptr;
+  uint32_t* fb = nullptr;
+  uint32_t* mflag = nullptr;
+};
+
+/// d_idx (listed admitted rows) is in use when n_idx > 0 or `indexed`.
+FlatPlan plan_flat_search(const qvh_flat* f, uint64_t nq, uint32_t k, bool indexed, uint64_t n_idx, int cus) {
   QVH_REQUIRE(nq <= 0xFFFFFFFFull, "flat search: too many queries in one call");
   if (k > kExactMaxK) {
     throw Failure(QVH_EUNSUPPORTED, "flat search: k > " + std::to_string(kExactMaxK) + " is not supported on the device path");
   }
+  FlatPlan p;
   // At most kFewMaxBatch queries with 32 <= dim <= kFewMaxDim and k <= kFewMaxK: the few-query
   // scan, kFewMaxQ queries per launch;
-  // other batches of at most kSplitMaxQueries: the exact kernel over row splits. Otherwise k <= 32:
-  // the MFMA scan with per-lane lists of KL = 16 or 32 and a shared bound; 32 < k <= kWideMaxK:
-  // the same scan without the shared bound and the wide merge (its rare fallback queries on the
-  // exact kernel); larger k or dim: the exact kernel.
-  const bool splittable = !d_idx && f->n >= 2 * kMinSplitRows;
+  // other batches of at most kSplitMaxQueries: the exact kernel over row splits. Otherwise k with a
+  // margin in a shared-bound list (shared_list_length): the MFMA scan with per-lane lists of KL = 16
+  // or 32 and a shared bound; larger k up to kWideMaxK: the same scan without the shared bound and
+  // the wide merge (its rare fallback queries on the exact kernel); larger k or dim: the exact kernel.
+  const bool splittable = !indexed && f->n >= 2 * kMinSplitRows;
   const bool few = splittable && nq <= kFewMaxBatch && k <= (f->dim % 32 == 0 ? kFewMaxK : 64u) && f->dim >= 32 &&
                    f->dim <= kFewMaxDim;
   const bool split = splittable && !few && nq <= kSplitMaxQueries;
-  const bool wide = !few && !split && shared_list_length(k) == 0 && k <= kWideMaxK &&
-                    f->dp <= static_cast<uint32_t>(kMaxDp) && !d_idx;
-  const bool exact_only = !few && !split && !wide && (shared_list_length(k) == 0 || f->dp > static_cast<uint32_t>(kMaxDp));
-  f->last_fb = !few && !split && !exact_only;
+  p.wide = !few && !split && shared_list_length(k) == 0 && k <= kWideMaxK && f->dp <= static_cast<uint32_t>(kMaxDp) &&
+           !indexed;
+  const bool exact_only = !few && !split && !p.wide && (shared_list_length(k) == 0 || f->dp > static_cast<uint32_t>(kMaxDp));
+  p.path = few ? FlatPlan::kFew : split ? FlatPlan::kSplit : exact_only ? FlatPlan::kExactOnly : FlatPlan::kMfma;
+  if (f->metric == QVH_METRIC_COSINE) p.stage = nq * f->dim * sizeof(float);
+  p.q = nq * f->dp * sizeof(float);
+  if (p.path == FlatPlan::kFew) {
+    // A few queries of moderate width: the coalesced few-query kernel reads each row once for
+    // each launch of up to kFewMaxQ queries, over enough row splits to give every CU four
+    // work-groups; one merge then serves the whole batch.
+    uint64_t g = std::min<uint64_t>({static_cast<uint64_t>(kFewMaxSplits), f->n / kMinSplitRows,
+                                     static_cast<uint64_t>(cus) * 4});
+    p.rps = ceil_div(ceil_div(f->n, g), kFewRowsPerStep) * kFewRowsPerStep;
+    p.g = ceil_div(f->n, p.rps);
+  } else if (p.path == FlatPlan::kSplit) {
+    // A few queries: the MFMA scan's 256-query blocks would run mostly empty. Split each query's
+    // rows over enough exact-kernel work-groups to give every CU eight, then merge.
+    const uint64_t want = ceil_div(static_cast<uint64_t>(cus) * 8, nq);
+    uint64_t g = std::min<uint64_t>({want, kMaxRowSplits, f->n / kMinSplitRows});
+    p.rps = ceil_div(ceil_div(f->n, g), kExactThreads) * kExactThreads;
+    p.g = ceil_div(ceil_div(f->n, p.rps), 8) * 8;  // the XCD mapping takes whole groups of 8 splits
+  }
+  if (p.path == FlatPlan::kFew || p.path == FlatPlan::kSplit) {
+    const size_t parts = static_cast<size_t>(nq) * p.g * k;
+    p.pr = parts * sizeof(uint32_t);
+    p.pd = parts * sizeof(float);
+    p.mflag = nq * sizeof(uint32_t);
+    return p;
+  }
+  if (p.path == FlatPlan::kExactOnly) return p;
+  p.qn = nq * sizeof(float);
+  p.delta = nq * sizeof(float);
+  p.kl = p.wide ? 32 : shared_list_length(k);
+  p.qblocks = static_cast<uint32_t>(ceil_div(nq, kQueriesPerBlock));
+  p.scan_rows = indexed ? n_idx : f->n;
+  const uint64_t tiles = std::max<uint64_t>(1, ceil_div(p.scan_rows, kTileRows));
+  // One workgroup per CU at a time: pick the split count (a multiple of 8 for the XCD mapping)
+  // whose workgroup count best fills whole rounds of the CUs; fewer splits on ties. A split keeps
+  // at least four tiles: with fewer rows per split the per-split top-k lists take in most rows
+  // (1.18M x 100 cosine with 0.5% of the ids allowed: 32 splits 0.47 ms, 16 splits 0.37 ms).
+  {
+    const uint64_t cap = std::max<uint64_t>(1, std::min<uint64_t>(tiles / 4, kMaxSplits));
+    double best = -1.0;
+    for (uint64_t c = 1; c <= cap; c = c < 8 ? c + 1 : c + 8) {
+      if (c >= 8 && c % 8) continue;
+      const uint64_t total = p.qblocks * c;
+      const uint64_t rounds = ceil_div(total, static_cast<uint64_t>(cus));
+      // prefer enough parallelism (>= 4 rounds when the rows allow) and full rounds
+      const double fill = static_cast<double>(total) / static_cast<double>(rounds * cus);
+      const double par = std::min(1.0, static_cast<double>(total) / (4.0 * cus));
+      const double score = fill * par;
+      if (score > best + 1e-9) {
+        best = score;
+        p.nsplit = c;
+      }
+    }
+  }
+  p.rows_per_split = ceil_div(tiles, p.nsplit) * kTileRows;
+  const size_t parts = static_cast<size_t>(nq) * 2 * p.nsplit * p.kl;
+  p.pd = parts * sizeof(float);
+  p.pr = parts * sizeof(uint32_t);
+  p.thr = nq * sizeof(uint32_t);
+  p.fb = (nq + 1) * sizeof(uint32_t);
+  return p;
+}
+
+/// The plan's workspace on the handle's own buffers (grown on demand).
+FlatBuffers handle_buffers(qvh_flat* f, const FlatPlan& p) {
+  FlatBuffers b;
+  auto take = [](DeviceBuffer& buf, size_t bytes) { return bytes ? buf.reserve(bytes) : nullptr; };
+  b.stage = static_cast<float*>(take(f->w_stage, p.stage));
+  b.q = static_cast<float*>(take(f->w_q, p.q));
+  b.qn = static_cast<float*>(take(f->w_qn, p.qn));
+  b.delta = static_cast<float*>(take(f->w_delta, p.delta));
+  b.pd = static_cast<float*>(take(f->w_pd, p.pd));
+  b.pr = static_cast<uint32_t*>(take(f->w_pr, p.pr));
+  b.thr = static_cast<uint32_t*>(take(f->w_thr, p.thr));
+  b.fb = static_cast<uint32_t*>(take(f->w_fb, p.fb));
+  b.mflag = static_cast<uint32_t*>(take(f->w_mflag, p.mflag));
+  return b;
+}
+
+/// Queries into b.q ([nq][dp], normalized for cosine in b.stage) and, for the MFMA scan, their
+/// squared norms into b.qn and their re-score bounds into b.delta.
+void flat_prep_queries(qvh_flat* f, const FlatBuffers& b, const float* d_raw, uint64_t nq, hipStream_t s) {
+  const float* qs = d_raw;
+  if (f->metric == QVH_METRIC_COSINE) {  // normalized in a copy
+    if (b.stage != d_raw) {
+      QVH_HIP(hipMemcpyAsync(b.stage, d_raw, nq * f->dim * sizeof(float), hipMemcpyDeviceToDevice, s));
+    }
+    launch_normalize_rows(b.stage, nq, f->dim, s);
+    qs = b.stage;
+  }
+  const uint64_t total = nq * f->dp;
+  hipLaunchKernelGGL(pack_rows_kernel, dim3(static_cast<unsigned>(ceil_div(total, 256))), dim3(256), 0, s,
+                     qs, b.q, nq, f->dim, f->dp);
+  if (b.qn) {
+    hipLaunchKernelGGL(query_norms_kernel, dim3(static_cast<unsigned>(ceil_div(nq, 256))), dim3(256), 0, s,
+                       b.q, b.qn, static_cast<uint32_t>(nq), f->dp, f->meta.as<uint32_t>(),
+                       f->metric == QVH_METRIC_L2 ? 1 : 0, b.delta);
+  }
+  QVH_HIP(hipGetLastError());
+}
+
+/// Runs a planned search on its workspace. d_idx (nullable, n_idx entries, ascending) lists the
+/// admitted rows for the MFMA scan; the caller passes it instead of the bitmap when few rows are
+/// admitted.
+void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const float* d_queries, uint64_t nq,
+                     uint32_t k, const uint64_t* d_bitmap, uint32_t* d_rows, float* d_dist, hipStream_t s,
+                     const uint32_t* d_idx = nullptr, uint64_t n_idx = 0) {
+  f->last_fb = p.path == FlatPlan::kMfma;
+  f->last_fb_count = b.fb;
   f->timed = f->timing;
   if (f->timed) QVH_HIP(hipEventRecord(f->ev[0], s));
-  flat_prep_queries(f, d_queries, nq, s, !(few || split || exact_only));
+  flat_prep_queries(f, b, d_queries, nq, s);
   if (f->timed) QVH_HIP(hipEventRecord(f->ev[1], s));
   ExactArgs e{};
   e.X = f->rows.as<float>();
   e.dp = f->dp;
   e.dim = f->dim;
   e.n = f->n;
-  e.Q = f->w_q.as<float>();
+  e.Q = b.q;
   e.k = k;
   e.l2 = f->metric == QVH_METRIC_L2;
   e.bitmap = d_bitmap;
@@ -1411,21 +1527,9 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
   e.out_dist = d_dist;
   e.qlist = nullptr;
   e.qcount = nullptr;
-  int cus = 256;
-  (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, f->device);
-  if (few) {
-    // A few queries of moderate width: the coalesced few-query kernel reads each row once for
-    // each launch of up to kFewMaxQ queries, over enough row splits to give every CU four
-    // work-groups; one merge then serves the whole batch.
-    uint64_t g = std::min<uint64_t>({static_cast<uint64_t>(kFewMaxSplits), f->n / kMinSplitRows,
-                                     static_cast<uint64_t>(cus) * 4});
-    const uint64_t rps = ceil_div(ceil_div(f->n, g), kFewRowsPerStep) * kFewRowsPerStep;
-    g = ceil_div(f->n, rps);
-    const size_t parts = static_cast<size_t>(nq) * g * k;
-    uint32_t* part_r = static_cast<uint32_t*>(f->w_pr.reserve(parts * sizeof(uint32_t)));
-    float* part_d = static_cast<float*>(f->w_pd.reserve(parts * sizeof(float)));
+  if (p.path == FlatPlan::kFew) {
     const bool l2 = f->metric == QVH_METRIC_L2;
-    const dim3 grid(static_cast<unsigned>(g)), block(kFewThreads);
+    const dim3 grid(static_cast<unsigned>(p.g)), block(kFewThreads);
     const bool tail = f->dim % 32 != 0;
     for (uint64_t q0 = 0; q0 < nq; q0 += kFewMaxQ) {
       const uint64_t nc = std::min<uint64_t>(kFewMaxQ, nq - q0);
@@ -1434,14 +1538,14 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
       fa.dp = f->dp;
       fa.dim = f->dim;
       fa.n = f->n;
-      fa.Q = f->w_q.as<float>() + q0 * f->dp;
+      fa.Q = b.q + q0 * f->dp;
       fa.nq = static_cast<uint32_t>(nc);
       fa.k = k;
       fa.bitmap = d_bitmap;
-      fa.rows_per_split = rps;
-      fa.nsplit = static_cast<uint32_t>(g);
-      fa.part_r = part_r + q0 * g * k;  // [query][split][k]
-      fa.part_d = part_d + q0 * g * k;
+      fa.rows_per_split = p.rps;
+      fa.nsplit = static_cast<uint32_t>(p.g);
+      fa.part_r = b.pr + q0 * p.g * k;  // [query][split][k]
+      fa.part_d = b.pd + q0 * p.g * k;
       auto go = [&](auto nqc) {
         constexpr int NQ = decltype(nqc)::value;
         auto kern = k > 64 ? (l2 ? flat_few_kernel<NQ, true, false, 256> : flat_few_kernel<NQ, false, false, 256>)
@@ -1461,34 +1565,25 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
       QVH_HIP(hipGetLastError());
     }
     if (f->timed) QVH_HIP(hipEventRecord(f->ev[2], s));
-    launch_sorted_merge(part_r, part_d, nq, static_cast<uint32_t>(g), k, d_rows, d_dist,
-                        static_cast<uint32_t*>(f->w_mflag.reserve(nq * sizeof(uint32_t))), s);
-    f->last_nsplit = g;
+    launch_sorted_merge(b.pr, b.pd, nq, static_cast<uint32_t>(p.g), k, d_rows, d_dist, b.mflag, s);
+    f->last_nsplit = p.g;
     if (f->timed) QVH_HIP(hipEventRecord(f->ev[3], s));
     return;
   }
-  if (split) {
-    // A few queries: the MFMA scan's 256-query blocks would run mostly empty. Split each query's
-    // rows over enough exact-kernel work-groups to give every CU eight, then merge.
-    const uint64_t want = ceil_div(static_cast<uint64_t>(cus) * 8, nq);
-    uint64_t g = std::min<uint64_t>({want, kMaxRowSplits, f->n / kMinSplitRows});
-    const uint64_t rps = ceil_div(ceil_div(f->n, g), kExactThreads) * kExactThreads;
-    g = ceil_div(ceil_div(f->n, rps), 8) * 8;  // the XCD mapping takes whole groups of 8 splits
-    const size_t parts = static_cast<size_t>(nq) * g * k;
-    e.nsplit = static_cast<uint32_t>(g);
+  if (p.path == FlatPlan::kSplit) {
+    e.nsplit = static_cast<uint32_t>(p.g);
     e.nq = static_cast<uint32_t>(nq);
-    e.rows_per_split = rps;
-    e.out_rows = static_cast<uint32_t*>(f->w_pr.reserve(parts * sizeof(uint32_t)));
-    e.out_dist = static_cast<float*>(f->w_pd.reserve(parts * sizeof(float)));
+    e.rows_per_split = p.rps;
+    e.out_rows = b.pr;
+    e.out_dist = b.pd;
     launch_exact(e, nq, s);
     if (f->timed) QVH_HIP(hipEventRecord(f->ev[2], s));
-    launch_sorted_merge(e.out_rows, e.out_dist, nq, e.nsplit, k, d_rows, d_dist,
-                        static_cast<uint32_t*>(f->w_mflag.reserve(nq * sizeof(uint32_t))), s);
-    f->last_nsplit = g;
+    launch_sorted_merge(b.pr, b.pd, nq, e.nsplit, k, d_rows, d_dist, b.mflag, s);
+    f->last_nsplit = p.g;
     if (f->timed) QVH_HIP(hipEventRecord(f->ev[3], s));
     return;
   }
-  if (exact_only) {
+  if (p.path == FlatPlan::kExactOnly) {
     launch_exact(e, nq, s);
     f->last_nsplit = 0;
     if (f->timed) {
@@ -1497,58 +1592,29 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
     }
     return;
   }
-  const int kl = wide ? 32 : shared_list_length(k);
-
-  const uint32_t qblocks = static_cast<uint32_t>(ceil_div(nq, kQueriesPerBlock));
-  const uint64_t scan_rows = d_idx ? n_idx : f->n;
-  const uint64_t tiles = std::max<uint64_t>(1, ceil_div(scan_rows, kTileRows));
-  // One workgroup per CU at a time: pick the split count (a multiple of 8 for the XCD mapping)
-  // whose workgroup count best fills whole rounds of the CUs; fewer splits on ties. A split keeps
-  // at least four tiles: with fewer rows per split the per-split top-k lists take in most rows
-  // (1.18M x 100 cosine with 0.5% of the ids allowed: 32 splits 0.47 ms, 16 splits 0.37 ms).
-  uint64_t nsplit = 1;
-  {
-    const uint64_t cap = std::max<uint64_t>(1, std::min<uint64_t>(tiles / 4, kMaxSplits));
-    double best = -1.0;
-    for (uint64_t c = 1; c <= cap; c = c < 8 ? c + 1 : c + 8) {
-      if (c >= 8 && c % 8) continue;
-      const uint64_t total = qblocks * c;
-      const uint64_t rounds = ceil_div(total, static_cast<uint64_t>(cus));
-      // prefer enough parallelism (>= 4 rounds when the rows allow) and full rounds
-      const double fill = static_cast<double>(total) / static_cast<double>(rounds * cus);
-      const double par = std::min(1.0, static_cast<double>(total) / (4.0 * cus));
-      const double score = fill * par;
-      if (score > best + 1e-9) {
-        best = score;
-        nsplit = c;
-      }
-    }
-  }
-  const uint64_t rows_per_split = ceil_div(tiles, nsplit) * kTileRows;
-  const size_t parts = static_cast<size_t>(nq) * 2 * nsplit * kl;
   ScanArgs a;
   a.X = f->rows.as<float>();
   a.xnorm = f->norms.as<float>();
-  a.n = scan_rows;
-  a.Q = f->w_q.as<float>();
-  a.qnorm = f->w_qn.as<float>();
+  a.n = p.scan_rows;
+  a.Q = b.q;
+  a.qnorm = b.qn;
   a.nq = static_cast<uint32_t>(nq);
   a.bitmap = d_idx ? nullptr : d_bitmap;
   a.idx = d_idx;
   a.l2 = f->metric == QVH_METRIC_L2;
-  a.nsplit = static_cast<uint32_t>(nsplit);
-  a.qblocks = qblocks;
-  a.rows_per_split = rows_per_split;
-  a.part_d = static_cast<float*>(f->w_pd.reserve(parts * sizeof(float)));
-  a.part_r = static_cast<uint32_t*>(f->w_pr.reserve(parts * sizeof(uint32_t)));
-  a.qthr = static_cast<uint32_t*>(f->w_thr.reserve(nq * sizeof(uint32_t)));
-  a.share = wide ? 0 : 1;
+  a.nsplit = static_cast<uint32_t>(p.nsplit);
+  a.qblocks = p.qblocks;
+  a.rows_per_split = p.rows_per_split;
+  a.part_d = b.pd;
+  a.part_r = b.pr;
+  a.qthr = b.thr;
+  a.share = p.wide ? 0 : 1;
   hipLaunchKernelGGL(fill_u32_kernel, dim3(static_cast<unsigned>(ceil_div(nq, 256))), dim3(256), 0, s,
                      a.qthr, nq, 0xFF800000u);  // ordered bits of +inf
-  launch_scan(f->dp, kl, dim3(static_cast<unsigned>(qblocks * nsplit)), a, s);
+  launch_scan(f->dp, p.kl, dim3(static_cast<unsigned>(p.qblocks * p.nsplit)), a, s);
   QVH_HIP(hipGetLastError());
   if (f->timed) QVH_HIP(hipEventRecord(f->ev[2], s));
-  f->last_nsplit = nsplit;
+  f->last_nsplit = p.nsplit;
 
   MergeArgs m;
   m.X = a.X;
@@ -1558,24 +1624,24 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
   m.nq = a.nq;
   m.k = k;
   m.l2 = a.l2;
-  m.nlists = static_cast<uint32_t>(2 * nsplit);
+  m.nlists = static_cast<uint32_t>(2 * p.nsplit);
   m.part_d = a.part_d;
   m.part_r = a.part_r;
   m.idx = d_idx;
   m.out_rows = d_rows;
   m.out_dist = d_dist;
-  m.delta = f->w_delta.as<float>();
+  m.delta = b.delta;
   // fb[0] counts the queries whose selection the merge could not certify (or, in the wide merge,
   // whose list ran out), fb[1..] lists them; the exact kernel then recomputes only those.
-  uint32_t* fb = static_cast<uint32_t*>(f->w_fb.reserve((nq + 1) * sizeof(uint32_t)));
+  uint32_t* fb = b.fb;
   hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(256), 0, s, fb, 1, 0u);
   m.fallback = fb + 1;
   m.nfallback = fb;
   const dim3 mgrid(static_cast<unsigned>(ceil_div(nq, 4)));
-  if (wide) {
+  if (p.wide) {
     const uint32_t sel_n = k + std::max<uint32_t>(16, k / 2);
     hipLaunchKernelGGL(flat_merge_wide_kernel, mgrid, dim3(256), 0, s, m, sel_n);
-  } else if (kl == 16) {
+  } else if (p.kl == 16) {
     hipLaunchKernelGGL(flat_merge_kernel<16>, mgrid, dim3(256), 0, s, m);
   } else {
     hipLaunchKernelGGL(flat_merge_kernel<32>, mgrid, dim3(256), 0, s, m);
@@ -1590,6 +1656,20 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
   }
   launch_exact(e, nq, s);
   if (f->timed) QVH_HIP(hipEventRecord(f->ev[3], s));
+}
+
+int device_cus(int device) {
+  int cus = 256;
+  (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+  return cus;
+}
+
+/// A search on the handle's own workspace. d_idx as for flat_search_run.
+void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t k,
+                      const uint64_t* d_bitmap, uint32_t* d_rows, float* d_dist, hipStream_t s,
+                      const uint32_t* d_idx = nullptr, uint64_t n_idx = 0) {
+  const FlatPlan p = plan_flat_search(f, nq, k, d_idx != nullptr, n_idx, device_cus(f->device));
+  flat_search_run(f, p, handle_buffers(f, p), d_queries, nq, k, d_bitmap, d_rows, d_dist, s, d_idx, n_idx);
 }
 
 }  // namespace
@@ -1618,6 +1698,9 @@ qvh_status qvh_flat_create(uint32_t dim, int metric, qvh_flat** out) {
       f->meta.reserve(2 * sizeof(uint32_t));
       hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, f->stream, f->meta.as<uint32_t>(), 2, 0u);
       QVH_HIP(hipGetLastError());
+      // Created here rather than on the first call from another stream, so that the search
+      // without allocation never creates one.
+      QVH_HIP(hipEventCreateWithFlags(&f->join, hipEventDisableTiming));
       QVH_HIP(hipStreamSynchronize(f->stream));
     } catch (...) {
       qvh_flat_destroy(f);
@@ -1661,7 +1744,7 @@ qvh_status qvh_flat_last_fallbacks(qvh_flat* f, uint32_t* count) {
     *count = 0;
     if (!f->last_fb) return;
     QVH_HIP(hipStreamSynchronize(f->stream));
-    QVH_HIP(hipMemcpy(count, f->w_fb.ptr, sizeof(uint32_t), hipMemcpyDeviceToHost));
+    QVH_HIP(hipMemcpy(count, f->last_fb_count, sizeof(uint32_t), hipMemcpyDeviceToHost));
   });
 }
 
@@ -1809,6 +1892,89 @@ qvh_status qvh_flat_search_device(qvh_flat* f, const float* d_queries, uint64_t 
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : f->stream;
     on_handle_timeline(f->stream, f->join, s, [&](hipStream_t st) {
       flat_search_impl(f, d_queries, nq, k, d_row_bitmap, d_out_rows, d_out_dist, st);
+    });
+  });
+}
+
+}  // extern "C"
+
+// ---- search without allocation ------------------------------------------------------------------
+//
+// qvh_flat_search_device_noalloc takes every buffer beyond its inputs and outputs (prepared queries,
+// norms, bounds, partial lists, counters) from `scratch`, a fixed array in device memory that each
+// GPU the library runs on holds until the process ends. Its device address on the current device
+// comes from hipGetSymbolAddress on the first call there (the name `scratch` is a host-side
+// stand-in, not a device address). All calls on one GPU share that GPU's array: calls that overlap
+// on one GPU race, and every call clears what must start at zero (bounds, counters) itself.
+
+constexpr size_t kScratchBytes = size_t{64} << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+/// The scratch array's address on `device`, which must be the current device.
+unsigned char* scratch_on(int device) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  QVH_REQUIRE(device >= 0 && device < kMaxScratchDevices, "device index out of range for the scratch array");
+  if (g_scratch_ptr[device] == nullptr) {
+    void* ptr = nullptr;
+    QVH_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    QVH_REQUIRE(ptr != nullptr, "hipGetSymbolAddress returned no address for the scratch array");
+    g_scratch_ptr[device] = ptr;
+  }
+  return static_cast<unsigned char*>(g_scratch_ptr[device]);
+}
+
+/// The plan's workspace carved from the scratch array, each buffer 256-byte aligned.
+FlatBuffers scratch_buffers(unsigned char* base, const FlatPlan& p) {
+  size_t at = 0;
+  auto take = [&](size_t bytes) -> void* {
+    if (bytes == 0) return nullptr;
+    void* out = base + at;
+    at += FlatPlan::aligned(bytes);
+    return out;
+  };
+  FlatBuffers b;
+  b.stage = static_cast<float*>(take(p.stage));
+  b.q = static_cast<float*>(take(p.q));
+  b.qn = static_cast<float*>(take(p.qn));
+  b.delta = static_cast<float*>(take(p.delta));
+  b.pd = static_cast<float*>(take(p.pd));
+  b.pr = static_cast<uint32_t*>(take(p.pr));
+  b.thr = static_cast<uint32_t*>(take(p.thr));
+  b.fb = static_cast<uint32_t*>(take(p.fb));
+  b.mflag = static_cast<uint32_t*>(take(p.mflag));
+  return b;
+}
+
+}  // namespace
+
+extern "C" {
+
+qvh_status qvh_flat_search_device_noalloc(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t k,
+                                          const uint64_t* d_row_bitmap, uint32_t* d_out_rows, float* d_out_dist,
+                                          void* stream) {
+  return guarded([&] {
+    QVH_REQUIRE(f != nullptr, "qvh_flat_search_device_noalloc: null handle");
+    if (nq == 0 || k == 0) return;
+    QVH_REQUIRE(d_queries && d_out_rows && d_out_dist, "qvh_flat_search_device_noalloc: null buffer");
+    std::lock_guard<std::mutex> lock(f->mu);
+    QVH_HIP(hipSetDevice(f->device));
+    unsigned char* base = scratch_on(f->device);
+    const FlatPlan p = plan_flat_search(f, nq, k, false, 0, device_cus(f->device));
+    if (p.total() > kScratchBytes) {
+      throw Failure(QVH_EINVAL, "qvh_flat_search_device_noalloc: this search needs " + std::to_string(p.total()) +
+                                    " bytes of workspace, above the fixed scratch of " +
+                                    std::to_string(kScratchBytes) + " bytes; search fewer queries per call");
+    }
+    const FlatBuffers b = scratch_buffers(base, p);
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : f->stream;
+    on_handle_timeline(f->stream, f->join, s, [&](hipStream_t st) {
+      flat_search_run(f, p, b, d_queries, nq, k, d_row_bitmap, d_out_rows, d_out_dist, st);
     });
   });
 }
