@@ -284,8 +284,8 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
       for (int blk = 0; blk < 2; ++blk) {
         const f32x16 acc = blk ? acc1 : acc0;
         const uint32_t lane_bits = static_cast<uint32_t>(admit >> (32 * blk)) >> (4 * h);
-        // Fast path: distance and "may pass" test. NaN passes here (!(d > thr)) so the slow
-        // path can turn it into +inf as the reference does.
+        // Pass test: !(d > thr). Ties pass (a tied row may still win on row number), and so
+        // does NaN, which the flush turns into +inf as the reference does.
         const float thr = fminf(pthr, Ld[KL - 1]);
         float d[16];
 #pragma unroll
@@ -298,8 +298,11 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
         }
         bool any = false;
         if (!masked) {  // wave-uniform: full tile, no filter
+          // One test of the smallest distance (fminf skips NaN; all-NaN gives NaN, which passes).
+          float m = d[0];
 #pragma unroll
-          for (int r = 0; r < 16; ++r) any = any || !(d[r] > thr);
+          for (int r = 1; r < 16; ++r) m = fminf(m, d[r]);
+          any = !(m > thr);
         } else {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
@@ -317,12 +320,11 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
             const int bit = 8 * (r >> 2) + (r & 3);
             bool p = !(d[r] > thr);
             if (masked) p = p && ((lane_bits >> bit) & 1u);
-            if (p) {
-              s_qd[qcount * kThreads + tid] = d[r];
-              s_qr[qcount * kThreads + tid] =
-                  static_cast<uint32_t>(tile_row0 + 32 * blk + 4 * h + bit);
-              ++qcount;
-            }
+            // Written whether or not it passes (no branch per element); a failing entry is
+            // overwritten by the next. The flush above leaves room for all 16.
+            s_qd[qcount * kThreads + tid] = d[r];
+            s_qr[qcount * kThreads + tid] = static_cast<uint32_t>(tile_row0 + 32 * blk + 4 * h + bit);
+            qcount += p ? 1 : 0;
           }
         }
       }

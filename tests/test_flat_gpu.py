@@ -207,6 +207,21 @@ def test_integer_data_exact_ties(oracle):
     print(stats)
 
 
+@pytest.mark.parametrize("metric", ["l2", "ip"])
+def test_overflowing_distances_fill_the_tail(oracle, metric):
+    """Only rows 0-5 have finite distances. Rows at 3e19 overflow to +inf; rows at 3e38 also
+    overflow the dot product, so the scan's expanded form sees inf - inf = NaN. The k - 6 slots
+    after the finite rows hold what the reference puts there (+inf distances, smallest rows
+    first), so those candidates must survive the scan's prune test while lists are not full."""
+    rng = np.random.default_rng(17)
+    base = rng.standard_normal((6000, 32)).astype(np.float32)
+    base[6:3000] *= np.float32(3e19)
+    base[3000:] = np.sign(base[3000:]) * np.float32(3e38)
+    q = (2.0 * rng.standard_normal((64, 32))).astype(np.float32)
+    _check(oracle, base, q, 10, metric)
+    _check(oracle, base[::-1].copy(), q, 10, metric)
+
+
 def test_fewer_rows_than_k_and_selective_filter(oracle):
     rng = np.random.default_rng(3)
     base = rng.standard_normal((10, 8)).astype(np.float32)
