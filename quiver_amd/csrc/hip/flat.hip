@@ -31,6 +31,7 @@ namespace {
 
 using namespace qvh;
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -85,12 +86,13 @@ template <int DP, int KL, bool L2, int MODE>
 __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
   constexpr bool FILTER = MODE == 1;
   constexpr int H = DP / 2;                   // dims per lane half (K split in two halves)
-  constexpr int STRIDE = DP + 4;              // LDS row stride in floats: conflict-free b128 reads
+  // LDS row stride in floats: conflict-free b128 reads. Columns DP and DP + 1 of a row hold the
+  // augmented operand (||x||^2, 1) for L2, (1, 1) for the inner product.
+  constexpr int STRIDE = DP + 4;
   constexpr int C4 = DP / 4;                  // float4 chunks per row
   constexpr int CHUNKS = kTileRows * C4;
   constexpr int PER_THREAD = (CHUNKS + kThreads - 1) / kThreads;
   __shared__ __attribute__((aligned(16))) float s_tile[2][kTileRows * STRIDE];
-  __shared__ float s_norm[2][kTileRows];
   __shared__ uint64_t s_bits[2];
   // Per-lane candidate queues, entry-major (entry e of thread t at e * kThreads + t) so lanes
   // appending at different depths never share a bank.
@@ -120,19 +122,24 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
 
   // This lane's half of its query: dims [h*H, h*H + H). MFMA step s pairs dim h*H+s of the query
   // (B operand, lane = (k=h, col=j)) with the same dim of a base row (A operand, lane = (row j, k=h)).
+  // The matrix unit produces the distance itself: the query enters scaled by -2 (L2) or -1 (inner
+  // product), both exact, and one more step adds the augmented pair, row (||x||^2, 1) against
+  // query (1, ||q||^2) for L2 and (1, 1) against (1, 0) for the inner product, so the accumulator
+  // ends at ||x||^2 + ||q||^2 - 2<q,x> or 1 - <q,x>.
+  constexpr float kScale = L2 ? -2.0f : -1.0f;
   float qreg[H];
   {
     const f32x4* qp = reinterpret_cast<const f32x4*>(a.Q + static_cast<size_t>(qvalid ? q : 0) * DP + h * H);
 #pragma unroll
     for (int s = 0; s < H / 4; ++s) {
       const f32x4 v = qvalid ? qp[s] : f32x4{0.f, 0.f, 0.f, 0.f};
-      qreg[4 * s + 0] = v[0];
-      qreg[4 * s + 1] = v[1];
-      qreg[4 * s + 2] = v[2];
-      qreg[4 * s + 3] = v[3];
+      qreg[4 * s + 0] = kScale * v[0];
+      qreg[4 * s + 1] = kScale * v[1];
+      qreg[4 * s + 2] = kScale * v[2];
+      qreg[4 * s + 3] = kScale * v[3];
     }
   }
-  const float qn = qvalid ? a.qnorm[q] : 0.0f;
+  const float qaug = h == 0 ? 1.0f : (L2 && qvalid ? a.qnorm[q] : 0.0f);
 
   float Ld[KL];
   uint32_t Lr[KL];
@@ -201,10 +208,12 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
       if constexpr (MODE == 2) gr = a.idx[gr];
       stage[p] = *reinterpret_cast<const f32x4*>(a.X + gr * DP + 4 * col);
     }
-    uint64_t gn = base + (tid & (kTileRows - 1));
-    gn = gn < last_row ? gn : last_row;
-    if constexpr (MODE == 2) gn = a.idx[gn];
-    stage_norm = a.xnorm[gn];
+    if constexpr (L2) {
+      uint64_t gn = base + (tid & (kTileRows - 1));
+      gn = gn < last_row ? gn : last_row;
+      if constexpr (MODE == 2) gn = a.idx[gn];
+      stage_norm = a.xnorm[gn];
+    }
     if constexpr (FILTER) stage_bits = a.bitmap[base >> 6];
   };
   auto store_tile = [&](int buf) {
@@ -216,7 +225,9 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
         *reinterpret_cast<f32x4*>(&s_tile[buf][row * STRIDE + 4 * col]) = stage[p];
       }
     }
-    if (tid < kTileRows) s_norm[buf][tid] = stage_norm;
+    if (tid < kTileRows) {
+      *reinterpret_cast<f32x2*>(&s_tile[buf][tid * STRIDE + DP]) = f32x2{L2 ? stage_norm : 1.0f, 1.0f};
+    }
     if (FILTER && tid == kTileRows) s_bits[buf] = stage_bits;
   };
 
@@ -231,19 +242,13 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
     const bool prefetch = t + 1 < ntiles;
     if (!wave_active && prefetch) load_tile(t + 1);
     if (wave_active) {
-      // Row norms of this lane's 32 rows: rows 8*g + 4*h + (0..3) of each 32-row block, g=0..3,
-      // four b128 reads per block, issued before the MFMAs so their latency is covered.
-      f32x4 xn[2][4];
-      if constexpr (L2) {
-#pragma unroll
-        for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-          for (int g = 0; g < 4; ++g)
-            xn[blk][g] = *reinterpret_cast<const f32x4*>(&s_norm[buf][32 * blk + 8 * g + 4 * h]);
-      }
       f32x16 acc0 = {}, acc1 = {};
       const float* a0 = &s_tile[buf][j * STRIDE + h * H];
       const float* a1 = &s_tile[buf][(32 + j) * STRIDE + h * H];
+      // The augmented step's row operands (column DP + h), read first so they are in registers
+      // by the end of the chain.
+      const float aug0 = s_tile[buf][j * STRIDE + DP + h];
+      const float aug1 = s_tile[buf][(32 + j) * STRIDE + DP + h];
       // Software-pipelined: the next step's two b128 LDS reads are issued before this step's
       // eight MFMAs (8 x 64 cycles), and the scheduling barrier keeps the compiler from hoisting
       // every read of the tile at once (which would spill).
@@ -272,6 +277,8 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
         if (s == 4 && prefetch) load_tile(t + 1);
         if (s == 4) __builtin_amdgcn_sched_barrier(0);
       }
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(aug0, qaug, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(aug1, qaug, acc1, 0, 0, 0);
       // D[row][col] of a 32x32 block: col = lane % 32 (query j), row = 8*(r/4) + 4*h + r%4 in
       // register r. Per lane the rows visited increase, so ties resolve to the smaller row.
       const uint64_t tile_row0 = r0 + static_cast<uint64_t>(t) * kTileRows;
@@ -289,13 +296,7 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
         const float thr = fminf(pthr, Ld[KL - 1]);
         float d[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          if constexpr (L2) {
-            d[r] = fmaf(-2.0f, acc[r], qn + xn[blk][r >> 2][r & 3]);
-          } else {
-            d[r] = 1.0f - acc[r];
-          }
-        }
+        for (int r = 0; r < 16; ++r) d[r] = acc[r];
         bool any = false;
         if (!masked) {  // wave-uniform: full tile, no filter
           // One test of the smallest distance (fminf skips NaN; all-NaN gives NaN, which passes).
