@@ -62,7 +62,7 @@ struct ScanArgs {
   int share;                // 0: every lane list keeps its own KL best (k > KL: no shared bound)
 };
 
-constexpr int kShareEvery = 4;  // tiles between exchanges of the shared per-query threshold
+constexpr int kShareEvery = 8;  // tiles between exchanges of the shared per-query threshold
 constexpr int kQueueCap = 20;   // queued candidates per lane before a wave-wide flush
 
 /// Inserts (d, r) into the ascending list (Ld, Lr) in (distance, row) order, dropping the last.
