@@ -55,6 +55,7 @@ struct NearestArgs {
   uint32_t* out32;       // nearest mode: out32[p]
   uint8_t* out8;         // sqdiff mode: out8[p * out_stride + sub]
   uint32_t out_stride;
+  const uint32_t* list;  // if set: the points list[1 .. list[0]] only (nearest mode)
 };
 
 /// SQDIFF = false: CentroidTable::nearest_batch (src/internal/centroid_table.h:94-144):
@@ -68,9 +69,16 @@ __global__ void __launch_bounds__(kNearThreads) nearest_kernel(NearestArgs a) {
   __shared__ float s_x[kNearJC][kNearThreads];
   __shared__ __attribute__((aligned(16))) float s_c[kNearJC][kNearCT];
   const int tid = threadIdx.x;
-  const uint64_t p = static_cast<uint64_t>(blockIdx.x) * kNearThreads + tid;
+  uint64_t p = static_cast<uint64_t>(blockIdx.x) * kNearThreads + tid;
   const uint32_t sub = blockIdx.y;
-  const bool valid = p < a.n;
+  bool valid = p < a.n;
+  if (a.list) {
+    // The grid covers every point; blocks past the listed count leave before any barrier.
+    const uint32_t cnt = a.list[0];
+    if (static_cast<uint64_t>(blockIdx.x) * kNearThreads >= cnt) return;
+    valid = p < cnt;
+    p = valid ? a.list[1 + p] : 0;
+  }
   const uint64_t prow = valid ? p : 0;
   const float* xrow = a.x + prow * a.x_stride + a.x_off + static_cast<uint64_t>(sub) * a.dim;
   const float* ct = a.ct + static_cast<uint64_t>(sub) * a.dim * a.k;
@@ -139,6 +147,335 @@ __global__ void __launch_bounds__(kNearThreads) nearest_kernel(NearestArgs a) {
     a.out32[p] = r;
   }
 }
+
+
+// ---- MFMA assignment with a certificate -------------------------------------------------------
+//
+// CentroidTable::nearest_batch (src/internal/centroid_table.h:94-144) for many points: the matrix
+// unit computes g_c = ||c||^2 - 2<x,c> (or -<x,c>) for every centroid, the point entering as the
+// B operand scaled by -2 (or -1, both exact) and one more MFMA step adding the augmented column
+// (||c||^2, or 0; +inf for padding rows). Each point keeps its smallest g (first index on ties) and
+// the second smallest g over the other centroids. With |g_c - e_c| <= delta for the reference's
+// in-order value e_c, only centroids with g_c <= best + 2 * delta can be the reference's answer
+// (any other c has e_c >= g_c - delta > best + delta >= e_best). Each point keeps its kAsgList
+// smallest (g, c); when the last of them lies above that band, the band's members are all in the
+// list: one member is the answer, and two or more are re-scored in the reference's own order and
+// arithmetic. A list whose last entry is inside the band leaves the point to the exact kernel.
+// Candidates above the running best + 2 delta are not kept: they cannot be in the final band. delta = (4(dp + 1) + 16) u (P + R)^2 for L2 and (...) u P R for the
+// inner product, P = ||x||, R = the largest ||c||: the bound on two differently ordered float sums
+// of terms whose absolute values add up to at most (P + R)^2 (resp. P R), with a factor of two over
+// the derivation for the norms' own rounding and a faithfully rounding matrix unit.
+// (1M int-mixture points against 2048 centroids: 11% have two centroids in the band, 0.4% four.)
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kAsgThreads = 512;  // 8 waves of 32 points
+constexpr int kAsgPoints = 256;
+constexpr int kAsgTile = 64;      // centroid rows per LDS tile
+constexpr uint32_t kAsgMaxDp = 128;
+constexpr uint64_t kAsgMinPoints = 1024;  // smaller batches stay on the exact kernel
+constexpr int kAsgList = 4;                // (g, c) kept per point
+
+/// Inserts (g, c) into the ascending (g, c)-ordered list, dropping the last.
+template <int L>
+__device__ __forceinline__ void asg_insert(float (&lg)[L], uint32_t (&lc)[L], float g, uint32_t c) {
+#pragma unroll
+  for (int x = 0; x < L; ++x) {
+    const bool lt = (g < lg[x]) | ((g == lg[x]) & (c < lc[x]));
+    const float tg = lg[x];
+    const uint32_t tc = lc[x];
+    lg[x] = lt ? g : tg;
+    lc[x] = lt ? c : tc;
+    g = lt ? tg : g;
+    c = lt ? tc : c;
+  }
+}
+
+struct AssignArgs {
+  const float* x;        // point p at x[p * x_stride], dim floats, 16-byte aligned rows
+  uint64_t n;
+  uint32_t dim;
+  uint64_t x_stride;
+  const float* crow;     // [kp][dp] centroid rows, zero-padded
+  const float* aug;      // [kp] ||c||^2 (L2) or 0 (inner product); +inf for padding rows
+  uint32_t kp;           // rows of crow, a multiple of kAsgTile
+  const float* rmax;     // [1] the largest ||c||
+  float coef;            // (4 (dp + 1) + 16) * 2^-24
+  uint32_t* out32;       // out32[p] for the certified points
+  uint32_t* fb;          // fb[0] count, fb[1 + i]: points left to the exact kernel
+};
+
+template <int DP, bool L2>
+__global__ void __launch_bounds__(kAsgThreads) assign_mfma_kernel(AssignArgs a) {
+  constexpr int H = DP / 2;  // dims per lane half
+  constexpr int STRIDE = DP + 4;
+  constexpr int C4 = DP / 4;
+  constexpr int CHUNKS = kAsgTile * C4;
+  constexpr int PER_THREAD = (CHUNKS + kAsgThreads - 1) / kAsgThreads;
+  __shared__ __attribute__((aligned(16))) float s_tile[2][kAsgTile * STRIDE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 31, h = lane >> 5;
+  const uint64_t p0 = static_cast<uint64_t>(blockIdx.x) * kAsgPoints + wave * 32;
+  const uint64_t p = p0 + j;
+  const bool wave_active = p0 < a.n;
+  const bool valid = p < a.n;
+
+  // Point operand (B, lane = (k = h, col = j)): dims [h*H, h*H + H), scaled.
+  constexpr float kScale = L2 ? -2.0f : -1.0f;
+  float qreg[H];
+  float pp = 0.0f;
+  {
+    const float* xr = a.x + (valid ? p : 0) * a.x_stride;
+#pragma unroll
+    for (int s = 0; s < H / 4; ++s) {
+      const uint32_t d0 = static_cast<uint32_t>(h * H + 4 * s);
+      const f32x4 v = valid && d0 < a.dim ? *reinterpret_cast<const f32x4*>(xr + d0) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        qreg[4 * s + e] = kScale * v[e];
+        pp = pp + v[e] * v[e];
+      }
+    }
+  }
+  const float p2 = pp + __shfl_xor(pp, 32, 64);
+  const float qaug = h == 0 ? 1.0f : 0.0f;
+  const float P = sqrtf(p2), R = a.rmax[0];
+  const float delta = L2 ? a.coef * (P + R) * (P + R) : a.coef * P * R;
+
+  const uint32_t ntiles = a.kp / kAsgTile;
+  f32x4 stage[PER_THREAD];
+  float stage_aug = 0.0f;
+  auto load_tile = [&](uint32_t t) {
+    const float* base = a.crow + static_cast<uint64_t>(t) * kAsgTile * DP;
+#pragma unroll
+    for (int pi = 0; pi < PER_THREAD; ++pi) {
+      int c = tid + pi * kAsgThreads;
+      if (CHUNKS % kAsgThreads != 0) c = c < CHUNKS ? c : CHUNKS - 1;
+      stage[pi] = *reinterpret_cast<const f32x4*>(base + (c / C4) * DP + 4 * (c % C4));
+    }
+    stage_aug = a.aug[static_cast<uint64_t>(t) * kAsgTile + (tid & (kAsgTile - 1))];
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int pi = 0; pi < PER_THREAD; ++pi) {
+      const int c = tid + pi * kAsgThreads;
+      if (c < CHUNKS) *reinterpret_cast<f32x4*>(&s_tile[buf][(c / C4) * STRIDE + 4 * (c % C4)]) = stage[pi];
+    }
+    // Column DP + 1 meets the zero of the point's second augmented slot: it must be finite.
+    if (tid < kAsgTile) *reinterpret_cast<f32x2*>(&s_tile[buf][tid * STRIDE + DP]) = f32x2{stage_aug, 0.0f};
+  };
+
+  float lg[kAsgList];
+  uint32_t lc[kAsgList];
+#pragma unroll
+  for (int x = 0; x < kAsgList; ++x) {
+    lg[x] = __builtin_huge_valf();
+    lc[x] = 0xFFFFFFFFu;
+  }
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+  for (uint32_t t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    const bool prefetch = t + 1 < ntiles;
+    if (!wave_active && prefetch) load_tile(t + 1);
+    if (wave_active) {
+      f32x16 acc0 = {}, acc1 = {};
+      const float* r0 = &s_tile[buf][j * STRIDE + h * H];
+      const float* r1 = &s_tile[buf][(32 + j) * STRIDE + h * H];
+      const float aug0 = s_tile[buf][j * STRIDE + DP + h];
+      const float aug1 = s_tile[buf][(32 + j) * STRIDE + DP + h];
+      f32x4 x0 = *reinterpret_cast<const f32x4*>(r0);
+      f32x4 x1 = *reinterpret_cast<const f32x4*>(r1);
+#pragma unroll
+      for (int s = 0; s < H; s += 4) {
+        f32x4 n0 = x0, n1 = x1;
+        if (s + 4 < H) {
+          n0 = *reinterpret_cast<const f32x4*>(r0 + s + 4);
+          n1 = *reinterpret_cast<const f32x4*>(r1 + s + 4);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0[e], qreg[s + e], acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1[e], qreg[s + e], acc1, 0, 0, 0);
+        }
+        x0 = n0;
+        x1 = n1;
+        __builtin_amdgcn_sched_barrier(0);
+        if (s == 4 && prefetch) load_tile(t + 1);
+        if (s == 4) __builtin_amdgcn_sched_barrier(0);
+      }
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(aug0, qaug, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(aug1, qaug, acc1, 0, 0, 0);
+      // D[row][col]: col = point j, row = 8*(r/4) + 4*h + r%4 in register r; a lane visits its
+      // centroids in increasing order, so a tie with the list's last entry never enters.
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk) {
+        const f32x16 acc = blk ? acc1 : acc0;
+        float mn = acc[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mn = fminf(mn, acc[r]);
+        // Above the current best + 2 delta a centroid can never join the final band (the best only
+        // decreases), so it need not enter the list either.
+        const float lim = fminf(lg[kAsgList - 1], lg[0] + 2.0f * delta);
+        if (mn < lim) {  // NaN never enters
+          const uint32_t cb = t * kAsgTile + 32 * blk + 4 * h;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            if (acc[r] < fminf(lg[kAsgList - 1], lg[0] + 2.0f * delta)) {
+              asg_insert<kAsgList>(lg, lc, acc[r], cb + 8 * (r >> 2) + (r & 3));
+            }
+          }
+        }
+      }
+    }
+    if (prefetch) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  // The two lanes of a point saw disjoint centroids: the list of the point is the kAsgList
+  // smallest (g, c) of the union of theirs.
+  {
+    float og[kAsgList];
+    uint32_t oc[kAsgList];
+#pragma unroll
+    for (int x = 0; x < kAsgList; ++x) {
+      og[x] = __shfl_xor(lg[x], 32, 64);
+      oc[x] = static_cast<uint32_t>(__shfl_xor(static_cast<int>(lc[x]), 32, 64));
+    }
+#pragma unroll
+    for (int x = 0; x < kAsgList; ++x) asg_insert<kAsgList>(lg, lc, og[x], oc[x]);
+  }
+  // Both lanes of a point hold the same list from here on and decide alike; lane h = 1 writes.
+  const float band = lg[0] + 2.0f * delta;
+  const bool listed = valid && lg[0] < __builtin_huge_valf() && !(lg[kAsgList - 1] <= band);
+  // Exact values of the band's members (a prefix of the list) when there are two or more, in the
+  // reference's order and arithmetic: dot = sum_t x_t * c_t from t = 0 (lane h = 0 sums its half,
+  // lane h = 1 continues from that partial sum; the zero padding adds +0), then ||c||^2 - 2 dot or
+  // -dot; the smaller value wins, the smaller index on equal values. x_t is recovered exactly from
+  // the scaled operand.
+  constexpr float kUnscale = L2 ? -0.5f : -1.0f;
+  float be = __builtin_huge_valf();
+  uint32_t bc = 0xFFFFFFFFu;
+  const int nband = !listed ? 0 : !(lg[1] <= band) ? 1 : !(lg[2] <= band) ? 2 : 3;
+  for (int i = 0; i < kAsgList - 1; ++i) {
+    if (nband < 2 || i >= nband) break;
+    const uint32_t c = lc[i];
+    const f32x4* cr = reinterpret_cast<const f32x4*>(a.crow + static_cast<uint64_t>(c) * DP + h * H);
+    float part = 0.0f;
+    if (h == 0) {
+#pragma unroll
+      for (int s4 = 0; s4 < H / 4; ++s4) {
+        const f32x4 cv = cr[s4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) part = part + (kUnscale * qreg[4 * s4 + e]) * cv[e];
+      }
+    }
+    part = __shfl_xor(part, 32, 64);
+    if (h == 1) {
+#pragma unroll
+      for (int s4 = 0; s4 < H / 4; ++s4) {
+        const f32x4 cv = cr[s4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) part = part + (kUnscale * qreg[4 * s4 + e]) * cv[e];
+      }
+      const float ev = L2 ? a.aug[c] - 2.0f * part : -part;
+      if (ev < be || (ev == be && c < bc)) {
+        be = ev;
+        bc = c;
+      }
+    }
+  }
+  if (!valid || h != 1) return;
+  const bool decided = nband == 1 || (nband >= 2 && bc != 0xFFFFFFFFu);
+  if (decided) {
+    a.out32[p] = nband == 1 ? lc[0] : bc;
+  } else {
+    const uint32_t i = atomicAdd(&a.fb[0], 1u);
+    a.fb[1 + i] = static_cast<uint32_t>(p);
+  }
+}
+
+/// CentroidTable::nearest_batch for the points listed in list[1 .. list[0]] (those the MFMA pass
+/// left open): a work-group per point, its threads across the centroids, each dot product summed
+/// in order of t, then the smallest (value, index) among values below +inf (index 0 if none), as
+/// the reference's "first strictly smaller" scan returns. Transposed centroids ct [dim][k].
+constexpr int kListedCPT = 8;  // centroids per thread per pass
+__global__ void __launch_bounds__(256) nearest_listed_kernel(NearestArgs a) {
+  __shared__ float s_x[kAsgMaxDp];
+  __shared__ uint64_t s_min[4];
+  const int tid = threadIdx.x;
+  const uint32_t cnt = a.list[0];
+  for (uint32_t i = blockIdx.x; i < cnt; i += gridDim.x) {
+    const uint64_t p = a.list[1 + i];
+    __syncthreads();
+    if (static_cast<uint32_t>(tid) < a.dim) s_x[tid] = a.x[p * a.x_stride + tid];
+    __syncthreads();
+    uint64_t best = ~0ull;
+    for (uint32_t c0 = 0; c0 < a.k; c0 += 256 * kListedCPT) {
+      float acc[kListedCPT];
+#pragma unroll
+      for (int e = 0; e < kListedCPT; ++e) acc[e] = 0.0f;
+      for (uint32_t t = 0; t < a.dim; ++t) {
+        const float xv = s_x[t];
+#pragma unroll
+        for (int e = 0; e < kListedCPT; ++e) {
+          const uint32_t c = c0 + e * 256 + tid;
+          const float cv = c < a.k ? a.ct[static_cast<uint64_t>(t) * a.k + c] : 0.0f;
+          acc[e] = acc[e] + xv * cv;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < kListedCPT; ++e) {
+        const uint32_t c = c0 + e * 256 + tid;
+        const float d = a.max_ip ? -acc[e] : a.norms[c < a.k ? c : 0] - 2.0f * acc[e];
+        if (c < a.k && d < __builtin_huge_valf()) {
+          const uint64_t key = make_key(d, c);
+          best = key < best ? key : best;
+        }
+      }
+    }
+    best = wave_min_u64(best);
+    if ((tid & 63) == 0) s_min[tid >> 6] = best;
+    __syncthreads();
+    if (tid == 0) {
+      const uint64_t b = min(min(s_min[0], s_min[1]), min(s_min[2], s_min[3]));
+      a.out32[p] = b == ~0ull ? 0u : static_cast<uint32_t>(b);
+    }
+  }
+}
+
+/// The MFMA assignment's centroid operand: rows [kp][dp] zero-padded, the augmented column and
+/// (block 0, thread 0) the largest ||c||.
+__global__ void assign_rows_kernel(const float* __restrict__ cent, const float* __restrict__ norms, uint32_t k,
+                                   uint32_t dim, uint32_t dp, uint32_t kp, int max_ip, float* __restrict__ crow,
+                                   float* __restrict__ aug) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= static_cast<uint64_t>(kp) * dp) return;
+  const uint32_t c = static_cast<uint32_t>(i / dp), t = static_cast<uint32_t>(i % dp);
+  crow[i] = c < k && t < dim ? cent[static_cast<uint64_t>(c) * dim + t] : 0.0f;
+  if (t == 0) aug[c] = c < k ? (max_ip ? 0.0f : norms[c]) : __builtin_huge_valf();
+}
+
+__global__ void __launch_bounds__(256) norm_max_kernel(const float* __restrict__ norms, uint32_t k,
+                                                       float* __restrict__ rmax) {
+  __shared__ float s_m[256];
+  float m = 0.0f;
+  for (uint32_t c = threadIdx.x; c < k; c += 256) m = fmaxf(m, norms[c]);
+  s_m[threadIdx.x] = m;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (static_cast<int>(threadIdx.x) < w) s_m[threadIdx.x] = fmaxf(s_m[threadIdx.x], s_m[threadIdx.x + w]);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) rmax[0] = sqrtf(s_m[0]);
+}
+
+__global__ void assign_reset_kernel(uint32_t* fb) { fb[0] = 0; }
 
 /// ||c||^2 summed in order (centroid_table.h:50-57) and the transposed table t[j][c].
 __global__ void centroid_prep_kernel(const float* __restrict__ cent, uint32_t k, uint32_t dim,
@@ -1856,6 +2193,83 @@ void launch_nearest(bool sqdiff, const NearestArgs& a, uint32_t nsub, hipStream_
   QVH_HIP(hipGetLastError());
 }
 
+/// The MFMA assignment's operand for one centroid table, prepared once per table.
+struct AssignTable {
+  DeviceBuffer crow, aug, rmax;
+  uint32_t dim = 0, dp = 0, kp = 0;
+  bool ready = false;
+};
+
+/// Prepares `t` for centroids d_cent [k][dim] with in-order norms d_norms (centroid_prep_kernel).
+/// Dims that are not a multiple of 4 or above kAsgMaxDp leave it unprepared (exact kernel only).
+void prepare_assign_table(AssignTable& t, const float* d_cent, const float* d_norms, uint32_t k, uint32_t dim,
+                          int max_ip, hipStream_t s) {
+  t.ready = false;
+  if (k == 0 || dim % 4 != 0 || dim > kAsgMaxDp) return;
+  t.dim = dim;
+  t.dp = (dim + 31) / 32 * 32;
+  t.kp = static_cast<uint32_t>(ceil_div(k, kAsgTile) * kAsgTile);
+  const uint64_t cells = static_cast<uint64_t>(t.kp) * t.dp;
+  t.crow.reserve(cells * sizeof(float));
+  t.aug.reserve(t.kp * sizeof(float));
+  t.rmax.reserve(sizeof(float));
+  hipLaunchKernelGGL(assign_rows_kernel, dim3(static_cast<unsigned>(ceil_div(cells, 256))), dim3(256), 0, s, d_cent,
+                     d_norms, k, dim, t.dp, t.kp, max_ip, t.crow.as<float>(), t.aug.as<float>());
+  hipLaunchKernelGGL(norm_max_kernel, dim3(1), dim3(256), 0, s, d_norms, k, t.rmax.as<float>());
+  QVH_HIP(hipGetLastError());
+  t.ready = true;
+}
+
+template <int DP>
+void launch_assign_dp(bool l2, const AssignArgs& a, dim3 grid, hipStream_t s) {
+  if (l2) {
+    hipLaunchKernelGGL((assign_mfma_kernel<DP, true>), grid, dim3(kAsgThreads), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((assign_mfma_kernel<DP, false>), grid, dim3(kAsgThreads), 0, s, a);
+  }
+}
+
+/// Nearest centroids (nearest mode of `na`) of na.n points: the MFMA kernel where the table is
+/// prepared and the batch is large, then the exact kernel for the points it could not certify;
+/// the exact kernel for every point otherwise. `fb` is workspace (n + 1 words).
+void launch_assign(const NearestArgs& na, const AssignTable& t, DeviceBuffer& fb, hipStream_t s) {
+  if (na.n == 0) return;
+  const bool mfma = t.ready && na.dim == t.dim && na.n >= kAsgMinPoints && na.n < 0xFFFFFFFFull &&
+                    na.x_stride % 4 == 0 && reinterpret_cast<uintptr_t>(na.x) % 16 == 0;
+  if (!mfma) {
+    launch_nearest(false, na, 1, s);
+    return;
+  }
+  uint32_t* list = static_cast<uint32_t*>(fb.reserve((na.n + 1) * sizeof(uint32_t)));
+  hipLaunchKernelGGL(assign_reset_kernel, dim3(1), dim3(1), 0, s, list);
+  AssignArgs a{};
+  a.x = na.x;
+  a.n = na.n;
+  a.dim = na.dim;
+  a.x_stride = na.x_stride;
+  a.crow = t.crow.as<float>();
+  a.aug = t.aug.as<float>();
+  a.kp = t.kp;
+  a.rmax = t.rmax.as<float>();
+  a.coef = ldexpf(4.0f * static_cast<float>(t.dp + 1) + 16.0f, -24);
+  a.out32 = na.out32;
+  a.fb = list;
+  const dim3 grid(static_cast<unsigned>(ceil_div(na.n, kAsgPoints)));
+  const bool l2 = !na.max_ip;
+  switch (t.dp) {
+    case 32: launch_assign_dp<32>(l2, a, grid, s); break;
+    case 64: launch_assign_dp<64>(l2, a, grid, s); break;
+    case 96: launch_assign_dp<96>(l2, a, grid, s); break;
+    default: launch_assign_dp<128>(l2, a, grid, s); break;
+  }
+  QVH_HIP(hipGetLastError());
+  NearestArgs ex = na;
+  ex.list = list;
+  const uint64_t blocks = std::min<uint64_t>(na.n, 2048);
+  hipLaunchKernelGGL(nearest_listed_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, ex);
+  QVH_HIP(hipGetLastError());
+}
+
 }  // namespace
 
 namespace qvh {
@@ -1919,12 +2333,13 @@ struct qvh_ivfpq {
   uint64_t count = 0;
   std::vector<uint64_t> h_off;  // host copy of the list offsets
   DeviceBuffer cent, cent_t, cent_norm, cb, cbt, cbc, pre;
+  AssignTable asg;  // the centroids as the MFMA assignment's operand
   DeviceBuffer off, codes, t1, vec;
   DeviceBuffer pmax;  // [nlist] sum_j max_c |pre[l][j][c]| (the L2 ranking's certificate)
   DeviceBuffer cmax;  // [m] largest codeword norm per sub-space (the same)
   hipStream_t stream = nullptr;
   std::mutex mu;
-  DeviceBuffer w_x, w_res, w_assign, w_codes, w_codes_p, w_t1, w_dest, w_shift;
+  DeviceBuffer w_x, w_res, w_assign, w_afb, w_codes, w_codes_p, w_t1, w_dest, w_shift;
   DeviceBuffer w_q, w_scores, w_probes, w_bits, w_refs, w_dist, w_bytes, w_sel, w_selcnt, w_key, w_order;
   DeviceBuffer w_pkeys, w_pcnt, w_pdone;  // sliced queries of the streaming scan
   DeviceBuffer w_delta, w_fb;             // certificate bounds; uncertified queries (count, list)
@@ -1963,7 +2378,7 @@ void ivf_encode_device(qvh_ivfpq* h, const float* d_x, uint64_t n, hipStream_t s
   na.k = h->nlist;
   na.max_ip = h->metric == QVH_METRIC_IP;
   na.out32 = assign;
-  launch_nearest(false, na, 1, s);
+  launch_assign(na, h->asg, h->w_afb, s);
   float* res = static_cast<float*>(h->w_res.reserve(n * h->dim * sizeof(float)));
   hipLaunchKernelGGL(residual_kernel, dim3(static_cast<unsigned>(ceil_div(n * h->dim, 256))), dim3(256), 0, s,
                      d_x, assign, h->cent.as<float>(), n, h->dim, res);
@@ -2331,6 +2746,8 @@ qvh_status qvh_ivfpq_set_trained(qvh_ivfpq* h, const float* centroids, const flo
     QVH_HIP(hipMemcpyAsync(h->cb.ptr, codebook, bbytes, hipMemcpyHostToDevice, s));
     hipLaunchKernelGGL(centroid_prep_kernel, dim3(static_cast<unsigned>(ceil_div(h->nlist, 256))), dim3(256), 0, s,
                        h->cent.as<float>(), h->nlist, h->dim, h->cent_t.as<float>(), h->cent_norm.as<float>());
+    prepare_assign_table(h->asg, h->cent.as<float>(), h->cent_norm.as<float>(), h->nlist, h->dim,
+                         h->metric == QVH_METRIC_IP, s);
     hipLaunchKernelGGL(codebook_prep_kernel, dim3(static_cast<unsigned>(ceil_div(uint64_t(h->m) * 256 * h->dsub, 256))),
                        dim3(256), 0, s, h->cb.as<float>(), h->m, h->dsub, h->cbt.as<float>());
     hipLaunchKernelGGL(codebook_cmajor_kernel, dim3(static_cast<unsigned>(ceil_div(uint64_t(h->m) * 256 * h->dsub, 256))),
@@ -2678,7 +3095,8 @@ struct qvh_points {
   uint64_t n = 0;
   uint32_t dim = 0;
   int device = 0;
-  DeviceBuffer x, cent, ct, norms, out;
+  DeviceBuffer x, cent, ct, norms, out, fb;
+  AssignTable asg;
   std::mutex mu;
 };
 
@@ -2732,7 +3150,8 @@ qvh_status qvh_points_nearest(qvh_points* p, const float* centroids, uint32_t k,
     na.k = k;
     na.max_ip = max_inner_product;
     na.out32 = p->out.as<uint32_t>();
-    launch_nearest(false, na, 1, nullptr);
+    prepare_assign_table(p->asg, p->cent.as<float>(), p->norms.as<float>(), k, p->dim, max_inner_product, nullptr);
+    launch_assign(na, p->asg, p->fb, nullptr);
     QVH_HIP(hipMemcpy(out_assign, p->out.ptr, p->n * sizeof(uint32_t), hipMemcpyDeviceToHost));
   });
 }

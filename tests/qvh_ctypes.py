@@ -48,9 +48,25 @@ class Qvh:
         L.qvh_pq_tables.argtypes = [C.c_void_p, _f32p, C.c_uint64, C.c_int, _f32p]
         L.qvh_pq_adc.argtypes = [C.c_void_p, _f32p, _u8p, C.c_uint64, _f32p]
         L.qvh_nearest_centroid.argtypes = [_f32p, C.c_uint64, _f32p, C.c_uint32, C.c_uint32, _u32p]
+        L.qvh_points_create.argtypes = [_f32p, C.c_uint64, C.c_uint32, C.POINTER(C.c_void_p)]
+        L.qvh_points_destroy.argtypes = [C.c_void_p]
+        L.qvh_points_nearest.argtypes = [C.c_void_p, _f32p, C.c_uint32, C.c_int, _u32p]
 
     def pq(self, dim, m, codebook):
         return QvhPq(self, dim, m, codebook)
+
+    def points_nearest(self, x, cent, max_inner_product=False):
+        """qvh_points_nearest (CentroidTable::nearest_batch) of the rows of x against cent."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        cent = np.ascontiguousarray(cent, dtype=np.float32)
+        h = C.c_void_p()
+        self.check(self.lib.qvh_points_create(x, x.shape[0], x.shape[1], C.byref(h)))
+        try:
+            out = np.empty(x.shape[0], dtype=np.uint32)
+            self.check(self.lib.qvh_points_nearest(h, cent, cent.shape[0], int(max_inner_product), out))
+        finally:
+            self.lib.qvh_points_destroy(h)
+        return out
 
     def nearest_centroid(self, x, cent):
         """qvh_nearest_centroid of each row of x against the rows of cent."""

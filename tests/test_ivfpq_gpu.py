@@ -72,6 +72,49 @@ def test_kmeans_matches_oracle(oracle):
                           oracle.kmeans(x, 8, 5, max_points_per_centroid=100, seed=7))
 
 
+@pytest.mark.parametrize("max_ip", [False, True])
+@pytest.mark.parametrize("dim,n,k", [(128, 20_000, 2048), (100, 8_000, 300), (32, 5_000, 64), (64, 3_000, 1),
+                                     (30, 4_000, 100), (128, 500, 256)])
+def test_points_nearest_matches_oracle(oracle, max_ip, dim, n, k):
+    """CentroidTable::nearest_batch (src/internal/centroid_table.h:94-144) for a batch of points:
+    the MFMA assignment (dims that are multiples of 4, up to 128, batches of 1024 or more) with its
+    certificate, or the exact kernel (dim 30, 500 points); cell ids bit-equal to the oracle."""
+    print(f"case: dim={dim} n={n} k={k} max_ip={max_ip}", flush=True)
+    x = clustered(n, dim, 64, 21)
+    cent = clustered(k, dim, 64, 22)
+    got = Qvh().points_nearest(x, cent, max_ip)
+    assert np.array_equal(got, oracle.nearest(x, cent, max_ip))
+
+
+@pytest.mark.parametrize("max_ip", [False, True])
+def test_points_nearest_ties_fall_back_exactly(oracle, max_ip):
+    """Points exactly between two centroids, points within rounding of a tie, and duplicated
+    centroids: the first of equal values must win, as in the reference, which the MFMA pass
+    cannot decide; it leaves those points to the exact kernel."""
+    rng = np.random.default_rng(5)
+    dim, k = 64, 512
+    cent = rng.standard_normal((k, dim)).astype(np.float32)
+    cent[300:310] = cent[10:20]                       # duplicated centroids (ties at every point near them)
+    x = rng.standard_normal((6000, dim)).astype(np.float32)
+    i = np.arange(2000)
+    mid = (0.5 * (cent[i % 200] + cent[200 + i % 100])).astype(np.float32)
+    x[:2000] = mid                                    # equidistant from two centroids (up to rounding)
+    x[2000:2600] = cent[np.arange(600) % k] + np.float32(1e-6)
+    x[2600:3000] = cent[np.arange(10, 20).repeat(40)]  # on a duplicated centroid
+    got = Qvh().points_nearest(x, cent, max_ip)
+    assert np.array_equal(got, oracle.nearest(x, cent, max_ip))
+
+
+def test_integer_points_assign_exactly(oracle):
+    """Integer-valued points and integer centroids: every g is exact, so ties (common) are
+    decided by the exact kernel and everything else by the MFMA pass."""
+    rng = np.random.default_rng(8)
+    x = rng.integers(-8, 9, (20_000, 32)).astype(np.float32)
+    cent = rng.integers(-8, 9, (256, 32)).astype(np.float32)
+    got = Qvh().points_nearest(x, cent)
+    assert np.array_equal(got, oracle.nearest(x, cent))
+
+
 @pytest.mark.parametrize("metric,store,refine", [("l2", False, 0), ("l2", True, 4), ("cosine", True, 4),
                                                  ("ip", True, 8)])
 def test_ivfpq_small_matches_oracle(oracle, metric, store, refine):
