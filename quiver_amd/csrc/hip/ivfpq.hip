@@ -175,6 +175,7 @@ constexpr int kAsgThreads = 512;  // 8 waves of 32 points
 constexpr int kAsgPoints = 256;
 constexpr int kAsgTile = 64;      // centroid rows per LDS tile
 constexpr uint32_t kAsgMaxDp = 128;
+constexpr uint32_t kAsgMinDim = 32;
 constexpr uint64_t kAsgMinPoints = 1024;  // smaller batches stay on the exact kernel
 constexpr int kAsgList = 4;                // (g, c) kept per point
 
@@ -2201,11 +2202,12 @@ struct AssignTable {
 };
 
 /// Prepares `t` for centroids d_cent [k][dim] with in-order norms d_norms (centroid_prep_kernel).
-/// Dims that are not a multiple of 4 or above kAsgMaxDp leave it unprepared (exact kernel only).
+/// Dims that are not a multiple of 4, below kAsgMinDim (PQ sub-spaces: mostly padding, and the
+/// VALU kernel is fast there) or above kAsgMaxDp leave it unprepared (exact kernel only).
 void prepare_assign_table(AssignTable& t, const float* d_cent, const float* d_norms, uint32_t k, uint32_t dim,
                           int max_ip, hipStream_t s) {
   t.ready = false;
-  if (k == 0 || dim % 4 != 0 || dim > kAsgMaxDp) return;
+  if (k == 0 || dim % 4 != 0 || dim < kAsgMinDim || dim > kAsgMaxDp) return;
   t.dim = dim;
   t.dp = (dim + 31) / 32 * 32;
   t.kp = static_cast<uint32_t>(ceil_div(k, kAsgTile) * kAsgTile);

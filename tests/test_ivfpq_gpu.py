@@ -74,11 +74,12 @@ def test_kmeans_matches_oracle(oracle):
 
 @pytest.mark.parametrize("max_ip", [False, True])
 @pytest.mark.parametrize("dim,n,k", [(128, 20_000, 2048), (100, 8_000, 300), (32, 5_000, 64), (64, 3_000, 1),
-                                     (30, 4_000, 100), (128, 500, 256)])
+                                     (30, 4_000, 100), (16, 4_000, 256), (128, 500, 256)])
 def test_points_nearest_matches_oracle(oracle, max_ip, dim, n, k):
     """CentroidTable::nearest_batch (src/internal/centroid_table.h:94-144) for a batch of points:
-    the MFMA assignment (dims that are multiples of 4, up to 128, batches of 1024 or more) with its
-    certificate, or the exact kernel (dim 30, 500 points); cell ids bit-equal to the oracle."""
+    the MFMA assignment (dims that are multiples of 4 from 32 to 128, batches of 1024 or more)
+    with its certificate, or the exact kernel (dims 30 and 16, 500 points); cell ids bit-equal to
+    the oracle."""
     print(f"case: dim={dim} n={n} k={k} max_ip={max_ip}", flush=True)
     x = clustered(n, dim, 64, 21)
     cent = clustered(k, dim, 64, 22)
@@ -103,6 +104,22 @@ def test_points_nearest_ties_fall_back_exactly(oracle, max_ip):
     x[2600:3000] = cent[np.arange(10, 20).repeat(40)]  # on a duplicated centroid
     got = Qvh().points_nearest(x, cent, max_ip)
     assert np.array_equal(got, oracle.nearest(x, cent, max_ip))
+
+
+@pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
+def test_large_batches_select_probes_exactly(oracle, metric):
+    """2,000 queries (the multi-query coarse kernel and the streaming scan), a third of them
+    planted exactly between two centroids so that coarse scores tie at the probe boundary, where
+    ties go to the smaller list id; results equal the oracle's at every nprobe."""
+    base = clustered(20_000, 64, 80, 31)
+    idx, st = build_pair(oracle, base, metric, 256, 16, metric != "ip", train_n=8000, iters=6)
+    q = clustered(2000, 64, 80, 32)
+    cent = idx.centroids
+    i = np.arange(700)
+    q[:700] = (0.5 * (cent[i % 128] + cent[128 + i % 97])).astype(np.float32)
+    for nprobe in (1, 8, 33, 64):
+        print(f"case: {metric} nprobe={nprobe}", flush=True)
+        print(compare_search(oracle, idx, st, q, 10, nprobe, refine=2 if metric != "ip" else 0))
 
 
 def test_integer_points_assign_exactly(oracle):
