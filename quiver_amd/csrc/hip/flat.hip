@@ -60,6 +60,7 @@ struct ScanArgs {
   uint32_t* part_r;
   uint32_t* qthr;           // [nq] shared prune threshold (ordered float bits), starts at +inf
   int share;                // 0: every lane list keeps its own KL best (k > KL: no shared bound)
+  uint32_t dp;              // row width (the chunked scan; the register scan has it as DP)
 };
 
 constexpr int kShareEvery = 8;  // tiles between exchanges of the shared per-query threshold
@@ -77,6 +78,143 @@ __device__ __forceinline__ void list_insert(float (&Ld)[KL], uint32_t (&Lr)[KL],
     Lr[x] = lt ? r : tr;
     d = lt ? td : d;
     r = lt ? tr : r;
+  }
+}
+
+/// A scan lane's selection state: its list of the KL best (distance, row) among the rows it has
+/// seen, its candidate queue (CAP entries in LDS, entry-major: entry e of thread t at e * kThreads
+/// + t, so lanes appending at different depths never share a bank) and its prune threshold.
+/// Candidates are appended in row order and inserted into the list by a wave-wide flush. Shared
+/// by the scan kernels.
+template <int KL, int CAP>
+struct LaneScan {
+  float Ld[KL];
+  uint32_t Lr[KL];
+  int qcount;
+  // Prune threshold: the smaller of this lane's KL-th best and the shared per-query value. Any
+  // list's KL-th best bounds the KL-th best of the union of all lists, so candidates above it can
+  // never be among the query's KL best (equal distances pass: ties are decided by row).
+  float pthr;
+  int tid;
+
+  __device__ __forceinline__ void init(int thread, float thr0) {
+#pragma unroll
+    for (int x = 0; x < KL; ++x) {
+      Ld[x] = __builtin_huge_valf();
+      Lr[x] = QVH_EMPTY_ROW;
+    }
+    qcount = 0;
+    pthr = thr0;
+    tid = thread;
+  }
+
+  /// All lanes of the wave together: queued candidates into the lists (NaN becomes +inf). s_qd and
+  /// s_qr are the work-group's queue arrays (CAP * kThreads entries).
+  __device__ __forceinline__ void flush(const float* s_qd, const uint32_t* s_qr) {
+    int m = qcount;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = max(m, __shfl_xor(m, off, 64));
+    for (int e = 0; e < m; ++e) {
+      if (e < qcount) {
+        float v = s_qd[e * kThreads + tid];
+        v = v == v ? v : __builtin_huge_valf();
+        if (v <= Ld[KL - 1]) list_insert<KL>(Ld, Lr, v, s_qr[e * kThreads + tid]);
+      }
+    }
+    qcount = 0;
+  }
+
+  /// Exchange through the per-query value *qthr (null for lanes past the last query). The two
+  /// lanes of a query (j, j + 32) hold disjoint rows: their union has KL candidates at or below
+  /// max(own[KL/2-1], other[KL/2-1]) as well as below either list's KL-th.
+  __device__ __forceinline__ void share(uint32_t* qthr, int h, int j) {
+    const float own_k = Ld[KL - 1], own_h = Ld[KL / 2 - 1];
+    const float oth_k = __shfl_xor(own_k, 32, 64), oth_h = __shfl_xor(own_h, 32, 64);
+    float t = fminf(fminf(own_k, oth_k), fmaxf(own_h, oth_h));
+    if (qthr) {
+      uint32_t g = 0;
+      if (h == 0) g = atomicMin(qthr, float_to_ordered(t));
+      g = __shfl(g, j, 64);
+      t = fminf(t, ordered_to_float(g));
+    }
+    pthr = fminf(pthr, t);
+  }
+
+  /// One 32x32 block of distances (register r: row 8*(r/4) + 4*h + r%4 of the block, rows
+  /// row0 + 8*(r/4) + r%4 with row0 = block's first row + 4*h); lane_bits: admission of those rows
+  /// (bit 8*(r/4) + r%4), tested when `masked` (wave-uniform). Per lane the rows visited increase,
+  /// so ties resolve to the smaller row.
+  __device__ __forceinline__ void block(const f32x16& acc, uint32_t lane_bits, bool masked, bool qvalid,
+                                        uint32_t row0, float* s_qd, uint32_t* s_qr) {
+    // Pass test: !(d > thr). Ties pass (a tied row may still win on row number), and so does
+    // NaN, which the flush turns into +inf as the reference does.
+    const float thr = fminf(pthr, Ld[KL - 1]);
+    bool any = false;
+    if (!masked) {
+      // One test of the smallest distance (fminf skips NaN; all-NaN gives NaN, which passes).
+      float m = acc[0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) m = fminf(m, acc[r]);
+      any = !(m > thr);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        any = any || (!(acc[r] > thr) && ((lane_bits >> (8 * (r >> 2) + (r & 3))) & 1u));
+      }
+    }
+    // Lanes past the last query never queue: their zero query makes every inner-product
+    // distance 1 exactly, a tie with their own list that would admit every row.
+    any = any && qvalid;
+    if (__builtin_amdgcn_ballot_w64(qcount > CAP - 16)) flush(s_qd, s_qr);
+    if (any) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int bit = 8 * (r >> 2) + (r & 3);
+        bool p = !(acc[r] > thr);
+        if (masked) p = p && ((lane_bits >> bit) & 1u);
+        // Written whether or not it passes (no branch per element); a failing entry is
+        // overwritten by the next. The flush above leaves room for all 16.
+        s_qd[qcount * kThreads + tid] = acc[r];
+        s_qr[qcount * kThreads + tid] = row0 + static_cast<uint32_t>(bit);
+        qcount += p ? 1 : 0;
+      }
+    }
+  }
+
+  /// The two blocks of a 64-row tile starting at tile_row0, `left` of its rows inside the split,
+  /// `admit` the filter's bits for the tile (all ones without a filter).
+  __device__ __forceinline__ void tile(const f32x16& acc0, const f32x16& acc1, uint64_t tile_row0, uint64_t left,
+                                       uint64_t admit, bool filter, bool qvalid, int h, float* s_qd, uint32_t* s_qr) {
+    if (left < 64) admit &= (1ull << left) - 1;
+    const bool masked = filter || left < 64;
+    block(acc0, static_cast<uint32_t>(admit) >> (4 * h), masked, qvalid, static_cast<uint32_t>(tile_row0 + 4 * h),
+          s_qd, s_qr);
+    block(acc1, static_cast<uint32_t>(admit >> 32) >> (4 * h), masked, qvalid,
+          static_cast<uint32_t>(tile_row0 + 32 + 4 * h), s_qd, s_qr);
+  }
+
+  /// The lane's list into part_d / part_r at offset o.
+  __device__ __forceinline__ void store(float* part_d, uint32_t* part_r, size_t o) const {
+#pragma unroll
+    for (int x = 0; x < KL; ++x) {
+      part_d[o + x] = Ld[x];
+      part_r[o + x] = Lr[x];
+    }
+  }
+};
+
+/// Row split and query block of work-group blockIdx.x. Work-group w runs on XCD w % 8; each XCD
+/// gets its own row splits, so the work-groups resident on one XCD at a time stream the same base
+/// rows through that XCD's L2.
+__device__ __forceinline__ void scan_block_coords(const ScanArgs& a, uint32_t& qb, uint32_t& split) {
+  const uint32_t wg = blockIdx.x;
+  if (a.nsplit % 8 == 0) {
+    const uint32_t x = wg % 8, li = wg / 8;
+    split = (li / a.qblocks) * 8 + x;
+    qb = li % a.qblocks;
+  } else {
+    split = wg / a.qblocks;
+    qb = wg % a.qblocks;
   }
 }
 
@@ -347,6 +485,157 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
       a.part_r[o + x] = Lr[x];
     }
   }
+}
+
+// ---- the chunked scan: rows wider than kMaxDp ------------------------------------------------
+//
+// The same search for any padded width: each step stages one kKc-dim chunk of a 64-row tile and of
+// the block's 256 queries (scaled by -2 or -1 on the way in) in LDS, and every wave accumulates its
+// 32 queries x 64 rows over the chunks; after a tile's last chunk the augmented step adds
+// (||x||^2, 1) x (1, ||q||^2) and the tile goes through the same selection as the register scan.
+// The next step's loads are in flight while a step's 32 MFMAs per wave run.
+constexpr int kKc = 32;              // dims per chunk
+constexpr int kKcStride = kKc + 4;   // LDS row stride of a row chunk (floats)
+constexpr int kKcQueueCap = 18;      // queue entries per lane (LDS holds both chunk buffers too)
+constexpr uint32_t kMaxChunkedDp = 4096;
+
+template <int KL, bool L2, int MODE>
+__global__ void __launch_bounds__(kThreads) flat_scan_k_kernel(ScanArgs a) {
+  constexpr bool FILTER = MODE == 1;
+  constexpr int C4 = kKc / 4;  // float4 slots per chunk row
+  __shared__ __attribute__((aligned(16))) float s_x[2][kTileRows * kKcStride];
+  // Query chunks: slot (row, c) of row-major [256][C4] float4 slots at row * C4 + (c ^ (row % 8)),
+  // so a wave's 32 rows reading one column spread over the banks.
+  __shared__ __attribute__((aligned(16))) float s_q[2][kQueriesPerBlock * kKc];
+  __shared__ float s_aug[2][kTileRows];
+  __shared__ uint64_t s_bits[2];
+  __shared__ float s_qd[kKcQueueCap * kThreads];
+  __shared__ uint32_t s_qr[kKcQueueCap * kThreads];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 31, h = lane >> 5;
+  uint32_t qb, split;
+  scan_block_coords(a, qb, split);
+  const uint32_t q = qb * kQueriesPerBlock + wave * 32 + j;
+  const bool wave_active = qb * kQueriesPerBlock + wave * 32 < a.nq;
+  const bool qvalid = q < a.nq;
+  constexpr float kScale = L2 ? -2.0f : -1.0f;
+  const float qaug = h == 0 ? 1.0f : (L2 && qvalid ? a.qnorm[q] : 0.0f);
+
+  LaneScan<KL, kKcQueueCap> ls;
+  ls.init(tid, qvalid ? ordered_to_float(a.qthr[q]) : __builtin_huge_valf());
+
+  const uint64_t r0 = static_cast<uint64_t>(split) * a.rows_per_split;
+  const uint64_t r1 = r0 < a.n ? (a.n < r0 + a.rows_per_split ? a.n : r0 + a.rows_per_split) : r0;
+  const uint32_t ntiles = static_cast<uint32_t>(ceil_div(r1 - r0, kTileRows));
+  const uint32_t nchunks = (a.dp + kKc - 1) / kKc;
+  const uint64_t nsteps = static_cast<uint64_t>(ntiles) * nchunks;
+  const uint64_t last_row = r1 > r0 ? r1 - 1 : r0;
+
+  // Staging registers: one row slot and four query slots per thread, and per tile the row norm
+  // (threads 0-63) and the filter word (thread 64).
+  const int xrow = tid / C4, xc = tid % C4;  // 64 rows x 8 slots = 512 = kThreads
+  uint64_t xg = 0;                           // global row of xrow in the current tile
+  f32x4 sx, sq[4];
+  float sn = 0.0f;
+  uint64_t sb = ~0ull;
+  auto load_step = [&](uint64_t i) {
+    const uint32_t t = static_cast<uint32_t>(i / nchunks), c = static_cast<uint32_t>(i % nchunks);
+    const uint64_t base = r0 + static_cast<uint64_t>(t) * kTileRows;
+    if (c == 0) {
+      uint64_t gr = base + xrow;
+      gr = gr < last_row ? gr : last_row;
+      if constexpr (MODE == 2) gr = a.idx[gr];
+      xg = gr;
+      if (L2 && tid < kTileRows) {
+        uint64_t gn = base + tid;
+        gn = gn < last_row ? gn : last_row;
+        if constexpr (MODE == 2) gn = a.idx[gn];
+        sn = a.xnorm[gn];
+      }
+      if (FILTER && tid == kTileRows) sb = a.bitmap[base >> 6];
+    }
+    const uint32_t col = c * kKc + 4 * xc;
+    sx = col < a.dp ? *reinterpret_cast<const f32x4*>(a.X + xg * a.dp + col) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int item = tid + p * kThreads, qr = item / C4, qc = item % C4;
+      uint32_t qg = qb * kQueriesPerBlock + qr;
+      qg = qg < a.nq ? qg : a.nq - 1;
+      const uint32_t qcol = c * kKc + 4 * qc;
+      sq[p] = qcol < a.dp ? *reinterpret_cast<const f32x4*>(a.Q + static_cast<uint64_t>(qg) * a.dp + qcol)
+                          : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  auto store_step = [&](uint64_t i, int buf) {
+    const uint32_t t = static_cast<uint32_t>(i / nchunks), c = static_cast<uint32_t>(i % nchunks);
+    *reinterpret_cast<f32x4*>(&s_x[buf][xrow * kKcStride + 4 * xc]) = sx;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int item = tid + p * kThreads, qr = item / C4, qc = item % C4;
+      *reinterpret_cast<f32x4*>(&s_q[buf][4 * (qr * C4 + (qc ^ (qr % 8)))]) = kScale * sq[p];
+    }
+    if (c == 0) {
+      if (tid < kTileRows) s_aug[t & 1][tid] = L2 ? sn : 1.0f;
+      if (FILTER && tid == kTileRows) s_bits[t & 1] = sb;
+    }
+  };
+
+  if (nsteps > 0) {
+    load_step(0);
+    store_step(0, 0);
+  }
+  __syncthreads();
+
+  f32x16 acc0 = {}, acc1 = {};
+  const int qrow = wave * 32 + j;
+  for (uint64_t i = 0; i < nsteps; ++i) {
+    const int buf = static_cast<int>(i & 1);
+    const uint32_t t = static_cast<uint32_t>(i / nchunks), c = static_cast<uint32_t>(i % nchunks);
+    const bool prefetch = i + 1 < nsteps;
+    if (prefetch) load_step(i + 1);
+    if (wave_active) {
+      if (c == 0) {
+        acc0 = f32x16{};
+        acc1 = f32x16{};
+      }
+      // Lane (j, h): dims h*16 .. h*16+15 of the chunk, as four float4 slots.
+      f32x4 b[4], x0[4], x1[4];
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const int slot = h * 4 + s4;
+        b[s4] = *reinterpret_cast<const f32x4*>(&s_q[buf][4 * (qrow * C4 + (slot ^ (qrow % 8)))]);
+        x0[s4] = *reinterpret_cast<const f32x4*>(&s_x[buf][j * kKcStride + 4 * slot]);
+        x1[s4] = *reinterpret_cast<const f32x4*>(&s_x[buf][(32 + j) * kKcStride + 4 * slot]);
+      }
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0[s4][e], b[s4][e], acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1[s4][e], b[s4][e], acc1, 0, 0, 0);
+        }
+      }
+      if (c + 1 == nchunks) {
+        const float aug0 = h == 0 ? s_aug[t & 1][j] : 1.0f;
+        const float aug1 = h == 0 ? s_aug[t & 1][32 + j] : 1.0f;
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(aug0, qaug, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(aug1, qaug, acc1, 0, 0, 0);
+        const uint64_t tile_row0 = r0 + static_cast<uint64_t>(t) * kTileRows;
+        ls.tile(acc0, acc1, tile_row0, r1 - tile_row0, FILTER ? s_bits[t & 1] : ~0ull, FILTER, qvalid, h, s_qd, s_qr);
+        if ((t % kShareEvery) == kShareEvery - 1) {
+          ls.flush(s_qd, s_qr);
+          if (a.share) ls.share(qvalid ? &a.qthr[q] : nullptr, h, j);
+        }
+      }
+    }
+    if (prefetch) store_step(i + 1, buf ^ 1);
+    __syncthreads();
+  }
+
+  if (wave_active) ls.flush(s_qd, s_qr);
+  if (qvalid) ls.store(a.part_d, a.part_r, (static_cast<size_t>(q) * (2 * a.nsplit) + 2 * split + h) * KL);
 }
 
 struct MergeArgs {
@@ -685,8 +974,9 @@ struct ExactArgs {
   const uint64_t* bitmap;
   uint32_t* out_rows;
   float* out_dist;
-  const uint32_t* qlist;   // queries to run (block b runs qlist[b] while b < *qcount), or null: all
-  const uint32_t* qcount;
+  const uint32_t* qlist;   // queries to run (block b runs qlist[qskip + b] while qskip + b < *qcount),
+  const uint32_t* qcount;  // or null: all. With row splits: list entries 0..nq-1, output slot = entry.
+  uint32_t qskip;
   const uint32_t* idx;     // admitted rows, ascending, at positions 0..n-1 (bitmap unused), or null
   // Row splits (nsplit > 1, a multiple of 8; qlist unused): split g scans rows
   // [g * rows_per_split, (g + 1) * rows_per_split) and writes its k best to slot q * nsplit + g of
@@ -708,14 +998,22 @@ __global__ void __launch_bounds__(kExactThreads) flat_exact_kernel(ExactArgs a) 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  uint32_t q = blockIdx.x, split = 0;
+  uint32_t q = blockIdx.x, split = 0, oslot = 0;
   if (a.nsplit > 1) {
     const uint32_t j = blockIdx.x >> 3;
     q = j % a.nq;
     split = (j / a.nq) * 8 + (blockIdx.x & 7);
+    oslot = q;
+    if (a.qlist) {
+      if (q >= *a.qcount) return;  // block-uniform, before any barrier
+      q = a.qlist[q];
+    }
   } else if (a.qlist) {
-    if (blockIdx.x >= *a.qcount) return;  // block-uniform, before any barrier
-    q = a.qlist[blockIdx.x];
+    if (a.qskip + blockIdx.x >= *a.qcount) return;  // block-uniform, before any barrier
+    q = a.qlist[a.qskip + blockIdx.x];
+    oslot = q;
+  } else {
+    oslot = q;
   }
   const float* qv = a.Q + static_cast<uint64_t>(q) * a.dp;
   if (tid == 0) s_thr = 0xFFFFFFFFu;
@@ -738,7 +1036,7 @@ __global__ void __launch_bounds__(kExactThreads) flat_exact_kernel(ExactArgs a) 
   };
   const uint64_t r_begin = min(a.n, static_cast<uint64_t>(split) * a.rows_per_split);
   const uint64_t r_end = a.nsplit > 1 ? min(a.n, r_begin + a.rows_per_split) : a.n;
-  const uint64_t slot = static_cast<uint64_t>(q) * max(a.nsplit, 1u) + split;
+  const uint64_t slot = static_cast<uint64_t>(oslot) * max(a.nsplit, 1u) + split;
   for (uint64_t r0 = r_begin; r0 < r_end; r0 += kExactThreads) {
     uint64_t r = r0 + tid;
     bool ok = r < r_end;
@@ -1121,7 +1419,8 @@ __device__ void merge_sorted_lists(const uint32_t* __restrict__ part_r, const fl
 /// fewer lists than k, T0 is the padding key and every real key is gathered, nsplit * k < k * k of
 /// them. So for k <= 64 the kSelectMergeCap = 4096 buffer always suffices; above, a query that
 /// gathers more is flagged (overflow[q] = 1, else 0) for the sequential merge of the same lists,
-/// which gives the same k keys.
+/// which gives the same k keys. With qlist: work-group b merges slot b for query qlist[b] while
+/// b < *qcount.
 constexpr uint32_t kSelectMergeMaxK = 256;
 constexpr uint32_t kSelectMergeLists = 1024;
 constexpr uint32_t kSelectMergeCap = 4096;
@@ -1131,12 +1430,16 @@ __global__ void __launch_bounds__(1024) flat_merge_select_kernel(const uint32_t*
                                                                  uint32_t nsplit, uint32_t k,
                                                                  uint32_t* __restrict__ out_rows,
                                                                  float* __restrict__ out_dist,
-                                                                 uint32_t* __restrict__ overflow) {
+                                                                 uint32_t* __restrict__ overflow,
+                                                                 const uint32_t* __restrict__ qlist = nullptr,
+                                                                 const uint32_t* __restrict__ qcount = nullptr) {
   __shared__ uint64_t s_heads[kSelectMergeLists];
   __shared__ uint64_t s_cand[kSelectMergeCap];
   __shared__ uint32_t s_count;
   const uint32_t tid = threadIdx.x;
   const uint32_t q = blockIdx.x;
+  if (qlist && q >= *qcount) return;  // block-uniform, before any barrier
+  const uint64_t oq = qlist ? qlist[q] : q;
   const uint32_t* pr = part_r + static_cast<uint64_t>(q) * nsplit * k;
   const float* pd = part_d + static_cast<uint64_t>(q) * nsplit * k;
   const uint64_t o = static_cast<uint64_t>(tid) * k;
@@ -1173,9 +1476,8 @@ __global__ void __launch_bounds__(1024) flat_merge_select_kernel(const uint32_t*
   block_sort_keys(s_cand, n2);
   for (uint32_t j = tid; j < k; j += 1024) {
     const bool real = j < c;
-    out_rows[static_cast<uint64_t>(q) * k + j] = real ? static_cast<uint32_t>(s_cand[j]) : QVH_EMPTY_ROW;
-    out_dist[static_cast<uint64_t>(q) * k + j] =
-        real ? ordered_to_float(static_cast<uint32_t>(s_cand[j] >> 32)) : __builtin_huge_valf();
+    out_rows[oq * k + j] = real ? static_cast<uint32_t>(s_cand[j]) : QVH_EMPTY_ROW;
+    out_dist[oq * k + j] = real ? ordered_to_float(static_cast<uint32_t>(s_cand[j] >> 32)) : __builtin_huge_valf();
   }
 }
 
@@ -1242,6 +1544,22 @@ void launch_exact(const ExactArgs& a, uint64_t nq, hipStream_t s) {
   QVH_HIP(hipGetLastError());
 }
 
+int device_cus(int device) {
+  int cus = 256;
+  (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+  return cus;
+}
+
+/// Listed fallback queries that run over row splits, and their split count for n rows: up to 128
+/// splits of at least kMinSplitRows rows (a multiple of 8 for the XCD mapping), about four
+/// work-groups per CU in all; 0 when the rows are too few to split.
+constexpr uint32_t kFallbackSplitQueries = 8;
+uint32_t fallback_splits(uint64_t n, int cus) {
+  const uint64_t want = std::max<uint64_t>(8, static_cast<uint64_t>(cus) * 4 / kFallbackSplitQueries);
+  const uint64_t g = std::min<uint64_t>({want, 128, n / kMinSplitRows}) / 8 * 8;
+  return static_cast<uint32_t>(g);
+}
+
 /// Row stride in floats: the dimension rounded up to 16 (the MFMA scan's K step).
 uint32_t padded_dim(uint32_t dim) { return (dim + 15u) / 16u * 16u; }
 
@@ -1283,9 +1601,39 @@ void launch_scan_dp(int kl, bool l2, int mode, dim3 grid, const ScanArgs& a, hip
   }
 }
 
+template <int KL>
+void launch_scan_chunked_kl(bool l2, int mode, dim3 grid, const ScanArgs& a, hipStream_t s) {
+  if (l2) {
+    if (mode == 1) {
+      hipLaunchKernelGGL((flat_scan_k_kernel<KL, true, 1>), grid, dim3(kThreads), 0, s, a);
+    } else if (mode == 2) {
+      hipLaunchKernelGGL((flat_scan_k_kernel<KL, true, 2>), grid, dim3(kThreads), 0, s, a);
+    } else {
+      hipLaunchKernelGGL((flat_scan_k_kernel<KL, true, 0>), grid, dim3(kThreads), 0, s, a);
+    }
+  } else {
+    if (mode == 1) {
+      hipLaunchKernelGGL((flat_scan_k_kernel<KL, false, 1>), grid, dim3(kThreads), 0, s, a);
+    } else if (mode == 2) {
+      hipLaunchKernelGGL((flat_scan_k_kernel<KL, false, 2>), grid, dim3(kThreads), 0, s, a);
+    } else {
+      hipLaunchKernelGGL((flat_scan_k_kernel<KL, false, 0>), grid, dim3(kThreads), 0, s, a);
+    }
+  }
+}
+
+/// The MFMA scan for padded width dp: register-resident queries up to kMaxDp, chunked above.
 void launch_scan(uint32_t dp, int kl, dim3 grid, const ScanArgs& a, hipStream_t s) {
   const bool l2 = a.l2 != 0;
   const int filter = a.idx ? 2 : a.bitmap ? 1 : 0;
+  if (dp > static_cast<uint32_t>(kMaxDp)) {
+    if (kl == 16) {
+      launch_scan_chunked_kl<16>(l2, filter, grid, a, s);
+    } else {
+      launch_scan_chunked_kl<32>(l2, filter, grid, a, s);
+    }
+    return;
+  }
   switch (dp) {
     case 16: launch_scan_dp<16>(kl, l2, filter, grid, a, s); break;
     case 32: launch_scan_dp<32>(kl, l2, filter, grid, a, s); break;
@@ -1397,13 +1745,14 @@ FlatPlan plan_flat_search(const qvh_flat* f, uint64_t nq, uint32_t k, bool index
   // margin in a shared-bound list (shared_list_length): the MFMA scan with per-lane lists of KL = 16
   // or 32 and a shared bound; larger k up to kWideMaxK: the same scan without the shared bound and
   // the wide merge (its rare fallback queries on the exact kernel); larger k or dim: the exact kernel.
+  // Rows wider than kMaxDp (up to kMaxChunkedDp) take the chunked form of the MFMA scan.
   const bool splittable = !indexed && f->n >= 2 * kMinSplitRows;
   const bool few = splittable && nq <= kFewMaxBatch && k <= (f->dim % 32 == 0 ? kFewMaxK : 64u) && f->dim >= 32 &&
                    f->dim <= kFewMaxDim;
   const bool split = splittable && !few && nq <= kSplitMaxQueries;
-  p.wide = !few && !split && shared_list_length(k) == 0 && k <= kWideMaxK && f->dp <= static_cast<uint32_t>(kMaxDp) &&
+  p.wide = !few && !split && shared_list_length(k) == 0 && k <= kWideMaxK && f->dp <= kMaxChunkedDp &&
            !indexed;
-  const bool exact_only = !few && !split && !p.wide && (shared_list_length(k) == 0 || f->dp > static_cast<uint32_t>(kMaxDp));
+  const bool exact_only = !few && !split && !p.wide && (shared_list_length(k) == 0 || f->dp > kMaxChunkedDp);
   p.path = few ? FlatPlan::kFew : split ? FlatPlan::kSplit : exact_only ? FlatPlan::kExactOnly : FlatPlan::kMfma;
   if (f->metric == QVH_METRIC_COSINE) p.stage = nq * f->dim * sizeof(float);
   p.q = nq * f->dp * sizeof(float);
@@ -1612,6 +1961,7 @@ void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const
   a.part_r = b.pr;
   a.qthr = b.thr;
   a.share = p.wide ? 0 : 1;
+  a.dp = f->dp;
   hipLaunchKernelGGL(fill_u32_kernel, dim3(static_cast<unsigned>(ceil_div(nq, 256))), dim3(256), 0, s,
                      a.qthr, nq, 0xFF800000u);  // ordered bits of +inf
   launch_scan(f->dp, p.kl, dim3(static_cast<unsigned>(p.qblocks * p.nsplit)), a, s);
@@ -1657,14 +2007,26 @@ void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const
     e.n = n_idx;
     e.bitmap = nullptr;
   }
+  // The first kFallbackSplitQueries listed queries run over row splits (a single work-group per
+  // query would read every row alone: 1024-d, 500k rows, three uncertified queries took 112 ms),
+  // into the scan's partial lists, which the merge has consumed; the rest one work-group each.
+  const uint32_t fsplit = fallback_splits(e.n, device_cus(f->device));
+  const size_t part_entries = static_cast<size_t>(nq) * 2 * p.nsplit * p.kl;
+  if (k <= 64 && fsplit >= 8 && static_cast<size_t>(kFallbackSplitQueries) * fsplit * k <= part_entries) {
+    ExactArgs es = e;
+    es.nsplit = fsplit;
+    es.nq = kFallbackSplitQueries;
+    es.rows_per_split = ceil_div(ceil_div(e.n, fsplit), kExactThreads) * kExactThreads;
+    es.out_rows = b.pr;
+    es.out_dist = b.pd;
+    launch_exact(es, kFallbackSplitQueries, s);
+    hipLaunchKernelGGL(flat_merge_select_kernel, dim3(kFallbackSplitQueries), dim3(1024), 0, s, b.pr, b.pd, fsplit, k,
+                       d_rows, d_dist, nullptr, fb + 1, fb);
+    QVH_HIP(hipGetLastError());
+    e.qskip = kFallbackSplitQueries;
+  }
   launch_exact(e, nq, s);
   if (f->timed) QVH_HIP(hipEventRecord(f->ev[3], s));
-}
-
-int device_cus(int device) {
-  int cus = 256;
-  (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
-  return cus;
 }
 
 /// A search on the handle's own workspace. d_idx as for flat_search_run.
@@ -1829,7 +2191,7 @@ qvh_status qvh_flat_search(qvh_flat* f, const float* queries, uint64_t nq, uint3
         if (w + 1 == words && f->n % 64) bits &= (1ull << (f->n % 64)) - 1;
         admitted += static_cast<uint64_t>(__builtin_popcountll(bits));
       }
-      if (shared_list_length(k) != 0 && f->dp <= static_cast<uint32_t>(kMaxDp) && 2 * admitted < f->n) {
+      if (shared_list_length(k) != 0 && f->dp <= kMaxChunkedDp && 2 * admitted < f->n) {
         listed.reserve(admitted);
         for (size_t w = 0; w < words; ++w) {
           uint64_t bits = row_bitmap[w];

@@ -97,16 +97,33 @@ def test_awkward_dimensions(oracle, dim):
         _check(oracle, base, q, 7, metric)
 
 
-@pytest.mark.parametrize("dim", [129, 200, 257, 1000])
-@pytest.mark.parametrize("metric", ["l2", "cosine"])
-def test_dimensions_above_the_mfma_width(oracle, dim, metric):
-    """dim > 128 takes the general exact kernel (distances computed in the reference's order)."""
+@pytest.mark.parametrize("dim", [129, 200, 257, 384, 768, 1000, 1024])
+@pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
+def test_dimensions_above_the_register_width(oracle, dim, metric):
+    """dim > 128: the chunked MFMA scan (32-dim chunks of rows and queries staged through LDS) over
+    20k rows in several splits; k = 10 with the shared bound, a 10% filter (listed rows), a 60%
+    filter (bitmap) and k = 40 (unshared lists, wide merge); the merge re-scores in the reference's
+    order, so distances are bit-identical."""
     rng = np.random.default_rng(dim)
-    base = rng.standard_normal((3_000, dim)).astype(np.float32)
-    q = rng.standard_normal((20, dim)).astype(np.float32)
+    base = rng.standard_normal((20_000, dim)).astype(np.float32)
+    q = rng.standard_normal((300, dim)).astype(np.float32)
     print(_check(oracle, base, q, 10, metric))
-    allowed = np.sort(rng.choice(3_000, 300, replace=False)).astype(np.uint64)
+    allowed = np.sort(rng.choice(20_000, 2_000, replace=False)).astype(np.uint64)
     print(_check(oracle, base, q, 7, metric, allowed))
+    allowed = np.sort(rng.choice(20_000, 12_000, replace=False)).astype(np.uint64)
+    print(_check(oracle, base, q[:100], 5, metric, allowed))
+    print(_check(oracle, base, q[:50], 40, metric))
+
+
+def test_wide_rows_integer_data_and_ties(oracle):
+    """Integer-valued 256-d rows with duplicated rows (exact ties resolve to the smaller row) on the
+    chunked scan, and a batch of 17 queries (just above the few-query kernel's batch limit)."""
+    rng = np.random.default_rng(77)
+    base = rng.integers(0, 16, (30_000, 256)).astype(np.float32)
+    base[15_000:15_500] = base[:500]
+    q = base[rng.choice(30_000, 400, replace=False)] + rng.integers(-1, 2, (400, 256)).astype(np.float32)
+    print(_check(oracle, base, q, 10, "l2"))
+    print(_check(oracle, base, q[:17], 10, "l2"))
 
 
 @pytest.mark.parametrize("k", [33, 64, 100, 256, 300, 1024])
@@ -347,6 +364,38 @@ def test_near_ties_within_rounding_fall_back_exactly(oracle, metric):
           assert_same_topk(got_l, got_d, rows.astype(np.int64), dist, _true_dist(oracle, base, q, metric)))
     if metric == "l2":
         assert 1 <= fallbacks <= 3, fallbacks  # query 0 (and nothing like the others)
+
+
+@pytest.mark.parametrize("dim", [64, 1024])
+@pytest.mark.parametrize("allowed_frac", [None, 0.3, 0.8])
+def test_many_uncertified_queries(oracle, dim, allowed_frac):
+    """20 queries, each with 40 planted rows at one true distance (as above), cannot be certified:
+    the first eight listed re-run over row splits with a select merge, the other twelve on one
+    work-group each; also under a 30% filter (listed rows) and an 80% filter (bitmap). Results
+    equal the oracle's."""
+    rng = np.random.default_rng(29 + dim)
+    n = 80_000 if dim == 64 else 40_000
+    base = (4.0 * rng.standard_normal((n, dim))).astype(np.float32)
+    q = (4.0 * rng.standard_normal((60, dim))).astype(np.float32)
+    for qi in range(20):
+        v = (0.7 * rng.standard_normal(dim)).astype(np.float32)
+        for i in range(40):
+            base[500 + 1_900 * qi + 37 * i] = q[qi] + v[rng.permutation(dim)]
+    allowed = None
+    if allowed_frac is not None:
+        allowed = np.sort(rng.choice(n, int(n * allowed_frac), replace=False)).astype(np.uint64)
+    print(f"case: uncertified dim={dim} allowed={allowed_frac}", flush=True)
+    idx = quiver.FlatIndex(dim, "l2")
+    idx.add(base)
+    got_l, got_d = idx.search(q, 10, filter=allowed)
+    fallbacks = Qvh().last_fallbacks(idx._index._device_handle)
+    bm = None if allowed is None else rows_bitmap(allowed.astype(np.int64), n)
+    rows, dist = oracle.flat_search(base, q, 10, "l2", bm)
+    exp_l = rows.astype(np.int64)
+    exp_l[rows == np.uint32(0xFFFFFFFF)] = -1
+    print("fallbacks", fallbacks, assert_same_topk(got_l, got_d, exp_l, dist, _true_dist(oracle, base, q, "l2")))
+    if allowed is None:
+        assert fallbacks >= 9, fallbacks
 
 
 def test_integer_rows_certify_exactly(oracle):
