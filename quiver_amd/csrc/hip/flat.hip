@@ -19,6 +19,8 @@
 #include <vector>
 #include <type_traits>
 
+#include <rocprim/device/device_segmented_radix_sort.hpp>
+
 #include "common.hpp"
 #include "exact.hpp"
 #include "select.hpp"
@@ -1544,6 +1546,95 @@ void launch_exact(const ExactArgs& a, uint64_t nq, hipStream_t s) {
   QVH_HIP(hipGetLastError());
 }
 
+// ---- k above kExactMaxK: score every admitted row, sort, keep k ------------------------------
+//
+// FlatIndex::search_batch for any k (src/flat_index.cc:84-107): every admitted row of a query is
+// scored in the reference's order, its (distance, row) keys sorted by a segmented radix sort and
+// the first k kept; rows not admitted get the largest key and come out as empty slots.
+constexpr uint64_t kSortMaxKeys = uint64_t{1} << 26;  // keys per pass (two 512 MiB key buffers)
+
+size_t sorted_scratch_bytes(uint64_t keys, uint32_t segments) {
+  size_t bytes = 0;
+  QVH_HIP(rocprim::segmented_radix_sort_keys(nullptr, bytes, static_cast<const uint64_t*>(nullptr),
+                                             static_cast<uint64_t*>(nullptr), static_cast<unsigned int>(keys),
+                                             segments, static_cast<const uint32_t*>(nullptr),
+                                             static_cast<const uint32_t*>(nullptr)));
+  return std::max<size_t>(bytes, 1);
+}
+
+/// keys[y][pos] for query q0 + y and position pos < n (rows, or listed rows idx[pos]).
+__global__ void sort_keys_kernel(ExactArgs a, uint32_t q0, uint64_t* __restrict__ keys) {
+  const uint64_t pos = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (pos >= a.n) return;
+  const uint32_t y = blockIdx.y;
+  uint64_t row = pos;
+  bool ok = true;
+  if (a.idx) {
+    row = a.idx[pos];
+  } else if (a.bitmap) {
+    ok = (a.bitmap[row >> 6] >> (row & 63)) & 1ull;
+  }
+  uint64_t key = ~0ull;
+  if (ok) {
+    const float d = exact_flat_distance(a.Q + static_cast<uint64_t>(q0 + y) * a.dp, a.X + row * a.dp, a.dim, a.l2 != 0);
+    key = make_key(d, static_cast<uint32_t>(pos));
+  }
+  keys[static_cast<uint64_t>(y) * a.n + pos] = key;
+}
+
+__global__ void sort_offsets_kernel(uint32_t* off, uint32_t segments, uint32_t n) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i <= segments) off[i] = i * n;
+}
+
+/// The first k sorted keys of query q0 + y as rows and distances (empty slots past the admitted).
+__global__ void sort_take_kernel(const uint64_t* __restrict__ keys, uint64_t n, uint32_t k, uint32_t q0,
+                                 const uint32_t* __restrict__ idx, uint32_t* __restrict__ out_rows,
+                                 float* __restrict__ out_dist) {
+  const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= k) return;
+  const uint32_t y = blockIdx.y;
+  const uint64_t key = j < n ? keys[static_cast<uint64_t>(y) * n + j] : ~0ull;
+  const uint64_t o = static_cast<uint64_t>(q0 + y) * k + j;
+  if (key == ~0ull) {
+    out_rows[o] = QVH_EMPTY_ROW;
+    out_dist[o] = __builtin_huge_valf();
+    return;
+  }
+  const uint32_t pos = static_cast<uint32_t>(key);
+  out_rows[o] = idx ? idx[pos] : pos;
+  out_dist[o] = ordered_to_float(static_cast<uint32_t>(key >> 32));
+}
+
+/// Workspace of run_sorted: keys [chunk][n] twice, chunk + 1 offsets, the sort's scratch.
+struct SortBuffers {
+  uint64_t chunk;
+  uint64_t* skin;
+  uint64_t* skout;
+  uint32_t* soff;
+  void* stmp;
+  size_t stmp_bytes;
+};
+
+void run_sorted(const SortBuffers& b, ExactArgs e, uint64_t nq, uint32_t k, hipStream_t s) {
+  const uint64_t n = e.n;
+  for (uint64_t q0 = 0; q0 < nq; q0 += b.chunk) {
+    const uint32_t nc = static_cast<uint32_t>(std::min<uint64_t>(b.chunk, nq - q0));
+    if (n > 0) {
+      hipLaunchKernelGGL(sort_keys_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256)), nc), dim3(256), 0, s, e,
+                         static_cast<uint32_t>(q0), b.skin);
+      hipLaunchKernelGGL(sort_offsets_kernel, dim3(static_cast<unsigned>(ceil_div(nc + 1, 256))), dim3(256), 0, s,
+                         b.soff, nc, static_cast<uint32_t>(n));
+      size_t bytes = b.stmp_bytes;
+      QVH_HIP(rocprim::segmented_radix_sort_keys(b.stmp, bytes, b.skin, b.skout, static_cast<unsigned int>(nc * n), nc,
+                                                 b.soff, b.soff + 1, 0, 64, s));
+    }
+    hipLaunchKernelGGL(sort_take_kernel, dim3(static_cast<unsigned>(ceil_div(k, 256)), nc), dim3(256), 0, s, b.skout, n,
+                       k, static_cast<uint32_t>(q0), e.idx, e.out_rows, e.out_dist);
+    QVH_HIP(hipGetLastError());
+  }
+}
+
 int device_cus(int device) {
   int cus = 256;
   (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
@@ -1662,6 +1753,7 @@ struct qvh_flat {
   std::mutex mu;
   // per-call workspace (grown on demand, serialized by mu)
   DeviceBuffer w_stage, w_q, w_qn, w_pd, w_pr, w_rows, w_dist, w_bits, w_thr, w_idx, w_fb, w_mflag, w_delta;
+  DeviceBuffer w_skin, w_skout, w_soff, w_stmp;  // k above kExactMaxK: sort keys and scratch
   // optional per-stage timing of the last search: events before prep, scan, merge and after
   bool timing = false;
   bool timed = false;
@@ -1702,7 +1794,7 @@ void flat_grow(qvh_flat* f, uint64_t need) {
 /// One search's path, launch geometry and workspace, decided on the host before anything is
 /// launched, so a caller with a fixed workspace can be refused up front.
 struct FlatPlan {
-  enum Path { kFew, kSplit, kExactOnly, kMfma } path = kMfma;
+  enum Path { kFew, kSplit, kExactOnly, kMfma, kSorted } path = kMfma;
   bool wide = false;
   int kl = 16;
   uint64_t g = 0, rps = 0;                       // few / split: row splits and rows per split
@@ -1711,11 +1803,14 @@ struct FlatPlan {
   uint64_t scan_rows = 0;
   // Bytes of each workspace buffer (0 = unused).
   size_t stage = 0, q = 0, qn = 0, delta = 0, pd = 0, pr = 0, thr = 0, fb = 0, mflag = 0;
+  // k above kExactMaxK: sort_chunk queries per pass; two key buffers, segment offsets, sort scratch.
+  uint64_t sort_chunk = 0;
+  size_t skeys = 0, soff = 0, stmp = 0;
 
   static size_t aligned(size_t b) { return (b + 255) / 256 * 256; }
   size_t total() const {
     return aligned(stage) + aligned(q) + aligned(qn) + aligned(delta) + aligned(pd) + aligned(pr) + aligned(thr) +
-           aligned(fb) + aligned(mflag);
+           aligned(fb) + aligned(mflag) + 2 * aligned(skeys) + aligned(soff) + aligned(stmp);
   }
 };
 
@@ -1730,15 +1825,30 @@ struct FlatBuffers {
   uint32_t* thr = nullptr;
   uint32_t* fb = nullptr;
   uint32_t* mflag = nullptr;
+  uint64_t* skin = nullptr;
+  uint64_t* skout = nullptr;
+  uint32_t* soff = nullptr;
+  void* stmp = nullptr;
 };
 
 /// d_idx (listed admitted rows) is in use when n_idx > 0 or `indexed`.
 FlatPlan plan_flat_search(const qvh_flat* f, uint64_t nq, uint32_t k, bool indexed, uint64_t n_idx, int cus) {
   QVH_REQUIRE(nq <= 0xFFFFFFFFull, "flat search: too many queries in one call");
-  if (k > kExactMaxK) {
-    throw Failure(QVH_EUNSUPPORTED, "flat search: k > " + std::to_string(kExactMaxK) + " is not supported on the device path");
-  }
   FlatPlan p;
+  if (k > kExactMaxK) {
+    // Every admitted row of a query scored exactly and the (distance, row) keys sorted: chunks of
+    // queries whose keys fit kSortMaxKeys.
+    p.path = FlatPlan::kSorted;
+    if (f->metric == QVH_METRIC_COSINE) p.stage = nq * f->dim * sizeof(float);
+    p.q = nq * f->dp * sizeof(float);
+    const uint64_t n_scan = std::max<uint64_t>(1, indexed ? n_idx : f->n);
+    QVH_REQUIRE(n_scan <= kSortMaxKeys, "flat search: too many rows for k above " + std::to_string(kExactMaxK));
+    p.sort_chunk = std::max<uint64_t>(1, std::min<uint64_t>(nq, kSortMaxKeys / n_scan));
+    p.skeys = p.sort_chunk * n_scan * sizeof(uint64_t);
+    p.soff = (p.sort_chunk + 1) * sizeof(uint32_t);
+    p.stmp = sorted_scratch_bytes(p.sort_chunk * n_scan, static_cast<uint32_t>(p.sort_chunk));
+    return p;
+  }
   // At most kFewMaxBatch queries with 32 <= dim <= kFewMaxDim and k <= kFewMaxK: the few-query
   // scan, kFewMaxQ queries per launch;
   // other batches of at most kSplitMaxQueries: the exact kernel over row splits. Otherwise k with a
@@ -1829,6 +1939,10 @@ FlatBuffers handle_buffers(qvh_flat* f, const FlatPlan& p) {
   b.thr = static_cast<uint32_t*>(take(f->w_thr, p.thr));
   b.fb = static_cast<uint32_t*>(take(f->w_fb, p.fb));
   b.mflag = static_cast<uint32_t*>(take(f->w_mflag, p.mflag));
+  b.skin = static_cast<uint64_t*>(take(f->w_skin, p.skeys));
+  b.skout = static_cast<uint64_t*>(take(f->w_skout, p.skeys));
+  b.soff = static_cast<uint32_t*>(take(f->w_soff, p.soff));
+  b.stmp = take(f->w_stmp, p.stmp);
   return b;
 }
 
@@ -1879,6 +1993,20 @@ void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const
   e.out_dist = d_dist;
   e.qlist = nullptr;
   e.qcount = nullptr;
+  if (p.path == FlatPlan::kSorted) {
+    if (d_idx) {
+      e.idx = d_idx;
+      e.n = n_idx;
+      e.bitmap = nullptr;
+    }
+    run_sorted(SortBuffers{p.sort_chunk, b.skin, b.skout, b.soff, b.stmp, p.stmp}, e, nq, k, s);
+    f->last_nsplit = 0;
+    if (f->timed) {
+      QVH_HIP(hipEventRecord(f->ev[2], s));
+      QVH_HIP(hipEventRecord(f->ev[3], s));
+    }
+    return;
+  }
   if (p.path == FlatPlan::kFew) {
     const bool l2 = f->metric == QVH_METRIC_L2;
     const dim3 grid(static_cast<unsigned>(p.g)), block(kFewThreads);
@@ -2313,6 +2441,10 @@ FlatBuffers scratch_buffers(unsigned char* base, const FlatPlan& p) {
   b.thr = static_cast<uint32_t*>(take(p.thr));
   b.fb = static_cast<uint32_t*>(take(p.fb));
   b.mflag = static_cast<uint32_t*>(take(p.mflag));
+  b.skin = static_cast<uint64_t*>(take(p.skeys));
+  b.skout = static_cast<uint64_t*>(take(p.skeys));
+  b.soff = static_cast<uint32_t*>(take(p.soff));
+  b.stmp = take(p.stmp);
   return b;
 }
 

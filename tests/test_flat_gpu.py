@@ -161,11 +161,17 @@ def test_large_k_crowded_lists_fall_back_exactly(oracle, metric):
     assert Qvh().last_fallbacks(idx._index._device_handle) == 0  # no crowded query: no fallback
 
 
-def test_k_above_the_device_limit_is_rejected():
-    idx = quiver.FlatIndex(8)
-    idx.add(np.random.default_rng(0).standard_normal((100, 8)).astype(np.float32))
-    with pytest.raises(ValueError, match="k > 1024"):
-        idx.search(np.zeros((1, 8), np.float32), 1025)
+@pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
+def test_k_above_1024_sorts_every_row(oracle, metric):
+    """k above 1024 (the reference has no limit, src/flat_index.cc:84-107): every admitted row is
+    scored and the keys sorted on the device. Integer mixture (many exact ties, resolved by row),
+    k = 1025 and 5000, a 10% filter (listed rows), a 70% filter (bitmap), and k above the row
+    count (empty slots)."""
+    base, q = D.int_mix(20_000, 12)
+    print(_check(oracle, base, q, 1025, metric))
+    print(_check(oracle, base, q[:3], 5000, metric, D.allowed_ids(base.shape[0], 0.1, seed=4)))
+    print(_check(oracle, base, q[:3], 2000, metric, D.allowed_ids(base.shape[0], 0.7, seed=6)))
+    print(_check(oracle, base[:3000], q[:2], 4000, metric))
 
 
 @pytest.mark.parametrize("k", [1, 2, 10, 16, 17, 32])
