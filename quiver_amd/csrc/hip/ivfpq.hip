@@ -849,9 +849,11 @@ __global__ void __launch_bounds__(256) probe_select_any_kernel(const float* __re
 // ---- search: the scan ---------------------------------------------------------------------------
 
 constexpr int kScanThreads = 256;
-constexpr int kCandCap = 2048;       // LDS candidate buffer (u64 keys)
+constexpr int kCandCap = 2048;       // LDS candidate buffer (u64 keys) for keep_sel <= kMaxKeepSel
 constexpr int kScanRound = 4;        // codes per thread between buffer checks
 constexpr uint32_t kMaxKeepSel = kCandCap - kScanThreads * kScanRound;  // 1024
+// Larger selections take a larger buffer: keep_sel + kScanThreads * kScanRound slots, rounded up to
+// a power of two, as far as LDS allows.
 
 // Scan order of the queries. Queries whose probe sets overlap read the same lists; run next to each
 // other, they find those lists in L2. Each query is keyed by the smallest list id it probes (a
@@ -906,6 +908,7 @@ struct ScanArgs {
   const float* vec;        // [count][dim] or null
   const uint64_t* bitmap;  // admitted positions, or null
   uint32_t keep, keep_sel;
+  uint32_t cand_cap;  // block-buffer scan: LDS candidate slots (a power of two, >= kCandCap)
   int refine;
   int exact_all;  // block-buffer scan: exact distances of every probed vector (saturated refine)
   uint64_t* out_refs;
@@ -1046,8 +1049,8 @@ __device__ __forceinline__ float adc_sum_rows(const float* lut, const uint32_t (
 template <int MPW>
 __device__ void ivf_scan_query(const ScanArgs& a, const uint32_t q) {
   extern __shared__ __attribute__((aligned(16))) unsigned char s_raw[];
-  uint64_t* s_cand = reinterpret_cast<uint64_t*>(s_raw);                       // [kCandCap]
-  uint64_t* s_pstart = s_cand + kCandCap;                                      // [nprobe + 1] flattened starts
+  uint64_t* s_cand = reinterpret_cast<uint64_t*>(s_raw);                       // [cand_cap]
+  uint64_t* s_pstart = s_cand + a.cand_cap;                                    // [nprobe + 1] flattened starts
   uint32_t* s_plist = reinterpret_cast<uint32_t*>(s_pstart + a.nprobe + 1);    // [nprobe]
   float* s_lut = reinterpret_cast<float*>(s_plist + ((a.nprobe + 1) & ~1u));  // [m][256]
   __shared__ uint32_t s_count;
@@ -1090,7 +1093,7 @@ __device__ void ivf_scan_query(const ScanArgs& a, const uint32_t q) {
   // Keeps the keep_sel smallest keys of the buffer and tightens the append threshold.
   auto compact = [&]() {
     __syncthreads();
-    const uint32_t cnt = min(s_count, static_cast<uint32_t>(kCandCap));
+    const uint32_t cnt = min(s_count, a.cand_cap);
     const uint32_t n2 = pow2_at_least(max(cnt, 2u));
     for (uint32_t i = cnt + tid; i < n2; i += kScanThreads) s_cand[i] = ~0ull;
     block_sort_u64(s_cand, n2);
@@ -1107,7 +1110,7 @@ __device__ void ivf_scan_query(const ScanArgs& a, const uint32_t q) {
     const uint64_t key = make_key(dist, static_cast<uint32_t>(pos));
     if (key < s_thr) {
       const uint32_t slot = atomicAdd(&s_count, 1u);
-      if (slot < kCandCap) s_cand[slot] = key;
+      if (slot < a.cand_cap) s_cand[slot] = key;
     }
   };
 
@@ -1157,7 +1160,7 @@ __device__ void ivf_scan_query(const ScanArgs& a, const uint32_t q) {
         }
       }
       __syncthreads();
-      if (s_count + kScanThreads * kScanRound > kCandCap) compact();
+      if (s_count + kScanThreads * kScanRound > a.cand_cap) compact();
     }
   } else {
     // L2 without the precomputed table: a residual table per list (src/ivfpq_index.cc:338-342).
@@ -1194,7 +1197,7 @@ __device__ void ivf_scan_query(const ScanArgs& a, const uint32_t q) {
           }
         }
         __syncthreads();
-        if (s_count + kScanThreads * kScanRound > kCandCap) compact();
+        if (s_count + kScanThreads * kScanRound > a.cand_cap) compact();
       }
     }
   }
@@ -2426,10 +2429,12 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
     keep = std::min<uint64_t>(k, count);
     keep_sel = keep;
   }
-  if (keep_sel > kMaxKeepSel) {
-    throw Failure(QVH_EUNSUPPORTED, "IVF-PQ search: k * refine_factor above " + std::to_string(kMaxKeepSel) +
-                                        " candidates is not supported on the device path yet");
+  if (keep_sel > (uint64_t{1} << 20)) {
+    throw Failure(QVH_EUNSUPPORTED, "IVF-PQ search: " + std::to_string(keep_sel) +
+                                        " candidates (k * refine_factor) exceed the on-chip candidate buffer");
   }
+  uint32_t cand_cap = kCandCap;
+  while (cand_cap < keep_sel + kScanThreads * kScanRound) cand_cap *= 2;
   QVH_REQUIRE(h->count < 0xFFFFFFFFull, "IVF-PQ device path holds fewer than 2^32 vectors");
   if (h->timed) QVH_HIP(hipEventRecord(h->ev[0], s));
   // prepared queries
@@ -2525,9 +2530,14 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   a.exact_all = exact_all ? 1 : 0;
   a.out_refs = d_refs;
   a.out_dist = d_dist;
-  const size_t lds = kCandCap * sizeof(uint64_t) + (nprobe + 1) * sizeof(uint64_t) +
+  a.cand_cap = cand_cap;
+  const size_t lds = static_cast<size_t>(cand_cap) * sizeof(uint64_t) + (nprobe + 1) * sizeof(uint64_t) +
                      ((nprobe + 1) & ~1u) * sizeof(uint32_t) + static_cast<size_t>(h->m) * 256 * sizeof(float);
-  QVH_REQUIRE(lds <= 150 * 1024, "IVF-PQ search: m and nprobe too large for the on-chip tables");
+  if (lds > 150 * 1024) {
+    throw Failure(QVH_EUNSUPPORTED, "IVF-PQ search: " + std::to_string(keep_sel) + " candidates (k * refine_factor) with m = " +
+                                        std::to_string(h->m) + " and nprobe = " + std::to_string(nprobe) +
+                                        " exceed the on-chip candidate buffer");
+  }
   const dim3 grid(static_cast<unsigned>(nq));
   const uint32_t mpw = h->mp / 4;
   // The block-buffer scan (every table mode, any candidate count up to kMaxKeepSel).

@@ -170,6 +170,19 @@ def test_ivfpq_large_candidate_sets(oracle, metric, k, refine):
         print(k, refine, qs.shape[0], compare_search(oracle, idx, st, qs, k, 16, refine))
 
 
+@pytest.mark.parametrize("metric,k,refine", [("l2", 1000, 0), ("ip", 2000, 0), ("l2", 100, 16), ("cosine", 50, 40),
+                                             ("l2", 3000, 2)])
+def test_ivfpq_candidate_sets_above_1024(oracle, metric, k, refine):
+    """k * refine_factor (plus the L2 re-score margin) above 1024 (the reference has no limit,
+    src/ivfpq_index.cc:303-308): the block-buffer scan with an LDS candidate buffer sized to the
+    selection; equal to the oracle, also for k above the probed count (empty slots)."""
+    base = clustered(30_000, 32, 24, seed=43)
+    q = clustered(40, 32, 24, seed=44)
+    idx, st = build_pair(oracle, base, metric, 64, 8, refine > 0)
+    print(k, refine, compare_search(oracle, idx, st, q, k, 32, refine))
+    print(k, refine, "nprobe 2", compare_search(oracle, idx, st, q[:5], k, 2, refine))
+
+
 @pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
 def test_ivfpq_saturated_refine(oracle, metric):
     """refine_factor 2^63: k * refine_factor wraps, the reference saturates it at the stored count and
