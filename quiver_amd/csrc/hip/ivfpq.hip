@@ -2692,8 +2692,8 @@ qvh_status qvh_ivfpq_create(uint32_t dim, int metric, uint32_t nlist, uint32_t m
     QVH_REQUIRE(metric >= QVH_METRIC_L2 && metric <= QVH_METRIC_COSINE, "unknown metric");
     QVH_REQUIRE(nlist >= 1 && nlist <= (1u << 24), "nlist must be in [1, 2^24]");
     QVH_REQUIRE(m >= 1 && dim % m == 0, "PQ: dimension must be divisible by m");
-    if (dim > 2048 || m > 128) {
-      throw Failure(QVH_EUNSUPPORTED, "IVF-PQ device path supports dim <= 2048 and m <= 128");
+    if (m > 128) {  // the scan's per-query table, m x 256 floats, lives in LDS
+      throw Failure(QVH_EUNSUPPORTED, "IVF-PQ device path supports m <= 128");
     }
     const int dev = current_device();
     auto* h = new qvh_ivfpq;

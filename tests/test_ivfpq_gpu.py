@@ -183,6 +183,16 @@ def test_ivfpq_candidate_sets_above_1024(oracle, metric, k, refine):
     print(k, refine, "nprobe 2", compare_search(oracle, idx, st, q[:5], k, 2, refine))
 
 
+@pytest.mark.parametrize("metric,dim,m", [("l2", 3072, 96), ("cosine", 4096, 128), ("ip", 2560, 64)])
+def test_ivfpq_wide_vectors(oracle, metric, dim, m):
+    """Vectors wider than 2048 dims (the reference has no limit): training, encoding and search
+    (residual and precomputed tables, refine) equal to the oracle."""
+    base = clustered(3_000, dim, 12, seed=45)
+    q = clustered(30, dim, 12, seed=46)
+    idx, st = build_pair(oracle, base, metric, 16, m, metric != "ip", iters=4)
+    print(compare_search(oracle, idx, st, q, 10, 8, 2 if metric != "ip" else 0))
+
+
 @pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
 def test_ivfpq_saturated_refine(oracle, metric):
     """refine_factor 2^63: k * refine_factor wraps, the reference saturates it at the stored count and
