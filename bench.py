@@ -13,8 +13,9 @@ resident in HBM):
 
 Prints ONE JSON line. `value` is the flat workload's queries per second (query prep + fused MFMA
 scan + merge/exact re-score), timed over K steps with the device synchronized on both sides;
-the "ivfpq" object carries the same fields for the IVF-PQ workload, and "flat_small_batches" the
-flat search time of one and of eight of the same queries. `roofline` is each
+the "ivfpq" object carries the same fields for the IVF-PQ workload, "flat_small_batches" the
+flat search time of one and of eight of the same queries, and "flat_wide_rows" a 500,000 x 768
+flat search (the chunked MFMA scan for rows wider than 128). `roofline` is each
 workload's dominant kernel measured with HIP events on the stream it runs on: the flat scan's
 algorithmic 2*n*d*nq FLOP per launch against the dense FP32 matrix peak (157.3 TFLOP/s), the
 IVF-PQ list scan's algorithmic code bytes (sum over queries and probed lists of len * m) against
@@ -415,6 +416,45 @@ def bench_flat_filtered(args, qvh: Qvh):
             "filters": out}
 
 
+def bench_flat_wide(args, hip: Hip, qvh: Qvh):
+    """Rows wider than the register-resident scan (the chunked MFMA scan): 500,000 x 768 N(0,1)
+    fp32, L2, k=10, 10,000 queries, device-resident, median of 3 after one warm-up."""
+    n, dim, nq, k = 500_000, 768, 10_000, 10
+    rng = np.random.default_rng(768)
+    base = rng.standard_normal((n, dim), dtype=np.float32)
+    queries = rng.standard_normal((nq, dim), dtype=np.float32)
+    h = C.c_void_p()
+    qvh.check(qvh.lib.qvh_flat_create(dim, 0, C.byref(h)), "create")
+    qvh.check(qvh.lib.qvh_flat_append(h, base.ctypes.data_as(C.c_void_p), n, None), "append")
+    del base
+    d_q = hip.malloc(queries.nbytes)
+    hip.h2d(d_q, queries)
+    d_rows = hip.malloc(nq * k * 4)
+    d_dist = hip.malloc(nq * k * 4)
+    qvh.check(qvh.lib.qvh_flat_set_timing(h, 1), "timing")
+    stages, walls = [], []
+    for i in range(4):
+        t0 = time.perf_counter()
+        qvh.check(qvh.lib.qvh_flat_search_device(h, d_q, nq, k, None, d_rows, d_dist, None), "search")
+        qvh.check(qvh.lib.qvh_flat_sync(h), "sync")
+        wall = time.perf_counter() - t0
+        p_, s_, m_, ns = C.c_float(), C.c_float(), C.c_float(), C.c_uint32()
+        qvh.check(qvh.lib.qvh_flat_last_timing(h, C.byref(p_), C.byref(s_), C.byref(m_), C.byref(ns)), "timing")
+        if i:
+            stages.append((p_.value, s_.value, m_.value))
+            walls.append(wall)
+    qvh.check(qvh.lib.qvh_flat_destroy(h), "destroy")
+    for ptr in (d_q, d_rows, d_dist):
+        hip.lib.hipFree(ptr)
+    st = np.median(np.array(stages), axis=0)
+    tflops = 2.0 * n * dim * nq / (st[1] * 1e-3) / 1e12
+    return {"config": {"workload": "flat exact L2 k=10: 500,000 x 768 N(0,1) fp32, 10,000 queries batched (chunked "
+                                   "MFMA scan)", "n": n, "dim": dim, "nq": nq, "k": k},
+            "qps": nq / float(np.median(walls)),
+            "stage_ms": {"prep": float(st[0]), "scan": float(st[1]), "merge": float(st[2])},
+            "scan_tflops": tflops, "frac_of_fp32_mfma_peak": tflops / FP32_MFMA_PEAK_TFLOPS}
+
+
 def bench_ivfpq_cosine_refine(args, hip: Hip, qvh: Qvh):
     """IVF-PQ cosine with exact re-ranking on the same 1,183,514 x 100 set: nlist 2048, m 25,
     stored vectors, refine_factor 8 (80 candidates re-ranked), k=10, nprobe 16 and 64."""
@@ -563,6 +603,7 @@ def main():
     if not args.no_extra:
         extra["flat_small_batches"] = flat["small_batches"]
         extra["flat_cosine_filtered"] = bench_flat_filtered(args, qvh)
+        extra["flat_wide_rows"] = bench_flat_wide(args, hip, qvh)
         extra["ivfpq_cosine_refine"] = bench_ivfpq_cosine_refine(args, hip, qvh)
     cpu = None
     ivf["cpu_baseline"] = None

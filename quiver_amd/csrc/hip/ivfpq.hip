@@ -154,18 +154,17 @@ __global__ void __launch_bounds__(kNearThreads) nearest_kernel(NearestArgs a) {
 // CentroidTable::nearest_batch (src/internal/centroid_table.h:94-144) for many points: the matrix
 // unit computes g_c = ||c||^2 - 2<x,c> (or -<x,c>) for every centroid, the point entering as the
 // B operand scaled by -2 (or -1, both exact) and one more MFMA step adding the augmented column
-// (||c||^2, or 0; +inf for padding rows). Each point keeps its smallest g (first index on ties) and
-// the second smallest g over the other centroids. With |g_c - e_c| <= delta for the reference's
-// in-order value e_c, only centroids with g_c <= best + 2 * delta can be the reference's answer
-// (any other c has e_c >= g_c - delta > best + delta >= e_best). Each point keeps its kAsgList
-// smallest (g, c); when the last of them lies above that band, the band's members are all in the
-// list: one member is the answer, and two or more are re-scored in the reference's own order and
-// arithmetic. A list whose last entry is inside the band leaves the point to the exact kernel.
-// Candidates above the running best + 2 delta are not kept: they cannot be in the final band. delta = (4(dp + 1) + 16) u (P + R)^2 for L2 and (...) u P R for the
-// inner product, P = ||x||, R = the largest ||c||: the bound on two differently ordered float sums
-// of terms whose absolute values add up to at most (P + R)^2 (resp. P R), with a factor of two over
-// the derivation for the norms' own rounding and a faithfully rounding matrix unit.
-// (1M int-mixture points against 2048 centroids: 11% have two centroids in the band, 0.4% four.)
+// (||c||^2, or 0; +inf for padding rows). With |g_c - e_c| <= delta for the reference's in-order
+// value e_c, only centroids with g_c <= best + 2 delta can be the reference's answer (any other c
+// has e_c >= g_c - delta > best + delta >= e_best). Each point keeps its kAsgList smallest (g, c),
+// admitting only candidates within 2 delta of its running best (the best only decreases, so the
+// others cannot join the final band). When the list's last entry lies above the band, the band's
+// members are all in the list: a single member is the answer, and two or more are re-scored in the
+// reference's own order and arithmetic. A list whose last entry is inside the band leaves the point
+// to the exact kernel. delta = (4(dp + 1) + 16) u (P + R)^2 for L2 and (4(dp + 1) + 16) u P R for
+// the inner product, P = ||x||, R = the largest ||c||: the bound on two differently ordered float
+// sums of terms whose absolute values add up to at most (P + R)^2 (resp. P R), with a factor of two
+// over the derivation for the norms' own rounding and a faithfully rounding matrix unit.
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -177,7 +176,7 @@ constexpr int kAsgTile = 64;      // centroid rows per LDS tile
 constexpr uint32_t kAsgMaxDp = 128;
 constexpr uint32_t kAsgMinDim = 32;
 constexpr uint64_t kAsgMinPoints = 1024;  // smaller batches stay on the exact kernel
-constexpr int kAsgList = 4;                // (g, c) kept per point
+constexpr int kAsgList = 8;                // (g, c) kept per point
 
 /// Inserts (g, c) into the ascending (g, c)-ordered list, dropping the last.
 template <int L>
@@ -362,7 +361,11 @@ __global__ void __launch_bounds__(kAsgThreads) assign_mfma_kernel(AssignArgs a) 
   constexpr float kUnscale = L2 ? -0.5f : -1.0f;
   float be = __builtin_huge_valf();
   uint32_t bc = 0xFFFFFFFFu;
-  const int nband = !listed ? 0 : !(lg[1] <= band) ? 1 : !(lg[2] <= band) ? 2 : 3;
+  int nband = 0;
+  if (listed) {
+#pragma unroll
+    for (int i = 0; i < kAsgList - 1; ++i) nband += lg[i] <= band ? 1 : 0;
+  }
   for (int i = 0; i < kAsgList - 1; ++i) {
     if (nband < 2 || i >= nband) break;
     const uint32_t c = lc[i];
