@@ -207,7 +207,7 @@ qvh_status qvh_ivfpq_sync(qvh_ivfpq* ivf);
 qvh_status qvh_ivfpq_last_fallbacks(qvh_ivfpq* ivf, uint32_t* count);
 /* Measurement hook (no counterpart in the reference). Level 1: HIP events around the probe
  * selection (query prep, coarse scores, top-nprobe, the ranking certificate's bounds) and the list
- * scan of each search (the scan kernel and, with refine, the re-ranking kernel; not the rescan of
+ * scan of each search (the scan kernel, which also re-ranks with refine; not the rescan of
  * uncertified queries that follows). Level 2
  * adds, after the scan, a count of the PQ code bytes the scan had to read (sum over queries and
  * probed lists of len * m), which qvh_ivfpq_last_timing returns in code_bytes (nullable). */

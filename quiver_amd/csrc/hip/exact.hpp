@@ -92,6 +92,55 @@ __device__ inline float exact_dot(const float* __restrict__ a, const float* __re
   return sum;
 }
 
+/// exact_l2sqr (L2) or exact_dot of one pair by an aligned group of eight lanes, bit for bit: lane l
+/// of the group holds lane l of the four 8-lane accumulators, the horizontal sum takes the same
+/// association through lane exchanges inside the group, and lane 0 of the group adds the scalar
+/// tail and returns the sum (the other lanes' results are meaningless). Every lane of the wave must
+/// call it together; lanes with valid == false read nothing.
+template <bool L2>
+__device__ inline float exact_group8(const float* __restrict__ a, const float* __restrict__ b, uint32_t dim,
+                                     bool valid) {
+  const uint32_t l = threadIdx.x & 7u;
+  auto term = [](float x, float y, float s) {
+    if constexpr (L2) {
+      const float d = x - y;
+      return fmaf(d, d, s);
+    } else {
+      return fmaf(x, y, s);
+    }
+  };
+  float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+  const uint32_t n8 = dim / 8 * 8;  // where the 32- and 8-element loops of exact_l2sqr stop
+  if (valid) {
+    uint32_t i = 0;
+    for (; i + 32 <= dim; i += 32) {
+      s0 = term(a[i + l], b[i + l], s0);
+      s1 = term(a[i + 8 + l], b[i + 8 + l], s1);
+      s2 = term(a[i + 16 + l], b[i + 16 + l], s2);
+      s3 = term(a[i + 24 + l], b[i + 24 + l], s3);
+    }
+    for (; i < n8; i += 8) s0 = term(a[i + l], b[i + l], s0);
+  }
+  const float v = (s0 + s1) + (s2 + s3);      // v[l]
+  const float lo = v + __shfl_down(v, 4, 8);  // lo[j] = v[j] + v[j + 4] on lanes 0..3
+  const float t = lo + __shfl_xor(lo, 1, 8);  // lo0 + lo1 on lane 0, lo2 + lo3 on lane 2
+  float sum = t + __shfl_xor(t, 2, 8);        // (lo0 + lo1) + (lo2 + lo3) on lane 0
+  if (valid && l == 0) {
+    uint32_t i = n8;
+    const uint32_t v4 = i + (dim - i) / 4 * 4;
+    for (; i < v4; ++i) {
+      if constexpr (L2) {
+        const float d = a[i] - b[i];
+        sum = sum + d * d;
+      } else {
+        sum = sum + a[i] * b[i];
+      }
+    }
+    for (; i < dim; ++i) sum = term(a[i], b[i], sum);
+  }
+  return sum;
+}
+
 /// simd::normalize (src/simd/dispatch.cc:119-135) of one row in place.
 __device__ inline void exact_normalize(float* v, uint32_t dim) {
   const float norm_sq = exact_dot(v, v, dim);

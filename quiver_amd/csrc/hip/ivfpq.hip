@@ -916,8 +916,6 @@ struct ScanArgs {
   int exact_all;  // block-buffer scan: exact distances of every probed vector (saturated refine)
   uint64_t* out_refs;
   float* out_dist;
-  uint64_t* sel;      // [nq][keep_sel] streaming scan -> finishing kernel
-  uint32_t* sel_cnt;  // [nq]
   const uint32_t* order;  // [nq] block -> query of the streaming scan, or null
   // Sliced queries of the streaming scan: blocks [0, nwhole) scan one query each; the rest scan
   // one of `parts` slices of a query's probed codes and leave their best keep keys in part_keys;
@@ -1011,24 +1009,42 @@ __device__ __forceinline__ float adc_sum(const float* lut, const uint32_t (&w)[M
   return s;
 }
 
-/// Code bytes of position pos as MPW dwords: whole 16-byte loads when the code fills all of them
-/// (FULL), else dword loads of the mp bytes and zeros after them.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+/// Code bytes of position pos as MPW dwords. FULL (mp == 4 * MPW): the code in 16-byte pieces and
+/// one 4-, 8- or 12-byte tail, each a single load (rows are only 4-byte aligned when mp is not a
+/// multiple of 16, and gfx950's global loads take any width at 4-byte alignment: a 28-byte code is
+/// two loads rather than seven). Otherwise dword loads of the mp bytes and zeros after them.
 template <int MPW, bool FULL>
 __device__ __forceinline__ void load_code_padded(const uint8_t* codes, uint64_t pos, uint32_t mp, uint32_t (&w)[MPW]) {
   const uint32_t* p = reinterpret_cast<const uint32_t*>(codes + pos * mp);
-  if constexpr (FULL && MPW % 4 == 0) {
+  if constexpr (FULL) {
+    constexpr int kTail = MPW % 4, kHead = MPW - kTail;
 #pragma unroll
-    for (int i = 0; i < MPW; i += 4) {
-      const uint4 v = *reinterpret_cast<const uint4*>(p + i);
+    for (int i = 0; i < kHead; i += 4) {
+      u32x4 v;
+      __builtin_memcpy(&v, p + i, sizeof(v));
       w[i] = v.x;
       w[i + 1] = v.y;
       w[i + 2] = v.z;
       w[i + 3] = v.w;
     }
-  } else if constexpr (FULL && MPW == 2) {
-    const uint2 v = *reinterpret_cast<const uint2*>(p);
-    w[0] = v.x;
-    w[1] = v.y;
+    if constexpr (kTail == 3) {
+      u32x3 v;
+      __builtin_memcpy(&v, p + kHead, sizeof(v));
+      w[kHead] = v.x;
+      w[kHead + 1] = v.y;
+      w[kHead + 2] = v.z;
+    } else if constexpr (kTail == 2) {
+      u32x2 v;
+      __builtin_memcpy(&v, p + kHead, sizeof(v));
+      w[kHead] = v.x;
+      w[kHead + 1] = v.y;
+    } else if constexpr (kTail == 1) {
+      w[kHead] = p[kHead];
+    }
   } else {
 #pragma unroll
     for (int i = 0; i < MPW; ++i) w[i] = 4 * i < static_cast<int>(mp) ? p[i] : 0u;
@@ -1303,8 +1319,9 @@ __global__ void __launch_bounds__(kScanThreads) ivf_scan_kernel(ScanArgs a) {
 // Candidates below the query's running threshold go to a queue private to their wave (no block
 // barrier and no atomics on the append path); a full queue is sorted inside the wave and cut to
 // keep_sel, and its keep_sel-th key tightens the threshold shared by the eight waves (each such key
-// bounds the query's final keep_sel-th key from above). At the end the eight lists are sorted
-// together and the keep_sel best go to the finishing kernel, which re-scores them exactly.
+// bounds the query's final keep_sel-th key from above). At the end the wave lists are merged and
+// the keep_sel best re-scored exactly (L2 with the precomputed table) and re-ranked against the
+// stored vectors (refine) before the block writes the query's results.
 
 #ifndef QVH_STREAM_ROT
 #define QVH_STREAM_ROT 0
@@ -1316,7 +1333,6 @@ template <int CAP>
 constexpr int stream_waves() { return CAP == 128 ? 4 : 8; }
 constexpr uint32_t kStreamMaxProbes = 256;
 constexpr uint32_t kStreamMaxSel = 256;
-constexpr int kFinishThreads = 128;
 constexpr uint32_t kStreamMaxM = 64;  // code bytes of the widest streaming kernel
 // Slices per query of a batch smaller than one resident generation of blocks.
 constexpr uint64_t kMaxSlices = 16;
@@ -1813,11 +1829,13 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
     load_code<MPW>(a.codes, pos, a.mp, wc);  // in flight during the list search
     const uint32_t pl = list_of(pos);
     const float* pre = a.pre + static_cast<uint64_t>(s_list[pl]) * m * 256;
-    // All 4 * MPW table loads go out together (rows past m re-read row m - 1 and are not added).
+    // All 4 * MPW table loads go out together. Rows past m (whole code dwords still carry up to three
+    // pad bytes when m is not a multiple of four) re-read row m - 1 and are not added: the list's
+    // table has exactly m rows, the next list's follow it.
     float pv[4 * MPW];
 #pragma unroll
     for (int j = 0; j < 4 * MPW; ++j) {
-      const int jr = FULL ? j : min(j, static_cast<int>(m) - 1);
+      const int jr = min(j, static_cast<int>(m) - 1);
       const uint32_t c = (wc[j >> 2] >> (8 * (j & 3))) & 0xFFu;
       pv[j] = pre[jr * 256 + c];
     }
@@ -1825,11 +1843,18 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
 #pragma unroll
     for (int j = 0; j < 4 * MPW; ++j) {
       const uint32_t c = (wc[j >> 2] >> (8 * (j & 3))) & 0xFFu;
-      if (FULL || j < static_cast<int>(m)) sum = sum + (pv[j] + s_lut[ROT ? c * kRows + j : j * 256 + c]);
+      if (j < static_cast<int>(m)) sum = sum + (pv[j] + s_lut[ROT ? c * kRows + j : j * 256 + c]);
     }
     float d = s_score[pl] + sum;
     d = d == d ? d : __builtin_huge_valf();
     return make_key(d, pos);
+  };
+  // Re-ranking key of a candidate (refine): its exact distance to the stored vector, summed in the
+  // reference's order (src/ivfpq_index.cc:139-142,363-373).
+  auto refine_key = [&](uint32_t pos) -> uint64_t {
+    const float* x = a.vec + static_cast<uint64_t>(pos) * a.dim;
+    const float e = l2 ? exact_l2sqr(qv, x, a.dim) : 1.0f - exact_dot(qv, x, a.dim);
+    return make_key(e, pos);
   };
   // Result j of the query: the list ref and distance of `key`, or an empty slot.
   auto emit = [&](uint32_t j, bool full_slot, uint64_t key) {
@@ -1941,13 +1966,13 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
       if (lane == 0) __hip_atomic_store(&a.part_done[tq], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     // An uncertified query is recomputed by the block-buffer scan with exact sums, which runs after
-    // this kernel (and the finishing kernel) and overwrites its results.
+    // this kernel and overwrites its results.
     if (!certified && lane == 0) a.fallback[atomicAdd(a.nfallback, 1u)] = q;
     if (a.refine) {
-      // Exact re-ranking needs the stored vectors: hand the candidates to the finishing kernel.
-      if (static_cast<uint32_t>(lane) < cnt_f) a.sel[static_cast<uint64_t>(q) * a.keep_sel + lane] = key;
-      if (lane == 0) a.sel_cnt[q] = cnt_f;
-      return;
+      // One candidate per lane, then a register sort by the exact distance.
+      uint64_t t[1] = {static_cast<uint32_t>(lane) < cnt_f ? refine_key(static_cast<uint32_t>(key)) : ~0ull};
+      wave_sort<1>(t);
+      key = t[0];
     }
     if (static_cast<uint32_t>(lane) < a.k) emit(lane, static_cast<uint32_t>(lane) < min(cnt_f, a.k), key);
     return;
@@ -1990,6 +2015,29 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
   }
   uint32_t cnt_f = min(merged, keep_sel);
   bool certified = true;
+  // Sorts s_queue[0, count) (count <= 256) ascending in wave 0's registers (no block barriers inside
+  // the sort); slots past count read as empty. The block waits before and after.
+  auto sort_front = [&](uint32_t count) {
+    __syncthreads();
+    if (wave == 0) {
+      if (count <= 128) {
+        uint64_t t[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) t[i] = static_cast<uint32_t>(i * 64 + lane) < count ? s_queue[i * 64 + lane] : ~0ull;
+        wave_sort<2>(t);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) s_queue[i * 64 + lane] = t[i];
+      } else {
+        uint64_t t[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) t[i] = static_cast<uint32_t>(i * 64 + lane) < count ? s_queue[i * 64 + lane] : ~0ull;
+        wave_sort<4>(t);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s_queue[i * 64 + lane] = t[i];
+      }
+    }
+    __syncthreads();
+  };
 
   // Exact re-score of the approximate ranking (L2 with the precomputed table): the reference's
   // table entry pre + qtab, summed in order of j, plus ||q - c||^2 (src/ivfpq_index.cc:334-346).
@@ -1997,24 +2045,7 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
     const uint64_t last = s_queue[cnt_f > 0 ? cnt_f - 1 : 0];
     __syncthreads();
     if (static_cast<uint32_t>(tid) < cnt_f) s_queue[tid] = rescore(s_queue[tid]);
-    const uint32_t n2 = pow2_at_least(max(cnt_f, 2u));
-    if (static_cast<uint32_t>(tid) >= cnt_f && static_cast<uint32_t>(tid) < n2) s_queue[tid] = ~0ull;
-    for (uint32_t size = 2; size <= n2; size <<= 1) {
-      for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-        __syncthreads();
-        for (uint32_t i = tid; i < n2 / 2; i += kStreamThreads) {
-          const uint32_t lo = 2 * i - (i & (stride - 1));
-          const uint32_t hi = lo + stride;
-          const bool up = (lo & size) == 0;
-          const uint64_t x = s_queue[lo], y = s_queue[hi];
-          if ((x > y) == up) {
-            s_queue[lo] = y;
-            s_queue[hi] = x;
-          }
-        }
-      }
-    }
-    __syncthreads();
+    sort_front(cnt_f);
     cnt_f = min(cnt_f, a.keep);
     const uint64_t kth = s_queue[cnt_f > 0 ? cnt_f - 1 : 0];
     const bool complete = merged <= keep_sel && s_thr == 0xFFFFFFFFu;
@@ -2080,13 +2111,22 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
     if (tid == 0) __hip_atomic_store(&a.part_done[tq], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next search
   }
   // An uncertified query is recomputed by the block-buffer scan with exact sums, which runs after
-  // this kernel (and the finishing kernel) and overwrites its results.
+  // this kernel and overwrites its results.
   if (!certified && tid == 0) a.fallback[atomicAdd(a.nfallback, 1u)] = q;
   if (a.refine) {
-    // Exact re-ranking needs the stored vectors: hand the candidates to the finishing kernel.
-    for (uint32_t i = tid; i < cnt_f; i += kStreamThreads) a.sel[static_cast<uint64_t>(q) * a.keep_sel + i] = s_queue[i];
-    if (tid == 0) a.sel_cnt[q] = cnt_f;
-    return;
+    // The cnt_f best keys are s_queue[0, cnt_f) here (every thread has passed a barrier since they
+    // were written). Eight lanes per candidate compute its exact distance (64 candidates per pass,
+    // each lane's loads coalesced with its group's), then a block sort by the exact distance.
+    constexpr uint32_t kGroups = kStreamThreads / 8;
+    for (uint32_t b = 0; b < cnt_f; b += kGroups) {
+      const uint32_t i = b + static_cast<uint32_t>(tid) / 8;
+      const bool valid = i < cnt_f;
+      const uint32_t pos = valid ? static_cast<uint32_t>(s_queue[i]) : 0u;
+      const float* x = a.vec + static_cast<uint64_t>(pos) * a.dim;
+      const float e = l2 ? exact_group8<true>(qv, x, a.dim, valid) : 1.0f - exact_group8<false>(qv, x, a.dim, valid);
+      if (valid && (tid & 7) == 0) s_queue[i] = make_key(e, pos);
+    }
+    sort_front(cnt_f);
   }
   const uint32_t nout = min(cnt_f, a.k);
   for (uint32_t j = tid; j < a.k; j += kStreamThreads) emit(j, j < nout, s_queue[j < nout ? j : 0]);
@@ -2103,90 +2143,6 @@ __attribute__((amdgpu_waves_per_eu(stream_waves<CAP>() == 4 || CAP == 512 ? 4 : 
 template <bool FULL, int CAP>
 __global__ void __launch_bounds__(stream_waves<CAP>() * 64) ivf_stream_wide_kernel(ScanArgs a) {
   stream_scan<16, FULL, CAP, false>(a);
-}
-
-/// Ascending bitonic sort of s[0, n) (n a power of two, n <= 2 * blockDim) by the block.
-__device__ __forceinline__ void finish_sort(uint64_t* s, uint32_t n) {
-  for (uint32_t size = 2; size <= n; size <<= 1) {
-    for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-      __syncthreads();
-      for (uint32_t i = threadIdx.x; i < n / 2; i += blockDim.x) {
-        const uint32_t lo = 2 * i - (i & (stride - 1));
-        const uint32_t hi = lo + stride;
-        const bool up = (lo & size) == 0;
-        const uint64_t x = s[lo], y = s[hi];
-        if ((x > y) == up) {
-          s[lo] = y;
-          s[hi] = x;
-        }
-      }
-    }
-  }
-  __syncthreads();
-}
-
-/// Exact re-ranking of the streaming scan's candidates with the stored vectors, and the k results
-/// of one query per block (src/ivfpq_index.cc:139-142,362-381).
-__global__ void __launch_bounds__(kFinishThreads) ivf_finish_kernel(ScanArgs a) {
-  __shared__ uint64_t s_key[kStreamMaxSel];
-  extern __shared__ __attribute__((aligned(16))) unsigned char f_raw[];
-  uint32_t* s_lo = reinterpret_cast<uint32_t*>(f_raw);  // [nprobe]
-  uint32_t* s_hi = s_lo + a.nprobe;
-  uint32_t* s_list = s_hi + a.nprobe;
-  float* s_score = reinterpret_cast<float*>(s_list + a.nprobe);
-  const uint32_t q = blockIdx.x;
-  const int tid = threadIdx.x;
-  const float* qv = a.Q + static_cast<uint64_t>(q) * a.dim;
-  for (uint32_t p = tid; p < a.nprobe; p += kFinishThreads) {
-    const uint32_t l = a.probes[static_cast<uint64_t>(q) * a.nprobe + p];
-    s_list[p] = l;
-    s_lo[p] = static_cast<uint32_t>(a.off[l]);
-    s_hi[p] = static_cast<uint32_t>(a.off[l + 1]);
-    s_score[p] = a.scores[static_cast<uint64_t>(q) * a.nlist + l];
-  }
-  uint32_t cnt = a.sel_cnt[q];
-  for (uint32_t i = tid; i < kStreamMaxSel; i += kFinishThreads) {
-    s_key[i] = i < cnt ? a.sel[static_cast<uint64_t>(q) * a.keep_sel + i] : ~0ull;
-  }
-  __syncthreads();
-  auto list_of = [&](uint32_t pos) {
-    for (uint32_t b = 0; b + 1 < a.nprobe; b += 8) {
-      uint32_t hit = 0;
-#pragma unroll
-      for (uint32_t i = 0; i < 8; ++i) {
-        const uint32_t pl = b + i;
-        if (pl < a.nprobe && s_lo[pl] <= pos && pos < s_hi[pl]) hit |= 1u << i;
-      }
-      if (hit) return b + static_cast<uint32_t>(__builtin_ctz(hit));
-    }
-    return a.nprobe - 1;
-  };
-  if (a.refine) {
-    // Exact re-ranking with the stored vectors (src/ivfpq_index.cc:139-142,363-373).
-    __syncthreads();
-    for (uint32_t i = tid; i < cnt; i += kFinishThreads) {
-      const uint32_t pos = static_cast<uint32_t>(s_key[i]);
-      const float* x = a.vec + static_cast<uint64_t>(pos) * a.dim;
-      const float d = a.mode == kModeIp ? 1.0f - exact_dot(qv, x, a.dim) : exact_l2sqr(qv, x, a.dim);
-      s_key[i] = make_key(d, pos);
-    }
-    finish_sort(s_key, pow2_at_least(max(cnt, 2u)));
-  }
-  __syncthreads();
-  const uint32_t nout = min(cnt, a.k);
-  for (uint32_t j = tid; j < a.k; j += kFinishThreads) {
-    uint64_t ref = QVH_EMPTY_REF;
-    float dist = __builtin_huge_valf();
-    if (j < nout) {
-      const uint64_t key = s_key[j];
-      const uint32_t pos = static_cast<uint32_t>(key);
-      const uint32_t pl = list_of(pos);
-      ref = (static_cast<uint64_t>(s_list[pl]) << 32) | (pos - s_lo[pl]);
-      dist = ordered_to_float(static_cast<uint32_t>(key >> 32));
-    }
-    a.out_refs[static_cast<uint64_t>(q) * a.k + j] = ref;
-    a.out_dist[static_cast<uint64_t>(q) * a.k + j] = dist;
-  }
 }
 
 void launch_nearest(bool sqdiff, const NearestArgs& a, uint32_t nsub, hipStream_t s) {
@@ -2348,7 +2304,7 @@ struct qvh_ivfpq {
   hipStream_t stream = nullptr;
   std::mutex mu;
   DeviceBuffer w_x, w_res, w_assign, w_afb, w_codes, w_codes_p, w_t1, w_dest, w_shift;
-  DeviceBuffer w_q, w_scores, w_probes, w_bits, w_refs, w_dist, w_bytes, w_sel, w_selcnt, w_key, w_order;
+  DeviceBuffer w_q, w_scores, w_probes, w_bits, w_refs, w_dist, w_bytes, w_key, w_order;
   DeviceBuffer w_pkeys, w_pcnt, w_pdone;  // sliced queries of the streaming scan
   DeviceBuffer w_delta, w_fb;             // certificate bounds; uncertified queries (count, list)
   bool last_certified = false;            // the last search ranked approximately (w_fb holds its count)
@@ -2578,7 +2534,7 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   };
   // The streaming scan covers the table modes with up to 256 probes, m <= 64 and a candidate set of
   // at most 256; the rest takes the block-buffer scan below.
-  const uint32_t mpw_t = mpw <= 2 ? 2 : mpw <= 4 ? 4 : mpw <= 8 ? 8 : 16;  // the kernel's code width in dwords
+  const uint32_t mpw_t = mpw <= 8 ? mpw : 16;  // the kernel's code width in dwords
   const bool full = h->mp == 4 * mpw_t;
   const bool small_sel = a.keep_sel <= 64 && k <= 64;
   const bool big_sel = !small_sel && (a.keep_sel > 128 || k > 128);  // 512-entry wave queues
@@ -2593,8 +2549,6 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   const size_t lds2 = mpw_t > 8 ? lds_total : lds_total - lds_table;
   if (!exact_all && mode != kModeResidual && h->mp <= kStreamMaxM && nprobe <= kStreamMaxProbes && a.keep_sel >= 1 &&
       a.keep_sel <= kStreamMaxSel && k <= kStreamMaxSel && lds_total <= 150 * 1024) {
-    a.sel = static_cast<uint64_t*>(h->w_sel.reserve(nq * a.keep_sel * sizeof(uint64_t)));
-    a.sel_cnt = static_cast<uint32_t*>(h->w_selcnt.reserve(nq * sizeof(uint32_t)));
     a.order = order;
     auto launch2 = [&](auto kernel) {
       const void* fn = reinterpret_cast<const void*>(kernel);
@@ -2630,8 +2584,7 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
 #define QVH_STREAM_CAP(KERNEL, ...)                                                    \
   (small_sel ? launch2(KERNEL<__VA_ARGS__, 128>)                                       \
              : big_sel ? launch2(KERNEL<__VA_ARGS__, 512>) : launch2(KERNEL<__VA_ARGS__, 256>))
-#define QVH_STREAM(MPW_) \
-  (full ? QVH_STREAM_CAP(ivf_stream_kernel, MPW_, true) : QVH_STREAM_CAP(ivf_stream_kernel, MPW_, false))
+#define QVH_STREAM(MPW_) QVH_STREAM_CAP(ivf_stream_kernel, MPW_, true)
     // Bank-rotated lookups: L2 with the precomputed table (re-scored exactly afterwards), four
     // dims per sub-space, 16- or 32-byte codes.
     const bool rot =
@@ -2640,10 +2593,20 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
       small_sel ? launch2(ivf_stream_kernel<8, true, 128, true>) : launch2(ivf_stream_kernel<8, true, 256, true>);
     } else if (rot) {
       small_sel ? launch2(ivf_stream_kernel<4, true, 128, true>) : launch2(ivf_stream_kernel<4, true, 256, true>);
+    } else if (mpw_t == 1) {
+      QVH_STREAM(1);
     } else if (mpw_t == 2) {
       QVH_STREAM(2);
+    } else if (mpw_t == 3) {
+      QVH_STREAM(3);
     } else if (mpw_t == 4) {
       QVH_STREAM(4);
+    } else if (mpw_t == 5) {
+      QVH_STREAM(5);
+    } else if (mpw_t == 6) {
+      QVH_STREAM(6);
+    } else if (mpw_t == 7) {
+      QVH_STREAM(7);
     } else if (mpw_t == 8) {
       QVH_STREAM(8);
     } else if (full) {
@@ -2654,10 +2617,6 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
 #undef QVH_STREAM
 #undef QVH_STREAM_CAP
     QVH_HIP(hipGetLastError());
-    if (a.refine) {
-      hipLaunchKernelGGL(ivf_finish_kernel, grid, dim3(kFinishThreads), 4 * static_cast<size_t>(nprobe) * sizeof(uint32_t),
-                         s, a);
-    }
   } else {
     launch_block_scan(a, grid);
   }

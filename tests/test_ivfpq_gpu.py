@@ -183,6 +183,33 @@ def test_ivfpq_candidate_sets_above_1024(oracle, metric, k, refine):
     print(k, refine, "nprobe 2", compare_search(oracle, idx, st, q[:5], k, 2, refine))
 
 
+@pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
+@pytest.mark.parametrize("dim,m", [(45, 15), (70, 14), (23, 23)])
+def test_ivfpq_refine_tail_dims(oracle, metric, dim, m):
+    """Re-ranking with the stored vectors at dims whose exact sums run the 8-wide loop and a scalar
+    tail with separately rounded and fused steps (45 = 32 + 8 + 4 + 1, 70 = 64 + 4 + 2, 23 = 16 + 4 + 3):
+    refine 3 re-ranks on one wave (a lane per candidate), refine 8 on the eight-wave block (eight
+    lanes per candidate); distances bit-identical to the oracle."""
+    base = clustered(6_000, dim, 24, seed=49 + dim)
+    q = clustered(200, dim, 24, seed=50 + dim)
+    idx, st = build_pair(oracle, base, metric, 32, m, True, iters=3)
+    for refine in (3, 8):
+        for nprobe in (2, 12):
+            print(refine, nprobe, compare_search(oracle, idx, st, q, 10, nprobe, refine))
+
+
+@pytest.mark.parametrize("dim,m", [(120, 30), (56, 14), (21, 7), (124, 31)])
+def test_ivfpq_partial_code_dwords(oracle, dim, m):
+    """m not a multiple of four (the last code dword carries pad bytes) with the precomputed L2
+    table: the streaming scan's exact re-score adds the list's m table rows only, never the rows of
+    the list stored after it; the last list's table ends the allocation."""
+    base = clustered(6_000, dim, 24, seed=47 + m)
+    q = clustered(300, dim, 24, seed=48 + m)
+    idx, st = build_pair(oracle, base, "l2", 24, m, False, iters=3)
+    for nprobe in (1, 5, 24):
+        print(compare_search(oracle, idx, st, q, 10, nprobe))
+
+
 @pytest.mark.parametrize("metric,dim,m", [("l2", 3072, 96), ("cosine", 4096, 128), ("ip", 2560, 64)])
 def test_ivfpq_wide_vectors(oracle, metric, dim, m):
     """Vectors wider than 2048 dims (the reference has no limit): training, encoding and search
