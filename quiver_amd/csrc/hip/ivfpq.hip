@@ -1330,7 +1330,7 @@ __global__ void __launch_bounds__(kScanThreads) ivf_scan_kernel(ScanArgs a) {
 // registers per lane), 8 with 256-entry queues (three blocks of ~49 KB per CU, 80 registers) or
 // with 512-entry queues for candidate sets of 129..256 (two blocks of ~66 KB per CU).
 template <int CAP>
-constexpr int stream_waves() { return CAP == 128 ? 4 : 8; }
+constexpr int stream_waves() { return CAP <= 192 ? 4 : 8; }
 constexpr uint32_t kStreamMaxProbes = 256;
 constexpr uint32_t kStreamMaxSel = 256;
 constexpr uint32_t kStreamMaxM = 64;  // code bytes of the widest streaming kernel
@@ -1631,8 +1631,9 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
   uint32_t thr_bits = 0xFFFFFFFFu;    // the same bound as ordered bits
 
   // Cuts the wave's queue to the entries whose distance is at most the keep_sel-th smallest one
-  // (found bit by bit with wave ballots), and publishes that distance as the shared bound.
-  auto flush = [&]() {
+  // (found bit by bit with wave ballots), and publishes that distance as the shared bound. Ties at
+  // that distance are all kept unless that would keep more than tie_limit (>= keep_sel) entries.
+  auto flush = [&](uint32_t tie_limit) {
     uint64_t k[QN];
     uint32_t d[QN];
 #pragma unroll
@@ -1653,7 +1654,7 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
       if (below < keep_sel) t |= 1u << b;
     }
     // t is the keep_sel-th smallest distance (as ordered bits); keep every entry at or below it,
-    // unless ties at t would keep more than CAP / 2: then also find the position u such that the
+    // unless ties at t would keep more than tie_limit: then also find the position u such that the
     // entries below t plus the ties at t with position <= u are exactly keep_sel.
     uint32_t kept = 0, under = 0;
 #pragma unroll
@@ -1664,7 +1665,7 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
       }
     }
     uint32_t u = 0xFFFFFFFFu;
-    if (kept > static_cast<uint32_t>(CAP / 2)) {
+    if (kept > tie_limit) {
       const uint32_t need = keep_sel - under;
       u = 0;
       for (int b = 31; b >= 0; --b) {
@@ -1702,8 +1703,9 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
     }
   };
   // Appends one code's candidates (at most 64) at a time and cuts the queue once it holds more than
-  // flush_at <= CAP / 2; a cut leaves at most CAP / 2, so the queue never holds more than CAP.
-  const uint32_t flush_at = min(static_cast<uint32_t>(CAP / 2), max(64u, 2 * keep_sel));
+  // flush_at = CAP - 64; a cut leaves at most CAP / 2 (keep_sel <= CAP / 2), so the queue never
+  // holds more than CAP, and at least CAP / 2 - 64 candidates arrive between two cuts.
+  const uint32_t flush_at = CAP - 64;
   auto offer = [&](bool pass, float d, uint32_t pos) {
     pass = pass && d <= thr;
     const uint64_t mk = __ballot(pass);
@@ -1712,7 +1714,7 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
                                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mk), 0u));
     if (pass) queue[cnt + below] = make_key(d, pos);
     cnt += static_cast<uint32_t>(__popcll(mk));
-    if (cnt > flush_at) flush();
+    if (cnt > flush_at) flush(CAP / 2);
   };
 
   // This block's slice [v_lo, v_hi) of the query's flattened probed positions.
@@ -1797,7 +1799,7 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
     }
     if (v0 == v_lo) {
       // Every wave cuts its first candidates and the block shares the tightest bound.
-      flush();
+      flush(CAP / 2);
       __syncthreads();
     }
     // An atomic load at workgroup scope stays an LDS read; a volatile read of this reference
@@ -1869,14 +1871,14 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
     a.out_refs[static_cast<uint64_t>(q) * a.k + j] = ref;
     a.out_dist[static_cast<uint64_t>(q) * a.k + j] = d;
   };
-  // Eight-wave blocks skip the final cut: every wave list holds at most CAP / 2 keys here, and a key
-  // a cut would drop has keep_sel better ones in its own list. Four-wave blocks cut, which keeps
-  // wave 0's sort below at <= 4 keep_sel keys.
+  // Eight-wave blocks cut only a list longer than CAP / 2 (a key a cut would drop has keep_sel
+  // better ones in its own list). Four-wave blocks always cut, which keeps wave 0's sort below at
+  // <= 4 keep_sel keys.
   if constexpr (kStreamWaves == 4) {
-    flush();
-    // Single-wave finish (four waves, k and keep_sel <= 64): the four cut lists (<= CAP / 2 = 64
-    // keys each) are packed in LDS, then wave 0 alone sorts, re-scores and emits them in registers,
-    // with no further block barrier.
+    flush(64);
+    // Single-wave finish (four waves, k and keep_sel <= 64): the four cut lists (<= 64 keys each)
+    // are packed in LDS, then wave 0 alone sorts, re-scores and emits them in registers, with no
+    // further block barrier.
     const uint64_t mine = static_cast<uint32_t>(lane) < cnt ? queue[lane] : ~0ull;
     if (lane == 0) s_wcount[wave] = cnt;
     __syncthreads();
@@ -1985,6 +1987,7 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
   // never reached.)
   uint32_t merged = 0;
   if constexpr (kStreamWaves == 8 && CAP >= 256) {
+  if (cnt > static_cast<uint32_t>(CAP / 2)) flush(CAP / 2);
   constexpr int NK = CAP / 128;
   constexpr int kList = CAP / 2;
   uint64_t mine[NK];
@@ -2538,7 +2541,11 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   const bool full = h->mp == 4 * mpw_t;
   const bool small_sel = a.keep_sel <= 64 && k <= 64;
   const bool big_sel = !small_sel && (a.keep_sel > 128 || k > 128);  // 512-entry wave queues
-  const uint32_t cap = small_sel ? 128 : big_sel ? 512 : 256;
+  // Four-wave blocks take 192-entry queues past 48 candidates, so that at least 64 candidates
+  // arrive between two cuts of a queue (1M x 128, nprobe 16: 60 candidates 0.97 -> 0.84 ms; at 36-40
+  // candidates the 128-entry queues measured 1-2% faster).
+  const bool mid_sel = small_sel && a.keep_sel > 48;
+  const uint32_t cap = small_sel ? (mid_sel ? 192 : 128) : big_sel ? 512 : 256;
   const size_t rows = 4 * mpw_t;
   // LDS of the streaming kernels: the table (static LDS for codes of up to 32 bytes), the wave
   // queues and the probed-list arrays (dynamic).
@@ -2581,14 +2588,14 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
       const dim3 sgrid(static_cast<unsigned>(a.nwhole + sliced * a.parts));
       hipLaunchKernelGGL(kernel, sgrid, dim3(waves * 64), lds2, s, a);
     };
-#define QVH_STREAM_CAP(KERNEL, ...)                                                    \
-  (small_sel ? launch2(KERNEL<__VA_ARGS__, 128>)                                       \
+#define QVH_STREAM_CAP(KERNEL, ...)                                                                       \
+  (small_sel ? (mid_sel ? launch2(KERNEL<__VA_ARGS__, 192>) : launch2(KERNEL<__VA_ARGS__, 128>))          \
              : big_sel ? launch2(KERNEL<__VA_ARGS__, 512>) : launch2(KERNEL<__VA_ARGS__, 256>))
 #define QVH_STREAM(MPW_) QVH_STREAM_CAP(ivf_stream_kernel, MPW_, true)
     // Bank-rotated lookups: L2 with the precomputed table (re-scored exactly afterwards), four
     // dims per sub-space, 16- or 32-byte codes.
     const bool rot =
-        QVH_STREAM_ROT && mode == kModePre && full && h->dsub == 4 && (mpw_t == 4 || mpw_t == 8) && !big_sel;
+        QVH_STREAM_ROT && mode == kModePre && full && h->dsub == 4 && (mpw_t == 4 || mpw_t == 8) && !big_sel && !mid_sel;
     if (rot && mpw_t == 8) {
       small_sel ? launch2(ivf_stream_kernel<8, true, 128, true>) : launch2(ivf_stream_kernel<8, true, 256, true>);
     } else if (rot) {

@@ -170,6 +170,22 @@ def test_ivfpq_large_candidate_sets(oracle, metric, k, refine):
         print(k, refine, qs.shape[0], compare_search(oracle, idx, st, qs, k, 16, refine))
 
 
+@pytest.mark.parametrize("metric,k,refine", [("l2", 32, 0), ("l2", 33, 0), ("l2", 40, 0), ("ip", 49, 0),
+                                             ("ip", 64, 0), ("cosine", 10, 5)])
+def test_ivfpq_mid_candidate_sets(oracle, metric, k, refine):
+    """Candidate sets of 49..64 stream through four-wave blocks with 192-entry wave queues (cut at
+    128, to exactly the candidate count at the end), 48 (L2 k = 32 with its re-score margin) through
+    128-entry ones: the same results as the oracle for whole queries, a sliced small batch and a
+    filter."""
+    base = clustered(12_000, 32, 24, seed=43)
+    q = clustered(700, 32, 24, seed=44)
+    idx, st = build_pair(oracle, base, metric, 64, 8, refine > 0)
+    for qs in (q, q[:3]):
+        print(k, refine, qs.shape[0], compare_search(oracle, idx, st, qs, k, 16, refine))
+    allowed = np.arange(0, 12_000, 5, dtype=np.uint64)
+    print("filtered", compare_search(oracle, idx, st, q, k, 16, refine, allowed))
+
+
 @pytest.mark.parametrize("metric,k,refine", [("l2", 1000, 0), ("ip", 2000, 0), ("l2", 100, 16), ("cosine", 50, 40),
                                              ("l2", 3000, 2)])
 def test_ivfpq_candidate_sets_above_1024(oracle, metric, k, refine):
