@@ -1363,9 +1363,13 @@ __global__ void __launch_bounds__(256) adc_bound_kernel(const float* __restrict_
                                                         uint32_t m, uint32_t dsub, const float* __restrict__ cmax,
                                                         const float* __restrict__ scores, uint32_t nlist,
                                                         const uint32_t* __restrict__ probes, uint32_t nprobe,
-                                                        const float* __restrict__ pmax, float* __restrict__ delta) {
+                                                        const float* __restrict__ pmax, float* __restrict__ delta,
+                                                        uint32_t* __restrict__ fallback_count) {
   const int lane = threadIdx.x & 63;
   const uint32_t q = blockIdx.x * 4 + (threadIdx.x >> 6);
+  // The scan's count of uncertified queries starts at zero (the previous search's kernels, on the
+  // same stream, are done with it).
+  if (blockIdx.x == 0 && threadIdx.x == 0) *fallback_count = 0u;
   if (q >= nq) return;  // whole wave
   const float* qv = Q + static_cast<uint64_t>(q) * dim;
   double tsum = 0.0;
@@ -2399,10 +2403,15 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   while (cand_cap < keep_sel + kScanThreads * kScanRound) cand_cap *= 2;
   QVH_REQUIRE(h->count < 0xFFFFFFFFull, "IVF-PQ device path holds fewer than 2^32 vectors");
   if (h->timed) QVH_HIP(hipEventRecord(h->ev[0], s));
-  // prepared queries
-  float* dq = static_cast<float*>(h->w_q.reserve(nq * h->dim * sizeof(float)));
-  if (dq != d_q_raw) QVH_HIP(hipMemcpyAsync(dq, d_q_raw, nq * h->dim * sizeof(float), hipMemcpyDeviceToDevice, s));
-  if (h->metric == QVH_METRIC_COSINE) launch_normalize_rows(dq, nq, h->dim, s);
+  // Prepared queries: the caller's rows as they are (L2, inner product; 16-byte aligned for the
+  // table build's vector loads), or a copy normalized in place (cosine).
+  const float* dq = d_q_raw;
+  if (h->metric == QVH_METRIC_COSINE || reinterpret_cast<uintptr_t>(d_q_raw) % 16 != 0) {
+    float* copy = static_cast<float*>(h->w_q.reserve(nq * h->dim * sizeof(float)));
+    if (copy != d_q_raw) QVH_HIP(hipMemcpyAsync(copy, d_q_raw, nq * h->dim * sizeof(float), hipMemcpyDeviceToDevice, s));
+    if (h->metric == QVH_METRIC_COSINE) launch_normalize_rows(copy, nq, h->dim, s);
+    dq = copy;
+  }
   // coarse scores + probes
   float* scores = static_cast<float*>(h->w_scores.reserve(nq * h->nlist * sizeof(float)));
   {
@@ -2452,11 +2461,10 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   uint32_t* fb = nullptr;
   if (certify) {
     delta = static_cast<float*>(h->w_delta.reserve(nq * sizeof(float)));
+    fb = static_cast<uint32_t*>(h->w_fb.reserve((nq + 1) * sizeof(uint32_t)));
     hipLaunchKernelGGL(adc_bound_kernel, dim3(static_cast<unsigned>(ceil_div(nq, 4))), dim3(256), 0, s, dq,
                        static_cast<uint32_t>(nq), h->dim, h->m, h->dsub, h->cmax.as<float>(), scores, h->nlist, probes,
-                       nprobe, h->pmax.as<float>(), delta);
-    fb = static_cast<uint32_t*>(h->w_fb.reserve((nq + 1) * sizeof(uint32_t)));
-    hipLaunchKernelGGL(zero_u32_kernel, dim3(1), dim3(64), 0, s, fb, 1);
+                       nprobe, h->pmax.as<float>(), delta, fb);
   }
   h->last_certified = certify;
   QVH_HIP(hipGetLastError());
