@@ -41,7 +41,7 @@ constexpr int kWaves = 8;                                 // 2 waves per SIMD
 constexpr int kThreads = kWaves * 64;
 constexpr int kTileRows = 64;                             // two 32-row MFMA blocks
 constexpr int kQueriesPerBlock = kWaves * 32;             // each wave owns 32 queries
-constexpr int kMaxListsPerLane = 4;                       // merge: lists per lane
+constexpr int kMaxListsPerLane = 8;                       // merge: lists per lane
 constexpr uint32_t kMaxSplits = 64 * kMaxListsPerLane / 2;
 constexpr int kMaxDp = 128;                               // register-resident query width
 
@@ -1109,7 +1109,9 @@ constexpr int kFewWaves = kFewThreads / 64;
 constexpr int kFewRowsPerStep = kFewWaves * 8;
 constexpr int kFewCap = 128;  // per (query, wave) queue for k <= 64; 256 for k <= 128
 constexpr uint32_t kFewMaxQ = 8;       // queries per launch
-constexpr uint32_t kFewMaxBatch = 16;  // larger batches take the MFMA scan
+// Larger batches take the MFMA scan (1M x 128: 16 queries 541 us in two few-query launches, 436 us
+// on the MFMA scan over 256 row splits; 9 queries 357 us against 436).
+constexpr uint32_t kFewMaxBatch = 12;
 constexpr uint32_t kFewMaxK = 128;     // dims that are multiples of 32; 64 for the others
 constexpr uint32_t kFewMaxDim = 159;  // four 32-element blocks, then up to three 8-blocks and a tail
 constexpr uint32_t kFewMaxDp = 160;

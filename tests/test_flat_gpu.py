@@ -196,18 +196,31 @@ def test_small_batches_split_rows(oracle, metric, nq, k, n):
 @pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
 @pytest.mark.parametrize("dim,nq,k,n", [(32, 1, 10, 700_000), (40, 2, 64, 100_000), (47, 3, 1, 60_000),
                                         (61, 8, 33, 120_000), (100, 5, 10, 2_048), (128, 4, 20, 150_000),
-                                        (159, 7, 64, 50_000), (96, 6, 16, 33_333), (64, 13, 10, 80_000),
-                                        (128, 16, 64, 40_000), (128, 3, 100, 200_000), (64, 8, 128, 60_000),
+                                        (159, 7, 64, 50_000), (96, 6, 16, 33_333), (64, 11, 10, 80_000),
+                                        (128, 12, 64, 40_000), (128, 3, 100, 200_000), (64, 8, 128, 60_000),
                                         (100, 2, 100, 50_000)])
 def test_few_query_coalesced_scan(oracle, metric, dim, nq, k, n):
-    """At most sixteen queries with 32 <= dim <= 159 and k <= 64: eight lanes per row replay the
+    """At most twelve queries with 32 <= dim <= 159 and k <= 64: eight lanes per row replay the
     reference's accumulation order (32-element blocks, 8-element blocks, the rounded and fused
     tail: dims 40, 47 and 61 take every branch); each launch reads a row once for up to eight
-    queries (13 and 16 queries: two launches, one merge). k up to 128 for dims that are multiples
+    queries (11 and 12 queries: two launches, one merge). k up to 128 for dims that are multiples
     of 32 (256-entry queues); dim 100 with k = 100 takes the split exact kernel."""
     base = D.gaussian(n, dim, seed=33)
     q = D.gaussian(nq, dim, seed=34)
     print(_check(oracle, base, q, k, metric))
+
+
+@pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
+@pytest.mark.parametrize("nq", [13, 16, 32, 64])
+def test_small_batches_on_256_row_splits(oracle, metric, nq):
+    """13 to 256 queries fill one 256-query block of the MFMA scan; its rows go to 256 splits
+    (512 lane lists per query in the merge, eight per merge lane) so that every CU scans. Integer
+    data adds exact ties across splits."""
+    base = D.gaussian(300_000, 128, seed=35)
+    q = D.gaussian(nq, 128, seed=36)
+    print(_check(oracle, base, q, 10, metric))
+    ib, iq = D.int_mix(300_000, nq)
+    print(_check(oracle, ib, iq, 10, metric))
 
 
 @pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
