@@ -63,6 +63,7 @@ struct ScanArgs {
   uint32_t* qthr;           // [nq] shared prune threshold (ordered float bits), starts at +inf
   int share;                // 0: every lane list keeps its own KL best (k > KL: no shared bound)
   uint32_t dp;              // row width (the chunked scan; the register scan has it as DP)
+  int rowsplit;             // register scan, unfiltered, at most 128 queries: two waves per query group
 };
 
 constexpr int kShareEvery = 8;  // tiles between exchanges of the shared per-query threshold
@@ -222,8 +223,12 @@ __device__ __forceinline__ void scan_block_coords(const ScanArgs& a, uint32_t& q
 
 // MODE: 0 every row, 1 rows admitted by a bitmap (tested per tile), 2 the admitted rows listed in
 // a.idx (positions 0..n-1 index that list; candidates carry positions, the merge maps them to rows).
-template <int DP, int KL, bool L2, int MODE>
+// RS (row split, small batches): the block serves 128 queries, and the two waves of a 32-query group
+// take the two 32-row halves of every tile, so a batch of 32 queries keeps two SIMDs of a CU busy
+// rather than one; at the end the odd wave's lists go through LDS into the even wave's.
+template <int DP, int KL, bool L2, int MODE, bool RS = false>
 __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
+  static_assert(!RS || 4 * 64 * KL <= kQueueCap * kThreads, "row-split hand-off must fit the queue arrays");
   constexpr bool FILTER = MODE == 1;
   constexpr int H = DP / 2;                   // dims per lane half (K split in two halves)
   // LDS row stride in floats: conflict-free b128 reads. Columns DP and DP + 1 of a row hold the
@@ -256,8 +261,11 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
     qb = wg % a.qblocks;
   }
 
-  const uint32_t q = qb * kQueriesPerBlock + wave * 32 + j;
-  const bool wave_active = qb * kQueriesPerBlock + wave * 32 < a.nq;
+  constexpr int kQPB = RS ? kQueriesPerBlock / 2 : kQueriesPerBlock;
+  const int qgroup = RS ? (wave >> 1) : wave;  // the wave's 32 queries
+  const int rb = RS ? (wave & 1) : 0;          // RS: the wave's 32-row half of each tile
+  const uint32_t q = qb * kQPB + qgroup * 32 + j;
+  const bool wave_active = qb * kQPB + qgroup * 32 < a.nq;
   const bool qvalid = q < a.nq;
 
   // This lane's half of its query: dims [h*H, h*H + H). MFMA step s pairs dim h*H+s of the query
@@ -381,7 +389,57 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
     const int buf = t & 1;
     const bool prefetch = t + 1 < ntiles;
     if (!wave_active && prefetch) load_tile(t + 1);
-    if (wave_active) {
+    if (wave_active && RS) {
+      // One 32-row half per wave: a single accumulation chain, four MFMAs per pair of b128 reads.
+      f32x16 acc = {};
+      const float* ar = &s_tile[buf][(32 * rb + j) * STRIDE + h * H];
+      const float augr = s_tile[buf][(32 * rb + j) * STRIDE + DP + h];
+      f32x4 x0 = *reinterpret_cast<const f32x4*>(ar);
+#pragma unroll
+      for (int s = 0; s < H; s += 4) {
+        f32x4 n0 = x0;
+        if (s + 4 < H) n0 = *reinterpret_cast<const f32x4*>(ar + s + 4);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x0[0], qreg[s + 0], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x0[1], qreg[s + 1], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x0[2], qreg[s + 2], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x0[3], qreg[s + 3], acc, 0, 0, 0);
+        x0 = n0;
+        __builtin_amdgcn_sched_barrier(0);
+        if (s == 4 && prefetch) load_tile(t + 1);
+        if (s == 4) __builtin_amdgcn_sched_barrier(0);
+      }
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(augr, qaug, acc, 0, 0, 0);
+      const uint64_t tile_row0 = r0 + static_cast<uint64_t>(t) * kTileRows;
+      const uint64_t left = r1 - tile_row0;
+      uint64_t admit = FILTER ? s_bits[buf] : ~0ull;
+      if (left < 64) admit &= (1ull << left) - 1;
+      const bool masked = FILTER || left < 64;
+      const uint32_t lane_bits = static_cast<uint32_t>(admit >> (32 * rb)) >> (4 * h);
+      const float thr = fminf(pthr, Ld[KL - 1]);
+      bool any = false;
+      if (!masked) {
+        float m = acc[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) m = fminf(m, acc[r]);
+        any = !(m > thr);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) any = any || (!(acc[r] > thr) && ((lane_bits >> (8 * (r >> 2) + (r & 3))) & 1u));
+      }
+      any = any && qvalid;
+      if (__builtin_amdgcn_ballot_w64(qcount > kQueueCap - 16)) flush_queue();
+      if (any) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int bit = 8 * (r >> 2) + (r & 3);
+          bool p = !(acc[r] > thr);
+          if (masked) p = p && ((lane_bits >> bit) & 1u);
+          s_qd[qcount * kThreads + tid] = acc[r];
+          s_qr[qcount * kThreads + tid] = static_cast<uint32_t>(tile_row0 + 32 * rb + 4 * h + bit);
+          qcount += p ? 1 : 0;
+        }
+      }
+    } else if (wave_active) {
       f32x16 acc0 = {}, acc1 = {};
       const float* a0 = &s_tile[buf][j * STRIDE + h * H];
       const float* a1 = &s_tile[buf][(32 + j) * STRIDE + h * H];
@@ -479,7 +537,28 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
   }
 
   if (wave_active) flush_queue();
-  if (qvalid) {
+  if constexpr (RS) {
+    // The odd wave of each query group hands its lists (rows of the tiles' second halves) to the
+    // even wave through the queue arrays, free once every wave has flushed.
+    __syncthreads();
+    const int slot = (qgroup * 64 + lane) * KL;  // < 4 * 64 * KL <= kQueueCap * kThreads
+    if (rb == 1) {
+#pragma unroll
+      for (int x = 0; x < KL; ++x) {
+        s_qd[slot + x] = Ld[x];
+        s_qr[slot + x] = Lr[x];
+      }
+    }
+    __syncthreads();
+    if (rb == 0) {
+#pragma unroll
+      for (int x = 0; x < KL; ++x) {
+        const float d = s_qd[slot + x];
+        if (d <= Ld[KL - 1]) list_insert<KL>(Ld, Lr, d, s_qr[slot + x]);
+      }
+    }
+  }
+  if (qvalid && rb == 0) {
     const size_t o = (static_cast<size_t>(q) * (2 * a.nsplit) + 2 * split + h) * KL;
 #pragma unroll
     for (int x = 0; x < KL; ++x) {
@@ -1109,9 +1188,9 @@ constexpr int kFewWaves = kFewThreads / 64;
 constexpr int kFewRowsPerStep = kFewWaves * 8;
 constexpr int kFewCap = 128;  // per (query, wave) queue for k <= 64; 256 for k <= 128
 constexpr uint32_t kFewMaxQ = 8;       // queries per launch
-// Larger batches take the MFMA scan (1M x 128: 16 queries 541 us in two few-query launches, 436 us
-// on the MFMA scan over 256 row splits; 9 queries 357 us against 436).
-constexpr uint32_t kFewMaxBatch = 12;
+// Larger batches take the MFMA scan (1M x 128: 9 queries 357 us in two few-query launches, 295 us on
+// the row-split MFMA scan over 256 row splits; 8 queries 274 us in one launch).
+constexpr uint32_t kFewMaxBatch = 8;
 constexpr uint32_t kFewMaxK = 128;     // dims that are multiples of 32; 64 for the others
 constexpr uint32_t kFewMaxDim = 159;  // four 32-element blocks, then up to three 8-blocks and a tail
 constexpr uint32_t kFewMaxDp = 160;
@@ -1666,6 +1745,14 @@ int shared_list_length(uint32_t k) {
 
 template <int DP, int KL>
 void launch_scan_kl(bool l2, int mode, dim3 grid, const ScanArgs& a, hipStream_t s) {
+  if (a.rowsplit) {  // unfiltered batches of at most 128 queries
+    if (l2) {
+      hipLaunchKernelGGL((flat_scan_kernel<DP, KL, true, 0, true>), grid, dim3(kThreads), 0, s, a);
+    } else {
+      hipLaunchKernelGGL((flat_scan_kernel<DP, KL, false, 0, true>), grid, dim3(kThreads), 0, s, a);
+    }
+    return;
+  }
   if (l2) {
     if (mode == 1) {
       hipLaunchKernelGGL((flat_scan_kernel<DP, KL, true, 1>), grid, dim3(kThreads), 0, s, a);
@@ -2092,6 +2179,9 @@ void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const
   a.qthr = b.thr;
   a.share = p.wide ? 0 : 1;
   a.dp = f->dp;
+  // One query block of at most 128 queries, unfiltered, register-resident queries: the row-split
+  // form of the scan (two waves per 32-query group).
+  a.rowsplit = nq <= static_cast<uint64_t>(kQueriesPerBlock / 2) && !d_idx && !d_bitmap && f->dp <= kMaxDp ? 1 : 0;
   hipLaunchKernelGGL(fill_u32_kernel, dim3(static_cast<unsigned>(ceil_div(nq, 256))), dim3(256), 0, s,
                      a.qthr, nq, 0xFF800000u);  // ordered bits of +inf
   launch_scan(f->dp, p.kl, dim3(static_cast<unsigned>(p.qblocks * p.nsplit)), a, s);

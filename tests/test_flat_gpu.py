@@ -117,7 +117,7 @@ def test_dimensions_above_the_register_width(oracle, dim, metric):
 
 def test_wide_rows_integer_data_and_ties(oracle):
     """Integer-valued 256-d rows with duplicated rows (exact ties resolve to the smaller row) on the
-    chunked scan, and a batch of 17 queries (just above the few-query kernel's batch limit)."""
+    chunked scan, and a batch of 17 queries (above the few-query kernel's batch limit of 8)."""
     rng = np.random.default_rng(77)
     base = rng.integers(0, 16, (30_000, 256)).astype(np.float32)
     base[15_000:15_500] = base[:500]
@@ -141,7 +141,7 @@ def test_large_k(oracle, k, metric):
 def test_large_k_crowded_lists_fall_back_exactly(oracle, metric):
     """200 near-copies of query 0 in consecutive rows: its 100 nearest crowd one split's 32-entry
     lists, so the wide merge hands that query to the exact kernel while the others stay on the
-    MFMA path (40 queries: above the small-batch kernels' 16); every result still equals the
+    MFMA path (40 queries: above the few-query kernel's 8); every result still equals the
     oracle's."""
     base, q = D.int_mix(40_000, 40)
     base = base.copy()
@@ -200,10 +200,10 @@ def test_small_batches_split_rows(oracle, metric, nq, k, n):
                                         (128, 12, 64, 40_000), (128, 3, 100, 200_000), (64, 8, 128, 60_000),
                                         (100, 2, 100, 50_000)])
 def test_few_query_coalesced_scan(oracle, metric, dim, nq, k, n):
-    """At most twelve queries with 32 <= dim <= 159 and k <= 64: eight lanes per row replay the
+    """At most eight queries with 32 <= dim <= 159 and k <= 64: eight lanes per row replay the
     reference's accumulation order (32-element blocks, 8-element blocks, the rounded and fused
     tail: dims 40, 47 and 61 take every branch); each launch reads a row once for up to eight
-    queries (11 and 12 queries: two launches, one merge). k up to 128 for dims that are multiples
+    queries (11 and 12 queries: the row-split MFMA scan). k up to 128 for dims that are multiples
     of 32 (256-entry queues); dim 100 with k = 100 takes the split exact kernel."""
     base = D.gaussian(n, dim, seed=33)
     q = D.gaussian(nq, dim, seed=34)
@@ -211,11 +211,12 @@ def test_few_query_coalesced_scan(oracle, metric, dim, nq, k, n):
 
 
 @pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
-@pytest.mark.parametrize("nq", [13, 16, 32, 64])
+@pytest.mark.parametrize("nq", [9, 16, 32, 64, 100])
 def test_small_batches_on_256_row_splits(oracle, metric, nq):
-    """13 to 256 queries fill one 256-query block of the MFMA scan; its rows go to 256 splits
-    (512 lane lists per query in the merge, eight per merge lane) so that every CU scans. Integer
-    data adds exact ties across splits."""
+    """9 to 128 queries: one block of the MFMA scan in its row-split form (the two waves of a 32-query
+    group take the two halves of each tile, and the odd wave's lists join the even wave's through
+    LDS), its rows over 256 splits (512 lane lists per query in the merge, eight per merge lane).
+    Integer data adds exact ties across splits and tile halves."""
     base = D.gaussian(300_000, 128, seed=35)
     q = D.gaussian(nq, 128, seed=36)
     print(_check(oracle, base, q, 10, metric))
