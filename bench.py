@@ -14,7 +14,7 @@ resident in HBM):
 Prints ONE JSON line. `value` is the flat workload's queries per second (query prep + fused MFMA
 scan + merge/exact re-score), timed over K steps with the device synchronized on both sides;
 the "ivfpq" object carries the same fields for the IVF-PQ workload, "flat_small_batches" the
-flat search time of one and of eight of the same queries, and "flat_wide_rows" a 500,000 x 768
+flat search time of 1, 8, 32 and 128 of the same queries, and "flat_wide_rows" a 500,000 x 768
 flat search (the chunked MFMA scan for rows wider than 128). `roofline` is each
 workload's dominant kernel measured with HIP events on the stream it runs on: the flat scan's
 algorithmic 2*n*d*nq FLOP per launch against the dense FP32 matrix peak (157.3 TFLOP/s), the
@@ -227,10 +227,11 @@ def bench_flat(args, hip: Hip, qvh: Qvh):
                           "note": "FlatIndex::search_batch, host numpy buffers in and out (PCIe included)"}
     del host_index
     if not args.no_extra:
-        # Small batches (the first 1 and 8 queries; the few-query kernels): device time of one
-        # search from its stage events, and the caller's wall time of search + sync.
+        # Small batches (the first 1 and 8 queries: the few-query kernel; 32 and 128: the row-split
+        # MFMA scan): device time of one search from its stage events, and the caller's wall time
+        # of search + sync.
         small = {}
-        for b in (1, 8):
+        for b in (1, 8, 32, 128):
             dev, wall = [], []
             for _ in range(21):
                 t = time.perf_counter()
