@@ -596,16 +596,26 @@ def main():
 
     hip, qvh = Hip(), Qvh()
     name, arch, cus = qvh.device()
+    t_start = time.perf_counter()
+
+    def done(stage):  # one progress line per finished stage (stderr; stdout carries the JSON line)
+        print(f"[bench] {stage} done at {time.perf_counter() - t_start:.1f} s", file=sys.stderr, flush=True)
+
     if args.copy_calibration:
         copy_calibration(hip)
     flat, base, queries = bench_flat(args, hip, qvh)
+    done("flat")
     idx, ivf = bench_ivfpq(args, hip, qvh, base, queries)
+    done("ivfpq")
     extra = {}
     if not args.no_extra:
         extra["flat_small_batches"] = flat["small_batches"]
         extra["flat_cosine_filtered"] = bench_flat_filtered(args, qvh)
+        done("flat_cosine_filtered")
         extra["flat_wide_rows"] = bench_flat_wide(args, hip, qvh)
+        done("flat_wide_rows")
         extra["ivfpq_cosine_refine"] = bench_ivfpq_cosine_refine(args, hip, qvh)
+        done("ivfpq_cosine_refine")
     cpu = None
     ivf["cpu_baseline"] = None
     cores = host_cores()
@@ -614,9 +624,11 @@ def main():
         cpu = with_one_thread(cpu_baseline_flat(base, queries, 10, args.cpu_seconds, threads),
                               cpu_baseline_flat(base, queries, 10, args.cpu_seconds / 3, 1))
         cpu["host"] = cores
+        done("cpu_baseline flat")
         ivf["cpu_baseline"] = with_one_thread(
             cpu_baseline_ivfpq(idx, queries, 10, 32, args.cpu_seconds / 3, threads),
             cpu_baseline_ivfpq(idx, queries, 10, 32, args.cpu_seconds / 3, 1))
+        done("cpu_baseline ivfpq")
     line = {
         "metric": METRIC,
         "value": flat["value"],
