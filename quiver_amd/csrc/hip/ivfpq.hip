@@ -855,6 +855,9 @@ constexpr int kScanThreads = 256;
 constexpr int kCandCap = 2048;       // LDS candidate buffer (u64 keys) for keep_sel <= kMaxKeepSel
 constexpr int kScanRound = 4;        // codes per thread between buffer checks
 constexpr uint32_t kMaxKeepSel = kCandCap - kScanThreads * kScanRound;  // 1024
+// Larger m keeps the block-buffer scan's per-query table (m x 256 floats) in global memory.
+constexpr uint32_t kScanMaxLdsM = 128;
+constexpr uint64_t kScanGlobalTableBytes = 256ull << 20;  // bound on those tables, all work-groups
 // Larger selections take a larger buffer: keep_sel + kScanThreads * kScanRound slots, rounded up to
 // a power of two, as far as LDS allows.
 
@@ -933,6 +936,9 @@ struct ScanArgs {
   int exact_pre;        // block-buffer scan: the reference's sum for every code, no re-score
   const uint32_t* qlist;   // block-buffer scan over listed queries (block b runs qlist[b] while
   const uint32_t* qcount;  // b < *qcount), or null: block b runs query b
+  // Block-buffer scan with m above kScanMaxLdsM: the per-query table lives in global memory, one
+  // [m][256] region per work-group, and the work-groups take the queries in turn.
+  float* lut_global;  // [gridDim.x][m][256], or null: the table is in LDS
 };
 
 /// Certificate of an approximate selection (mode pre). The scan kept the keep_sel best candidates by
@@ -1013,6 +1019,34 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+/// The code bytes [j0, j0 + 4 * MPW) of position pos as MPW dwords (zeros past the code's mp bytes).
+template <int MPW>
+__device__ __forceinline__ void load_code_chunk(const uint8_t* codes, uint64_t pos, uint32_t mp, uint32_t j0,
+                                                uint32_t (&w)[MPW]) {
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(codes + pos * mp + j0);
+  const int left = static_cast<int>(mp - j0);
+  if (mp % 16 == 0) {
+#pragma unroll
+    for (int i = 0; i < MPW; i += 4) {
+      if (4 * i < left) {
+        const uint4 v = *reinterpret_cast<const uint4*>(p + i);
+        w[i] = v.x;
+        if (i + 1 < MPW) w[i + 1] = v.y;
+        if (i + 2 < MPW) w[i + 2] = v.z;
+        if (i + 3 < MPW) w[i + 3] = v.w;
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (i + u < MPW) w[i + u] = 0u;
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < MPW; ++i) w[i] = 4 * i < left ? p[i] : 0u;
+  }
+}
+
 /// Code bytes of position pos as MPW dwords. FULL (mp == 4 * MPW): the code in 16-byte pieces and
 /// one 4-, 8- or 12-byte tail, each a single load (rows are only 4-byte aligned when mp is not a
 /// multiple of 16, and gfx950's global loads take any width at 4-byte alignment: a 28-byte code is
@@ -1071,7 +1105,9 @@ __device__ void ivf_scan_query(const ScanArgs& a, const uint32_t q) {
   uint64_t* s_cand = reinterpret_cast<uint64_t*>(s_raw);                       // [cand_cap]
   uint64_t* s_pstart = s_cand + a.cand_cap;                                    // [nprobe + 1] flattened starts
   uint32_t* s_plist = reinterpret_cast<uint32_t*>(s_pstart + a.nprobe + 1);    // [nprobe]
-  float* s_lut = reinterpret_cast<float*>(s_plist + ((a.nprobe + 1) & ~1u));  // [m][256]
+  // [m][256]: in LDS, or in this work-group's region of global memory for m above kScanMaxLdsM
+  float* s_lut = a.lut_global ? a.lut_global + static_cast<uint64_t>(blockIdx.x) * a.m * 256
+                              : reinterpret_cast<float*>(s_plist + ((a.nprobe + 1) & ~1u));
   __shared__ uint32_t s_count;
   __shared__ uint64_t s_thr;
   __shared__ uint32_t s_dropped;  // a compaction dropped candidates
@@ -1080,6 +1116,42 @@ __device__ void ivf_scan_query(const ScanArgs& a, const uint32_t q) {
   const float* qv = a.Q + static_cast<uint64_t>(q) * a.dim;
   const float* qscore = a.scores + static_cast<uint64_t>(q) * a.nlist;
   const uint32_t table = a.m * 256;
+  constexpr uint32_t kChunk = 4 * MPW;  // sub-spaces per pass over a code
+  // sum_j table[j][c_j] of position pos in order of j (ProductQuantizer::adc), kChunk at a time.
+  auto adc_pos = [&](uint64_t pos) -> float {
+    float sum = 0.0f;
+    for (uint32_t j0 = 0; j0 < a.m; j0 += kChunk) {
+      uint32_t w[MPW];
+      load_code_chunk<MPW>(a.codes, pos, a.mp, j0, w);
+      const float* lut = s_lut + j0 * 256;
+#pragma unroll
+      for (int j = 0; j < static_cast<int>(kChunk); ++j) {
+        if (j0 + j < a.m) {
+          const uint32_t c = (w[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+          sum = sum + lut[j * 256 + c];
+        }
+      }
+    }
+    return sum;
+  };
+  // sum_j (pre[l][j][c_j] + table[j][c_j]) in order of j (src/ivfpq_index.cc:334-346).
+  auto pre_pos = [&](uint64_t pos, const float* pre) -> float {
+    float sum = 0.0f;
+    for (uint32_t j0 = 0; j0 < a.m; j0 += kChunk) {
+      uint32_t w[MPW];
+      load_code_chunk<MPW>(a.codes, pos, a.mp, j0, w);
+      const float* lut = s_lut + j0 * 256;
+      const float* pr = pre + j0 * 256;
+#pragma unroll
+      for (int j = 0; j < static_cast<int>(kChunk); ++j) {
+        if (j0 + j < a.m) {
+          const uint32_t c = (w[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+          sum = sum + (pr[j * 256 + c] + lut[j * 256 + c]);
+        }
+      }
+    }
+    return sum;
+  };
 
   // Per-query table (src/ivfpq_index.cc:309-318): <q_j, C_{j,c}> in order of t, times -2 for L2.
   if (a.mode != kModeResidual && !a.exact_all) {
@@ -1152,27 +1224,15 @@ __device__ void ivf_scan_query(const ScanArgs& a, const uint32_t q) {
               offer(a.mode == kModeIp ? 1.0f - exact_dot(qv, x, a.dim) : exact_l2sqr(qv, x, a.dim), pos);
               continue;
             }
-            uint32_t w[MPW];
-            load_code<MPW>(a.codes, pos, a.mp, w);
             const float score = qscore[l];
             float dist;
             if (a.mode == kModeIp) {
-              dist = 1.0f - (-score + adc_sum<MPW>(s_lut, w, a.m));  // base = <q, c> (src/ivfpq_index.cc:333,346)
+              dist = 1.0f - (-score + adc_pos(pos));  // base = <q, c> (src/ivfpq_index.cc:333,346)
             } else if (a.exact_pre) {
-              // The reference's sum: table entry pre + qtab in order of j, plus ||q - c||^2
-              // (src/ivfpq_index.cc:334-346).
-              const float* pre = a.pre + static_cast<uint64_t>(l) * table;
-              float se = 0.0f;
-#pragma unroll
-              for (int j = 0; j < 4 * MPW; ++j) {
-                if (j < static_cast<int>(a.m)) {
-                  const uint32_t c = (w[j >> 2] >> (8 * (j & 3))) & 0xFFu;
-                  se = se + (pre[j * 256 + c] + s_lut[j * 256 + c]);
-                }
-              }
-              dist = score + se;
+              // The reference's sum: table entry pre + qtab in order of j, plus ||q - c||^2.
+              dist = score + pre_pos(pos, a.pre + static_cast<uint64_t>(l) * table);
             } else {
-              dist = score + (a.t1[pos] + adc_sum<MPW>(s_lut, w, a.m));
+              dist = score + (a.t1[pos] + adc_pos(pos));
             }
             offer(dist, pos);
           }
@@ -1209,9 +1269,7 @@ __device__ void ivf_scan_query(const ScanArgs& a, const uint32_t q) {
           if (i < len) {
             const uint64_t pos = b + i;
             if (!a.bitmap || ((a.bitmap[pos >> 6] >> (pos & 63)) & 1ull)) {
-              uint32_t w[MPW];
-              load_code<MPW>(a.codes, pos, a.mp, w);
-              offer(0.0f + adc_sum<MPW>(s_lut, w, a.m), pos);
+              offer(0.0f + adc_pos(pos), pos);
             }
           }
         }
@@ -1238,18 +1296,7 @@ __device__ void ivf_scan_query(const ScanArgs& a, const uint32_t q) {
     for (uint32_t i = tid; i < cnt; i += kScanThreads) {
       const uint32_t pos = static_cast<uint32_t>(s_cand[i]);
       const uint32_t l = list_pos(pos);
-      const float* pre = a.pre + static_cast<uint64_t>(l) * table;
-      uint32_t w[MPW];
-      load_code<MPW>(a.codes, pos, a.mp, w);
-      float s = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 4 * MPW; ++j) {
-        if (j < static_cast<int>(a.m)) {
-          const uint32_t c = (w[j >> 2] >> (8 * (j & 3))) & 0xFFu;
-          s = s + (pre[j * 256 + c] + s_lut[j * 256 + c]);
-        }
-      }
-      float dist = qscore[l] + s;
+      float dist = qscore[l] + pre_pos(pos, a.pre + static_cast<uint64_t>(l) * table);
       dist = dist == dist ? dist : __builtin_huge_valf();
       s_cand[i] = make_key(dist, pos);
     }
@@ -1299,6 +1346,14 @@ __device__ void ivf_scan_query(const ScanArgs& a, const uint32_t q) {
 /// Block b scans query b; with a query list, the blocks take the listed queries in turn.
 template <int MPW>
 __global__ void __launch_bounds__(kScanThreads) ivf_scan_kernel(ScanArgs a) {
+  if (!a.qlist && a.lut_global) {
+    // Tables in global memory: a bounded grid, the work-groups taking the queries in turn.
+    for (uint32_t q = blockIdx.x; q < a.nq; q += gridDim.x) {
+      ivf_scan_query<MPW>(a, q);
+      __syncthreads();  // the next query reuses the block's LDS and table region
+    }
+    return;
+  }
   if (!a.qlist) {
     ivf_scan_query<MPW>(a, blockIdx.x);
     return;
@@ -2311,7 +2366,7 @@ struct qvh_ivfpq {
   hipStream_t stream = nullptr;
   std::mutex mu;
   DeviceBuffer w_x, w_res, w_assign, w_afb, w_codes, w_codes_p, w_t1, w_dest, w_shift;
-  DeviceBuffer w_q, w_scores, w_probes, w_bits, w_refs, w_dist, w_bytes, w_key, w_order;
+  DeviceBuffer w_q, w_scores, w_probes, w_bits, w_refs, w_dist, w_bytes, w_key, w_order, w_lut;
   DeviceBuffer w_pkeys, w_pcnt, w_pdone;  // sliced queries of the streaming scan
   DeviceBuffer w_delta, w_fb;             // certificate bounds; uncertified queries (count, list)
   bool last_certified = false;            // the last search ranked approximately (w_fb holds its count)
@@ -2501,14 +2556,21 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   a.out_refs = d_refs;
   a.out_dist = d_dist;
   a.cand_cap = cand_cap;
+  // m above kScanMaxLdsM: the block-buffer scan's tables in global memory, one per work-group, and
+  // a bounded grid whose work-groups take the queries in turn.
+  const bool table_global = h->m > kScanMaxLdsM;
+  const size_t table_bytes = static_cast<size_t>(h->m) * 256 * sizeof(float);
+  const uint64_t block_grid = std::max<uint64_t>(
+      1, std::min<uint64_t>({nq, 2 * static_cast<uint64_t>(std::max(h->cus, 1)), kScanGlobalTableBytes / table_bytes}));
   const size_t lds = static_cast<size_t>(cand_cap) * sizeof(uint64_t) + (nprobe + 1) * sizeof(uint64_t) +
-                     ((nprobe + 1) & ~1u) * sizeof(uint32_t) + static_cast<size_t>(h->m) * 256 * sizeof(float);
+                     ((nprobe + 1) & ~1u) * sizeof(uint32_t) + (table_global ? 0 : table_bytes);
   if (lds > 150 * 1024) {
     throw Failure(QVH_EUNSUPPORTED, "IVF-PQ search: " + std::to_string(keep_sel) + " candidates (k * refine_factor) with m = " +
                                         std::to_string(h->m) + " and nprobe = " + std::to_string(nprobe) +
                                         " exceed the on-chip candidate buffer");
   }
-  const dim3 grid(static_cast<unsigned>(nq));
+  if (table_global) a.lut_global = static_cast<float*>(h->w_lut.reserve(block_grid * table_bytes));
+  const dim3 grid(static_cast<unsigned>(table_global ? block_grid : nq));
   const uint32_t mpw = h->mp / 4;
   // The block-buffer scan (every table mode, any candidate count up to kMaxKeepSel).
   auto launch_block_scan = [&](const ScanArgs& args, dim3 g) {
@@ -2527,10 +2589,8 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
       go(ivf_scan_kernel<8>);
     } else if (mpw <= 16) {
       go(ivf_scan_kernel<16>);
-    } else if (mpw <= 32) {
-      go(ivf_scan_kernel<32>);
     } else {
-      throw Failure(QVH_EUNSUPPORTED, "IVF-PQ device path supports m <= 128");
+      go(ivf_scan_kernel<32>);  // 128 sub-spaces per pass over a code
     }
   };
   if (keep == 0) {
@@ -2646,7 +2706,8 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
     fa.keep_sel = fa.keep;
     fa.qlist = fb + 1;
     fa.qcount = fb;
-    launch_block_scan(fa, dim3(static_cast<unsigned>(std::min<uint64_t>(nq, 2 * static_cast<uint64_t>(std::max(h->cus, 1))))));
+    launch_block_scan(fa, dim3(static_cast<unsigned>(table_global ? block_grid
+                                                                  : std::min<uint64_t>(nq, 2 * static_cast<uint64_t>(std::max(h->cus, 1))))));
     QVH_HIP(hipGetLastError());
   }
   if (h->timed_bytes) {
@@ -2669,9 +2730,7 @@ qvh_status qvh_ivfpq_create(uint32_t dim, int metric, uint32_t nlist, uint32_t m
     QVH_REQUIRE(metric >= QVH_METRIC_L2 && metric <= QVH_METRIC_COSINE, "unknown metric");
     QVH_REQUIRE(nlist >= 1 && nlist <= (1u << 24), "nlist must be in [1, 2^24]");
     QVH_REQUIRE(m >= 1 && dim % m == 0, "PQ: dimension must be divisible by m");
-    if (m > 128) {  // the scan's per-query table, m x 256 floats, lives in LDS
-      throw Failure(QVH_EUNSUPPORTED, "IVF-PQ device path supports m <= 128");
-    }
+
     const int dev = current_device();
     auto* h = new qvh_ivfpq;
     h->dim = dim;

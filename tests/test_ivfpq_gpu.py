@@ -214,6 +214,23 @@ def test_ivfpq_refine_tail_dims(oracle, metric, dim, m):
             print(refine, nprobe, compare_search(oracle, idx, st, q, 10, nprobe, refine))
 
 
+@pytest.mark.parametrize("metric,dim,m,nlist,refine", [("l2", 512, 256, 16, 0), ("ip", 384, 192, 16, 0),
+                                                       ("cosine", 512, 256, 16, 3), ("l2", 256, 256, 1100, 2)])
+def test_ivfpq_more_than_128_subspaces(oracle, metric, dim, m, nlist, refine):
+    """m above 128 (the reference has no limit on m, src/ivfpq_index.cc:95-103): the per-query table
+    no longer fits LDS, so the block-buffer scan keeps it in global memory and sums each code 128
+    sub-spaces at a time, in order. L2 with the precomputed table (its exact re-score too), inner
+    product, cosine with refine, and L2 with residual tables (nlist 1100 x m 256 exceeds the
+    precomputed table's 256 MiB budget)."""
+    base = clustered(5_000, dim, 12, seed=60 + m)
+    q = clustered(60, dim, 12, seed=61 + m)
+    idx, st = build_pair(oracle, base, metric, nlist, m, refine > 0, iters=3)
+    if metric == "l2":
+        assert (st.precomputed is None) == (nlist == 1100)
+    for nprobe in (2, 9):
+        print(nprobe, compare_search(oracle, idx, st, q, 10, nprobe, refine))
+
+
 @pytest.mark.parametrize("dim,m", [(120, 30), (56, 14), (21, 7), (124, 31)])
 def test_ivfpq_partial_code_dwords(oracle, dim, m):
     """m not a multiple of four (the last code dword carries pad bytes) with the precomputed L2
