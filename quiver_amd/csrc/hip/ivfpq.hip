@@ -857,7 +857,9 @@ constexpr int kScanRound = 4;        // codes per thread between buffer checks
 constexpr uint32_t kMaxKeepSel = kCandCap - kScanThreads * kScanRound;  // 1024
 // Larger m keeps the block-buffer scan's per-query table (m x 256 floats) in global memory.
 constexpr uint32_t kScanMaxLdsM = 128;
+constexpr size_t kScanMaxLds = 150 * 1024;  // dynamic LDS the block-buffer scan takes at most
 constexpr uint64_t kScanGlobalTableBytes = 256ull << 20;  // bound on those tables, all work-groups
+constexpr uint64_t kScanGlobalCandBytes = 512ull << 20;   // and on candidate buffers in global memory
 // Larger selections take a larger buffer: keep_sel + kScanThreads * kScanRound slots, rounded up to
 // a power of two, as far as LDS allows.
 
@@ -939,6 +941,9 @@ struct ScanArgs {
   // Block-buffer scan with m above kScanMaxLdsM: the per-query table lives in global memory, one
   // [m][256] region per work-group, and the work-groups take the queries in turn.
   float* lut_global;  // [gridDim.x][m][256], or null: the table is in LDS
+  // Block-buffer scan whose candidate buffer would not fit LDS next to the rest: one cand_cap-key
+  // region of global memory per work-group (the same bounded grid).
+  uint64_t* cand_global;  // [gridDim.x][cand_cap], or null: the buffer is in LDS
 };
 
 /// Certificate of an approximate selection (mode pre). The scan kept the keep_sel best candidates by
@@ -1102,8 +1107,10 @@ __device__ __forceinline__ float adc_sum_rows(const float* lut, const uint32_t (
 template <int MPW>
 __device__ void ivf_scan_query(const ScanArgs& a, const uint32_t q) {
   extern __shared__ __attribute__((aligned(16))) unsigned char s_raw[];
-  uint64_t* s_cand = reinterpret_cast<uint64_t*>(s_raw);                       // [cand_cap]
-  uint64_t* s_pstart = s_cand + a.cand_cap;                                    // [nprobe + 1] flattened starts
+  // [cand_cap]: in LDS, or in this work-group's region of global memory for large selections
+  uint64_t* s_cand = a.cand_global ? a.cand_global + static_cast<uint64_t>(blockIdx.x) * a.cand_cap
+                                   : reinterpret_cast<uint64_t*>(s_raw);
+  uint64_t* s_pstart = reinterpret_cast<uint64_t*>(s_raw) + (a.cand_global ? 0u : a.cand_cap);  // [nprobe + 1]
   uint32_t* s_plist = reinterpret_cast<uint32_t*>(s_pstart + a.nprobe + 1);    // [nprobe]
   // [m][256]: in LDS, or in this work-group's region of global memory for m above kScanMaxLdsM
   float* s_lut = a.lut_global ? a.lut_global + static_cast<uint64_t>(blockIdx.x) * a.m * 256
@@ -1346,8 +1353,9 @@ __device__ void ivf_scan_query(const ScanArgs& a, const uint32_t q) {
 /// Block b scans query b; with a query list, the blocks take the listed queries in turn.
 template <int MPW>
 __global__ void __launch_bounds__(kScanThreads) ivf_scan_kernel(ScanArgs a) {
-  if (!a.qlist && a.lut_global) {
-    // Tables in global memory: a bounded grid, the work-groups taking the queries in turn.
+  if (!a.qlist && (a.lut_global || a.cand_global)) {
+    // Tables or candidate buffers in global memory: a bounded grid, the work-groups taking the
+    // queries in turn.
     for (uint32_t q = blockIdx.x; q < a.nq; q += gridDim.x) {
       ivf_scan_query<MPW>(a, q);
       __syncthreads();  // the next query reuses the block's LDS and table region
@@ -2366,7 +2374,7 @@ struct qvh_ivfpq {
   hipStream_t stream = nullptr;
   std::mutex mu;
   DeviceBuffer w_x, w_res, w_assign, w_afb, w_codes, w_codes_p, w_t1, w_dest, w_shift;
-  DeviceBuffer w_q, w_scores, w_probes, w_bits, w_refs, w_dist, w_bytes, w_key, w_order, w_lut;
+  DeviceBuffer w_q, w_scores, w_probes, w_bits, w_refs, w_dist, w_bytes, w_key, w_order, w_lut, w_cand;
   DeviceBuffer w_pkeys, w_pcnt, w_pdone;  // sliced queries of the streaming scan
   DeviceBuffer w_delta, w_fb;             // certificate bounds; uncertified queries (count, list)
   bool last_certified = false;            // the last search ranked approximately (w_fb holds its count)
@@ -2452,7 +2460,7 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   }
   if (keep_sel > (uint64_t{1} << 20)) {
     throw Failure(QVH_EUNSUPPORTED, "IVF-PQ search: " + std::to_string(keep_sel) +
-                                        " candidates (k * refine_factor) exceed the on-chip candidate buffer");
+                                        " candidates (k * refine_factor) exceed the device path's 2^20");
   }
   uint32_t cand_cap = kCandCap;
   while (cand_cap < keep_sel + kScanThreads * kScanRound) cand_cap *= 2;
@@ -2560,17 +2568,23 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   // a bounded grid whose work-groups take the queries in turn.
   const bool table_global = h->m > kScanMaxLdsM;
   const size_t table_bytes = static_cast<size_t>(h->m) * 256 * sizeof(float);
+  // A candidate buffer that does not fit LDS beside the rest moves to global memory the same way.
+  const size_t cand_bytes = static_cast<size_t>(cand_cap) * sizeof(uint64_t);
+  const size_t lds_rest =
+      (nprobe + 1) * sizeof(uint64_t) + ((nprobe + 1) & ~1u) * sizeof(uint32_t) + (table_global ? 0 : table_bytes);
+  const bool cand_global = cand_bytes + lds_rest > kScanMaxLds;
   const uint64_t block_grid = std::max<uint64_t>(
-      1, std::min<uint64_t>({nq, 2 * static_cast<uint64_t>(std::max(h->cus, 1)), kScanGlobalTableBytes / table_bytes}));
-  const size_t lds = static_cast<size_t>(cand_cap) * sizeof(uint64_t) + (nprobe + 1) * sizeof(uint64_t) +
-                     ((nprobe + 1) & ~1u) * sizeof(uint32_t) + (table_global ? 0 : table_bytes);
-  if (lds > 150 * 1024) {
-    throw Failure(QVH_EUNSUPPORTED, "IVF-PQ search: " + std::to_string(keep_sel) + " candidates (k * refine_factor) with m = " +
-                                        std::to_string(h->m) + " and nprobe = " + std::to_string(nprobe) +
-                                        " exceed the on-chip candidate buffer");
+      1, std::min<uint64_t>({nq, 2 * static_cast<uint64_t>(std::max(h->cus, 1)), kScanGlobalTableBytes / table_bytes,
+                             cand_global ? kScanGlobalCandBytes / cand_bytes : nq}));
+  const size_t lds = (cand_global ? 0 : cand_bytes) + lds_rest;
+  if (lds > kScanMaxLds) {
+    throw Failure(QVH_EUNSUPPORTED, "IVF-PQ search: nprobe = " + std::to_string(nprobe) +
+                                        " probed lists exceed the block-buffer scan's on-chip list table");
   }
   if (table_global) a.lut_global = static_cast<float*>(h->w_lut.reserve(block_grid * table_bytes));
-  const dim3 grid(static_cast<unsigned>(table_global ? block_grid : nq));
+  if (cand_global) a.cand_global = static_cast<uint64_t*>(h->w_cand.reserve(block_grid * cand_bytes));
+  const bool bounded_grid = table_global || cand_global;
+  const dim3 grid(static_cast<unsigned>(bounded_grid ? block_grid : nq));
   const uint32_t mpw = h->mp / 4;
   // The block-buffer scan (every table mode, any candidate count up to kMaxKeepSel).
   auto launch_block_scan = [&](const ScanArgs& args, dim3 g) {
@@ -2706,7 +2720,7 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
     fa.keep_sel = fa.keep;
     fa.qlist = fb + 1;
     fa.qcount = fb;
-    launch_block_scan(fa, dim3(static_cast<unsigned>(table_global ? block_grid
+    launch_block_scan(fa, dim3(static_cast<unsigned>(bounded_grid ? block_grid
                                                                   : std::min<uint64_t>(nq, 2 * static_cast<uint64_t>(std::max(h->cus, 1))))));
     QVH_HIP(hipGetLastError());
   }

@@ -214,6 +214,18 @@ def test_ivfpq_refine_tail_dims(oracle, metric, dim, m):
             print(refine, nprobe, compare_search(oracle, idx, st, q, 10, nprobe, refine))
 
 
+@pytest.mark.parametrize("metric,k,refine", [("l2", 12_000, 0), ("ip", 20_000, 0), ("cosine", 5_000, 3)])
+def test_ivfpq_candidate_sets_beyond_lds(oracle, metric, k, refine):
+    """Candidate sets whose buffer does not fit LDS beside the query table (L2 k = 12,000 keeps
+    18,000 for the re-score; inner product 20,000; cosine 15,000 before refine): the block-buffer
+    scan keeps each work-group's buffer in global memory; equal to the oracle."""
+    base = clustered(30_000, 32, 24, seed=51)
+    q = clustered(12, 32, 24, seed=52)
+    idx, st = build_pair(oracle, base, metric, 16, 8, refine > 0, iters=3)
+    print(k, refine, compare_search(oracle, idx, st, q, k, 16, refine))
+    print(k, refine, compare_search(oracle, idx, st, q, k, 5, refine))
+
+
 @pytest.mark.parametrize("metric,dim,m,nlist,refine", [("l2", 512, 256, 16, 0), ("ip", 384, 192, 16, 0),
                                                        ("cosine", 512, 256, 16, 3), ("l2", 256, 256, 1100, 2)])
 def test_ivfpq_more_than_128_subspaces(oracle, metric, dim, m, nlist, refine):
