@@ -1732,8 +1732,14 @@ uint32_t fallback_splits(uint64_t n, int cus) {
   return static_cast<uint32_t>(g);
 }
 
-/// Row stride in floats: the dimension rounded up to 16 (the MFMA scan's K step).
-uint32_t padded_dim(uint32_t dim) { return (dim + 15u) / 16u * 16u; }
+/// Row stride in floats. Up to kMaxDp (the register-resident scan): the dimension rounded up to 8,
+/// at least 16 (each MFMA lane half takes dp / 2 dims in float4 steps, and a row stride of dp + 4
+/// floats is an odd multiple of 4, which keeps the b128 tile reads conflict-free); dim 100 runs 53
+/// MFMA steps per tile instead of 57. Wider rows: rounded up to 16 (the chunked scan).
+uint32_t padded_dim(uint32_t dim) {
+  if (dim <= static_cast<uint32_t>(kMaxDp)) return std::max(16u, (dim + 7u) / 8u * 8u);
+  return (dim + 15u) / 16u * 16u;
+}
 
 /// Per-lane list length of the MFMA scan with the shared bound for top-k: the re-score selects the
 /// KL best by GEMM-form distance, and the certificate needs some of them beyond the k-th, so KL
@@ -1816,12 +1822,19 @@ void launch_scan(uint32_t dp, int kl, dim3 grid, const ScanArgs& a, hipStream_t 
   }
   switch (dp) {
     case 16: launch_scan_dp<16>(kl, l2, filter, grid, a, s); break;
+    case 24: launch_scan_dp<24>(kl, l2, filter, grid, a, s); break;
     case 32: launch_scan_dp<32>(kl, l2, filter, grid, a, s); break;
+    case 40: launch_scan_dp<40>(kl, l2, filter, grid, a, s); break;
     case 48: launch_scan_dp<48>(kl, l2, filter, grid, a, s); break;
+    case 56: launch_scan_dp<56>(kl, l2, filter, grid, a, s); break;
     case 64: launch_scan_dp<64>(kl, l2, filter, grid, a, s); break;
+    case 72: launch_scan_dp<72>(kl, l2, filter, grid, a, s); break;
     case 80: launch_scan_dp<80>(kl, l2, filter, grid, a, s); break;
+    case 88: launch_scan_dp<88>(kl, l2, filter, grid, a, s); break;
     case 96: launch_scan_dp<96>(kl, l2, filter, grid, a, s); break;
+    case 104: launch_scan_dp<104>(kl, l2, filter, grid, a, s); break;
     case 112: launch_scan_dp<112>(kl, l2, filter, grid, a, s); break;
+    case 120: launch_scan_dp<120>(kl, l2, filter, grid, a, s); break;
     case 128: launch_scan_dp<128>(kl, l2, filter, grid, a, s); break;
     default: throw Failure(QVH_EUNSUPPORTED, "flat scan: unsupported padded dimension");
   }

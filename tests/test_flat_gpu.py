@@ -88,13 +88,28 @@ def test_normalize_entry_point_is_bit_exact(oracle):
         assert np.array_equal(got.view(np.uint32), exp.view(np.uint32)), d
 
 
-@pytest.mark.parametrize("dim", [1, 5, 13, 16, 24, 33, 64, 100, 127, 128])
+@pytest.mark.parametrize("dim", [1, 5, 13, 16, 24, 33, 50, 64, 70, 85, 100, 117, 127, 128])
 def test_awkward_dimensions(oracle, dim):
+    """Rows padded to a multiple of 8 up to 128 dims (at least 16): every register-scan width from
+    16 to 128 in steps of 8 is met (33 -> 40, 50 -> 56, 70 -> 72, 85 -> 88, 100 -> 104, 117 -> 120)."""
     rng = np.random.default_rng(dim)
     base = rng.standard_normal((3000, dim)).astype(np.float32)
     q = rng.standard_normal((37, dim)).astype(np.float32)
     for metric in ("l2", "ip"):
         _check(oracle, base, q, 7, metric)
+
+
+@pytest.mark.parametrize("dim", [50, 100, 117])
+@pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
+def test_eight_padded_widths_full_blocks(oracle, dim, metric):
+    """Rows padded to 56, 104 and 120 floats under whole 256-query blocks of the MFMA scan (the
+    full-tile form, several row splits), unfiltered and with a 60% filter."""
+    rng = np.random.default_rng(300 + dim)
+    base = rng.standard_normal((40_000, dim)).astype(np.float32)
+    q = rng.standard_normal((400, dim)).astype(np.float32)
+    print(_check(oracle, base, q, 10, metric))
+    allowed = np.sort(rng.choice(40_000, 24_000, replace=False)).astype(np.uint64)
+    print(_check(oracle, base, q, 10, metric, allowed))
 
 
 @pytest.mark.parametrize("dim", [129, 200, 257, 384, 768, 1000, 1024])
