@@ -744,20 +744,33 @@ __global__ void __launch_bounds__(256) probe_select_kernel(const float* __restri
   };
   uint64_t cur = smallest();
   if (nprobe <= 64) {
-    // Threshold T = the nprobe-th smallest of the 64 lane minima: nprobe distinct lanes hold a key
-    // <= T, so the nprobe smallest keys are all <= T. The keys <= T (usually a few dozen) are
-    // sorted in LDS; more than 128 of them falls through to the selection loop below.
-    uint64_t v = cur;
+    // Threshold T = the nprobe-th smallest of the 64 lane minima (nprobe <= 32), or of the lanes'
+    // two smallest keys each (33..64: the lane minima alone admit a few hundred keys there): at
+    // least nprobe distinct keys are <= T, so the nprobe smallest keys are all <= T. The keys <= T
+    // (usually a few dozen past nprobe) are sorted in LDS; more than 128 of them falls through to
+    // the selection loop below.
+    uint64_t T;
+    if (nprobe <= 32) {
+      uint64_t v = cur;
 #pragma unroll
-    for (int size = 2; size <= 64; size <<= 1) {
+      for (int size = 2; size <= 64; size <<= 1) {
 #pragma unroll
-      for (int stride = size >> 1; stride > 0; stride >>= 1) {
-        const uint64_t o = lane_xor_u64(v, stride);
-        const bool keep_min = ((lane & stride) == 0) == ((lane & size) == 0);
-        v = keep_min ? (o < v ? o : v) : (o > v ? o : v);
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+          const uint64_t o = lane_xor_u64(v, stride);
+          const bool keep_min = ((lane & stride) == 0) == ((lane & size) == 0);
+          v = keep_min ? (o < v ? o : v) : (o > v ? o : v);
+        }
       }
+      T = __shfl(v, static_cast<int>(nprobe) - 1, 64);
+    } else {
+      uint64_t second = ~0ull;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) second = key[i] != cur && key[i] < second ? key[i] : second;
+      uint64_t two[2] = {cur, second};
+      wave_sort<2>(two);  // element e = i * 64 + lane in two[i]
+      const int e = static_cast<int>(nprobe) - 1;
+      T = __shfl(e < 64 ? two[0] : two[1], e & 63, 64);
     }
-    const uint64_t T = __shfl(v, static_cast<int>(nprobe) - 1, 64);
     uint32_t n = 0;
 #pragma unroll
     for (int i = 0; i < PER; ++i) n += static_cast<uint32_t>(__popcll(__ballot(key[i] <= T)));
