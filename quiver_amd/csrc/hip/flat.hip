@@ -1507,6 +1507,7 @@ __device__ void merge_sorted_lists(const uint32_t* __restrict__ part_r, const fl
 constexpr uint32_t kSelectMergeMaxK = 256;
 constexpr uint32_t kSelectMergeLists = 1024;
 constexpr uint32_t kSelectMergeCap = 4096;
+constexpr uint32_t kSelectMergeFastK = 11;  // k * k <= 128: the gathered keys fit one wave's sort
 
 __global__ void __launch_bounds__(1024) flat_merge_select_kernel(const uint32_t* __restrict__ part_r,
                                                                  const float* __restrict__ part_d,
@@ -1526,10 +1527,40 @@ __global__ void __launch_bounds__(1024) flat_merge_select_kernel(const uint32_t*
   const uint32_t* pr = part_r + static_cast<uint64_t>(q) * nsplit * k;
   const float* pd = part_d + static_cast<uint64_t>(q) * nsplit * k;
   const uint64_t o = static_cast<uint64_t>(tid) * k;
-  s_heads[tid] = tid < nsplit ? make_key(pd[o], pr[o]) : ~0ull;
+  const uint64_t head = tid < nsplit ? make_key(pd[o], pr[o]) : ~0ull;
   if (tid == 0) s_count = 0;
-  block_sort_keys(s_heads, kSelectMergeLists);
-  const uint64_t t0 = s_heads[k - 1];
+  uint64_t t0;
+  const bool small_k = k <= kSelectMergeFastK;  // block-uniform
+  if (small_k) {
+    // Each wave sorts its 64 heads in registers; wave 0 then walks the 16 sorted runs, taking the
+    // smallest remaining head k times (lane i < 16 follows run i), instead of a 1024-key block
+    // bitonic sort (55 barrier steps).
+    __shared__ uint64_t s_t0;
+    uint64_t h[1] = {head};
+    wave_sort<1>(h);
+    s_heads[tid] = h[0];
+    __syncthreads();
+    if (tid < 64) {
+      const uint32_t lane = tid;
+      uint32_t at = 0;
+      uint64_t cur = lane < 16 ? s_heads[lane * 64] : ~0ull;
+      uint64_t m = ~0ull;
+      for (uint32_t step = 0; step < k; ++step) {
+        m = wave_min_u64(cur);
+        if (lane < 16 && cur == m && m != ~0ull) {
+          ++at;
+          cur = at < 64 ? s_heads[lane * 64 + at] : ~0ull;
+        }
+      }
+      if (lane == 0) s_t0 = m;
+    }
+    __syncthreads();
+    t0 = s_t0;
+  } else {
+    s_heads[tid] = head;
+    block_sort_keys(s_heads, kSelectMergeLists);
+    t0 = s_heads[k - 1];
+  }
   if (tid < nsplit) {
     // this list's keys <= t0, eight at a time
     for (uint32_t p0 = 0; p0 < k; p0 += 8) {
@@ -1553,6 +1584,19 @@ __global__ void __launch_bounds__(1024) flat_merge_select_kernel(const uint32_t*
   const uint32_t c = s_count;
   if (overflow && tid == 0) overflow[q] = c > kSelectMergeCap ? 1u : 0u;
   if (c > kSelectMergeCap) return;  // block-uniform
+  if (small_k) {
+    // At most k * k <= 121 keys: wave 0 sorts them in registers and writes the k best.
+    if (tid < 64) {
+      uint64_t x[2] = {tid < c ? s_cand[tid] : ~0ull, tid + 64 < c ? s_cand[tid + 64] : ~0ull};
+      wave_sort<2>(x);  // element e = i * 64 + lane in x[i]
+      if (tid < k) {
+        const bool real = tid < c;
+        out_rows[oq * k + tid] = real ? static_cast<uint32_t>(x[0]) : QVH_EMPTY_ROW;
+        out_dist[oq * k + tid] = real ? ordered_to_float(static_cast<uint32_t>(x[0] >> 32)) : __builtin_huge_valf();
+      }
+    }
+    return;
+  }
   uint32_t n2 = 1;
   while (n2 < c) n2 <<= 1;
   for (uint32_t i = c + tid; i < n2; i += 1024) s_cand[i] = ~0ull;
