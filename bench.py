@@ -287,12 +287,21 @@ def bench_ivfpq(args, hip: Hip, qvh: Qvh, base, queries):
                   "timing")
         return a.value, b.value, nb.value
 
+    # Each sweep point: one search that also counts the probed code bytes (level 2), then five
+    # back-to-back searches with stage events only (level 1); the stage times are the median of the
+    # last four, so a point is measured at the same steady state as the timed loop below.
     sweep = {}
     for p in (1, 4, 8, 16, 32, 64):
-        search(p)
+        qvh.check(qvh.lib.qvh_ivfpq_set_timing(h, 2), "timing")
         search(p)
         qvh.check(qvh.lib.qvh_ivfpq_sync(h), "sync")
-        sel, scan, nbytes = timing()
+        nbytes = timing()[2]
+        qvh.check(qvh.lib.qvh_ivfpq_set_timing(h, 1), "timing")
+        runs = []
+        for _ in range(5):
+            search(p)
+            runs.append(timing(with_bytes=False))
+        sel, scan = (float(np.median([r[i] for r in runs[1:]])) for i in (0, 1))
         sweep[str(p)] = {"select_ms": sel, "scan_ms": scan, "code_bytes": nbytes,
                          "scan_hbm_frac": nbytes / (scan * 1e-3) / (HBM_PEAK_GBS * 1e9)}
 
