@@ -1545,9 +1545,9 @@ __device__ __forceinline__ float adc_sum_rotated(const float* lut, const uint32_
   return s;
 }
 
-template <int MPW, bool FULL, int CAP, bool ROT>
+template <int MPW, bool FULL, int CAP, bool ROT, int W>
 __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
-  constexpr int kStreamWaves = stream_waves<CAP>();
+  constexpr int kStreamWaves = W;
   constexpr int kStreamThreads = kStreamWaves * 64;
   constexpr int QN = CAP / 64;     // queue keys per lane
   constexpr int kRows = 4 * MPW;   // table rows: the m sub-spaces, then zero rows
@@ -1951,10 +1951,10 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
     a.out_refs[static_cast<uint64_t>(q) * a.k + j] = ref;
     a.out_dist[static_cast<uint64_t>(q) * a.k + j] = d;
   };
-  // Eight-wave blocks cut only a list longer than CAP / 2 (a key a cut would drop has keep_sel
-  // better ones in its own list). Four-wave blocks always cut, which keeps wave 0's sort below at
-  // <= 4 keep_sel keys.
-  if constexpr (kStreamWaves == 4) {
+  // Blocks with 256- or 512-entry queues cut only a list longer than CAP / 2 (a key a cut would
+  // drop has keep_sel better ones in its own list). Four-wave blocks with smaller queues always
+  // cut, which keeps wave 0's sort below at <= 4 keep_sel keys.
+  if constexpr (kStreamWaves == 4 && CAP <= 192) {
     flush(64);
     // Single-wave finish (four waves, k and keep_sel <= 64): the four cut lists (<= 64 keys each)
     // are packed in LDS, then wave 0 alone sorts, re-scores and emits them in registers, with no
@@ -2059,14 +2059,14 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
     if (static_cast<uint32_t>(lane) < a.k) emit(lane, static_cast<uint32_t>(lane) < min(cnt_f, a.k), key);
     return;
   }
-  // Eight waves (keep_sel <= CAP / 2): each wave sorts its list (<= CAP / 2 keys, NK per lane) in
-  // registers; three rounds of pairwise merges then keep the CAP / 2 smallest: the elementwise
-  // minimum of one sorted list and the other reversed holds the CAP / 2 smallest of both as a
-  // bitonic sequence, which a register bitonic merge orders. Wave 0's region ends with the block's
-  // CAP / 2 smallest, sorted. (Four-wave blocks returned above; this is compiled for them too but
-  // never reached.)
+  // Queues of 256 or 512 entries (keep_sel <= CAP / 2): each wave sorts its list (<= CAP / 2
+  // keys, NK per lane) in registers; log2(waves) rounds of pairwise merges then keep the CAP / 2
+  // smallest: the elementwise minimum of one sorted list and the other reversed holds the CAP / 2
+  // smallest of both as a bitonic sequence, which a register bitonic merge orders. Wave 0's region
+  // ends with the block's CAP / 2 smallest, sorted. (Blocks with smaller queues returned above;
+  // this is compiled for them too but never reached.)
   uint32_t merged = 0;
-  if constexpr (kStreamWaves == 8 && CAP >= 256) {
+  if constexpr (CAP >= 256) {
   if (cnt > static_cast<uint32_t>(CAP / 2)) flush(CAP / 2);
   constexpr int NK = CAP / 128;
   constexpr int kList = CAP / 2;
@@ -2215,17 +2215,18 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
   for (uint32_t j = tid; j < a.k; j += kStreamThreads) emit(j, j < nout, s_queue[j < nout ? j : 0]);
 }
 
-// Up to 32 code bytes.
-template <int MPW, bool FULL, int CAP, bool ROT = false>
-__global__ void __launch_bounds__(stream_waves<CAP>() * 64)
-__attribute__((amdgpu_waves_per_eu(stream_waves<CAP>() == 4 || CAP == 512 ? 4 : 6))) ivf_stream_kernel(ScanArgs a) {
-  stream_scan<MPW, FULL, CAP, ROT>(a);
+// Up to 32 code bytes. W waves per block (four for queues of up to 192 entries, eight for 512,
+// either for 256).
+template <int MPW, bool FULL, int CAP, bool ROT = false, int W = stream_waves<CAP>()>
+__global__ void __launch_bounds__(W * 64)
+__attribute__((amdgpu_waves_per_eu(W == 4 || CAP == 512 ? 4 : 6))) ivf_stream_kernel(ScanArgs a) {
+  stream_scan<MPW, FULL, CAP, ROT, W>(a);
 }
 
 // 33 to 64 code bytes: no register cap.
-template <bool FULL, int CAP>
-__global__ void __launch_bounds__(stream_waves<CAP>() * 64) ivf_stream_wide_kernel(ScanArgs a) {
-  stream_scan<16, FULL, CAP, false>(a);
+template <bool FULL, int CAP, bool ROT = false, int W = stream_waves<CAP>()>
+__global__ void __launch_bounds__(W * 64) ivf_stream_wide_kernel(ScanArgs a) {
+  stream_scan<16, FULL, CAP, false, W>(a);
 }
 
 void launch_nearest(bool sqdiff, const NearestArgs& a, uint32_t nsub, hipStream_t s) {
@@ -2641,11 +2642,16 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   // candidates the 128-entry queues measured 1-2% faster).
   const bool mid_sel = small_sel && a.keep_sel > 48;
   const uint32_t cap = small_sel ? (mid_sel ? 192 : 128) : big_sel ? 512 : 256;
+  // 256-entry queues run on four waves, except for L2 with the precomputed table, whose block
+  // re-scores its selection: 1.18M x 100 cosine, refine 8 (80 candidates), nprobe 16 0.69 ->
+  // 0.66 ms and nprobe 64 1.86 -> 1.81 ms on four waves; 1M x 128 L2, k = 50 (75 candidates),
+  // nprobe 32 1.16 -> 1.25 ms.
+  const bool four256 = cap == 256 && mode != kModePre;
   const size_t rows = 4 * mpw_t;
   // LDS of the streaming kernels: the table (static LDS for codes of up to 32 bytes), the wave
   // queues and the probed-list arrays (dynamic).
   const size_t lds_table = rows * 256 * sizeof(float);
-  const uint32_t waves = small_sel ? stream_waves<128>() : stream_waves<256>();
+  const uint32_t waves = small_sel || four256 ? 4u : 8u;
   const size_t lds_total = lds_table + static_cast<size_t>(waves) * cap * sizeof(uint64_t) +
                            (4 * static_cast<size_t>(nprobe) + 2 + waves) * sizeof(uint32_t);
   const size_t lds2 = mpw_t > 8 ? lds_total : lds_total - lds_table;
@@ -2685,7 +2691,8 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
     };
 #define QVH_STREAM_CAP(KERNEL, ...)                                                                       \
   (small_sel ? (mid_sel ? launch2(KERNEL<__VA_ARGS__, 192>) : launch2(KERNEL<__VA_ARGS__, 128>))          \
-             : big_sel ? launch2(KERNEL<__VA_ARGS__, 512>) : launch2(KERNEL<__VA_ARGS__, 256>))
+   : big_sel ? launch2(KERNEL<__VA_ARGS__, 512>)                                                          \
+   : four256 ? launch2(KERNEL<__VA_ARGS__, 256, false, 4>) : launch2(KERNEL<__VA_ARGS__, 256>))
 #define QVH_STREAM(MPW_) QVH_STREAM_CAP(ivf_stream_kernel, MPW_, true)
     // Bank-rotated lookups: L2 with the precomputed table (re-scored exactly afterwards), four
     // dims per sub-space, 16- or 32-byte codes.

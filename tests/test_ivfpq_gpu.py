@@ -147,7 +147,8 @@ def test_ivfpq_small_matches_oracle(oracle, metric, store, refine):
 def test_ivfpq_batch_sizes_and_slices(oracle, metric, refine):
     """Batches below one resident generation of blocks scan each query in slices merged by the last
     one to finish (1 query, 300); larger ones scan whole queries (6000). refine 8 keeps 80
-    candidates: the eight-wave kernel and its block merge; the others take the single-wave finish."""
+    candidates (120 with L2's re-score margin): 256-entry queues and the block merge, on four waves
+    (inner product, cosine) or eight (L2); the others take the single-wave finish."""
     base = clustered(10_000, 32, 50, 12)
     idx, st = build_pair(oracle, base, metric, 64, 16, metric != "ip")
     for nq in (1, 300, 6_000):
@@ -165,6 +166,19 @@ def test_ivfpq_large_candidate_sets(oracle, metric, k, refine):
     sliced small batch."""
     base = clustered(12_000, 32, 24, seed=41)
     q = clustered(700, 32, 24, seed=42)
+    idx, st = build_pair(oracle, base, metric, 64, 8, refine > 0)
+    for qs in (q, q[:3]):
+        print(k, refine, qs.shape[0], compare_search(oracle, idx, st, qs, k, 16, refine))
+
+
+@pytest.mark.parametrize("metric,k,refine", [("ip", 65, 0), ("ip", 100, 0), ("cosine", 128, 0), ("cosine", 12, 8),
+                                             ("l2", 50, 0)])
+def test_ivfpq_256_entry_queues(oracle, metric, k, refine):
+    """Candidate sets of 65..128 stream through 256-entry wave queues: four-wave blocks for inner
+    product and cosine, eight-wave blocks for L2 (k = 50: 75 candidates with the re-score margin),
+    merged across the block's waves; whole queries and a sliced small batch against the oracle."""
+    base = clustered(12_000, 32, 24, seed=43)
+    q = clustered(700, 32, 24, seed=44)
     idx, st = build_pair(oracle, base, metric, 64, 8, refine > 0)
     for qs in (q, q[:3]):
         print(k, refine, qs.shape[0], compare_search(oracle, idx, st, qs, k, 16, refine))
