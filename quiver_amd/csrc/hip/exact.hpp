@@ -141,6 +141,66 @@ __device__ inline float exact_group8(const float* __restrict__ a, const float* _
   return sum;
 }
 
+/// exact_group8 for NC pairs (a, b[c]) at once, with the same arithmetic for each: the elements of
+/// a are loaded once for all NC, and the NC rows' loads go out together. Every b[c] must point at
+/// dim readable floats (a slot without a row may pass a itself and ignore its result). Lane 0 of
+/// the group returns the NC sums in out.
+template <bool L2, int NC>
+__device__ inline void exact_group8_n(const float* __restrict__ a, const float* const (&b)[NC], uint32_t dim,
+                                      float (&out)[NC]) {
+  const uint32_t l = threadIdx.x & 7u;
+  auto term = [](float x, float y, float s) {
+    if constexpr (L2) {
+      const float d = x - y;
+      return fmaf(d, d, s);
+    } else {
+      return fmaf(x, y, s);
+    }
+  };
+  float s[NC][4];
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) s[c][u] = 0.0f;
+  const uint32_t n8 = dim / 8 * 8;  // where the 32- and 8-element loops of exact_l2sqr stop
+  uint32_t i = 0;
+  for (; i + 32 <= dim; i += 32) {
+    float av[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) av[u] = a[i + 8 * u + l];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) s[c][u] = term(av[u], b[c][i + 8 * u + l], s[c][u]);
+  }
+  for (; i < n8; i += 8) {
+    const float a0 = a[i + l];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) s[c][0] = term(a0, b[c][i + l], s[c][0]);
+  }
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const float v = (s[c][0] + s[c][1]) + (s[c][2] + s[c][3]);  // v[l]
+    const float lo = v + __shfl_down(v, 4, 8);                   // lo[j] = v[j] + v[j + 4] on lanes 0..3
+    const float t = lo + __shfl_xor(lo, 1, 8);                   // lo0 + lo1 on lane 0, lo2 + lo3 on lane 2
+    float sum = t + __shfl_xor(t, 2, 8);                         // (lo0 + lo1) + (lo2 + lo3) on lane 0
+    if (l == 0) {
+      uint32_t k = n8;
+      const uint32_t v4 = k + (dim - k) / 4 * 4;
+      for (; k < v4; ++k) {
+        if constexpr (L2) {
+          const float d = a[k] - b[c][k];
+          sum = sum + d * d;
+        } else {
+          sum = sum + a[k] * b[c][k];
+        }
+      }
+      for (; k < dim; ++k) sum = term(a[k], b[c][k], sum);
+    }
+    out[c] = sum;
+  }
+}
+
 /// simd::normalize (src/simd/dispatch.cc:119-135) of one row in place.
 __device__ inline void exact_normalize(float* v, uint32_t dim) {
   const float norm_sq = exact_dot(v, v, dim);

@@ -2198,16 +2198,34 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
   if (!certified && tid == 0) a.fallback[atomicAdd(a.nfallback, 1u)] = q;
   if (a.refine) {
     // The cnt_f best keys are s_queue[0, cnt_f) here (every thread has passed a barrier since they
-    // were written). Eight lanes per candidate compute its exact distance (64 candidates per pass,
-    // each lane's loads coalesced with its group's), then a block sort by the exact distance.
+    // were written). Eight lanes per candidate compute its exact distance (each lane's loads
+    // coalesced with its group's), NC candidates per group at once so that every candidate's row
+    // loads are in flight together (keep_sel <= CAP / 2 candidates in one pass), then a block sort
+    // by the exact distance. Slots past cnt_f score the query against itself and are dropped.
     constexpr uint32_t kGroups = kStreamThreads / 8;
-    for (uint32_t b = 0; b < cnt_f; b += kGroups) {
-      const uint32_t i = b + static_cast<uint32_t>(tid) / 8;
-      const bool valid = i < cnt_f;
-      const uint32_t pos = valid ? static_cast<uint32_t>(s_queue[i]) : 0u;
-      const float* x = a.vec + static_cast<uint64_t>(pos) * a.dim;
-      const float e = l2 ? exact_group8<true>(qv, x, a.dim, valid) : 1.0f - exact_group8<false>(qv, x, a.dim, valid);
-      if (valid && (tid & 7) == 0) s_queue[i] = make_key(e, pos);
+    constexpr int NC = static_cast<int>((CAP / 2 + kGroups - 1) / kGroups);
+    for (uint32_t b = 0; b < cnt_f; b += NC * kGroups) {
+      uint32_t pos[NC];
+      const float* x[NC];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const uint32_t i = b + c * kGroups + static_cast<uint32_t>(tid) / 8;
+        pos[c] = i < cnt_f ? static_cast<uint32_t>(s_queue[i]) : 0u;
+        x[c] = i < cnt_f ? a.vec + static_cast<uint64_t>(pos[c]) * a.dim : qv;
+      }
+      float e[NC];
+      if (l2) {
+        exact_group8_n<true, NC>(qv, x, a.dim, e);
+      } else {
+        exact_group8_n<false, NC>(qv, x, a.dim, e);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) e[c] = 1.0f - e[c];
+      }
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const uint32_t i = b + c * kGroups + static_cast<uint32_t>(tid) / 8;
+        if (i < cnt_f && (tid & 7) == 0) s_queue[i] = make_key(e[c], pos[c]);
+      }
     }
     sort_front(cnt_f);
   }
