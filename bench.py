@@ -9,7 +9,8 @@ resident in HBM):
          quiver_amd/datasets.py), 10,000 queries from the same mixture.
   ivfpq  the same base and queries in an IVF-PQ index: nlist 2048, m 32 x 8 bits, L2, residual
          PQ trained on 100,000 rows of a seeded permutation (numpy default_rng(31)); k=10,
-         nprobe 32 (swept over 1..64 once each, untimed by the step clock).
+         nprobe 32 (swept over 1..64, each point the median of back-to-back searches, untimed by
+         the step clock).
 
 Prints ONE JSON line. `value` is the flat workload's queries per second (query prep + fused MFMA
 scan + merge/exact re-score), timed over K steps with the device synchronized on both sides;
@@ -376,7 +377,7 @@ def bench_ivfpq(args, hip: Hip, qvh: Qvh, base, queries):
         "ms_per_step": ms_per_step,
         "stage_ms": {"select": float(st[:, 0].mean()), "scan": scan_ms},
         "host_api": host_api,
-        "roofline": {"bound": "hbm", "kernel": "ivf_stream_kernel<8, true, 128, false>", "achieved": achieved,
+        "roofline": {"bound": "hbm", "kernel": "ivf_stream_kernel<8, true, 128, false, 4>", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": load_traffic("ivf_stream_int_mix_1m_nprobe32_pmc"),
                      "code_bytes_per_launch": code_bytes},
