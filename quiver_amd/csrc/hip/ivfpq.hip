@@ -1402,9 +1402,10 @@ __global__ void __launch_bounds__(kScanThreads) ivf_scan_kernel(ScanArgs a) {
 #ifndef QVH_STREAM_ROT
 #define QVH_STREAM_ROT 0
 #endif
-// Waves per streaming block: 4 with 128-entry wave queues (four blocks of ~37 KB LDS per CU, 128
-// registers per lane), 8 with 256-entry queues (three blocks of ~49 KB per CU, 80 registers) or
-// with 512-entry queues for candidate sets of 129..256 (two blocks of ~66 KB per CU).
+// Default waves per streaming block: 4 with 128- or 192-entry wave queues (four blocks of ~37 KB
+// LDS per CU, 128 registers per lane), 8 with 256-entry queues (three blocks of ~49 KB per CU, 80
+// registers) or with 512-entry queues for candidate sets of 129..256 (two blocks of ~66 KB per
+// CU). The host also runs 256-entry queues on 4 waves (inner product and cosine).
 template <int CAP>
 constexpr int stream_waves() { return CAP <= 192 ? 4 : 8; }
 constexpr uint32_t kStreamMaxProbes = 256;
@@ -2241,7 +2242,8 @@ __attribute__((amdgpu_waves_per_eu(W == 4 || CAP == 512 ? 4 : 6))) ivf_stream_ke
   stream_scan<MPW, FULL, CAP, ROT, W>(a);
 }
 
-// 33 to 64 code bytes: no register cap.
+// 33 to 64 code bytes: no register cap. (ROT is not used: it keeps the template arguments after
+// the code width the same as ivf_stream_kernel's, so one launch macro serves both.)
 template <bool FULL, int CAP, bool ROT = false, int W = stream_waves<CAP>()>
 __global__ void __launch_bounds__(W * 64) ivf_stream_wide_kernel(ScanArgs a) {
   stream_scan<16, FULL, CAP, false, W>(a);
