@@ -58,6 +58,19 @@ def test_flat_gaussian_10k_matches_oracle(oracle, metric, filtered):
     print(stats)
 
 
+@pytest.mark.parametrize("metric", ["l2", "ip"])
+@pytest.mark.parametrize("k", [1, 10, 12, 13])
+def test_integer_stores_short_lists(oracle, metric, k):
+    """A store of small integers keeps 12 candidates per lane list for k <= 12 (16 above): integer
+    queries then have exact GEMM-form distances; real-valued queries against the same store still
+    have their selections checked and fall back to the exact kernel when the check fails. Both
+    against the oracle, with ties (integer data has many) resolved by row."""
+    base, q_int = D.int_mix(40_000, 150)
+    q_real = q_int[:100] + np.random.default_rng(3).standard_normal((100, base.shape[1])).astype(np.float32) * 0.37
+    for q in (q_int, q_real):
+        print(_check(oracle, base, q, k, metric))
+
+
 @pytest.mark.parametrize("fraction", [0.005, 0.3, 0.49, 0.7])
 @pytest.mark.parametrize("metric", ["l2", "cosine"])
 def test_filter_densities(oracle, fraction, metric):
