@@ -209,7 +209,7 @@ def bench_flat(args, hip: Hip, qvh: Qvh):
         "ms_per_step": ms_per_step,
         "stage_ms": {"prep": float(st[:, 0].mean()), "scan": scan_ms, "merge": float(st[:, 2].mean())},
         "nsplit": int(st[0, 3]),
-        "roofline": {"bound": "mfma", "kernel": "flat_scan_kernel<128,12>", "achieved": achieved,
+        "roofline": {"bound": "mfma", "kernel": "flat_scan_kernel<128,10>", "achieved": achieved,
                      "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / FP32_MFMA_PEAK_TFLOPS,
                      "traffic": load_traffic("flat_scan_int_mix_1m_pmc")},

@@ -1792,12 +1792,12 @@ uint32_t padded_dim(uint32_t dim) {
 /// Per-lane list length of the MFMA scan for k, or 0 when k needs the wide merge. A margin of
 /// max(5, k/2) candidates past k lets the merge's re-score certify the selection when the GEMM-form
 /// distances differ from the exact ones in rounding. Stores of small integers (integral_rows) give
-/// integer queries exact GEMM-form distances (delta = 0, so any KL >= k is final), and take 12
-/// for k <= 12 (1M x 128 integer mixture, k = 10: scan 22.31 -> 21.79 ms, merge 82 -> 70 us); a
-/// query that is not integral still has its selection checked against delta, and a failed check
-/// sends it to the exact kernel.
+/// integer queries exact GEMM-form distances (delta = 0, so any KL >= k is final), and take 10
+/// for k <= 10 (1M x 128 integer mixture, k = 10: scan 22.30 -> 21.53 ms, merge 82 -> 65 us; 12
+/// entries gave 21.79 ms); a query that is not integral still has its selection checked against
+/// delta, and a failed check sends it to the exact kernel.
 int shared_list_length(uint32_t k, bool integral_rows) {
-  if (integral_rows && k <= 12) return 12;
+  if (integral_rows && k <= 10) return 10;
   const uint32_t need = k + std::max(5u, k / 2);
   return need <= 16 ? 16 : need <= 32 ? 32 : 0;
 }
@@ -1833,8 +1833,8 @@ void launch_scan_kl(bool l2, int mode, dim3 grid, const ScanArgs& a, hipStream_t
 
 template <int DP>
 void launch_scan_dp(int kl, bool l2, int mode, dim3 grid, const ScanArgs& a, hipStream_t s) {
-  if (kl == 12) {
-    launch_scan_kl<DP, 12>(l2, mode, grid, a, s);
+  if (kl == 10) {
+    launch_scan_kl<DP, 10>(l2, mode, grid, a, s);
   } else if (kl == 16) {
     launch_scan_kl<DP, 16>(l2, mode, grid, a, s);
   } else {
@@ -1868,8 +1868,8 @@ void launch_scan(uint32_t dp, int kl, dim3 grid, const ScanArgs& a, hipStream_t 
   const bool l2 = a.l2 != 0;
   const int filter = a.idx ? 2 : a.bitmap ? 1 : 0;
   if (dp > static_cast<uint32_t>(kMaxDp)) {
-    if (kl == 12) {
-      launch_scan_chunked_kl<12>(l2, filter, grid, a, s);
+    if (kl == 10) {
+      launch_scan_chunked_kl<10>(l2, filter, grid, a, s);
     } else if (kl == 16) {
       launch_scan_chunked_kl<16>(l2, filter, grid, a, s);
     } else {
@@ -2288,8 +2288,8 @@ void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const
   if (p.wide) {
     const uint32_t sel_n = k + std::max<uint32_t>(16, k / 2);
     hipLaunchKernelGGL(flat_merge_wide_kernel, mgrid, dim3(256), 0, s, m, sel_n);
-  } else if (p.kl == 12) {
-    hipLaunchKernelGGL(flat_merge_kernel<12>, mgrid, dim3(256), 0, s, m);
+  } else if (p.kl == 10) {
+    hipLaunchKernelGGL(flat_merge_kernel<10>, mgrid, dim3(256), 0, s, m);
   } else if (p.kl == 16) {
     hipLaunchKernelGGL(flat_merge_kernel<16>, mgrid, dim3(256), 0, s, m);
   } else {
