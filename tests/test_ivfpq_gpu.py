@@ -408,7 +408,7 @@ def test_uncertified_ranking_is_rescanned_exactly(oracle, refine):
     """L2 with the precomputed table ranks by base + (term1 + sum qtab) and re-scores the best
     keep + margin with the reference's sum base + sum (pre + qtab) (src/ivfpq_index.cc:334-346).
     A hundred copies of one vector next to query 0 share a list and a code, more than the selection
-    holds (keep + max(16, keep / 2): 26 for k = 10, 46 with refine 3), so the approximate and exact
+    holds (keep + max(6, keep / 2): 16 for k = 10, 45 with refine 3), so the approximate and exact
     sums of the whole selection differ only by rounding: the keep-th exact sum is not below the
     last approximate one minus the rounding bound, the ranking is not certified, and query 0 is
     rescanned with exact sums (in a batch of whole queries and alone, as a sliced query). Every
