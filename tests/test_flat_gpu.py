@@ -63,12 +63,18 @@ def test_flat_gaussian_10k_matches_oracle(oracle, metric, filtered):
 def test_integer_stores_short_lists(oracle, metric, k):
     """A store of small integers keeps 10 candidates per lane list for k <= 10 (16 above): integer
     queries then have exact GEMM-form distances; real-valued queries against the same store still
-    have their selections checked and fall back to the exact kernel when the check fails. Both
-    against the oracle, with ties (integer data has many) resolved by row."""
+    have their selections checked and fall back to the exact kernel when the check fails; and the
+    listed-row and bitmap forms of the filtered scan. All against the oracle, with ties (integer
+    data has many) resolved by row."""
     base, q_int = D.int_mix(40_000, 150)
     q_real = q_int[:100] + np.random.default_rng(3).standard_normal((100, base.shape[1])).astype(np.float32) * 0.37
     for q in (q_int, q_real):
         print(_check(oracle, base, q, k, metric))
+    # the listed-row (10% admitted) and bitmap (60%) forms of the filtered scan
+    rng = np.random.default_rng(4)
+    for n_allowed in (4_000, 24_000):
+        allowed = np.sort(rng.choice(40_000, n_allowed, replace=False)).astype(np.uint64)
+        print(_check(oracle, base, q_int, k, metric, allowed))
 
 
 @pytest.mark.parametrize("fraction", [0.005, 0.3, 0.49, 0.7])
