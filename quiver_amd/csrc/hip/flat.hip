@@ -65,7 +65,15 @@ struct ScanArgs {
   int share;                // 0: every lane list keeps its own KL best (k > KL: no shared bound)
   uint32_t dp;              // row width (the chunked scan; the register scan has it as DP)
   int rowsplit;             // register scan, unfiltered, at most 128 queries: two waves per query group
+  // Launch gate: when set, the launch does nothing unless (*gate != 0) == (gate_want != 0), read
+  // once at the start. Two list lengths are launched back to back and the device picks one.
+  const uint32_t* gate;
+  uint32_t gate_want;
 };
+
+__device__ __forceinline__ bool gate_closed(const uint32_t* gate, uint32_t want) {
+  return gate != nullptr && ((*gate != 0u) != (want != 0u));
+}
 
 constexpr int kShareEvery = 8;  // tiles between exchanges of the shared per-query threshold
 constexpr int kQueueCap = 20;   // queued candidates per lane before a wave-wide flush
@@ -230,6 +238,7 @@ __device__ __forceinline__ void scan_block_coords(const ScanArgs& a, uint32_t& q
 template <int DP, int KL, bool L2, int MODE, bool RS = false>
 __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
   static_assert(!RS || 4 * 64 * KL <= kQueueCap * kThreads, "row-split hand-off must fit the queue arrays");
+  if (gate_closed(a.gate, a.gate_want)) return;  // the same for every thread of the grid
   constexpr bool FILTER = MODE == 1;
   constexpr int H = DP / 2;                   // dims per lane half (K split in two halves)
   // LDS row stride in floats: conflict-free b128 reads. Columns DP and DP + 1 of a row hold the
@@ -583,6 +592,7 @@ constexpr uint32_t kMaxChunkedDp = 4096;
 
 template <int KL, bool L2, int MODE>
 __global__ void __launch_bounds__(kThreads) flat_scan_k_kernel(ScanArgs a) {
+  if (gate_closed(a.gate, a.gate_want)) return;  // the same for every thread of the grid
   constexpr bool FILTER = MODE == 1;
   constexpr int C4 = kKc / 4;  // float4 slots per chunk row
   __shared__ __attribute__((aligned(16))) float s_x[2][kTileRows * kKcStride];
@@ -735,6 +745,8 @@ struct MergeArgs {
   const float* delta;   // [nq] bound on |GEMM-form distance - exact distance| (query_norms_kernel)
   uint32_t* fallback;   // queries the exact kernel recomputes (uncertified selections)
   uint32_t* nfallback;  // their count
+  const uint32_t* gate;  // as ScanArgs::gate
+  uint32_t gate_want;
 };
 
 /// Certificate of a re-scored selection. The selection holds the `sel` best candidates by GEMM-form
@@ -752,6 +764,7 @@ __device__ __forceinline__ bool selection_certified(uint32_t count, uint32_t sel
 
 template <int KL>
 __global__ void __launch_bounds__(256) flat_merge_kernel(MergeArgs m) {
+  if (gate_closed(m.gate, m.gate_want)) return;
   const int lane = threadIdx.x & 63;
   const uint32_t q = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (q >= m.nq) return;  // whole wave; this kernel has no block barriers
@@ -1002,8 +1015,10 @@ __global__ void row_norms_kernel(const float* __restrict__ rows, float* __restri
 /// unit whose accumulation rounds faithfully rather than to nearest. delta is 0 when the query
 /// and every stored row are small integers and (P + R)^2 <= 2^24: every product, partial sum and
 /// difference of either form is then an integer below 2^24, so both forms are exact.
+/// any_delta (nullable) becomes nonzero when some query's delta is not 0.
 __global__ void query_norms_kernel(const float* __restrict__ qp, float* __restrict__ qn, uint32_t nq, uint32_t dp,
-                                   const uint32_t* __restrict__ meta, int l2, float* __restrict__ delta) {
+                                   const uint32_t* __restrict__ meta, int l2, float* __restrict__ delta,
+                                   uint32_t* __restrict__ any_delta) {
   const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
   if (q >= nq) return;
   bool integral = true;
@@ -1024,6 +1039,12 @@ __global__ void query_norms_kernel(const float* __restrict__ qp, float* __restri
   // Rounded up to float; an overflowing or NaN bound stays non-finite and fails every check.
   const float df = static_cast<float>(d);
   delta[q] = static_cast<double>(df) < d ? __uint_as_float(__float_as_uint(df) + 1u) : df;
+  if (any_delta != nullptr) {
+    const uint64_t inexact = __ballot(d != 0.0);  // one atomic per wave
+    if (inexact != 0 && (threadIdx.x & 63u) == static_cast<uint32_t>(__builtin_ctzll(inexact))) {
+      atomicOr(any_delta, 1u);
+    }
+  }
 }
 
 __global__ void fill_u32_kernel(uint32_t* p, uint64_t n, uint32_t v) {
@@ -1791,16 +1812,17 @@ uint32_t padded_dim(uint32_t dim) {
 /// leaves a margin of max(5, k / 2). 0: k is above that (the wide merge without a shared bound).
 /// Per-lane list length of the MFMA scan for k, or 0 when k needs the wide merge. A margin of
 /// max(5, k/2) candidates past k lets the merge's re-score certify the selection when the GEMM-form
-/// distances differ from the exact ones in rounding. Stores of small integers (integral_rows) give
-/// integer queries exact GEMM-form distances (delta = 0, so any KL >= k is final), and take 10
-/// for k <= 10 (1M x 128 integer mixture, k = 10: scan 22.30 -> 21.53 ms, merge 82 -> 65 us; 12
-/// entries gave 21.79 ms); a query that is not integral still has its selection checked against
-/// delta, and a failed check sends it to the exact kernel.
-int shared_list_length(uint32_t k, bool integral_rows) {
-  if (integral_rows && k <= 10) return 10;
+/// distances differ from the exact ones in rounding.
+int shared_list_length(uint32_t k) {
   const uint32_t need = k + std::max(5u, k / 2);
   return need <= 16 ? 16 : need <= 32 ? 32 : 0;
 }
+
+/// List length for a batch whose GEMM-form distances are all exact (every query's delta is 0:
+/// small-integer queries against a store of small integers), which needs no margin over k; 0 when
+/// none applies. 1M x 128 integer mixture, k = 10: scan 22.30 -> 21.53 ms, merge 82 -> 65 us (12
+/// entries: 21.79 ms).
+int exact_list_length(uint32_t k) { return k <= 10 ? 10 : 0; }
 
 template <int DP, int KL>
 void launch_scan_kl(bool l2, int mode, dim3 grid, const ScanArgs& a, hipStream_t s) {
@@ -1960,6 +1982,9 @@ struct FlatPlan {
   enum Path { kFew, kSplit, kExactOnly, kMfma, kSorted } path = kMfma;
   bool wide = false;
   int kl = 16;
+  // List length when every query's distances turn out exact (exact_list_length), or 0: the scan
+  // and merge are then launched for both lengths, and the device runs the one that applies.
+  int kl_exact = 0;
   uint64_t g = 0, rps = 0;                       // few / split: row splits and rows per split
   uint64_t nsplit = 1, rows_per_split = 0;       // MFMA scan
   uint32_t qblocks = 0;
@@ -2023,9 +2048,9 @@ FlatPlan plan_flat_search(const qvh_flat* f, uint64_t nq, uint32_t k, bool index
   const bool few = splittable && nq <= kFewMaxBatch && k <= (f->dim % 32 == 0 ? kFewMaxK : 64u) && f->dim >= 32 &&
                    f->dim <= kFewMaxDim;
   const bool split = splittable && !few && nq <= kSplitMaxQueries;
-  p.wide = !few && !split && shared_list_length(k, f->integral_rows) == 0 && k <= kWideMaxK && f->dp <= kMaxChunkedDp &&
+  p.wide = !few && !split && shared_list_length(k) == 0 && k <= kWideMaxK && f->dp <= kMaxChunkedDp &&
            !indexed;
-  const bool exact_only = !few && !split && !p.wide && (shared_list_length(k, f->integral_rows) == 0 || f->dp > kMaxChunkedDp);
+  const bool exact_only = !few && !split && !p.wide && (shared_list_length(k) == 0 || f->dp > kMaxChunkedDp);
   p.path = few ? FlatPlan::kFew : split ? FlatPlan::kSplit : exact_only ? FlatPlan::kExactOnly : FlatPlan::kMfma;
   if (f->metric == QVH_METRIC_COSINE) p.stage = nq * f->dim * sizeof(float);
   p.q = nq * f->dp * sizeof(float);
@@ -2055,7 +2080,8 @@ FlatPlan plan_flat_search(const qvh_flat* f, uint64_t nq, uint32_t k, bool index
   if (p.path == FlatPlan::kExactOnly) return p;
   p.qn = nq * sizeof(float);
   p.delta = nq * sizeof(float);
-  p.kl = p.wide ? 32 : shared_list_length(k, f->integral_rows);
+  p.kl = p.wide ? 32 : shared_list_length(k);
+  p.kl_exact = !p.wide && f->integral_rows ? exact_list_length(k) : 0;
   p.qblocks = static_cast<uint32_t>(ceil_div(nq, kQueriesPerBlock));
   p.scan_rows = indexed ? n_idx : f->n;
   const uint64_t tiles = std::max<uint64_t>(1, ceil_div(p.scan_rows, kTileRows));
@@ -2085,7 +2111,7 @@ FlatPlan plan_flat_search(const qvh_flat* f, uint64_t nq, uint32_t k, bool index
   p.pd = parts * sizeof(float);
   p.pr = parts * sizeof(uint32_t);
   p.thr = nq * sizeof(uint32_t);
-  p.fb = (nq + 1) * sizeof(uint32_t);
+  p.fb = (nq + 2) * sizeof(uint32_t);  // count, listed queries, then the launch gate word
   return p;
 }
 
@@ -2110,8 +2136,10 @@ FlatBuffers handle_buffers(qvh_flat* f, const FlatPlan& p) {
 }
 
 /// Queries into b.q ([nq][dp], normalized for cosine in b.stage) and, for the MFMA scan, their
-/// squared norms into b.qn and their re-score bounds into b.delta.
-void flat_prep_queries(qvh_flat* f, const FlatBuffers& b, const float* d_raw, uint64_t nq, hipStream_t s) {
+/// squared norms into b.qn and their re-score bounds into b.delta; any_delta (nullable) is cleared
+/// and then set when some query's bound is not 0.
+void flat_prep_queries(qvh_flat* f, const FlatBuffers& b, const float* d_raw, uint64_t nq, hipStream_t s,
+                       uint32_t* any_delta = nullptr) {
   const float* qs = d_raw;
   if (f->metric == QVH_METRIC_COSINE) {  // normalized in a copy
     if (b.stage != d_raw) {
@@ -2124,9 +2152,10 @@ void flat_prep_queries(qvh_flat* f, const FlatBuffers& b, const float* d_raw, ui
   hipLaunchKernelGGL(pack_rows_kernel, dim3(static_cast<unsigned>(ceil_div(total, 256))), dim3(256), 0, s,
                      qs, b.q, nq, f->dim, f->dp);
   if (b.qn) {
+    if (any_delta) hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, s, any_delta, 1, 0u);
     hipLaunchKernelGGL(query_norms_kernel, dim3(static_cast<unsigned>(ceil_div(nq, 256))), dim3(256), 0, s,
                        b.q, b.qn, static_cast<uint32_t>(nq), f->dp, f->meta.as<uint32_t>(),
-                       f->metric == QVH_METRIC_L2 ? 1 : 0, b.delta);
+                       f->metric == QVH_METRIC_L2 ? 1 : 0, b.delta, any_delta);
   }
   QVH_HIP(hipGetLastError());
 }
@@ -2141,7 +2170,8 @@ void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const
   f->last_fb_count = b.fb;
   f->timed = f->timing;
   if (f->timed) QVH_HIP(hipEventRecord(f->ev[0], s));
-  flat_prep_queries(f, b, d_queries, nq, s);
+  uint32_t* gate = p.path == FlatPlan::kMfma && p.kl_exact ? b.fb + nq + 1 : nullptr;
+  flat_prep_queries(f, b, d_queries, nq, s, gate);
   if (f->timed) QVH_HIP(hipEventRecord(f->ev[1], s));
   ExactArgs e{};
   e.X = f->rows.as<float>();
@@ -2236,6 +2266,8 @@ void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const
     return;
   }
   ScanArgs a;
+  a.gate = nullptr;
+  a.gate_want = 0;
   a.X = f->rows.as<float>();
   a.xnorm = f->norms.as<float>();
   a.n = p.scan_rows;
@@ -2258,12 +2290,21 @@ void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const
   a.rowsplit = nq <= static_cast<uint64_t>(kQueriesPerBlock / 2) && !d_idx && !d_bitmap && f->dp <= kMaxDp ? 1 : 0;
   hipLaunchKernelGGL(fill_u32_kernel, dim3(static_cast<unsigned>(ceil_div(nq, 256))), dim3(256), 0, s,
                      a.qthr, nq, 0xFF800000u);  // ordered bits of +inf
-  launch_scan(f->dp, p.kl, dim3(static_cast<unsigned>(p.qblocks * p.nsplit)), a, s);
+  const dim3 sgrid(static_cast<unsigned>(p.qblocks * p.nsplit));
+  if (gate) {  // exact distances for every query: the short lists; otherwise the margin's
+    a.gate = gate;
+    a.gate_want = 0;
+    launch_scan(f->dp, p.kl_exact, sgrid, a, s);
+    a.gate_want = 1;
+  }
+  launch_scan(f->dp, p.kl, sgrid, a, s);
   QVH_HIP(hipGetLastError());
   if (f->timed) QVH_HIP(hipEventRecord(f->ev[2], s));
   f->last_nsplit = p.nsplit;
 
   MergeArgs m;
+  m.gate = nullptr;
+  m.gate_want = 0;
   m.X = a.X;
   m.dim = f->dim;
   m.dp = f->dp;
@@ -2288,12 +2329,18 @@ void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const
   if (p.wide) {
     const uint32_t sel_n = k + std::max<uint32_t>(16, k / 2);
     hipLaunchKernelGGL(flat_merge_wide_kernel, mgrid, dim3(256), 0, s, m, sel_n);
-  } else if (p.kl == 10) {
-    hipLaunchKernelGGL(flat_merge_kernel<10>, mgrid, dim3(256), 0, s, m);
-  } else if (p.kl == 16) {
-    hipLaunchKernelGGL(flat_merge_kernel<16>, mgrid, dim3(256), 0, s, m);
   } else {
-    hipLaunchKernelGGL(flat_merge_kernel<32>, mgrid, dim3(256), 0, s, m);
+    if (gate) {  // the merge of the short lists, or (gate set) of the margin's
+      m.gate = gate;
+      m.gate_want = 0;
+      hipLaunchKernelGGL(flat_merge_kernel<10>, mgrid, dim3(256), 0, s, m);  // exact_list_length
+      m.gate_want = 1;
+    }
+    if (p.kl == 16) {
+      hipLaunchKernelGGL(flat_merge_kernel<16>, mgrid, dim3(256), 0, s, m);
+    } else {
+      hipLaunchKernelGGL(flat_merge_kernel<32>, mgrid, dim3(256), 0, s, m);
+    }
   }
   QVH_HIP(hipGetLastError());
   e.qlist = fb + 1;
@@ -2491,7 +2538,7 @@ qvh_status qvh_flat_search(qvh_flat* f, const float* queries, uint64_t nq, uint3
         if (w + 1 == words && f->n % 64) bits &= (1ull << (f->n % 64)) - 1;
         admitted += static_cast<uint64_t>(__builtin_popcountll(bits));
       }
-      if (shared_list_length(k, f->integral_rows) != 0 && f->dp <= kMaxChunkedDp && 2 * admitted < f->n) {
+      if (shared_list_length(k) != 0 && f->dp <= kMaxChunkedDp && 2 * admitted < f->n) {
         listed.reserve(admitted);
         for (size_t w = 0; w < words; ++w) {
           uint64_t bits = row_bitmap[w];

@@ -61,16 +61,28 @@ def test_flat_gaussian_10k_matches_oracle(oracle, metric, filtered):
 @pytest.mark.parametrize("metric", ["l2", "ip"])
 @pytest.mark.parametrize("k", [1, 10, 11])
 def test_integer_stores_short_lists(oracle, metric, k):
-    """A store of small integers keeps 10 candidates per lane list for k <= 10 (16 above): integer
-    queries then have exact GEMM-form distances; real-valued queries against the same store still
-    have their selections checked and fall back to the exact kernel when the check fails; and the
-    listed-row and bitmap forms of the filtered scan. All against the oracle, with ties (integer
-    data has many) resolved by row."""
+    """On a store of small integers, a batch of small-integer queries has exact GEMM-form distances
+    and scans with 10-entry lane lists for k <= 10 (no margin, nothing to certify: no fallback); a
+    batch holding any real-valued query takes the 16-entry lists with the margin instead (the
+    device picks between the two launches). Integer, real-valued and mixed batches, and the
+    listed-row and bitmap forms of the filtered scan, against the oracle, with ties (integer data
+    has many) resolved by row."""
     base, q_int = D.int_mix(40_000, 150)
     q_real = q_int[:100] + np.random.default_rng(3).standard_normal((100, base.shape[1])).astype(np.float32) * 0.37
-    for q in (q_int, q_real):
-        print(_check(oracle, base, q, k, metric))
-    # the listed-row (10% admitted) and bitmap (60%) forms of the filtered scan
+    q_mixed = np.concatenate([q_int[100:], q_real[:3]])
+    idx = quiver.FlatIndex(base.shape[1], metric)
+    idx.add(base)
+    for name, q in (("integer", q_int), ("real", q_real), ("mixed", q_mixed)):
+        print(name, _check(oracle, base, q, k, metric))
+        idx.search(q, k)
+        fallbacks = Qvh().last_fallbacks(idx._index._device_handle)
+        print(name, "fallbacks", fallbacks)
+        if name == "integer":
+            assert fallbacks == 0
+        else:
+            # the margin certifies all but near-ties (here the rounding bound is ~180 on squared
+            # distances of ~1e5 between dense integer rows); without it nearly every query would fall back
+            assert fallbacks <= 0.1 * q.shape[0], fallbacks
     rng = np.random.default_rng(4)
     for n_allowed in (4_000, 24_000):
         allowed = np.sort(rng.choice(40_000, n_allowed, replace=False)).astype(np.uint64)
