@@ -135,6 +135,10 @@ def host_cores():
 
 COPY_CALIBRATION_BYTES = 256 << 20
 
+# flat: the 1M x 128 L2 headline; ivfpq: IVF-PQ L2 on the same data; cosine: the 1.18M x 100 cosine
+# flat search with allowed-id filters; wide: 500k x 768 L2; ivfcos: IVF-PQ cosine with refine 8.
+WORKLOADS = ("flat", "ivfpq", "cosine", "wide", "ivfcos")
+
 
 def load_traffic(name: str):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary profiles/<name>.md (its
@@ -292,7 +296,7 @@ def bench_ivfpq(args, hip: Hip, qvh: Qvh, base, queries):
     # back-to-back searches with stage events only (level 1); the stage times are the median of the
     # last four, so a point is measured at the same steady state as the timed loop below.
     sweep = {}
-    for p in (1, 4, 8, 16, 32, 64):
+    for p in sorted(set(args.sweep) | {nprobe}):
         qvh.check(qvh.lib.qvh_ivfpq_set_timing(h, 2), "timing")
         search(p)
         qvh.check(qvh.lib.qvh_ivfpq_sync(h), "sync")
@@ -598,7 +602,18 @@ def main():
                     help="skip the filtered cosine flat and the cosine IVF-PQ refine workloads")
     ap.add_argument("--copy-calibration", action="store_true",
                     help=f"first run one {COPY_CALIBRATION_BYTES >> 20} MiB device copy (for rocprofv3 --pmc scaling)")
+    ap.add_argument("--workloads", default=",".join(WORKLOADS),
+                    help="comma-separated subset of " + ",".join(WORKLOADS) + " (for profiling one workload; "
+                         "the JSON line always carries flat, whose numbers are `value`)")
+    ap.add_argument("--sweep", default="1,4,8,16,32,64", help="nprobe points of the IVF-PQ sweep")
     args = ap.parse_args()
+    args.workloads = set(w for w in args.workloads.split(",") if w)
+    unknown = args.workloads - set(WORKLOADS)
+    if unknown:
+        ap.error(f"unknown workloads {sorted(unknown)}")
+    if args.no_extra:
+        args.workloads &= {"flat", "ivfpq"}
+    args.sweep = [int(p) for p in args.sweep.split(",") if p]
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build's search path runs on a single MI355X and "
               f"has no multi-GPU mode (asked for --gpus {args.gpus})", file=sys.stderr)
@@ -615,19 +630,25 @@ def main():
         copy_calibration(hip)
     flat, base, queries = bench_flat(args, hip, qvh)
     done("flat")
-    idx, ivf = bench_ivfpq(args, hip, qvh, base, queries)
-    done("ivfpq")
+    idx, ivf = None, None
+    if "ivfpq" in args.workloads:
+        idx, ivf = bench_ivfpq(args, hip, qvh, base, queries)
+        done("ivfpq")
     extra = {}
     if not args.no_extra:
         extra["flat_small_batches"] = flat["small_batches"]
+    if "cosine" in args.workloads:
         extra["flat_cosine_filtered"] = bench_flat_filtered(args, qvh)
         done("flat_cosine_filtered")
+    if "wide" in args.workloads:
         extra["flat_wide_rows"] = bench_flat_wide(args, hip, qvh)
         done("flat_wide_rows")
+    if "ivfcos" in args.workloads:
         extra["ivfpq_cosine_refine"] = bench_ivfpq_cosine_refine(args, hip, qvh)
         done("ivfpq_cosine_refine")
     cpu = None
-    ivf["cpu_baseline"] = None
+    if ivf is not None:
+        ivf["cpu_baseline"] = None
     cores = host_cores()
     if not args.no_cpu:
         threads = args.cpu_threads or cores["usable"]
@@ -635,10 +656,11 @@ def main():
                               cpu_baseline_flat(base, queries, 10, args.cpu_seconds / 3, 1))
         cpu["host"] = cores
         done("cpu_baseline flat")
-        ivf["cpu_baseline"] = with_one_thread(
-            cpu_baseline_ivfpq(idx, queries, 10, 32, args.cpu_seconds / 3, threads),
-            cpu_baseline_ivfpq(idx, queries, 10, 32, args.cpu_seconds / 3, 1))
-        done("cpu_baseline ivfpq")
+        if ivf is not None:
+            ivf["cpu_baseline"] = with_one_thread(
+                cpu_baseline_ivfpq(idx, queries, 10, 32, args.cpu_seconds / 3, threads),
+                cpu_baseline_ivfpq(idx, queries, 10, 32, args.cpu_seconds / 3, 1))
+            done("cpu_baseline ivfpq")
     line = {
         "metric": METRIC,
         "value": flat["value"],

@@ -52,6 +52,11 @@ typedef struct qvh_ivfpq qvh_ivfpq;
 /* Message of the last failed call on this thread ("" if none). */
 const char* qvh_last_error(void);
 
+/* Diagnostic (no counterpart in the reference): the number of device allocations the library has
+ * made in this process so far (every hipMalloc of its own buffers goes through one counter). Tests
+ * use it to check that an entry point allocates nothing. */
+qvh_status qvh_device_allocations(uint64_t* count);
+
 /* Selects and initializes the HIP device used by handles created afterwards on this thread's
  * process (default: device 0, initialized on first use). Fails with QVH_EDEVICE when no gfx950
  * device is present. */
@@ -119,8 +124,10 @@ qvh_status qvh_flat_search_device(qvh_flat* flat, const float* d_queries, uint64
  * the workspace (prepared queries, norms, bounds, partial lists, counters) comes from a fixed
  * 64 MiB array in device memory that each GPU the library runs on holds until the process ends. A
  * search that needs more (many queries, or few queries with a large k) fails with QVH_EINVAL
- * before anything is enqueued. All calls on one GPU share that GPU's array: calls that overlap on
- * one GPU (on any handles or streams) race; each call clears what must start at zero itself. */
+ * before anything is enqueued. All calls on one GPU share that GPU's array; the library orders them
+ * on the device (each call's stream waits for the previous call's last launch, through an event),
+ * so calls on different handles or streams take the array in turn. Under HIP graph capture that
+ * ordering is left to the caller. Each call clears what must start at zero itself. */
 qvh_status qvh_flat_search_device_noalloc(qvh_flat* flat, const float* d_queries, uint64_t nq,
                                           uint32_t k, const uint64_t* d_row_bitmap,
                                           uint32_t* d_out_rows, float* d_out_dist, void* stream);
@@ -164,15 +171,27 @@ qvh_status qvh_ivfpq_set_trained(qvh_ivfpq* ivf, const float* centroids, const f
 /* Copies the precomputed table [nlist][m][256] to the host. */
 qvh_status qvh_ivfpq_precomputed(qvh_ivfpq* ivf, float* out);
 
-/* Cells and PQ codes of n vectors without storing them (src/ivfpq_index.cc:235-246):
- * assign[n] (nullable), codes[n][m] (nullable), stored_out[n][dim] = the vectors as stored
- * (normalized for cosine; nullable). */
+/* The encode step of Impl::add (src/ivfpq_index.cc:218-247): cells and PQ codes of n vectors,
+ * without storing them: assign[n] (nullable), codes[n][m] (nullable), stored_out[n][dim] = the
+ * vectors as stored (normalized for cosine; nullable). It runs on a workspace and stream of its own
+ * and does not take the handle's lock, so searches on the same handle proceed meanwhile, as they do
+ * during the reference's encode (which holds no index lock). Concurrent encodes on one handle are
+ * serialized with each other. */
 qvh_status qvh_ivfpq_encode(qvh_ivfpq* ivf, const float* x, uint64_t n, uint32_t* assign,
                             uint8_t* codes, float* stored_out);
 
-/* Impl::add (src/ivfpq_index.cc:208-271): encodes n vectors and appends them to their lists in
- * input order. assign_out[n] (nullable) receives each vector's list, which the caller needs to
- * place its labels. */
+/* The append step of Impl::add (src/ivfpq_index.cc:249-270, the part the reference runs under
+ * the exclusive lock): stores n entries that qvh_ivfpq_encode produced, each after its list's
+ * existing entries in batch order. assign[n] and codes[n][m] are required; vectors[n][dim] (the
+ * stored form, normalized for cosine) is required when the index stores vectors and ignored
+ * otherwise. A cell out of range or a list that would pass 2^32 entries is rejected (QVH_EINVAL)
+ * before anything changes. */
+qvh_status qvh_ivfpq_append(qvh_ivfpq* ivf, const uint32_t* assign, const uint8_t* codes,
+                            const float* vectors, uint64_t n);
+
+/* Impl::add (src/ivfpq_index.cc:208-271) in one call: encodes n vectors and appends them to their
+ * lists in input order, holding the handle's lock throughout. assign_out[n] (nullable) receives
+ * each vector's list, which the caller needs to place its labels. */
 qvh_status qvh_ivfpq_add(qvh_ivfpq* ivf, const float* x, uint64_t n, uint32_t* assign_out);
 
 /* Installs whole lists into an empty trained index, as IvfPqIndex::load does from the LOFF /

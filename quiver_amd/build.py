@@ -37,7 +37,7 @@ HIPCC_FLAGS = [
     "-Wall", "-Wno-unused-function",
     f"-I{INCLUDE}", f"-I{os.path.join(CSRC, 'hip')}",
 ]
-CXX_FLAGS = ["-std=c++20", "-O2", "-fPIC", "-pthread", "-Wall", "-Wextra",
+CXX_FLAGS = ["-std=c++20", "-O2", "-fPIC", "-pthread", "-ffp-contract=off", "-Wall", "-Wextra",
              f"-I{INCLUDE}", f"-I{os.path.join(CSRC, 'host', 'include')}"]
 
 

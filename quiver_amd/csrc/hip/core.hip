@@ -97,6 +97,15 @@ extern "C" {
 
 const char* qvh_last_error(void) { return qvh::t_last_error.c_str(); }
 
+qvh_status qvh_device_allocations(uint64_t* count) {
+  if (count == nullptr) {
+    qvh::set_last_error("qvh_device_allocations: null output");
+    return QVH_EINVAL;
+  }
+  *count = static_cast<uint64_t>(qvh::g_alloc_count.load());
+  return QVH_OK;
+}
+
 qvh_status qvh_init(int device) {
   return qvh::guarded([&] {
     std::lock_guard<std::mutex> lock(qvh::g_device_mu);

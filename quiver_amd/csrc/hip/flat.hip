@@ -2616,8 +2616,13 @@ qvh_status qvh_flat_search_device(qvh_flat* f, const float* d_queries, uint64_t 
 // norms, bounds, partial lists, counters) from `scratch`, a fixed array in device memory that each
 // GPU the library runs on holds until the process ends. Its device address on the current device
 // comes from hipGetSymbolAddress on the first call there (the name `scratch` is a host-side
-// stand-in, not a device address). All calls on one GPU share that GPU's array: calls that overlap
-// on one GPU race, and every call clears what must start at zero (bounds, counters) itself.
+// stand-in, not a device address). All calls on one GPU share that GPU's array. The library orders
+// them on the device: each call's stream first waits for an event the previous call recorded after
+// its last launch (a host lock keeps the wait, the launches and the record of concurrent callers
+// apart), so calls on different handles or streams take the array in turn. Event waits allocate
+// nothing. Under HIP graph capture the calls are not ordered by the library (an event recorded
+// outside the graph cannot be waited on inside it): a caller that captures such calls orders its
+// replays itself. Every call clears what must start at zero (bounds, counters) itself.
 
 constexpr size_t kScratchBytes = size_t{64} << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
@@ -2625,20 +2630,33 @@ static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 namespace {
 
 constexpr int kMaxScratchDevices = 64;
-std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxScratchDevices] = {};
 
-/// The scratch array's address on `device`, which must be the current device.
-unsigned char* scratch_on(int device) {
+/// One device's scratch array: its address, the event its last user recorded, and the lock under
+/// which a call waits on that event, launches and records it.
+struct ScratchSlot {
+  void* ptr = nullptr;
+  hipEvent_t done = nullptr;
+  bool recorded = false;
+  std::mutex use;
+};
+
+std::mutex g_scratch_mu;
+ScratchSlot g_scratch[kMaxScratchDevices];
+
+/// The scratch slot of `device`, which must be the current device; its address and event are set up
+/// on the first call there.
+ScratchSlot& scratch_on(int device) {
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   QVH_REQUIRE(device >= 0 && device < kMaxScratchDevices, "device index out of range for the scratch array");
-  if (g_scratch_ptr[device] == nullptr) {
+  ScratchSlot& slot = g_scratch[device];
+  if (slot.ptr == nullptr) {
     void* ptr = nullptr;
     QVH_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
     QVH_REQUIRE(ptr != nullptr, "hipGetSymbolAddress returned no address for the scratch array");
-    g_scratch_ptr[device] = ptr;
+    QVH_HIP(hipEventCreateWithFlags(&slot.done, hipEventDisableTiming));
+    slot.ptr = ptr;
   }
-  return static_cast<unsigned char*>(g_scratch_ptr[device]);
+  return slot;
 }
 
 /// The plan's workspace carved from the scratch array, each buffer 256-byte aligned.
@@ -2680,7 +2698,9 @@ qvh_status qvh_flat_search_device_noalloc(qvh_flat* f, const float* d_queries, u
     QVH_REQUIRE(d_queries && d_out_rows && d_out_dist, "qvh_flat_search_device_noalloc: null buffer");
     std::lock_guard<std::mutex> lock(f->mu);
     QVH_HIP(hipSetDevice(f->device));
-    unsigned char* base = scratch_on(f->device);
+    ScratchSlot& slot = scratch_on(f->device);
+    std::lock_guard<std::mutex> use(slot.use);  // after the handle's lock, never before it
+    unsigned char* base = static_cast<unsigned char*>(slot.ptr);
     const FlatPlan p = plan_flat_search(f, nq, k, false, 0, device_cus(f->device));
     if (p.total() > kScratchBytes) {
       throw Failure(QVH_EINVAL, "qvh_flat_search_device_noalloc: this search needs " + std::to_string(p.total()) +
@@ -2690,7 +2710,15 @@ qvh_status qvh_flat_search_device_noalloc(qvh_flat* f, const float* d_queries, u
     const FlatBuffers b = scratch_buffers(base, p);
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : f->stream;
     on_handle_timeline(f->stream, f->join, s, [&](hipStream_t st) {
+      hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+      QVH_HIP(hipStreamIsCapturing(st, &capture));
+      const bool ordered = capture == hipStreamCaptureStatusNone;
+      if (ordered && slot.recorded) QVH_HIP(hipStreamWaitEvent(st, slot.done, 0));
       flat_search_run(f, p, b, d_queries, nq, k, d_row_bitmap, d_out_rows, d_out_dist, st);
+      if (ordered) {
+        QVH_HIP(hipEventRecord(slot.done, st));
+        slot.recorded = true;
+      }
     });
   });
 }

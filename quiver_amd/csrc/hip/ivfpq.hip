@@ -16,6 +16,7 @@
 // quantity, grouped differently), then re-scores the best keep + margin candidates exactly as the
 // reference adds them (base + sum_j (pre[l][j][c_j] + qtab[j][c_j])).
 #include <algorithm>
+#include <atomic>
 #include <cstring>
 #include <numeric>
 #include <vector>
@@ -2391,12 +2392,22 @@ __global__ void __launch_bounds__(256) probed_code_bytes_kernel(const uint32_t* 
 
 // ---- handle ---------------------------------------------------------------------------------------
 
+/// Workspace of the encode step (cells, residuals, codes of a batch being added). It has its own
+/// lock and stream, apart from the search workspace: the trained state it reads never changes once
+/// installed, so an add's encode runs on the device beside searches of the same handle, and only
+/// the append that follows takes the handle's lock (src/ivfpq_index.cc:226-249).
+struct EncodeSpace {
+  std::mutex mu;
+  hipStream_t stream = nullptr;
+  DeviceBuffer x, assign, afb, res, codes;
+};
+
 struct qvh_ivfpq {
   uint32_t dim = 0, nlist = 0, m = 0, dsub = 0, mp = 0;
   int metric = 0;
   int store_vectors = 0;
   int device = 0;
-  bool trained = false;
+  std::atomic<bool> trained{false};  // set once, after the trained state is on the device
   bool has_pre = false;
   uint64_t count = 0;
   std::vector<uint64_t> h_off;  // host copy of the list offsets
@@ -2407,7 +2418,8 @@ struct qvh_ivfpq {
   DeviceBuffer cmax;  // [m] largest codeword norm per sub-space (the same)
   hipStream_t stream = nullptr;
   std::mutex mu;
-  DeviceBuffer w_x, w_res, w_assign, w_afb, w_codes, w_codes_p, w_t1, w_dest, w_shift;
+  EncodeSpace enc;
+  DeviceBuffer w_x, w_assign, w_codes, w_codes_p, w_t1, w_dest, w_shift;  // the batch an append stores
   DeviceBuffer w_q, w_scores, w_probes, w_bits, w_refs, w_dist, w_bytes, w_key, w_order, w_lut, w_cand;
   DeviceBuffer w_pkeys, w_pcnt, w_pdone;  // sliced queries of the streaming scan
   DeviceBuffer w_delta, w_fb;             // certificate bounds; uncertified queries (count, list)
@@ -2432,9 +2444,10 @@ int ivf_mode(const qvh_ivfpq* h) {
 }
 
 /// Cells (src/ivfpq_index.cc:238) and codes (:239-245) of n device-resident rows `d_x` (already
-/// normalized for cosine). Results stay on the device in the handle workspace.
-void ivf_encode_device(qvh_ivfpq* h, const float* d_x, uint64_t n, hipStream_t s) {
-  uint32_t* assign = static_cast<uint32_t*>(h->w_assign.reserve(n * sizeof(uint32_t)));
+/// normalized for cosine), into the encode workspace `es` (its assign and codes buffers). The caller
+/// holds es.mu; `s` is the stream the work goes on.
+void ivf_encode_device(const qvh_ivfpq* h, EncodeSpace& es, const float* d_x, uint64_t n, hipStream_t s) {
+  uint32_t* assign = static_cast<uint32_t*>(es.assign.reserve(n * sizeof(uint32_t)));
   NearestArgs na{};
   na.x = d_x;
   na.n = n;
@@ -2446,11 +2459,11 @@ void ivf_encode_device(qvh_ivfpq* h, const float* d_x, uint64_t n, hipStream_t s
   na.k = h->nlist;
   na.max_ip = h->metric == QVH_METRIC_IP;
   na.out32 = assign;
-  launch_assign(na, h->asg, h->w_afb, s);
-  float* res = static_cast<float*>(h->w_res.reserve(n * h->dim * sizeof(float)));
+  launch_assign(na, h->asg, es.afb, s);
+  float* res = static_cast<float*>(es.res.reserve(n * h->dim * sizeof(float)));
   hipLaunchKernelGGL(residual_kernel, dim3(static_cast<unsigned>(ceil_div(n * h->dim, 256))), dim3(256), 0, s,
                      d_x, assign, h->cent.as<float>(), n, h->dim, res);
-  uint8_t* codes = static_cast<uint8_t*>(h->w_codes.reserve(n * h->m));
+  uint8_t* codes = static_cast<uint8_t*>(es.codes.reserve(n * h->m));
   NearestArgs pa{};
   pa.x = res;
   pa.n = n;
@@ -2802,7 +2815,11 @@ qvh_status qvh_ivfpq_create(uint32_t dim, int metric, uint32_t nlist, uint32_t m
     h->device = dev;
     if (hipDeviceGetAttribute(&h->cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) h->cus = 0;
     h->h_off.assign(nlist + 1, 0);
-    const hipError_t e = hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking);
+    hipError_t e = hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) {
+      e = hipStreamCreateWithFlags(&h->enc.stream, hipStreamNonBlocking);
+      if (e != hipSuccess) (void)hipStreamDestroy(h->stream);
+    }
     if (e != hipSuccess) {
       delete h;
       throw Failure(QVH_EDEVICE, std::string("hipStreamCreate: ") + hipGetErrorString(e));
@@ -2812,6 +2829,7 @@ qvh_status qvh_ivfpq_create(uint32_t dim, int metric, uint32_t nlist, uint32_t m
       QVH_HIP(hipMemcpy(h->off.ptr, h->h_off.data(), (nlist + 1) * sizeof(uint64_t), hipMemcpyHostToDevice));
     } catch (...) {
       (void)hipStreamDestroy(h->stream);
+      (void)hipStreamDestroy(h->enc.stream);
       delete h;
       throw;
     }
@@ -2825,6 +2843,10 @@ void qvh_ivfpq_destroy(qvh_ivfpq* h) {
   if (h->stream) {
     (void)hipStreamSynchronize(h->stream);
     (void)hipStreamDestroy(h->stream);
+  }
+  if (h->enc.stream) {
+    (void)hipStreamSynchronize(h->enc.stream);
+    (void)hipStreamDestroy(h->enc.stream);
   }
   for (hipEvent_t& e : h->ev) {
     if (e) (void)hipEventDestroy(e);
@@ -2874,7 +2896,7 @@ qvh_status qvh_ivfpq_set_trained(qvh_ivfpq* h, const float* centroids, const flo
     }
     QVH_HIP(hipGetLastError());
     QVH_HIP(hipStreamSynchronize(s));
-    h->trained = true;
+    h->trained.store(true, std::memory_order_release);
   });
 }
 
@@ -2895,18 +2917,130 @@ qvh_status qvh_ivfpq_encode(qvh_ivfpq* h, const float* x, uint64_t n, uint32_t* 
     QVH_REQUIRE(h != nullptr, "qvh_ivfpq_encode: null handle");
     if (n == 0) return;
     QVH_REQUIRE(x != nullptr, "qvh_ivfpq_encode: null vectors");
-    std::lock_guard<std::mutex> lock(h->mu);
-    ivf_check_trained(h);
+    EncodeSpace& es = h->enc;
+    std::lock_guard<std::mutex> lock(es.mu);  // not the handle's lock: searches go on meanwhile
+    QVH_REQUIRE(h->trained.load(std::memory_order_acquire), "IVF-PQ index must be trained before add()");
     QVH_HIP(hipSetDevice(h->device));
-    hipStream_t s = h->stream;
-    float* dx = static_cast<float*>(h->w_x.reserve(n * h->dim * sizeof(float)));
+    hipStream_t s = es.stream;
+    float* dx = static_cast<float*>(es.x.reserve(n * h->dim * sizeof(float)));
     QVH_HIP(hipMemcpyAsync(dx, x, n * h->dim * sizeof(float), hipMemcpyHostToDevice, s));
     if (h->metric == QVH_METRIC_COSINE) launch_normalize_rows(dx, n, h->dim, s);
-    ivf_encode_device(h, dx, n, s);
-    if (assign) QVH_HIP(hipMemcpyAsync(assign, h->w_assign.ptr, n * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
-    if (codes) QVH_HIP(hipMemcpyAsync(codes, h->w_codes.ptr, n * h->m, hipMemcpyDeviceToHost, s));
+    ivf_encode_device(h, es, dx, n, s);
+    if (assign) QVH_HIP(hipMemcpyAsync(assign, es.assign.ptr, n * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+    if (codes) QVH_HIP(hipMemcpyAsync(codes, es.codes.ptr, n * h->m, hipMemcpyDeviceToHost, s));
     if (stored_out) QVH_HIP(hipMemcpyAsync(stored_out, dx, n * h->dim * sizeof(float), hipMemcpyDeviceToHost, s));
     QVH_HIP(hipStreamSynchronize(s));
+  });
+}
+
+namespace {
+
+/// Appends n encoded entries to the lists, each after its list's existing entries in batch order
+/// (src/ivfpq_index.cc:250-269): cells d_assign / h_assign (device and host copies), codes d_codes
+/// [n][m], and with stored vectors d_vec [n][dim]. Builds the new CSR arrays on stream s and swaps
+/// them in once s is done. The caller holds the handle's lock.
+void ivf_append(qvh_ivfpq* h, const uint32_t* h_assign, const uint32_t* d_assign, const uint8_t* d_codes,
+                const float* d_vec, uint64_t n, hipStream_t s) {
+  const uint32_t nl = h->nlist;
+  std::vector<uint64_t> add(nl, 0);
+  for (uint64_t i = 0; i < n; ++i) {
+    QVH_REQUIRE(h_assign[i] < nl, "qvh_ivfpq_append: cell out of range");
+    ++add[h_assign[i]];
+  }
+  for (uint32_t l = 0; l < nl; ++l) {
+    QVH_REQUIRE(h->h_off[l + 1] - h->h_off[l] + add[l] <= 0xFFFFFFFFull,
+                "too many vectors in one IVF cell (2^32 limit); use a larger nlist");
+  }
+  const uint64_t total = h->count + n;
+  QVH_REQUIRE(total < 0xFFFFFFFFull, "IVF-PQ device path holds fewer than 2^32 vectors");
+  std::vector<uint64_t> shift(nl, 0), new_off(nl + 1, 0), cursor(nl, 0);
+  for (uint32_t l = 0; l < nl; ++l) {
+    shift[l] = l ? shift[l - 1] + add[l - 1] : 0;
+    new_off[l + 1] = new_off[l] + (h->h_off[l + 1] - h->h_off[l]) + add[l];
+    cursor[l] = new_off[l] + (h->h_off[l + 1] - h->h_off[l]);
+  }
+  std::vector<uint64_t> dest(n);
+  for (uint64_t i = 0; i < n; ++i) dest[i] = cursor[h_assign[i]]++;
+  // padded codes and term1 of the batch
+  uint8_t* cp = static_cast<uint8_t*>(h->w_codes_p.reserve(n * h->mp));
+  hipLaunchKernelGGL(pad_codes_kernel, dim3(static_cast<unsigned>(ceil_div(n * h->mp, 256))), dim3(256), 0, s,
+                     d_codes, h->m, h->mp, n, cp);
+  float* nt1 = nullptr;
+  if (h->has_pre) {
+    nt1 = static_cast<float*>(h->w_t1.reserve(n * sizeof(float)));
+    hipLaunchKernelGGL(term1_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, s,
+                       cp, h->mp, d_assign, h->pre.as<float>(), h->m, n, nt1);
+  }
+  uint64_t* ddest = static_cast<uint64_t*>(h->w_dest.reserve(n * sizeof(uint64_t)));
+  uint64_t* dshift = static_cast<uint64_t*>(h->w_shift.reserve(nl * sizeof(uint64_t)));
+  QVH_HIP(hipMemcpyAsync(ddest, dest.data(), n * sizeof(uint64_t), hipMemcpyHostToDevice, s));
+  QVH_HIP(hipMemcpyAsync(dshift, shift.data(), nl * sizeof(uint64_t), hipMemcpyHostToDevice, s));
+  // new CSR buffers
+  DeviceBuffer ncodes, nt1buf, nvec, noff;
+  ncodes.reserve(total * h->mp);
+  if (h->has_pre) nt1buf.reserve(total * sizeof(float));
+  if (h->store_vectors) nvec.reserve(total * h->dim * sizeof(float));
+  noff.reserve((nl + 1) * sizeof(uint64_t));
+  QVH_HIP(hipMemcpyAsync(noff.ptr, new_off.data(), (nl + 1) * sizeof(uint64_t), hipMemcpyHostToDevice, s));
+  ScatterArgs sa{};
+  sa.old_off = h->off.as<uint64_t>();
+  sa.shift = dshift;
+  sa.nlist = nl;
+  sa.old_count = h->count;
+  sa.n_new = n;
+  sa.dest = ddest;
+  sa.mp = h->mp;
+  sa.dim = h->dim;
+  sa.old_codes = h->codes.as<uint8_t>();
+  sa.new_codes = cp;
+  sa.codes = ncodes.as<uint8_t>();
+  sa.old_t1 = h->t1.as<float>();
+  sa.new_t1 = nt1;
+  sa.t1 = h->has_pre ? nt1buf.as<float>() : nullptr;
+  sa.old_vec = h->vec.as<float>();
+  sa.new_vec = d_vec;
+  sa.vec = h->store_vectors ? nvec.as<float>() : nullptr;
+  if (h->count) {
+    hipLaunchKernelGGL(scatter_old_kernel, dim3(static_cast<unsigned>(ceil_div(h->count, 256))), dim3(256), 0, s, sa);
+  }
+  hipLaunchKernelGGL(scatter_new_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, s, sa);
+  QVH_HIP(hipGetLastError());
+  QVH_HIP(hipStreamSynchronize(s));
+  std::swap(h->codes.ptr, ncodes.ptr);
+  std::swap(h->codes.bytes, ncodes.bytes);
+  std::swap(h->t1.ptr, nt1buf.ptr);
+  std::swap(h->t1.bytes, nt1buf.bytes);
+  std::swap(h->vec.ptr, nvec.ptr);
+  std::swap(h->vec.bytes, nvec.bytes);
+  std::swap(h->off.ptr, noff.ptr);
+  std::swap(h->off.bytes, noff.bytes);
+  h->h_off = std::move(new_off);
+  h->count = total;
+}
+
+}  // namespace
+
+qvh_status qvh_ivfpq_append(qvh_ivfpq* h, const uint32_t* assign, const uint8_t* codes, const float* vectors,
+                            uint64_t n) {
+  return guarded([&] {
+    QVH_REQUIRE(h != nullptr, "qvh_ivfpq_append: null handle");
+    if (n == 0) return;
+    QVH_REQUIRE(assign != nullptr && codes != nullptr, "qvh_ivfpq_append: null cells or codes");
+    QVH_REQUIRE(!h->store_vectors || vectors != nullptr, "qvh_ivfpq_append: the index stores vectors: pass them");
+    std::lock_guard<std::mutex> lock(h->mu);
+    QVH_REQUIRE(h->trained.load(std::memory_order_acquire), "IVF-PQ index must be trained before add()");
+    QVH_HIP(hipSetDevice(h->device));
+    hipStream_t s = h->stream;
+    uint32_t* da = static_cast<uint32_t*>(h->w_assign.reserve(n * sizeof(uint32_t)));
+    uint8_t* dc = static_cast<uint8_t*>(h->w_codes.reserve(n * h->m));
+    QVH_HIP(hipMemcpyAsync(da, assign, n * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+    QVH_HIP(hipMemcpyAsync(dc, codes, n * h->m, hipMemcpyHostToDevice, s));
+    float* dv = nullptr;
+    if (h->store_vectors) {
+      dv = static_cast<float*>(h->w_x.reserve(n * h->dim * sizeof(float)));
+      QVH_HIP(hipMemcpyAsync(dv, vectors, n * h->dim * sizeof(float), hipMemcpyHostToDevice, s));
+    }
+    ivf_append(h, assign, da, dc, dv, n, s);
   });
 }
 
@@ -2916,90 +3050,19 @@ qvh_status qvh_ivfpq_add(qvh_ivfpq* h, const float* x, uint64_t n, uint32_t* ass
     if (n == 0) return;
     QVH_REQUIRE(x != nullptr, "qvh_ivfpq_add: null vectors");
     std::lock_guard<std::mutex> lock(h->mu);
-    ivf_check_trained(h);
+    EncodeSpace& es = h->enc;
+    std::lock_guard<std::mutex> enc_lock(es.mu);  // always after the handle's lock
+    QVH_REQUIRE(h->trained.load(std::memory_order_acquire), "IVF-PQ index must be trained before add()");
     QVH_HIP(hipSetDevice(h->device));
     hipStream_t s = h->stream;
-    float* dx = static_cast<float*>(h->w_x.reserve(n * h->dim * sizeof(float)));
+    float* dx = static_cast<float*>(es.x.reserve(n * h->dim * sizeof(float)));
     QVH_HIP(hipMemcpyAsync(dx, x, n * h->dim * sizeof(float), hipMemcpyHostToDevice, s));
     if (h->metric == QVH_METRIC_COSINE) launch_normalize_rows(dx, n, h->dim, s);
-    ivf_encode_device(h, dx, n, s);
+    ivf_encode_device(h, es, dx, n, s);
     std::vector<uint32_t> assign(n);
-    QVH_HIP(hipMemcpyAsync(assign.data(), h->w_assign.ptr, n * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+    QVH_HIP(hipMemcpyAsync(assign.data(), es.assign.ptr, n * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
     QVH_HIP(hipStreamSynchronize(s));
-    // Destinations: each batch entry goes after its list's existing entries, in input order
-    // (src/ivfpq_index.cc:263-269).
-    const uint32_t nl = h->nlist;
-    std::vector<uint64_t> add(nl, 0);
-    for (uint64_t i = 0; i < n; ++i) ++add[assign[i]];
-    for (uint32_t l = 0; l < nl; ++l) {
-      QVH_REQUIRE(h->h_off[l + 1] - h->h_off[l] + add[l] <= 0xFFFFFFFFull,
-                  "too many vectors in one IVF cell (2^32 limit); use a larger nlist");
-    }
-    std::vector<uint64_t> shift(nl, 0), new_off(nl + 1, 0), cursor(nl, 0);
-    for (uint32_t l = 0; l < nl; ++l) {
-      shift[l] = l ? shift[l - 1] + add[l - 1] : 0;
-      new_off[l + 1] = new_off[l] + (h->h_off[l + 1] - h->h_off[l]) + add[l];
-      cursor[l] = new_off[l] + (h->h_off[l + 1] - h->h_off[l]);
-    }
-    std::vector<uint64_t> dest(n);
-    for (uint64_t i = 0; i < n; ++i) dest[i] = cursor[assign[i]]++;
-    const uint64_t total = h->count + n;
-    QVH_REQUIRE(total < 0xFFFFFFFFull, "IVF-PQ device path holds fewer than 2^32 vectors");
-    // padded codes and term1 of the batch
-    uint8_t* cp = static_cast<uint8_t*>(h->w_codes_p.reserve(n * h->mp));
-    hipLaunchKernelGGL(pad_codes_kernel, dim3(static_cast<unsigned>(ceil_div(n * h->mp, 256))), dim3(256), 0, s,
-                       h->w_codes.as<uint8_t>(), h->m, h->mp, n, cp);
-    float* nt1 = nullptr;
-    if (h->has_pre) {
-      nt1 = static_cast<float*>(h->w_t1.reserve(n * sizeof(float)));
-      hipLaunchKernelGGL(term1_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, s,
-                         cp, h->mp, h->w_assign.as<uint32_t>(), h->pre.as<float>(), h->m, n, nt1);
-    }
-    uint64_t* ddest = static_cast<uint64_t*>(h->w_dest.reserve(n * sizeof(uint64_t)));
-    uint64_t* dshift = static_cast<uint64_t*>(h->w_shift.reserve(nl * sizeof(uint64_t)));
-    QVH_HIP(hipMemcpyAsync(ddest, dest.data(), n * sizeof(uint64_t), hipMemcpyHostToDevice, s));
-    QVH_HIP(hipMemcpyAsync(dshift, shift.data(), nl * sizeof(uint64_t), hipMemcpyHostToDevice, s));
-    // new CSR buffers
-    DeviceBuffer ncodes, nt1buf, nvec, noff;
-    ncodes.reserve(total * h->mp);
-    if (h->has_pre) nt1buf.reserve(total * sizeof(float));
-    if (h->store_vectors) nvec.reserve(total * h->dim * sizeof(float));
-    noff.reserve((nl + 1) * sizeof(uint64_t));
-    QVH_HIP(hipMemcpyAsync(noff.ptr, new_off.data(), (nl + 1) * sizeof(uint64_t), hipMemcpyHostToDevice, s));
-    ScatterArgs sa{};
-    sa.old_off = h->off.as<uint64_t>();
-    sa.shift = dshift;
-    sa.nlist = nl;
-    sa.old_count = h->count;
-    sa.n_new = n;
-    sa.dest = ddest;
-    sa.mp = h->mp;
-    sa.dim = h->dim;
-    sa.old_codes = h->codes.as<uint8_t>();
-    sa.new_codes = cp;
-    sa.codes = ncodes.as<uint8_t>();
-    sa.old_t1 = h->t1.as<float>();
-    sa.new_t1 = nt1;
-    sa.t1 = h->has_pre ? nt1buf.as<float>() : nullptr;
-    sa.old_vec = h->vec.as<float>();
-    sa.new_vec = dx;
-    sa.vec = h->store_vectors ? nvec.as<float>() : nullptr;
-    if (h->count) {
-      hipLaunchKernelGGL(scatter_old_kernel, dim3(static_cast<unsigned>(ceil_div(h->count, 256))), dim3(256), 0, s, sa);
-    }
-    hipLaunchKernelGGL(scatter_new_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, s, sa);
-    QVH_HIP(hipGetLastError());
-    QVH_HIP(hipStreamSynchronize(s));
-    std::swap(h->codes.ptr, ncodes.ptr);
-    std::swap(h->codes.bytes, ncodes.bytes);
-    std::swap(h->t1.ptr, nt1buf.ptr);
-    std::swap(h->t1.bytes, nt1buf.bytes);
-    std::swap(h->vec.ptr, nvec.ptr);
-    std::swap(h->vec.bytes, nvec.bytes);
-    std::swap(h->off.ptr, noff.ptr);
-    std::swap(h->off.bytes, noff.bytes);
-    h->h_off = std::move(new_off);
-    h->count = total;
+    ivf_append(h, assign.data(), es.assign.as<uint32_t>(), es.codes.as<uint8_t>(), dx, n, s);
     if (assign_out) std::memcpy(assign_out, assign.data(), n * sizeof(uint32_t));
   });
 }

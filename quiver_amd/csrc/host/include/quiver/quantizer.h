@@ -4,10 +4,11 @@
 // k-means runs its control flow (subsample, random initialization, double-precision centroid sums,
 // empty-cluster splitting) on the host with the reference's random engine; every assignment step is
 // one call of the device's exact nearest-centroid kernel (qvh_points_nearest), so the centroids
-// come out bit-identical to the reference's. nearest_centroid and every ProductQuantizer operation
-// run on the device (qvh_nearest_centroid, qvh_pq_*), batched: the reference's per-vector methods
-// are batches of one, and the *_batch methods (no reference counterpart) take many vectors per
-// device call.
+// come out bit-identical to the reference's. The reference's per-vector methods (nearest_centroid,
+// ProductQuantizer::encode / decode / compute_*_table / adc / adc_batch) run on the host in the
+// reference's float order and cannot fail, as the reference's noexcept versions cannot; the
+// *_batch methods (no reference counterpart) run many vectors per device call (qvh_nearest_centroid,
+// qvh_pq_*) with the same arithmetic and throw quiver::Error on a device failure.
 #pragma once
 
 #include <cstddef>
@@ -34,8 +35,8 @@ struct KMeansParams {
 std::vector<float> kmeans(const float* vectors, std::size_t n, std::size_t dim,
                           const KMeansParams& params, ThreadPool* pool = nullptr);
 
-/// Index of the centroid nearest to `x` (squared L2; the first of equal ones; 0 when no distance
-/// is finite). A device failure here terminates the process: the reference's version cannot fail.
+/// Index of the centroid nearest to `x` (squared L2 in the AVX2 kernels' order; the first of equal
+/// ones; 0 when no distance is finite). Host code.
 std::size_t nearest_centroid(const float* x, const float* centroids, std::size_t k,
                              std::size_t dim) noexcept;
 
@@ -45,9 +46,9 @@ void nearest_centroid_batch(const float* x, std::size_t n, const float* centroid
 
 /// PQ: the vector is split into `m` sub-vectors, each replaced by the id of its nearest of 256
 /// sub-centroids, so a vector costs `m` bytes; distances to a query use asymmetric distance
-/// computation over an m x 256 table. The codebook lives on the device once trained or set; copies
-/// share it. The noexcept methods terminate the process on a device failure (the reference's CPU
-/// versions cannot fail); the *_batch methods throw quiver::Error instead.
+/// computation over an m x 256 table. The codebook is kept on the host and on the device once
+/// trained or set; copies share the device copy. The noexcept methods compute on the host; the
+/// *_batch methods on the device, throwing quiver::Error if it fails.
 class ProductQuantizer {
  public:
   static constexpr std::size_t kSubCentroids = 256;

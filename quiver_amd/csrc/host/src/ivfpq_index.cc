@@ -165,6 +165,10 @@ struct IvfPqIndex::Impl {
     commit(std::move(cent), std::move(cb));
   }
 
+  // Impl::add of the reference (src/ivfpq_index.cc:208-271). The encode runs on the device without
+  // the index lock (the trained state it reads never changes once set; the reference likewise
+  // only observes `trained` under the shared lock), so searches proceed meanwhile; the exclusive
+  // lock is taken only to append the encoded entries and place their labels.
   void add(const float* in, std::size_t n, const Label* new_labels) {
     if (n == 0) return;
     check_finite(in, n * params.dim);
@@ -172,10 +176,21 @@ struct IvfPqIndex::Impl {
       QUIVER_CHECK(std::find(new_labels, new_labels + n, kInvalidLabel) == new_labels + n,
                    "label 2^64-1 is reserved (it marks empty result slots)");
     }
-    std::unique_lock lock(mu);
-    QUIVER_CHECK(trained, "IVF-PQ index must be trained before add()");
+    {
+      std::shared_lock lock(mu);
+      QUIVER_CHECK(trained, "IVF-PQ index must be trained before add()");
+    }
     std::vector<std::uint32_t> assign(n);
-    qvh_check(qvh_ivfpq_add(dev.get(), in, n, assign.data()), "IvfPqIndex::add");
+    std::vector<std::uint8_t> codes(n * params.m);
+    std::vector<float> stored(params.store_vectors ? n * params.dim : 0);
+    qvh_check(qvh_ivfpq_encode(dev.get(), in, n, assign.data(), codes.data(),
+                               params.store_vectors ? stored.data() : nullptr),
+              "IvfPqIndex::add");
+
+    std::unique_lock lock(mu);
+    qvh_check(qvh_ivfpq_append(dev.get(), assign.data(), codes.data(),
+                               params.store_vectors ? stored.data() : nullptr, n),
+              "IvfPqIndex::add");
     // The device appended each vector after its list's entries in input order; place the
     // labels the same way (src/ivfpq_index.cc:263-269).
     const std::size_t nl = params.nlist;

@@ -1,6 +1,6 @@
-#include <cstdio>
-#include <cstdlib>
+#include <cmath>
 #include <cstring>
+#include <limits>
 #include <string>
 
 #include "device_util.h"
@@ -10,20 +10,88 @@ namespace quiver {
 
 namespace {
 
-/// The reference's noexcept quantizer methods cannot fail; on the device they can, and then the
-/// process stops with the message rather than returning garbage.
-[[noreturn]] void fatal(const char* what, const std::exception& e) noexcept {
-  std::fprintf(stderr, "quiver: %s failed: %s\n", what, e.what());
-  std::abort();
+constexpr std::size_t kBook = ProductQuantizer::kSubCentroids;
+
+/// out[c] = sum over t of (x_t - book[c][t])^2 for the 256 codewords of one sub-space, each sum
+/// taken in order of t from 0.0f with separately rounded products: CentroidTable::l2
+/// (src/internal/centroid_table.h:65-75) visits t in the outer loop, which gives every c the same
+/// sequence of additions.
+void codeword_l2(const float* x, const float* book, std::size_t dsub, float* out) noexcept {
+  for (std::size_t c = 0; c < kBook; ++c) {
+    const float* w = book + c * dsub;
+    float acc = 0.0f;
+    for (std::size_t t = 0; t < dsub; ++t) {
+      const float diff = x[t] - w[t];
+      acc += diff * diff;
+    }
+    out[c] = acc;
+  }
 }
 
-template <class F>
-void or_die(const char* what, F&& f) noexcept {
-  try {
-    f();
-  } catch (const std::exception& e) {
-    fatal(what, e);
+/// out[c] = sum over t of x_t * book[c][t], in order of t from 0.0f (CentroidTable::dot,
+/// src/internal/centroid_table.h:78-85).
+void codeword_dot(const float* x, const float* book, std::size_t dsub, float* out) noexcept {
+  for (std::size_t c = 0; c < kBook; ++c) {
+    const float* w = book + c * dsub;
+    float acc = 0.0f;
+    for (std::size_t t = 0; t < dsub; ++t) acc += x[t] * w[t];
+    out[c] = acc;
   }
+}
+
+/// The index CentroidTable::argmin_n returns (src/internal/centroid_table.h:155-170): the smallest
+/// value that is not NaN (+inf if every value is NaN), then the first index holding a value equal
+/// to it; 0 when none does (all NaN). Signed zeros compare equal, so which zero the minimum holds
+/// does not matter.
+std::size_t first_minimum(const float* v, std::size_t n) noexcept {
+  float lowest = std::numeric_limits<float>::infinity();
+  for (std::size_t i = 0; i < n; ++i) {
+    if (v[i] < lowest) lowest = v[i];
+  }
+  for (std::size_t i = 0; i < n; ++i) {
+    if (v[i] == lowest) return i;
+  }
+  return 0;
+}
+
+/// simd::l2sqr with the AVX2 kernels (src/simd/kernels_avx2.cc:35-56), the kernel the reference
+/// dispatches to on x86-64 (src/simd/dispatch.cc:108-117): eight-lane fused accumulators over
+/// blocks of 32 elements and then of 8, the pairwise horizontal sum, and the tail as GCC compiles
+/// it (the first four remaining products rounded and added, the rest fused).
+float l2sqr_avx2_order(const float* a, const float* b, std::size_t dim) noexcept {
+  float acc[4][8] = {};
+  std::size_t i = 0;
+  for (; i + 32 <= dim; i += 32) {
+    for (std::size_t block = 0; block < 4; ++block) {
+      for (std::size_t lane = 0; lane < 8; ++lane) {
+        const float diff = a[i + block * 8 + lane] - b[i + block * 8 + lane];
+        acc[block][lane] = std::fma(diff, diff, acc[block][lane]);
+      }
+    }
+  }
+  for (; i + 8 <= dim; i += 8) {
+    for (std::size_t lane = 0; lane < 8; ++lane) {
+      const float diff = a[i + lane] - b[i + lane];
+      acc[0][lane] = std::fma(diff, diff, acc[0][lane]);
+    }
+  }
+  float lanes[8];
+  for (std::size_t lane = 0; lane < 8; ++lane) {
+    lanes[lane] = (acc[0][lane] + acc[1][lane]) + (acc[2][lane] + acc[3][lane]);
+  }
+  float half[4];
+  for (std::size_t j = 0; j < 4; ++j) half[j] = lanes[j] + lanes[j + 4];
+  float sum = (half[0] + half[1]) + (half[2] + half[3]);
+  const std::size_t rounded_end = i + (dim - i) / 4 * 4;
+  for (; i < rounded_end; ++i) {
+    const float diff = a[i] - b[i];
+    sum += diff * diff;
+  }
+  for (; i < dim; ++i) {
+    const float diff = a[i] - b[i];
+    sum = std::fma(diff, diff, sum);
+  }
+  return sum;
 }
 
 }  // namespace
@@ -39,11 +107,20 @@ void nearest_centroid_batch(const float* x, std::size_t n, const float* centroid
                       "nearest_centroid");
 }
 
+// nearest_centroid (src/product_quantizer.cc:14-27) for one point, on the host: the AVX2-order
+// distance to each centroid in turn, a strictly smaller one replacing the best. It cannot fail,
+// like the reference's; nearest_centroid_batch runs the same arithmetic on the device.
 std::size_t nearest_centroid(const float* x, const float* centroids, std::size_t k, std::size_t dim) noexcept {
-  std::uint32_t out = 0;
-  if (k == 0) return 0;
-  or_die("nearest_centroid", [&] { nearest_centroid_batch(x, 1, centroids, k, dim, &out); });
-  return out;
+  std::size_t best = 0;
+  float best_dist = std::numeric_limits<float>::infinity();
+  for (std::size_t c = 0; c < k; ++c) {
+    const float dist = l2sqr_avx2_order(x, centroids + c * dim, dim);
+    if (dist < best_dist) {
+      best_dist = dist;
+      best = c;
+    }
+  }
+  return best;
 }
 
 ProductQuantizer::ProductQuantizer() = default;
@@ -116,35 +193,55 @@ void ProductQuantizer::compute_tables(const float* queries, std::size_t nq, bool
   internal::qvh_check(qvh_pq_tables(device(), queries, nq, inner_product ? 1 : 0, tables), "PQ tables");
 }
 
+// The per-vector methods below run on the host, in the reference's float order, so they are
+// bit-identical to it and to the device batch methods, and they cannot fail (the reference's are
+// noexcept). Before a codebook is installed they leave their outputs untouched (encode, decode,
+// tables) or return 0 (adc).
+
 void ProductQuantizer::encode(const float* vector, std::uint8_t* code) const noexcept {
-  or_die("ProductQuantizer::encode", [&] { encode_batch(vector, 1, code); });
+  if (!trained()) return;
+  float dist[kBook];
+  for (std::size_t j = 0; j < m_; ++j) {
+    codeword_l2(vector + j * dsub_, centroids_.data() + j * kBook * dsub_, dsub_, dist);
+    code[j] = static_cast<std::uint8_t>(first_minimum(dist, kBook));
+  }
 }
 
 void ProductQuantizer::decode(const std::uint8_t* code, float* vector) const noexcept {
-  or_die("ProductQuantizer::decode", [&] { decode_batch(code, 1, vector); });
+  if (!trained()) return;
+  for (std::size_t j = 0; j < m_; ++j) {
+    const float* word = centroids_.data() + (j * kBook + code[j]) * dsub_;
+    std::memcpy(vector + j * dsub_, word, dsub_ * sizeof(float));
+  }
 }
 
 void ProductQuantizer::compute_l2_table(const float* query, float* table) const noexcept {
-  or_die("ProductQuantizer::compute_l2_table", [&] { compute_tables(query, 1, false, table); });
+  if (!trained()) return;
+  for (std::size_t j = 0; j < m_; ++j) {
+    codeword_l2(query + j * dsub_, centroids_.data() + j * kBook * dsub_, dsub_, table + j * kBook);
+  }
 }
 
 void ProductQuantizer::compute_ip_table(const float* query, float* table) const noexcept {
-  or_die("ProductQuantizer::compute_ip_table", [&] { compute_tables(query, 1, true, table); });
+  if (!trained()) return;
+  for (std::size_t j = 0; j < m_; ++j) {
+    codeword_dot(query + j * dsub_, centroids_.data() + j * kBook * dsub_, dsub_, table + j * kBook);
+  }
 }
 
+// ProductQuantizer::adc (src/product_quantizer.cc:188-192): the table entries a code selects,
+// added in order of the sub-spaces from 0.0f.
 float ProductQuantizer::adc(const float* table, const std::uint8_t* code) const noexcept {
-  float out = 0.0f;
-  adc_batch(table, code, 1, &out);
-  return out;
+  float sum = 0.0f;
+  for (std::size_t j = 0; j < m_; ++j) sum += table[j * kBook + code[j]];
+  return sum;
 }
 
+// ProductQuantizer::adc_batch (src/product_quantizer.cc:194-217) interleaves four codes, but each
+// code's sum is still taken in order of j, so every out[i] equals adc of code i.
 void ProductQuantizer::adc_batch(const float* table, const std::uint8_t* codes, std::size_t n,
                                  float* out) const noexcept {
-  if (n == 0) return;
-  or_die("ProductQuantizer::adc_batch", [&] {
-    QUIVER_CHECK(table != nullptr && codes != nullptr && out != nullptr, "PQ adc: null buffer");
-    internal::qvh_check(qvh_pq_adc(device(), table, codes, n, out), "PQ adc");
-  });
+  for (std::size_t i = 0; i < n; ++i) out[i] = adc(table, codes + i * m_);
 }
 
 }  // namespace quiver

@@ -7,7 +7,8 @@
 
 #include <algorithm>
 #include <cstring>
-#include <map>
+#include <utility>
+#include <vector>
 #include <memory>
 #include <mutex>
 
@@ -24,30 +25,46 @@ namespace {
 using FloatMatrix = py::array_t<float, py::array::c_style>;
 using LabelArray = py::array_t<std::uint64_t, py::array::c_style>;
 
-/// One cached pool per requested size (python/quiver_ext.cc:28-37).
-quiver::ThreadPool* pool_for(std::size_t num_threads) {
-  if (num_threads == 0) return &quiver::ThreadPool::global();
-  if (num_threads > 1024) throw py::value_error("num_threads must be at most 1024");
-  static std::mutex mu;
-  static std::map<std::size_t, std::unique_ptr<quiver::ThreadPool>> pools;
-  std::lock_guard<std::mutex> lock(mu);
-  auto& p = pools[num_threads];
-  if (!p) p = std::make_unique<quiver::ThreadPool>(num_threads);
-  return p.get();
-}
+/// Host thread pools the Python calls may ask for. num_threads = 0 is the process-wide pool; any
+/// other size is created on first request and kept for the life of the module, so repeated calls
+/// with one size reuse its threads (python/quiver_ext.cc:28-37 keeps one per size too).
+class PoolRegistry {
+ public:
+  static constexpr std::size_t kMaxThreads = 1024;
 
-/// The cheaper filter for a set of allowed labels: a bitset unless labels are very sparse
-/// (the same rule as python/quiver_ext.cc:40-51).
-std::unique_ptr<quiver::Filter> make_filter(const LabelArray& allowed) {
-  const std::uint64_t* p = allowed.data();
-  const std::size_t n = static_cast<std::size_t>(allowed.size());
-  const std::uint64_t max_label = n == 0 ? 0 : *std::max_element(p, p + n);
-  if (max_label < (std::uint64_t{1} << 32) && max_label / 64 <= 16 * n + 1024) {
-    auto f = std::make_unique<quiver::BitsetFilter>(static_cast<std::size_t>(max_label) + 1);
-    for (std::size_t i = 0; i < n; ++i) f->insert(p[i]);
-    return f;
+  static quiver::ThreadPool* get(std::size_t threads) {
+    if (threads == 0) return &quiver::ThreadPool::global();
+    if (threads > kMaxThreads) throw py::value_error("num_threads must be at most 1024");
+    static PoolRegistry registry;
+    std::lock_guard<std::mutex> lock(registry.mu_);
+    for (const auto& entry : registry.pools_) {
+      if (entry.first == threads) return entry.second.get();
+    }
+    registry.pools_.emplace_back(threads, std::make_unique<quiver::ThreadPool>(threads));
+    return registry.pools_.back().second.get();
   }
-  return std::make_unique<quiver::LabelSetFilter>(p, p + n);
+
+ private:
+  std::mutex mu_;
+  std::vector<std::pair<std::size_t, std::unique_ptr<quiver::ThreadPool>>> pools_;
+};
+
+/// The Filter an allowed-label array becomes. A bitset over [0, largest label] answers a lookup
+/// with one word read; a hash set costs about 16 bytes per label. The bitset is chosen while its
+/// words (largest / 64) stay within 16 per label plus 1024 and the largest label is below 2^32,
+/// the rule python/quiver_ext.cc:40-51 applies, so both builds pick the same filter type.
+std::unique_ptr<quiver::Filter> allowed_filter(const LabelArray& allowed) {
+  const std::size_t count = static_cast<std::size_t>(allowed.size());
+  const std::uint64_t* first = allowed.data();
+  const std::uint64_t* last = first + count;
+  std::uint64_t largest = 0;
+  for (const std::uint64_t* it = first; it != last; ++it) largest = std::max(largest, *it);
+  const bool fits_u32 = largest >> 32 == 0;
+  const bool bitset_small = largest / 64 <= 16 * static_cast<std::uint64_t>(count) + 1024;
+  if (!(fits_u32 && bitset_small)) return std::make_unique<quiver::LabelSetFilter>(first, last);
+  auto bits = std::make_unique<quiver::BitsetFilter>(static_cast<std::size_t>(largest) + 1);
+  for (const std::uint64_t* it = first; it != last; ++it) bits->insert(*it);
+  return bits;
 }
 
 void check_matrix(const FloatMatrix& x, std::size_t dim) {
@@ -58,28 +75,29 @@ void check_matrix(const FloatMatrix& x, std::size_t dim) {
   }
 }
 
-/// nq * k, rejecting sizes that would overflow or that no machine could allocate
+/// The two result arrays of a search, allocated as numpy arrays before the search runs so the C++
+/// call writes straight into them: labels int64 [nq, k] (written as quiver::Label, whose empty
+/// value 2^64 - 1 reads back as -1) and distances float32 [nq, k]. More than 2^40 result slots,
+/// or an nq * k that overflows, is refused with the reference's message
 /// (python/quiver_ext.cc:62-68).
-std::size_t result_size(std::size_t nq, std::size_t k) {
-  std::size_t total = 0;
-  if (__builtin_mul_overflow(nq, k, &total) || total > (std::size_t{1} << 40)) {
-    throw py::value_error("nq * k is too large");
-  }
-  return total;
-}
+struct SearchResults {
+  py::array_t<std::int64_t> labels;
+  py::array_t<float> distances;
 
-/// (labels int64 [nq, k] with -1 for empty slots, distances float32 [nq, k]).
-py::tuple make_results(std::size_t nq, std::size_t k, std::vector<std::uint64_t>&& labels,
-                       std::vector<float>&& dist) {
-  auto* l = new std::vector<std::uint64_t>(std::move(labels));
-  auto* d = new std::vector<float>(std::move(dist));
-  py::capsule lc(l, [](void* p) { delete static_cast<std::vector<std::uint64_t>*>(p); });
-  py::capsule dc(d, [](void* p) { delete static_cast<std::vector<float>*>(p); });
-  // kInvalidLabel (2^64 - 1) reinterpreted as int64 is exactly -1.
-  py::array_t<std::int64_t> la({nq, k}, reinterpret_cast<std::int64_t*>(l->data()), lc);
-  py::array_t<float> da({nq, k}, d->data(), dc);
-  return py::make_tuple(la, da);
-}
+  SearchResults(std::size_t nq, std::size_t k) {
+    std::size_t slots = 0;
+    if (__builtin_mul_overflow(nq, k, &slots) || slots > (std::size_t{1} << 40)) {
+      throw py::value_error("nq * k is too large");
+    }
+    const std::vector<py::ssize_t> shape{static_cast<py::ssize_t>(nq), static_cast<py::ssize_t>(k)};
+    labels = py::array_t<std::int64_t>(shape);
+    distances = py::array_t<float>(shape);
+  }
+
+  quiver::Label* label_data() { return reinterpret_cast<quiver::Label*>(labels.mutable_data()); }
+  float* distance_data() { return distances.mutable_data(); }
+  py::tuple as_tuple() const { return py::make_tuple(labels, distances); }
+};
 
 const std::uint64_t* optional_labels(const py::object& labels, std::size_t n, LabelArray& hold) {
   if (labels.is_none()) return nullptr;
@@ -143,16 +161,17 @@ PYBIND11_MODULE(_quiver, m) {
              const py::object& allowed, std::size_t threads) {
             check_matrix(q, self.dim());
             std::unique_ptr<quiver::Filter> filter;
-            if (!allowed.is_none()) filter = make_filter(allowed.cast<LabelArray>());
+            if (!allowed.is_none()) filter = allowed_filter(allowed.cast<LabelArray>());
             const std::size_t nq = q.shape(0);
-            std::vector<std::uint64_t> labels(result_size(nq, k));
-            std::vector<float> dist(labels.size());
-            quiver::ThreadPool* pool = pool_for(threads);
+            SearchResults out(nq, k);
+            quiver::Label* labels = out.label_data();
+            float* dist = out.distance_data();
+            quiver::ThreadPool* pool = PoolRegistry::get(threads);
             {
               py::gil_scoped_release release;
-              self.search_batch(q.data(), nq, k, labels.data(), dist.data(), filter.get(), pool);
+              self.search_batch(q.data(), nq, k, labels, dist, filter.get(), pool);
             }
-            return make_results(nq, k, std::move(labels), std::move(dist));
+            return out.as_tuple();
           },
           py::arg("queries"), py::arg("k"), py::arg("allowed").none(true), py::arg("num_threads"))
       .def("save", &quiver::FlatIndex::save, py::arg("path"), py::call_guard<py::gil_scoped_release>())
@@ -189,7 +208,7 @@ PYBIND11_MODULE(_quiver, m) {
           py::arg("stream"))
       .def("_row_bitmap",
            [](const quiver::FlatIndex& self, const LabelArray& allowed) {
-             const auto filter = make_filter(allowed);
+             const auto filter = allowed_filter(allowed);
              std::vector<std::uint64_t> bits;
              {
                py::gil_scoped_release release;
@@ -225,7 +244,7 @@ PYBIND11_MODULE(_quiver, m) {
           "_train",
           [](quiver::IvfPqIndex& self, const FloatMatrix& x, std::size_t threads) {
             check_matrix(x, self.dim());
-            quiver::ThreadPool* pool = pool_for(threads);
+            quiver::ThreadPool* pool = PoolRegistry::get(threads);
             py::gil_scoped_release release;
             self.train(x.data(), x.shape(0), pool);
           },
@@ -236,7 +255,7 @@ PYBIND11_MODULE(_quiver, m) {
             check_matrix(x, self.dim());
             LabelArray hold;
             const std::uint64_t* lp = optional_labels(labels, x.shape(0), hold);
-            quiver::ThreadPool* pool = pool_for(threads);
+            quiver::ThreadPool* pool = PoolRegistry::get(threads);
             py::gil_scoped_release release;
             self.add(x.data(), x.shape(0), lp, pool);
           },
@@ -247,20 +266,21 @@ PYBIND11_MODULE(_quiver, m) {
              std::size_t refine_factor, const py::object& allowed, std::size_t threads) {
             check_matrix(q, self.dim());
             std::unique_ptr<quiver::Filter> filter;
-            if (!allowed.is_none()) filter = make_filter(allowed.cast<LabelArray>());
+            if (!allowed.is_none()) filter = allowed_filter(allowed.cast<LabelArray>());
             const std::size_t nq = q.shape(0);
-            std::vector<std::uint64_t> labels(result_size(nq, k));
-            std::vector<float> dist(labels.size());
+            SearchResults out(nq, k);
+            quiver::Label* labels = out.label_data();
+            float* dist = out.distance_data();
             quiver::IvfPqSearchParams p;
             p.nprobe = nprobe;
             p.refine_factor = refine_factor;
             p.filter = filter.get();
-            quiver::ThreadPool* pool = pool_for(threads);
+            quiver::ThreadPool* pool = PoolRegistry::get(threads);
             {
               py::gil_scoped_release release;
-              self.search_batch(q.data(), nq, k, labels.data(), dist.data(), p, pool);
+              self.search_batch(q.data(), nq, k, labels, dist, p, pool);
             }
-            return make_results(nq, k, std::move(labels), std::move(dist));
+            return out.as_tuple();
           },
           py::arg("queries"), py::arg("k"), py::arg("nprobe"), py::arg("refine_factor"),
           py::arg("allowed").none(true), py::arg("num_threads"))
@@ -296,7 +316,7 @@ PYBIND11_MODULE(_quiver, m) {
           py::arg("bitmap"), py::arg("refs"), py::arg("distances"), py::arg("stream"))
       .def("_position_bitmap",
            [](const quiver::IvfPqIndex& self, const LabelArray& allowed) {
-             const auto filter = make_filter(allowed);
+             const auto filter = allowed_filter(allowed);
              std::vector<std::uint64_t> bits;
              {
                py::gil_scoped_release release;
@@ -392,7 +412,7 @@ PYBIND11_MODULE(_quiver, m) {
         kp.seed = seed;
         std::vector<float> c;
         const std::size_t n = x.shape(0), d = x.shape(1);
-        quiver::ThreadPool* pool = pool_for(threads);
+        quiver::ThreadPool* pool = PoolRegistry::get(threads);
         {
           py::gil_scoped_release release;
           c = quiver::kmeans(x.data(), n, d, kp, pool);

@@ -5,16 +5,22 @@
 // run on the GPU. Prints one line per case and exits non-zero on a failure.
 
 #include <algorithm>
+#include <atomic>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <filesystem>
+#include <cstring>
 #include <functional>
+#include <limits>
 #include <random>
 #include <string>
+#include <thread>
 #include <unordered_set>
 #include <vector>
 
+#include "qvh.h"
 #include "quiver/common.h"
 #include "quiver/filter.h"
 #include "quiver/flat_index.h"
@@ -342,6 +348,94 @@ void pq_adc_equals_distance_to_reconstruction() {
   EXPECT(std::equal(c1.begin(), c1.end(), codes.begin() + 3 * static_cast<std::ptrdiff_t>(m)) && c1 == c2);
 }
 
+bool same_bits(const float* a, const float* b, std::size_t n) { return std::memcmp(a, b, n * sizeof(float)) == 0; }
+
+/// Bit-identical, except that two NaNs match whatever their sign: a NaN codeword gives the host
+/// (x86, like the reference) a positive NaN table entry and the device a negative one. A NaN
+/// distance never ranks (the scans map it to +inf), so only the table's bits can show the sign.
+bool same_bits_or_nan(const float* a, const float* b, std::size_t n) {
+  for (std::size_t i = 0; i < n; ++i) {
+    if (std::isnan(a[i]) && std::isnan(b[i])) continue;
+    if (std::memcmp(a + i, b + i, sizeof(float)) != 0) return false;
+  }
+  return true;
+}
+
+// The per-vector ProductQuantizer methods and nearest_centroid run on the host, the *_batch methods
+// and the C-ABI's qvh_pq_adc on the device (those are checked against the reference's golden
+// vectors and the oracle in tests/test_pq_gpu.py). Both follow the reference's float order
+// (src/product_quantizer.cc:14-27,165-217, src/internal/centroid_table.h:65-85,155-170), so they
+// must agree bit for bit: sub-spaces of 1 to 8 dims, NaN and infinite codewords (argmin_n takes
+// the first index holding the smallest non-NaN value, 0 when all are NaN), and point dims 1-70,
+// which cover every tail length of the AVX2-order distance.
+void pq_per_vector_host_matches_device_batch() {
+  const std::pair<std::size_t, std::size_t> shapes[] = {{128, 32}, {100, 25}, {96, 12}, {30, 30}, {56, 7}};
+  for (const auto& [dim, m] : shapes) {
+    const std::size_t dsub = dim / m, n = 300;
+    auto book = normal_vectors(m * 256 * dsub, 1, dim + m);
+    // sub-space 0: codeword 0 NaN, 1-255 +inf (the first +inf wins); sub-space 1: every codeword NaN
+    const float nan = std::numeric_limits<float>::quiet_NaN(), inf = std::numeric_limits<float>::infinity();
+    for (std::size_t c = 0; c < 256; ++c) {
+      for (std::size_t t = 0; t < dsub; ++t) {
+        book[c * dsub + t] = c == 0 ? nan : inf;
+        book[(256 + c) * dsub + t] = nan;
+      }
+    }
+    quiver::ProductQuantizer pq(dim, m);
+    pq.set_centroids(book);
+    const auto x = normal_vectors(n, dim, 77 + dim);
+    std::vector<std::uint8_t> batch(n * m), one(m);
+    pq.encode_batch(x.data(), n, batch.data());
+    std::size_t code_mismatch = 0;
+    for (std::size_t i = 0; i < n; ++i) {
+      pq.encode(x.data() + i * dim, one.data());
+      code_mismatch += !std::equal(one.begin(), one.end(), batch.begin() + static_cast<std::ptrdiff_t>(i * m));
+    }
+    EXPECT(code_mismatch == 0);
+    EXPECT(batch[0] == 1 && batch[1] == 0);
+    std::vector<float> dec(n * dim), rec(dim);
+    pq.decode_batch(batch.data(), n, dec.data());
+    for (std::size_t i = 0; i < n; i += 7) {
+      pq.decode(batch.data() + i * m, rec.data());
+      EXPECT(same_bits(rec.data(), dec.data() + i * dim, dim));
+    }
+    const std::size_t nq = 5;
+    std::vector<float> l2(nq * m * 256), ip(nq * m * 256), t(m * 256);
+    pq.compute_tables(x.data(), nq, false, l2.data());
+    pq.compute_tables(x.data(), nq, true, ip.data());
+    for (std::size_t q = 0; q < nq; ++q) {
+      pq.compute_l2_table(x.data() + q * dim, t.data());
+      EXPECT(same_bits_or_nan(t.data(), l2.data() + q * m * 256, m * 256));
+      pq.compute_ip_table(x.data() + q * dim, t.data());
+      EXPECT(same_bits_or_nan(t.data(), ip.data() + q * m * 256, m * 256));
+    }
+    // adc over the inner-product table of query 0 (finite entries only in sub-spaces >= 2)
+    qvh_pq* dev = nullptr;
+    EXPECT(qvh_pq_create(static_cast<std::uint32_t>(dim), static_cast<std::uint32_t>(m), book.data(), &dev) == QVH_OK);
+    std::vector<float> host_adc(n), dev_adc(n), single(n);
+    pq.adc_batch(ip.data(), batch.data(), n, host_adc.data());
+    EXPECT(qvh_pq_adc(dev, ip.data(), batch.data(), n, dev_adc.data()) == QVH_OK);
+    for (std::size_t i = 0; i < n; ++i) single[i] = pq.adc(ip.data(), batch.data() + i * m);
+    qvh_pq_destroy(dev);
+    EXPECT(same_bits_or_nan(host_adc.data(), dev_adc.data(), n) && same_bits_or_nan(single.data(), dev_adc.data(), n));
+  }
+  for (std::size_t dim = 1; dim <= 70; ++dim) {
+    const std::size_t k = 97, n = 40;
+    auto cent = normal_vectors(k, dim, 1000 + dim);
+    for (std::size_t j = 0; j < dim; ++j) cent[5 * dim + j] = cent[60 * dim + j];  // equal centroids
+    const auto x = normal_vectors(n, dim, 2000 + dim);
+    std::vector<std::uint32_t> batch(n);
+    quiver::nearest_centroid_batch(x.data(), n, cent.data(), k, dim, batch.data());
+    std::size_t mismatch = 0;
+    for (std::size_t i = 0; i < n; ++i) {
+      mismatch += quiver::nearest_centroid(x.data() + i * dim, cent.data(), k, dim) != batch[i];
+    }
+    EXPECT(mismatch == 0);
+    // a point on the duplicated centroid picks the first copy
+    EXPECT(quiver::nearest_centroid(cent.data() + 60 * dim, cent.data(), k, dim) == 5);
+  }
+}
+
 // tests/test_quantizer.cc:94-99
 void pq_rejects_bad_shapes() {
   EXPECT(throws_error([] { quiver::ProductQuantizer(10, 3); }));
@@ -350,6 +444,74 @@ void pq_rejects_bad_shapes() {
   EXPECT(throws_error([&] { pq.train(few.data(), 100); }));
   EXPECT(throws_error([&] { pq.set_centroids(std::vector<float>(7)); }));
   EXPECT(throws_error([&] { quiver::ProductQuantizer().train(few.data(), 100); }));
+}
+
+// src/ivfpq_index.cc:218-249: add() encodes without holding the index lock and takes the exclusive
+// lock only to append, so search_batch calls from another thread keep returning while a 1M-vector
+// add() encodes. Each of them sees the index as it was before the add or as it is after it, never
+// a partial state, and the add's lists equal those of the same add without concurrent searches.
+void ivfpq_search_proceeds_during_add() {
+  using clock = std::chrono::steady_clock;
+  const std::size_t dim = 128, n0 = 20000, nbig = 1000000, nq = 64, k = 10;
+  const auto train = blob_vectors(n0, dim, 50, 11);
+  const auto big = blob_vectors(nbig, dim, 50, 12);
+  const auto q = blob_vectors(nq, dim, 50, 13);
+  quiver::IvfPqParams p;
+  p.dim = dim;
+  p.nlist = 1024;
+  p.m = 32;
+  quiver::IvfPqIndex index(p), serial(p);
+  index.train(train.data(), n0);
+  serial.set_trained(index.centroids().data(), index.codebook().data());
+  index.add(train.data(), n0);
+  serial.add(train.data(), n0);
+  quiver::IvfPqSearchParams sp;
+  sp.nprobe = 8;
+  auto search = [&](quiver::IvfPqIndex& ix) {
+    std::pair<std::vector<quiver::Label>, std::vector<float>> r{std::vector<quiver::Label>(nq * k),
+                                                                std::vector<float>(nq * k)};
+    ix.search_batch(q.data(), nq, k, r.first.data(), r.second.data(), sp);
+    return r;
+  };
+  const auto before = search(index);
+  std::atomic<bool> started{false}, finished{false};
+  clock::time_point add_begin, add_end;
+  std::thread adder([&] {
+    add_begin = clock::now();
+    started = true;
+    index.add(big.data(), nbig);
+    add_end = clock::now();
+    finished = true;
+  });
+  while (!started) std::this_thread::yield();
+  std::vector<std::pair<clock::time_point, decltype(search(index))>> done;
+  while (!finished) {
+    auto r = search(index);
+    done.emplace_back(clock::now(), std::move(r));
+  }
+  adder.join();
+  serial.add(big.data(), nbig);
+  const auto after = search(index);
+  EXPECT(after == search(serial));
+  EXPECT(index.list_labels() == serial.list_labels() && index.list_codes() == serial.list_codes());
+  std::size_t during = 0, mixed = 0;
+  double max_gap = 0;
+  auto last = add_begin;
+  for (const auto& [t, r] : done) {
+    if (t >= add_end) break;
+    ++during;
+    mixed += !(r == before || r == after);
+    max_gap = std::max(max_gap, std::chrono::duration<double>(t - last).count());
+    last = t;
+  }
+  max_gap = std::max(max_gap, std::chrono::duration<double>(add_end - last).count());
+  const double add_s = std::chrono::duration<double>(add_end - add_begin).count();
+  std::printf("    add of %zu vectors %.1f ms; %zu searches returned during it; longest wait between them "
+              "%.1f ms\n", nbig, add_s * 1e3, during, max_gap * 1e3);
+  EXPECT(mixed == 0);
+  EXPECT(during >= 5);
+  // Holding the exclusive lock across the encode would stall every search for most of the add.
+  EXPECT(max_gap < 0.35 * add_s);
 }
 
 // IvfPqIndex::list_sizes / memory_bytes (src/ivfpq_index.cc:446-463): the sizes add up to size(),
@@ -392,8 +554,10 @@ int main() {
       {"kmeans_handles_duplicate_points", kmeans_handles_duplicate_points},
       {"pq_reconstruction_beats_coarser_codes", pq_reconstruction_beats_coarser_codes},
       {"pq_adc_equals_distance_to_reconstruction", pq_adc_equals_distance_to_reconstruction},
+      {"pq_per_vector_host_matches_device_batch", pq_per_vector_host_matches_device_batch},
       {"pq_rejects_bad_shapes", pq_rejects_bad_shapes},
       {"ivfpq_list_sizes_and_memory_bytes", ivfpq_list_sizes_and_memory_bytes},
+      {"ivfpq_search_proceeds_during_add", ivfpq_search_proceeds_during_add},
   };
   for (const auto& [name, fn] : cases) {
     const int before = g_failures;

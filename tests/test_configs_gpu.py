@@ -2,17 +2,20 @@
 reference's golden vectors.
 
 Each test runs the whole query batch on the device (the batch shape fixes the scan's row splits,
-shared bounds, slicing and query order) and checks a 200-query subset spread over the batch against
-the oracle on the same inputs (src/flat_index.cc:69-140, src/ivfpq_index.cc:144-381):
+shared bounds, slicing and query order) and checks every query of it against the oracle on the same
+inputs (src/flat_index.cc:69-140, src/ivfpq_index.cc:144-381), the last, partially filled query
+block of the scans included:
 
-* 1,000,000 x 128 integer mixture, flat L2, k = 10 (10,000 queries; also the few-query kernels);
+* 1,000,000 x 128 integer mixture, flat L2, k = 10 (10,000 queries; also batches of 1, 8, 16, 32
+  and 128 queries: the few-query kernels and the row-split scan);
 * 1,183,514 x 100 unit-norm mixture, flat cosine, k = 10: unfiltered, 10% and 0.5% allowed ids;
 * IVF-PQ L2 on the 1M mixture, nlist 2048, m 32, trained on the 100,000-row sample: trained
   state, cells, codes and list order against the SHA-256 of the compiled reference's own run
   (tests/golden/ivfpq_1m.json), its first 200 searches at nprobe 32 bit for bit, and the nprobe
   sweep {1, 4, 8, 16, 32, 64} against the oracle on the same state;
 * IVF-PQ cosine on the 1.18M set, nlist 2048, m 25, stored vectors, refine 8, nprobe 16 and 64:
-  training against the oracle's, cells and codes of a 20k-row sample, stored vectors, searches.
+  training against the oracle's, the cells and codes of all 1,183,514 rows against the oracle's
+  encode, stored vectors, searches.
 """
 
 import json
@@ -31,7 +34,6 @@ from qvh_ctypes import Qvh
 pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
-SUBSET = np.arange(0, 10_000, 50)  # 200 queries spread over the batch
 _CACHE = {}
 
 
@@ -75,14 +77,13 @@ def test_flat_l2_int_mixture_1m(oracle):
     got_l, got_d = idx.search(q, 10)
     # integer rows and queries: both distance forms are exact, so every selection is certified
     assert Qvh().last_fallbacks(idx._index._device_handle) == 0
-    rows, dist = oracle.flat_search(base, q[SUBSET], 10)
-    sq = np.ascontiguousarray(q[SUBSET])
-    print(assert_same_topk(got_l[SUBSET], got_d[SUBSET], _rows_to_labels(rows), dist,
-                           _true_dist(oracle, base, sq, "l2")))
-    for nq in (1, 8, 16):  # the few-query kernels over the same million rows
+    rows, dist = oracle.flat_search(base, q, 10)
+    print(assert_same_topk(got_l, got_d, _rows_to_labels(rows), dist, _true_dist(oracle, base, q, "l2")))
+    # the few-query kernels (up to 16) and the row-split MFMA scan (up to 128) over the same rows
+    for nq in (1, 8, 16, 32, 128):
         print(f"case: flat l2 1M nq={nq}", flush=True)
-        gl, gd = idx.search(sq[:nq], 10)
-        print(assert_same_topk(gl, gd, _rows_to_labels(rows[:nq]), dist[:nq], _true_dist(oracle, base, sq, "l2")))
+        gl, gd = idx.search(q[:nq], 10)
+        print(assert_same_topk(gl, gd, _rows_to_labels(rows[:nq]), dist[:nq], _true_dist(oracle, base, q, "l2")))
 
 
 @pytest.mark.parametrize("fraction", [None, 0.1, 0.005])
@@ -99,10 +100,8 @@ def test_flat_cosine_unit_mixture_filtered(oracle, fraction):
     got_l, got_d = idx.search(q, 10, filter=allowed)
     print("fallbacks", Qvh().last_fallbacks(idx._index._device_handle))
     bm = None if allowed is None else rows_bitmap(allowed.astype(np.int64), n)
-    sq = np.ascontiguousarray(q[SUBSET])
-    rows, dist = oracle.flat_search(stored, sq, 10, "cosine", bm)
-    print(assert_same_topk(got_l[SUBSET], got_d[SUBSET], _rows_to_labels(rows), dist,
-                           _true_dist(oracle, stored, sq, "cosine")))
+    rows, dist = oracle.flat_search(stored, q, 10, "cosine", bm)
+    print(assert_same_topk(got_l, got_d, _rows_to_labels(rows), dist, _true_dist(oracle, stored, q, "cosine")))
 
 
 def _ivf_state(metric, cent, cb, pre, off, labels, codes, vectors=None):
@@ -138,13 +137,12 @@ def test_ivfpq_l2_int_mixture_1m_matches_reference(oracle):
     exp_d = np.array(g["search_dist_bits"], dtype=np.uint32).view(np.float32)
     print("reference's first 200:", assert_same_topk(got_l[:200], got_d[:200], exp_l, exp_d))
     st = _ivf_state("l2", cent, cb, oracle.ivfpq_precompute(cent, cb), off, labels, codes)
-    sq = np.ascontiguousarray(q[SUBSET])
     for nprobe in (1, 4, 8, 16, 32, 64):
         print(f"case: IVF-PQ l2 1M nprobe={nprobe}", flush=True)
         got_l, got_d = idx.search(q, 10, nprobe=nprobe)
-        refs, dist = oracle.ivfpq_search(st, sq, 10, nprobe)
+        refs, dist = oracle.ivfpq_search(st, q, 10, nprobe)
         print(nprobe, "fallbacks", Qvh().ivf_last_fallbacks(idx._index._device_handle),
-              assert_same_topk(got_l[SUBSET], got_d[SUBSET], st.ref_to_label(refs), dist))
+              assert_same_topk(got_l, got_d, st.ref_to_label(refs), dist))
 
 
 def test_ivfpq_cosine_refine_unit_mixture(oracle):
@@ -163,17 +161,18 @@ def test_ivfpq_cosine_refine_unit_mixture(oracle):
     assert np.array_equal(np.sort(labels), np.arange(n, dtype=np.uint64))
     pos = np.empty(n, dtype=np.int64)
     pos[labels.astype(np.int64)] = np.arange(n)
-    rows = np.arange(0, n, 59)  # ~20k rows: cells and codes against the oracle's encode
-    assign, exp_codes, _ = oracle.ivfpq_encode(cent, cb, "cosine", np.ascontiguousarray(base[rows]))
-    cell = np.searchsorted(off.astype(np.int64), pos[rows], side="right") - 1
+    print("case: cells and codes of all 1,183,514 rows against the oracle's encode", flush=True)
+    assign, exp_codes, _ = oracle.ivfpq_encode(cent, cb, "cosine", base)
+    cell = np.searchsorted(off.astype(np.int64), pos, side="right") - 1
     assert np.array_equal(cell, assign.astype(np.int64)), "cells differ"
-    assert np.array_equal(codes[pos[rows]], exp_codes), "PQ codes differ"
+    assert np.array_equal(codes[pos], exp_codes), "PQ codes differ"
+    # list order: within each list, rows in input order (src/ivfpq_index.cc:263-269)
+    assert np.array_equal(labels.astype(np.int64), np.argsort(assign, kind="stable")), "list order differs"
     vectors = idx.list_vectors()
     assert np.array_equal(vectors.view(np.uint32), stored[labels.astype(np.int64)].view(np.uint32))
     st = _ivf_state("cosine", cent, cb, None, off, labels, codes, vectors)
-    sq = np.ascontiguousarray(q[SUBSET])
     for nprobe in (16, 64):
         print(f"case: IVF-PQ cosine refine 8 nprobe={nprobe}", flush=True)
         got_l, got_d = idx.search(q, 10, nprobe=nprobe, refine_factor=8)
-        refs, dist = oracle.ivfpq_search(st, sq, 10, nprobe, 8)
-        print(nprobe, assert_same_topk(got_l[SUBSET], got_d[SUBSET], st.ref_to_label(refs), dist))
+        refs, dist = oracle.ivfpq_search(st, q, 10, nprobe, 8)
+        print(nprobe, assert_same_topk(got_l, got_d, st.ref_to_label(refs), dist))
