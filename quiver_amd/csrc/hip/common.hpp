@@ -161,6 +161,15 @@ __device__ __forceinline__ uint64_t lane_xor_u64(uint64_t v, int stride) {
   return (static_cast<uint64_t>(phi) << 32) | plo;
 }
 
+/// The 32-bit value of lane (lane ^ stride), with the same DPP moves as lane_xor_u64.
+__device__ __forceinline__ uint32_t lane_xor_u32(uint32_t v, int stride) {
+  if (stride == 1) return dpp_u32<0xB1>(v);
+  if (stride == 2) return dpp_u32<0x4E>(v);
+  if (stride == 4) return dpp_u32<0x1B>(dpp_u32<0x141>(v));
+  if (stride == 8) return dpp_u32<0x128>(v);
+  return static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), stride, 64));
+}
+
 /// Wave-wide (64 lanes) minimum of a 64-bit key.
 __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
 #pragma unroll

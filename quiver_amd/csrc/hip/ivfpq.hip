@@ -863,6 +863,481 @@ __global__ void __launch_bounds__(256) probe_select_any_kernel(const float* __re
   if (min_probe && lane == 0) min_probe[q] = mn;
 }
 
+// ---- search: coarse scores on the matrix unit ----------------------------------------------------
+//
+// Batches of at least kCgMinQueries queries score the centroids on the matrix unit: g_c =
+// ||c||^2 - 2<q,c> for L2 (the query enters scaled by -2, exact, and one more MFMA step adds the
+// augmented column ||c||^2 of the assignment operand) or -<q,c> for inner product and cosine. g
+// differs from the reference's in-order sum e_c (src/internal/centroid_table.h:65-85) by the
+// constant ||q||^2 (L2) and by rounding: |(||q||^2 + g_c) - e_c| <= delta with the assignment
+// kernel's bound, delta = (4 (dp + 1) + 16) u (P + R)^2 for L2 and (4 (dp + 1) + 16) u P R for the
+// inner product (P = ||q||, R = the largest ||c||). Let G_n be the nprobe-th smallest g. The
+// nprobe lists of smallest g all have e <= G_n + ||q||^2 + delta, so the nprobe-th smallest e is at
+// most that, and every list of the reference's probe set has g <= G_n + 2 delta. Those lists (the
+// band) are re-scored in the reference's order and arithmetic and the nprobe smallest (e, list)
+// are the probes, exactly as the in-order kernels would choose them. The exact scores of the band
+// overwrite their approximate values in the score array, which the scan then reads for the probed
+// lists only.
+
+constexpr int kCgWaves = 8;               // 4 x 2 over the work-group's output tile
+constexpr int kCgThreads = kCgWaves * 64;
+constexpr uint32_t kCgTileQ = 128;        // queries per work-group tile (32 per wave row)
+constexpr uint32_t kCgTileC = 128;        // centroids per work-group tile (64 per wave column)
+constexpr uint32_t kCgKC = 32;            // dims per LDS chunk
+constexpr int kCgPitch = kCgKC + 4;       // LDS row pitch in floats: conflict-free 16-byte reads
+constexpr int kCgOutPitch = 64 + 4;       // the epilogue's per-wave block of 32 queries x 64 centroids
+constexpr uint64_t kCgMinQueries = 1024;  // smaller batches: coarse_kernel
+constexpr uint32_t kCgMaxProbes = 64;
+constexpr uint32_t kCgMaxLists = 64 * 32;
+constexpr int kBandCap = 128;             // band members re-scored and sorted in registers
+constexpr uint32_t kBandKC = 16;          // dims per staged chunk of the band's centroid rows
+constexpr int kBandPitch = kBandKC + 4;   // staged row pitch in floats
+static_assert(kCgWaves * 32 * kCgOutPitch <= 2 * static_cast<int>(kCgTileQ + kCgTileC) * kCgPitch,
+              "the epilogue blocks fit the operand buffers");
+
+struct CoarseGemmArgs {
+  const float* Q;         // [nq][dim], 16-byte aligned rows, dim a multiple of 4
+  uint32_t nq, dim;
+  const float* crow;      // [kp][dp] centroid rows, zero padded (the assignment operand)
+  const float* aug;       // [kp] ||c||^2; read for L2 only
+  uint32_t kp, dp, nlist;
+  uint32_t ncb;           // centroid tiles
+  uint32_t qb_per_xcd;    // query tiles per XCD
+  uint32_t nqb;           // query tiles
+  float* g;               // [nq][nlist] approximate scores
+};
+
+/// g for one 128-query x 128-centroid tile per work-group: wave w owns queries 32 (w % 4) .. and
+/// centroids 64 (w / 4) .. of the tile (two 32 x 32 MFMA blocks sharing the query operand). Both
+/// operands pass through LDS in chunks of 32 dims, double buffered, the next chunk's global loads
+/// in flight during this chunk's MFMAs. Each wave's finished block goes through LDS so that the
+/// scores leave as whole 256-byte row segments. Work-group b runs on XCD b % 8 (the dispatcher's
+/// round robin); each XCD takes a contiguous range of query tiles with all their centroid tiles,
+/// so its L2 holds its queries and the whole centroid operand.
+template <bool L2>
+__global__ void __launch_bounds__(kCgThreads) coarse_gemm_kernel(CoarseGemmArgs a) {
+  __shared__ __attribute__((aligned(16))) float s_buf[2 * (kCgTileC + kCgTileQ) * kCgPitch];
+  auto s_c = [&](int buf) { return s_buf + buf * kCgTileC * kCgPitch; };
+  auto s_qt = [&](int buf) { return s_buf + 2 * kCgTileC * kCgPitch + buf * kCgTileQ * kCgPitch; };
+  const uint32_t r = blockIdx.x >> 3;
+  const uint32_t qb = (blockIdx.x & 7u) * a.qb_per_xcd + r / a.ncb;
+  const uint32_t cb = r % a.ncb;
+  if (qb >= a.nqb) return;  // whole work-group
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 31, h = lane >> 5;
+  const uint32_t wq = wave & 3, wc = wave >> 2;
+  const uint32_t q0 = qb * kCgTileQ, c0 = cb * kCgTileC;
+  constexpr float kScale = L2 ? -2.0f : -1.0f;
+
+  // Chunk element e = tid + 512 i: row e / 8, dims 4 (e % 8) .. of the chunk. The loads are
+  // unconditional (clamped addresses) and nothing uses their values before the store to LDS, so
+  // they stay in flight across the chunk's MFMAs; rows past the batch and dims past the query's
+  // width become zeros (and the scaling is applied) only at the store.
+  f32x4 st_c[2], st_q[2];
+  auto load_chunk = [&](uint32_t kc) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t e = static_cast<uint32_t>(tid) + kCgThreads * i;
+      const uint32_t row = e >> 3, d = kc + 4 * (e & 7u);
+      const uint32_t c = min(c0 + row, a.kp - 1);
+      st_c[i] = *reinterpret_cast<const f32x4*>(a.crow + static_cast<uint64_t>(c) * a.dp + d);
+      const uint32_t p = min(q0 + row, a.nq - 1);
+      st_q[i] = *reinterpret_cast<const f32x4*>(a.Q + static_cast<uint64_t>(p) * a.dim + min(d, a.dim - 4));
+    }
+  };
+  auto store_chunk = [&](int buf, uint32_t kc) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t e = static_cast<uint32_t>(tid) + kCgThreads * i;
+      const uint32_t row = e >> 3, d = kc + 4 * (e & 7u);
+      const uint32_t o = row * kCgPitch + 4 * (e & 7u);
+      const float sq = q0 + row < a.nq && d < a.dim ? kScale : 0.0f;
+      *reinterpret_cast<f32x4*>(&s_c(buf)[o]) = st_c[i];
+      *reinterpret_cast<f32x4*>(&s_qt(buf)[o]) = f32x4{sq * st_q[i][0], sq * st_q[i][1], sq * st_q[i][2], sq * st_q[i][3]};
+    }
+  };
+
+  f32x16 acc[2] = {};  // the wave's two centroid blocks
+  const uint32_t nk = a.dp / kCgKC;
+  load_chunk(0);
+  store_chunk(0, 0);
+  __syncthreads();
+  for (uint32_t kc = 0; kc < nk; ++kc) {
+    const int buf = kc & 1;
+    const bool more = kc + 1 < nk;
+    if (more) load_chunk((kc + 1) * kCgKC);
+    // Lane (j, h) feeds k = h: dims [16 h, 16 h + 16) of the chunk, four per 16-byte read.
+    const float* pc = s_c(buf) + (64 * wc + j) * kCgPitch + 16 * h;
+    const float* pq = s_qt(buf) + (32 * wq + j) * kCgPitch + 16 * h;
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+      const f32x4 c0v = *reinterpret_cast<const f32x4*>(pc + 4 * s4);
+      const f32x4 c1v = *reinterpret_cast<const f32x4*>(pc + 32 * kCgPitch + 4 * s4);
+      const f32x4 qv = *reinterpret_cast<const f32x4*>(pq + 4 * s4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(c0v[e], qv[e], acc[0], 0, 0, 0);
+        acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(c1v[e], qv[e], acc[1], 0, 0, 0);
+      }
+    }
+    if (more) store_chunk(buf ^ 1, (kc + 1) * kCgKC);
+    __syncthreads();
+  }
+  if (L2) {
+    // (||c||^2, 0) . (1, 0): lane half 0 feeds the norm and the one.
+    const float qaug = h == 0 ? 1.0f : 0.0f;
+#pragma unroll
+    for (int bc = 0; bc < 2; ++bc) {
+      const uint32_t c = min(c0 + 64 * wc + 32 * bc + j, a.kp - 1);
+      const float ca = h == 0 ? a.aug[c] : 0.0f;
+      acc[bc] = __builtin_amdgcn_mfma_f32_32x32x2f32(ca, qaug, acc[bc], 0, 0, 0);
+    }
+  }
+  // D[row][col]: col = query j, row = centroid 8 (r / 4) + 4 h + r % 4 of the block in register r.
+  // The wave's block goes to LDS as 32 query rows of 64 centroids (the operand buffers are free
+  // after the loop's last barrier), then out in 256-byte row segments.
+  float* so = s_buf + wave * 32 * kCgOutPitch;
+#pragma unroll
+  for (int bc = 0; bc < 2; ++bc) {
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      *reinterpret_cast<f32x4*>(&so[j * kCgOutPitch + 32 * bc + 8 * r4 + 4 * h]) =
+          f32x4{acc[bc][4 * r4], acc[bc][4 * r4 + 1], acc[bc][4 * r4 + 2], acc[bc][4 * r4 + 3]};
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  const bool vec_out = (a.nlist & 3u) == 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = 4 * i + (lane >> 4), col = 4 * (lane & 15);
+    const uint32_t p = q0 + 32 * wq + row;
+    const uint32_t c = c0 + 64 * wc + col;
+    if (p >= a.nq) continue;
+    const f32x4 v = *reinterpret_cast<const f32x4*>(&so[row * kCgOutPitch + col]);
+    float* dst = a.g + static_cast<uint64_t>(p) * a.nlist + c;
+    if (vec_out) {
+      if (c < a.nlist) *reinterpret_cast<f32x4*>(dst) = v;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (c + e < a.nlist) dst[e] = v[e];
+      }
+    }
+  }
+}
+
+/// The L2 ranking's rounding bound for one query (one wave; every lane returns it): (2m + 16) u
+/// times (the largest |score_l| + pmax[l] over the probed lists, of which each lane brings its
+/// share in bp, plus T_q = 2 sum_j ||q_j|| cmax[j]), rounded up. See adc_bound_kernel.
+__device__ float adc_delta(const float* qv, uint32_t m, uint32_t dsub, const float* __restrict__ cmax, float bp) {
+  const int lane = threadIdx.x & 63;
+  double tsum = 0.0;
+  for (uint32_t j = lane; j < m; j += 64) {
+    double norm2 = 0.0;
+    for (uint32_t t = 0; t < dsub; ++t) {
+      const double v = qv[static_cast<uint64_t>(j) * dsub + t];
+      norm2 += v * v;
+    }
+    tsum += sqrt(norm2) * static_cast<double>(cmax[j]);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) tsum += __shfl_xor(tsum, off, 64);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) bp = fmaxf(bp, __shfl_xor(bp, off, 64));
+  // (1 + 2^-20) covers the float rounding of |score| + pmax, the double sums and dsub u; a NaN or
+  // overflowing bound stays non-finite and certifies nothing.
+  const double tq = 2.0 * tsum;
+  const double d = (2.0 * m + 16.0) / 16777216.0 * ((static_cast<double>(bp) + tq) * (1.0 + 1.0 / 1048576.0));
+  const float df = static_cast<float>(d);
+  return static_cast<double>(df) < d ? __uint_as_float(__float_as_uint(df) + 1u) : df;
+}
+
+struct BandArgs {
+  const float* Q;          // [nq][dim], 16-byte aligned rows, dim a multiple of 4, at most kAsgMaxDp
+  uint32_t nq, dim;
+  const float* cent;       // [nlist][dim]
+  uint32_t nlist, nprobe;  // nprobe <= kCgMaxProbes
+  const float* rmax;       // [1] the largest ||c||
+  float coef;              // (4 (dp + 1) + 16) * 2^-24
+  float* scores;           // [nq][nlist]: approximate g in; the exact score of every re-scored list out
+  uint32_t* probes;        // [nq][nprobe]
+  uint32_t* min_probe;     // [nq] smallest probed list, or null
+  // L2 with the precomputed table: the scan's certificate bound per query (adc_delta), or null.
+  float* adc_bound;        // [nq]
+  const float* cmax;       // [m]
+  const float* pmax;       // [nlist]
+  uint32_t m, dsub;
+  uint32_t* fb_count;      // the scan's count of uncertified queries, reset here (with adc_bound)
+};
+
+/// The reference's coarse score of list l: sum_j (q_j - c_j)^2 or -sum_j q_j c_j in order of j,
+/// unfused (src/internal/centroid_table.h:65-85), the query from LDS.
+template <bool IP>
+__device__ __forceinline__ float coarse_exact(const float* __restrict__ sq, const float* __restrict__ crow,
+                                              uint32_t dim) {
+  float acc = 0.0f;
+  for (uint32_t j = 0; j < dim; j += 4) {
+    const f32x4 c = *reinterpret_cast<const f32x4*>(crow + j);
+    const f32x4 q = *reinterpret_cast<const f32x4*>(sq + j);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (IP) {
+        acc = acc + q[e] * c[e];
+      } else {
+        const float d = q[e] - c[e];
+        acc = acc + d * d;
+      }
+    }
+  }
+  return IP ? -acc : acc;
+}
+
+/// coarse_exact as a call: the every-list path of the band kernel runs it 32 times per lane.
+template <bool IP>
+__device__ __attribute__((noinline)) float coarse_exact_call(const float* sq, const float* crow, uint32_t dim) {
+  return coarse_exact<IP>(sq, crow, dim);
+}
+
+/// The probes of one query per wave from the approximate scores (std::partial_sort of
+/// src/ivfpq_index.cc:298-300, ties broken by the list id). U, the nprobe-th smallest of the lanes'
+/// minima (nprobe <= 32) or of their two smallest scores each (33..64), has at least nprobe scores
+/// at or below it, so U >= G_n and every list with g <= U + 2 delta is re-scored exactly: a
+/// superset of the band, usually a few lists past nprobe. When that set exceeds kBandCap, G_n
+/// itself is found (bit by bit) and the band proper is re-scored; a band beyond kBandCap (many
+/// lists within rounding of each other) re-scores every list of the query.
+/// Lane `lane` holds lists 256 i + 4 lane + e in og[4 i + e] (the scores as ordered 32-bit keys;
+/// a non-finite approximation comes with a non-finite delta, which admits every list).
+template <bool IP, int PER4>
+__global__ void __launch_bounds__(256) coarse_band_kernel(BandArgs a) {
+  constexpr int PER = 4 * PER4;
+  __shared__ __attribute__((aligned(16))) float s_q[4][kAsgMaxDp];
+  __shared__ uint32_t s_u[4][kBandCap];
+  __shared__ __attribute__((aligned(16))) float s_rows[4][64 * kBandPitch];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const uint32_t q = blockIdx.x * 4 + w;
+  // The scan's count of uncertified queries starts at zero (the previous search's kernels, on the
+  // same stream, are done with it).
+  if (a.fb_count && blockIdx.x == 0 && threadIdx.x == 0) *a.fb_count = 0u;
+  if (q >= a.nq) return;  // whole wave
+  const uint32_t dim = a.dim, nlist = a.nlist, nprobe = a.nprobe;
+  float pp = 0.0f;
+  for (uint32_t d = 4 * lane; d < dim; d += 256) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(a.Q + static_cast<uint64_t>(q) * dim + d);
+    *reinterpret_cast<f32x4*>(&s_q[w][d]) = v;
+    pp = pp + v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) pp = pp + __shfl_xor(pp, off, 64);
+  // ||q|| from a sum in some order: its relative error is far inside the bound's factor of two.
+  const float P = sqrtf(pp), R = a.rmax[0];
+  const float delta = IP ? a.coef * P * R : a.coef * (P + R) * (P + R);
+  // Ordered key of g + 2 delta rounded up: the next float above the float sum covers its rounding;
+  // a non-finite limit admits everything.
+  auto band_limit = [&](uint32_t gkey) {
+    const float s = ordered_to_float(gkey) + 2.0f * delta;
+    if (!(s < __builtin_huge_valf())) return 0xFFFFFFFFu;
+    const float up = s == 0.0f ? __uint_as_float(1u)
+                               : __uint_as_float(s > 0.0f ? __float_as_uint(s) + 1u : __float_as_uint(s) - 1u);
+    return float_to_ordered(up);
+  };
+
+  float* sc = a.scores + static_cast<uint64_t>(q) * nlist;
+  const bool vec = (nlist & 3u) == 0;
+  uint32_t og[PER];
+#pragma unroll
+  for (int i = 0; i < PER4; ++i) {
+    const uint32_t l0 = 256 * i + 4 * lane;
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (vec && l0 < nlist) {
+      v = *reinterpret_cast<const f32x4*>(sc + l0);
+    } else if (!vec) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = l0 + e < nlist ? sc[l0 + e] : 0.0f;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) og[4 * i + e] = l0 + e < nlist ? float_to_ordered(v[e]) : 0xFFFFFFFFu;
+  }
+  auto count_at_most = [&](uint32_t lim) {
+    uint32_t n = 0;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) n += static_cast<uint32_t>(__popcll(__ballot(og[i] <= lim)));
+    return n;
+  };
+  uint32_t U;
+  if (nprobe <= 32) {
+    uint32_t m1 = og[0];
+#pragma unroll
+    for (int i = 1; i < PER; ++i) m1 = min(m1, og[i]);
+    uint32_t one[1] = {m1};
+    wave_sort_u32<1>(one);
+    U = static_cast<uint32_t>(__shfl(static_cast<int>(one[0]), static_cast<int>(nprobe) - 1, 64));
+  } else {
+    uint32_t m1 = 0xFFFFFFFFu, m2 = 0xFFFFFFFFu;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const uint32_t v = og[i];
+      m2 = v < m1 ? m1 : min(v, m2);
+      m1 = min(v, m1);
+    }
+    uint32_t two[2] = {m1, m2};
+    wave_sort_u32<2>(two);
+    const int e = static_cast<int>(nprobe) - 1;
+    U = static_cast<uint32_t>(__shfl(static_cast<int>(e < 64 ? two[0] : two[1]), e & 63, 64));
+  }
+  // A saturated limit (non-finite bound) sends the query to the exact re-score of every list.
+  uint32_t lim = band_limit(U);
+  uint32_t n = lim == 0xFFFFFFFFu ? 0xFFFFFFFFu : count_at_most(lim);
+  if (n > static_cast<uint32_t>(kBandCap) && lim != 0xFFFFFFFFu) {
+    // U too loose: G_n bit by bit, the smallest t with at least nprobe scores at or below it.
+    uint32_t gn = 0;
+    for (int b = 31; b >= 0; --b) {
+      const uint32_t probe = gn | ((1u << b) - 1u);
+      if (count_at_most(probe) < nprobe) gn |= 1u << b;
+    }
+    lim = band_limit(gn);
+    n = lim == 0xFFFFFFFFu ? 0xFFFFFFFFu : count_at_most(lim);
+  }
+  uint32_t* pr = a.probes + static_cast<uint64_t>(q) * nprobe;
+  if (n <= static_cast<uint32_t>(kBandCap)) {
+    uint32_t* su = s_u[w];
+    {
+      uint32_t at = 0;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const bool pass = og[i] <= lim;
+        const uint64_t mk = __ballot(pass);
+        if (pass) su[at + lane_rank(mk)] = 256 * (i / 4) + 4 * lane + (i % 4);
+        at += static_cast<uint32_t>(__popcll(mk));
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+    // Exact scores, 64 lists at a time: 16-dim chunks of their centroid rows are staged in LDS
+    // with coalesced loads (four lanes per row), then each lane sums its list's row in order.
+    uint64_t key[2] = {~0ull, ~0ull};
+    float* rows = s_rows[w];
+    for (uint32_t base = 0; base < n; base += 64) {
+      const uint32_t nbp = min(64u, n - base);
+      const uint32_t myl = static_cast<uint32_t>(lane) < nbp ? su[base + lane] : 0u;
+      const float* src[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t b = 16 * i + (lane >> 2);
+        src[i] = a.cent + static_cast<uint64_t>(b < nbp ? su[base + b] : 0u) * dim + 4 * (lane & 3);
+      }
+      float acc = 0.0f;
+      for (uint32_t dc = 0; dc < dim; dc += kBandKC) {
+        const bool part_in = dc + 4 * (lane & 3) < dim;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t b = 16 * i + (lane >> 2);
+          if (b < nbp && part_in) {
+            *reinterpret_cast<f32x4*>(&rows[b * kBandPitch + 4 * (lane & 3)]) = *reinterpret_cast<const f32x4*>(src[i] + dc);
+          }
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (static_cast<uint32_t>(lane) < nbp) {
+#pragma unroll
+          for (int s4 = 0; s4 < 4; ++s4) {
+            const uint32_t d = dc + 4 * s4;
+            if (d < dim) {
+              const f32x4 c = *reinterpret_cast<const f32x4*>(&rows[lane * kBandPitch + 4 * s4]);
+              const f32x4 qv = *reinterpret_cast<const f32x4*>(&s_q[w][d]);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                if (IP) {
+                  acc = acc + qv[e] * c[e];
+                } else {
+                  const float df = qv[e] - c[e];
+                  acc = acc + df * df;
+                }
+              }
+            }
+          }
+        }
+        __builtin_amdgcn_wave_barrier();
+      }
+      if (static_cast<uint32_t>(lane) < nbp) {
+        const float s = IP ? -acc : acc;
+        sc[myl] = s;
+        const uint64_t kk = make_key(s == s ? s : __builtin_huge_valf(), myl);
+        if (base == 0) {
+          key[0] = kk;
+        } else {
+          key[1] = kk;
+        }
+      }
+    }
+    if (n > 64) {
+      wave_sort<2>(key);
+    } else {
+      uint64_t one[1] = {key[0]};
+      wave_sort<1>(one);
+      key[0] = one[0];
+    }
+    const uint32_t l = static_cast<uint32_t>(key[0]);
+    const bool probed = static_cast<uint32_t>(lane) < nprobe;
+    if (probed) pr[lane] = l;
+    if (a.min_probe) {
+      uint32_t mn = probed ? l : 0xFFFFFFFFu;
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) mn = min(mn, static_cast<uint32_t>(__shfl_xor(mn, off, 64)));
+      if (lane == 0) a.min_probe[q] = mn;
+    }
+    if (a.adc_bound) {
+      const float bp = probed ? fabsf(ordered_to_float(static_cast<uint32_t>(key[0] >> 32))) + a.pmax[l] : 0.0f;
+      const float d = adc_delta(s_q[w], a.m, a.dsub, a.cmax, bp);
+      if (lane == 0) a.adc_bound[q] = d;
+    }
+    return;
+  }
+  // Many lists within rounding of each other: every list's exact score, then the nprobe smallest
+  // (score, list) one at a time.
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const uint32_t l = 256 * (i / 4) + 4 * lane + (i % 4);
+    og[i] = 0xFFFFFFFFu;
+    if (l < nlist) {
+      const float s = coarse_exact_call<IP>(s_q[w], a.cent + static_cast<uint64_t>(l) * dim, dim);
+      sc[l] = s;
+      og[i] = float_to_ordered(s == s ? s : __builtin_huge_valf());
+    }
+  }
+  auto lane_best = [&]() {
+    uint64_t b = ~0ull;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const uint64_t k = og[i] == 0xFFFFFFFFu ? ~0ull
+                                              : (static_cast<uint64_t>(og[i]) << 32) | (256 * (i / 4) + 4 * lane + (i % 4));
+      b = k < b ? k : b;
+    }
+    return b;
+  };
+  uint64_t cur = lane_best();
+  uint32_t mn = 0xFFFFFFFFu;
+  float bp = 0.0f;
+  for (uint32_t p = 0; p < nprobe; ++p) {
+    const uint64_t best = wave_min_u64(cur);
+    const uint32_t bl = static_cast<uint32_t>(best);
+    if (lane == 0) pr[p] = bl;
+    mn = min(mn, bl);
+    if (a.adc_bound && lane == 0) bp = fmaxf(bp, fabsf(ordered_to_float(static_cast<uint32_t>(best >> 32))) + a.pmax[bl]);
+    if (cur == best) {
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        if (256 * (i / 4) + 4 * lane + (i % 4) == bl) og[i] = 0xFFFFFFFFu;
+      }
+      cur = lane_best();
+    }
+  }
+  if (a.min_probe && lane == 0) a.min_probe[q] = mn;
+  if (a.adc_bound) {
+    const float d = adc_delta(s_q[w], a.m, a.dsub, a.cmax, bp);
+    if (lane == 0) a.adc_bound[q] = d;
+  }
+}
+
 // ---- search: the scan ---------------------------------------------------------------------------
 
 constexpr int kScanThreads = 256;
@@ -1449,32 +1924,13 @@ __global__ void __launch_bounds__(256) adc_bound_kernel(const float* __restrict_
   // same stream, are done with it).
   if (blockIdx.x == 0 && threadIdx.x == 0) *fallback_count = 0u;
   if (q >= nq) return;  // whole wave
-  const float* qv = Q + static_cast<uint64_t>(q) * dim;
-  double tsum = 0.0;
-  for (uint32_t j = lane; j < m; j += 64) {
-    double norm2 = 0.0;
-    for (uint32_t t = 0; t < dsub; ++t) {
-      const double v = qv[static_cast<uint64_t>(j) * dsub + t];
-      norm2 += v * v;
-    }
-    tsum += sqrt(norm2) * static_cast<double>(cmax[j]);
-  }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) tsum += __shfl_xor(tsum, off, 64);
   float bp = 0.0f;
   for (uint32_t p = lane; p < nprobe; p += 64) {
     const uint32_t l = probes[static_cast<uint64_t>(q) * nprobe + p];
     bp = fmaxf(bp, fabsf(scores[static_cast<uint64_t>(q) * nlist + l]) + pmax[l]);
   }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) bp = fmaxf(bp, __shfl_xor(bp, off, 64));
-  if (lane != 0) return;
-  // (1 + 2^-20) covers the float rounding of |score| + pmax, the double sums and dsub u; a NaN or
-  // overflowing bound stays non-finite and certifies nothing.
-  const double tq = 2.0 * tsum;
-  const double d = (2.0 * m + 16.0) / 16777216.0 * ((static_cast<double>(bp) + tq) * (1.0 + 1.0 / 1048576.0));
-  const float df = static_cast<float>(d);
-  delta[q] = static_cast<double>(df) < d ? __uint_as_float(__float_as_uint(df) + 1u) : df;
+  const float d = adc_delta(Q + static_cast<uint64_t>(q) * dim, m, dsub, cmax, bp);
+  if (lane == 0) delta[q] = d;
 }
 
 /// cmax[j] = max_c ||codebook[j][c]||, computed in double and rounded up. One thread per sub-space.
@@ -2529,7 +2985,66 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   }
   // coarse scores + probes
   float* scores = static_cast<float*>(h->w_scores.reserve(nq * h->nlist * sizeof(float)));
-  {
+  uint32_t* probes = static_cast<uint32_t*>(h->w_probes.reserve(nq * nprobe * sizeof(uint32_t)));
+  // Block order of the streaming scan (queries grouped by their smallest probed list): for batches
+  // of up to 64k queries and up to 32k lists (the counts fit one block's LDS).
+  const bool ordered = nq > 1 && nq <= 65536 && h->nlist <= 32768 && mode != kModeResidual && h->mp <= kStreamMaxM &&
+                       nprobe <= kStreamMaxProbes;
+  uint32_t* min_probe = ordered ? static_cast<uint32_t*>(h->w_key.reserve(nq * sizeof(uint32_t))) : nullptr;
+  const bool mfma_coarse = h->asg.ready && h->asg.dim == h->dim && nq >= kCgMinQueries && nq < 0xFFFFFFFFull &&
+                           nprobe <= kCgMaxProbes && h->nlist <= kCgMaxLists;
+  if (mfma_coarse) {
+    const bool ip = h->metric != QVH_METRIC_L2;
+    CoarseGemmArgs ga{};
+    ga.Q = dq;
+    ga.nq = static_cast<uint32_t>(nq);
+    ga.dim = h->dim;
+    ga.crow = h->asg.crow.as<float>();
+    ga.aug = h->asg.aug.as<float>();
+    ga.kp = h->asg.kp;
+    ga.dp = h->asg.dp;
+    ga.nlist = h->nlist;
+    ga.ncb = static_cast<uint32_t>(ceil_div(h->nlist, kCgTileC));
+    ga.nqb = static_cast<uint32_t>(ceil_div(nq, kCgTileQ));
+    ga.qb_per_xcd = static_cast<uint32_t>(ceil_div(ga.nqb, 8));
+    ga.g = scores;
+    const dim3 grid(8u * ga.qb_per_xcd * ga.ncb);
+    if (ip) {
+      hipLaunchKernelGGL(coarse_gemm_kernel<false>, grid, dim3(kCgThreads), 0, s, ga);
+    } else {
+      hipLaunchKernelGGL(coarse_gemm_kernel<true>, grid, dim3(kCgThreads), 0, s, ga);
+    }
+    BandArgs ba{};
+    ba.Q = dq;
+    ba.nq = static_cast<uint32_t>(nq);
+    ba.dim = h->dim;
+    ba.cent = h->cent.as<float>();
+    ba.nlist = h->nlist;
+    ba.nprobe = nprobe;
+    ba.rmax = h->asg.rmax.as<float>();
+    ba.coef = ldexpf(4.0f * static_cast<float>(h->asg.dp + 1) + 16.0f, -24);
+    ba.scores = scores;
+    ba.probes = probes;
+    ba.min_probe = min_probe;
+    if (mode == kModePre && !exact_all && keep > 0) {
+      ba.adc_bound = static_cast<float*>(h->w_delta.reserve(nq * sizeof(float)));
+      ba.fb_count = static_cast<uint32_t*>(h->w_fb.reserve((nq + 1) * sizeof(uint32_t)));
+      ba.cmax = h->cmax.as<float>();
+      ba.pmax = h->pmax.as<float>();
+      ba.m = h->m;
+      ba.dsub = h->dsub;
+    }
+    const dim3 bgrid(static_cast<unsigned>(ceil_div(nq, 4)));
+    void (*band)(BandArgs);
+    if (h->nlist <= 256 * 2) {
+      band = ip ? coarse_band_kernel<true, 2> : coarse_band_kernel<false, 2>;
+    } else if (h->nlist <= 256 * 4) {
+      band = ip ? coarse_band_kernel<true, 4> : coarse_band_kernel<false, 4>;
+    } else {
+      band = ip ? coarse_band_kernel<true, 8> : coarse_band_kernel<false, 8>;
+    }
+    hipLaunchKernelGGL(band, bgrid, dim3(256), 0, s, ba);
+  } else {
     const bool single = nq <= kCoarseSingleMaxQ;
     const dim3 grid(static_cast<unsigned>(ceil_div(h->nlist, 256)),
                     static_cast<unsigned>(single ? nq : ceil_div(nq, kCoarseQ)));
@@ -2538,22 +3053,14 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
                        : (ip ? coarse_kernel<true, kCoarseQ> : coarse_kernel<false, kCoarseQ>);
     hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, dq, static_cast<uint32_t>(nq), h->dim, h->cent_t.as<float>(),
                        h->nlist, scores);
-  }
-  uint32_t* probes = static_cast<uint32_t*>(h->w_probes.reserve(nq * nprobe * sizeof(uint32_t)));
-  // Block order of the streaming scan (queries grouped by their smallest probed list): for batches
-  // of up to 64k queries and up to 32k lists (the counts fit one block's LDS).
-  const bool ordered = nq > 1 && nq <= 65536 && h->nlist <= 32768 && mode != kModeResidual && h->mp <= kStreamMaxM &&
-                       nprobe <= kStreamMaxProbes;
-  uint32_t* min_probe = ordered ? static_cast<uint32_t*>(h->w_key.reserve(nq * sizeof(uint32_t))) : nullptr;
-  {
-    const dim3 grid(static_cast<unsigned>(ceil_div(nq, 4)));
+    const dim3 sgrid(static_cast<unsigned>(ceil_div(nq, 4)));
     const uint32_t nq32 = static_cast<uint32_t>(nq);
     if (h->nlist <= 64 * 8) {
-      hipLaunchKernelGGL(probe_select_kernel<8>, grid, dim3(256), 0, s, scores, nq32, h->nlist, nprobe, probes, min_probe);
+      hipLaunchKernelGGL(probe_select_kernel<8>, sgrid, dim3(256), 0, s, scores, nq32, h->nlist, nprobe, probes, min_probe);
     } else if (h->nlist <= 64 * 32) {
-      hipLaunchKernelGGL(probe_select_kernel<32>, grid, dim3(256), 0, s, scores, nq32, h->nlist, nprobe, probes, min_probe);
+      hipLaunchKernelGGL(probe_select_kernel<32>, sgrid, dim3(256), 0, s, scores, nq32, h->nlist, nprobe, probes, min_probe);
     } else {
-      hipLaunchKernelGGL(probe_select_any_kernel, grid, dim3(256), 0, s, scores, nq32, h->nlist, nprobe, probes,
+      hipLaunchKernelGGL(probe_select_any_kernel, sgrid, dim3(256), 0, s, scores, nq32, h->nlist, nprobe, probes,
                          min_probe);
     }
   }
@@ -2577,6 +3084,8 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   if (certify) {
     delta = static_cast<float*>(h->w_delta.reserve(nq * sizeof(float)));
     fb = static_cast<uint32_t*>(h->w_fb.reserve((nq + 1) * sizeof(uint32_t)));
+  }
+  if (certify && !mfma_coarse) {  // the band kernel computes the bound itself
     hipLaunchKernelGGL(adc_bound_kernel, dim3(static_cast<unsigned>(ceil_div(nq, 4))), dim3(256), 0, s, dq,
                        static_cast<uint32_t>(nq), h->dim, h->m, h->dsub, h->cmax.as<float>(), scores, h->nlist, probes,
                        nprobe, h->pmax.as<float>(), delta, fb);

@@ -52,6 +52,41 @@ __device__ __forceinline__ void wave_sort(uint64_t (&k)[N]) {
   }
 }
 
+/// Ascending bitonic sort of N * 64 32-bit values held by one wave, element e = i * 64 + lane in
+/// k[i] (duplicates allowed).
+template <int N>
+__device__ __forceinline__ void wave_sort_u32(uint32_t (&k)[N]) {
+  const int lane = threadIdx.x & 63;
+  constexpr int total = N * 64;
+#pragma unroll
+  for (int size = 2; size <= total; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      if (stride >= 64) {
+        const int is = stride / 64;
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+          const int j = i ^ is;
+          if (j > i) {
+            const bool up = ((i * 64) & size) == 0;
+            const uint32_t x = k[i], y = k[j];
+            k[i] = up ? min(x, y) : max(x, y);
+            k[j] = up ? max(x, y) : min(x, y);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+          const uint32_t other = lane_xor_u32(k[i], stride);
+          const bool up = ((i * 64 + lane) & size) == 0;
+          const bool lower = (lane & stride) == 0;
+          k[i] = (lower == up) ? min(other, k[i]) : max(other, k[i]);
+        }
+      }
+    }
+  }
+}
+
 /// Ascending sort of a bitonic sequence of N * 64 keys held by one wave (element e = i * 64 + lane
 /// in k[i]): the last merge stage of the bitonic sort.
 template <int N>

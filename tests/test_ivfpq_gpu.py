@@ -438,3 +438,68 @@ def test_real_valued_l2_rescans_are_rare(oracle, refine):
         fb = Qvh().ivf_last_fallbacks(idx._index._device_handle)
         print(f"nprobe={nprobe} refine={refine}: {fb} of {q.shape[0]} queries rescanned", stats)
         assert fb <= q.shape[0] // 100
+
+
+def _given_state_pair(oracle, cent, cb, metric, base):
+    """Product index installed with the given trained state and filled with `base`, and the oracle's
+    state from the same arrays."""
+    idx = quiver.IvfPqIndex(cent.shape[1], metric, nlist=cent.shape[0], m=cb.shape[0])
+    idx.set_trained(cent, cb)
+    idx.add(base)
+    pre = oracle.ivfpq_precompute(cent, cb) if metric == "l2" else None
+    assign, codes, _ = oracle.ivfpq_encode(cent, cb, metric, base)
+    st = IvfPqState(metric, cent, cb, pre).set_lists(assign, codes, np.arange(base.shape[0], dtype=np.uint64))
+    off, lab, got_codes = idx.lists()
+    assert np.array_equal(off, st.offsets) and np.array_equal(lab, st.labels)
+    assert np.array_equal(got_codes, st.codes)
+    return idx, st
+
+
+@pytest.mark.parametrize("metric", ["l2", "ip"])
+def test_coarse_bands_beyond_the_register_sort(oracle, metric):
+    """Batches of 1,024 queries or more score the centroids on the matrix unit and re-score, in the
+    reference's order, only the lists within the rounding bound of the nprobe-th approximate score
+    (src/ivfpq_index.cc:285-300). Two centroid layouts force its rare paths, with 1,024 queries at
+    one point (plus noise far below the score spacing):
+    (a) 186 near lists sit in 31 of the 64 lane strides (list l is held by lane l % 64), every other
+        list far away, so the nprobe-th smallest lane minimum lies far above the nprobe-th score and
+        admits more candidates than the register sort holds: the nprobe-th score is found by
+        selection instead;
+    (b) 200 copies of one centroid tie exactly at the nearest score, a band larger than the register
+        sort: every list of the query is re-scored exactly and ties go to the smaller list id.
+    Probes and results equal the oracle's."""
+    rng = np.random.default_rng(401)
+    dim, nlist, m = 32, 512, 8
+    q0 = (3.0 * rng.standard_normal(dim)).astype(np.float32)
+    unit = rng.standard_normal((nlist, dim))
+    unit /= np.linalg.norm(unit, axis=1, keepdims=True)
+    cb = rng.standard_normal((m, 256, dim // m)).astype(np.float32)
+    lists = np.arange(nlist)
+    near = (lists % 64 < 31) & (lists // 64 < 6)
+    assert near.sum() == 186
+    layouts = {}
+    if metric == "l2":
+        r = np.full(nlist, 50.0)
+        r[near] = 1.0 + 0.25 * rng.permutation(186)
+        layouts["lanes"] = (q0[None, :] + r[:, None] * unit).astype(np.float32)
+        tied = np.full(nlist, 50.0)
+        tied[:200] = 1.0
+        u = np.array(unit)
+        u[:200] = unit[0]
+        layouts["ties"] = (q0[None, :] + tied[:, None] * u).astype(np.float32)
+    else:
+        s = np.full(nlist, -1.0)
+        s[near] = 2.0 + 0.05 * rng.permutation(186)
+        layouts["lanes"] = (s[:, None] * q0[None, :] + 0.01 * unit).astype(np.float32)
+        s = np.full(nlist, -1.0)
+        s[:200] = 3.0
+        c = s[:, None] * q0[None, :] + 0.01 * unit
+        c[:200] = c[0]
+        layouts["ties"] = c.astype(np.float32)
+    q = (q0[None, :] + 1e-4 * rng.standard_normal((1024, dim))).astype(np.float32)
+    for name, cent in layouts.items():
+        base = (q0[None, :] + 2.0 * rng.standard_normal((6000, dim))).astype(np.float32)
+        idx, st = _given_state_pair(oracle, cent, cb, metric, base)
+        for nprobe in (16, 32, 64):
+            print(f"case: {metric} {name} nprobe={nprobe}", flush=True)
+            print(compare_search(oracle, idx, st, q, 10, nprobe))
