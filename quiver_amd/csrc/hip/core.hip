@@ -42,10 +42,26 @@ void check_device(int dev) {
   }
 }
 
-// One thread per row; rows are independent.
+// simd::normalize (src/simd/dispatch.cc:119-135) of every row in place, eight lanes per row: the
+// group computes the row's dot product in the reference's order (exact_group8, bit for bit as
+// exact_dot), every lane then scales its share of the row by the same 1/sqrt(norm^2). A non-finite
+// sum takes the double-precision redo in the group's first lane, as exact_normalize does.
 __global__ void normalize_rows_kernel(float* __restrict__ rows, uint64_t n, uint32_t dim) {
-  const uint64_t r = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (r < n) exact_normalize(rows + r * dim, dim);
+  const uint64_t t = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const uint64_t r = t >> 3;
+  const uint32_t l = static_cast<uint32_t>(t & 7u);
+  const bool valid = r < n;
+  float* v = rows + (valid ? r : 0) * dim;
+  const float lead = exact_group8<false>(v, v, dim, valid);  // every lane of the wave takes part
+  const float norm_sq = __shfl(lead, 0, 8);
+  if (!valid) return;
+  if (!isfinite(norm_sq)) {
+    if (l == 0) exact_normalize(v, dim);
+    return;
+  }
+  if (norm_sq <= 0.0f) return;
+  const float inv = 1.0f / sqrtf(norm_sq);
+  for (uint32_t i = l; i < dim; i += 8) v[i] = v[i] * inv;
 }
 
 }  // namespace
@@ -85,8 +101,8 @@ void device_free(void* p) noexcept {
 
 void launch_normalize_rows(float* d_rows, uint64_t n, uint32_t dim, hipStream_t stream) {
   if (n == 0) return;
-  const unsigned block = 128;
-  hipLaunchKernelGGL(normalize_rows_kernel, dim3(static_cast<unsigned>(ceil_div(n, block))),
+  const unsigned block = 256;  // 32 rows
+  hipLaunchKernelGGL(normalize_rows_kernel, dim3(static_cast<unsigned>(ceil_div(n * 8, block))),
                      dim3(block), 0, stream, d_rows, n, dim);
   QVH_HIP(hipGetLastError());
 }

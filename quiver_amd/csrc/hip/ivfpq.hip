@@ -1363,7 +1363,7 @@ constexpr uint64_t kScanGlobalCandBytes = 512ull << 20;   // and on candidate bu
 __global__ void __launch_bounds__(1024) probe_order_kernel(const uint32_t* __restrict__ key, uint32_t nq,
                                                            uint32_t nlist, uint32_t* __restrict__ order) {
   extern __shared__ uint32_t s_count[];  // [nlist]
-  __shared__ uint32_t s_part[1024];
+  __shared__ uint32_t s_part[33];        // wave totals, wave bases, chunk total
   __shared__ uint32_t s_carry;
   const uint32_t tid = threadIdx.x;
   for (uint32_t g = tid; g < nlist; g += 1024) s_count[g] = 0u;
@@ -1371,19 +1371,34 @@ __global__ void __launch_bounds__(1024) probe_order_kernel(const uint32_t* __res
   __syncthreads();
   for (uint32_t q = tid; q < nq; q += 1024) atomicAdd(&s_count[key[q]], 1u);
   __syncthreads();
+  // Exclusive prefix sum over the counts, 1024 at a time: an inclusive scan inside each wave
+  // (shuffles), the 16 wave totals scanned by wave 0, then every count offset by its wave's base.
+  const uint32_t lane = tid & 63u, wave = tid >> 6;
   for (uint32_t b = 0; b < nlist; b += 1024) {
     const uint32_t v = b + tid < nlist ? s_count[b + tid] : 0u;
-    s_part[tid] = v;
-    __syncthreads();
-    for (uint32_t off = 1; off < 1024; off <<= 1) {
-      const uint32_t add = tid >= off ? s_part[tid - off] : 0u;
-      __syncthreads();
-      s_part[tid] += add;
-      __syncthreads();
+    uint32_t incl = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t o = __shfl_up(incl, off, 64);
+      if (lane >= static_cast<uint32_t>(off)) incl += o;
     }
-    if (b + tid < nlist) s_count[b + tid] = s_carry + s_part[tid] - v;
+    if (lane == 63) s_part[wave] = incl;
     __syncthreads();
-    if (tid == 1023) s_carry += s_part[1023];
+    if (wave == 0) {
+      const uint32_t t = lane < 16 ? s_part[lane] : 0u;
+      uint32_t ti = t;
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) {
+        const uint32_t o = __shfl_up(ti, off, 64);
+        if (lane >= static_cast<uint32_t>(off)) ti += o;
+      }
+      if (lane < 16) s_part[16 + lane] = ti - t;  // exclusive base of wave `lane`
+      if (lane == 15) s_part[32] = ti;            // the chunk's total
+    }
+    __syncthreads();
+    if (b + tid < nlist) s_count[b + tid] = s_carry + s_part[16 + wave] + incl - v;
+    __syncthreads();
+    if (tid == 0) s_carry += s_part[32];
     __syncthreads();
   }
   for (uint32_t q = tid; q < nq; q += 1024) order[atomicAdd(&s_count[key[q]], 1u)] = q;
