@@ -57,7 +57,7 @@ struct ScanArgs {
   int l2;
   uint32_t nsplit;
   uint32_t qblocks;
-  uint64_t rows_per_split;  // multiple of kTileRows
+  uint64_t rows_per_split;  // multiple of kTileRows (of 32 for the ring scan)
   const uint32_t* idx;      // admitted rows, ascending (indexed mode), or null
   float* part_d;            // [nq][2*nsplit][KL]
   uint32_t* part_r;
@@ -574,6 +574,423 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
     for (int x = 0; x < KL; ++x) {
       a.part_d[o + x] = Ld[x];
       a.part_r[o + x] = Lr[x];
+    }
+  }
+}
+
+// ---- the ring scan: small unfiltered batches -------------------------------------------------
+//
+// At most 32 queries are one 32-query group, which leaves the MFMA scan's 256-query blocks one wave
+// in eight (or two in eight in its row-split form) and a single 64-row tile in flight per CU. Here
+// each work-group is a row split and each of its four waves (one per SIMD) streams every fourth
+// 32-row block of the split through a ring of LDS slots of its own. A slot holds one quarter of a
+// block (32 rows x 32 dims), filled by direct global-to-LDS loads (global_load_lds_dwordx4, 16
+// bytes per lane) several slots ahead of the MFMAs. Those loads are issued from inline assembly and
+// waited for with explicit vmcnt counts: the compiler's own wait insertion would wait for every
+// ring load in flight before each LDS read and drain the ring. The streaming loop issues no other
+// vector memory instruction, so vmcnt counts exactly the ring's loads, which complete in issue
+// order. Each slot's next quarter is read into registers while the current one's MFMAs run.
+//
+// Slot layout: lane i of load m writes 16-byte unit P = 64 m + i, which holds row P / 8 and the
+// quarter's float4 column (P % 8) ^ (row % 8). MFMA lane (j, h) reads row j, columns 2u + h for
+// u = 0..3, eight lanes of a read touching eight different columns (no bank conflicts).
+//
+// Distances are the MFMA scan's GEMM form: step t of quarter qq pairs dim 32 qq + 8 (t / 4) + 4 h
+// + t % 4 of row j (A, lane (j, h)) with the same dim of query j scaled by -2 or -1 (B), and each
+// block starts with the augmented step (||x||^2, 1) x (1, ||q||^2), or (1, 1) x (1, 0). The four
+// waves keep per-lane lists and queues as the MFMA scan does and share a per-query bound through
+// LDS and, across splits, through a per-query word in device memory; at the end their lists are
+// merged into the first wave's, which writes two lists per query and split in the MFMA scan's
+// format for the same merge, re-score and certificate.
+
+constexpr int kRingWaves = 4;
+constexpr int kRingThreads = kRingWaves * 64;
+constexpr int kRingSlots = 7;           // quarter-block slots per wave
+constexpr int kRingCap = 18;            // queued candidates per lane
+constexpr int kRingSlotFloats = 32 * 32;
+constexpr int kRingShareEvery = 2;      // blocks between exchanges of the shared bound
+constexpr uint32_t kRingMinQueries = 5;   // up to four queries the few-query kernel is faster
+constexpr uint32_t kRingMaxQueries = 32;
+constexpr uint64_t kRingMinSplitRows = 1024;  // rows per split at least (eight blocks per wave)
+constexpr uint32_t kRingMaxSplits = 256;   // two lists per query and split: the merge's 512
+constexpr uint32_t kRingBoundStride = 32;  // words between queries' shared bounds (one 128-byte line each)
+
+/// LDS byte address of a shared-memory pointer.
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)(p)));
+}
+
+/// One direct global-to-LDS load: lane i's 16 bytes at sbase + voff go to LDS address lds + 16 i.
+/// M0 carries the LDS address for the load and gets its old value back afterwards. Vector memory
+/// instructions other than these loads (the shared bound's atomic, which returns nothing) may only
+/// make the explicit waits below wait longer: loads complete in issue order.
+__device__ __forceinline__ void lds_load16(uint32_t lds, const void* sbase, uint32_t voff) {
+  uint32_t save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, %3\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(save)
+      : "s"(lds), "v"(voff), "s"(sbase)
+      : "memory");
+}
+
+/// 4 bytes per lane from a per-lane address (lane i's to lds + 4 i).
+__device__ __forceinline__ void lds_load4(uint32_t lds, const void* addr) {
+  uint32_t save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dword %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(save)
+      : "s"(lds), "v"(addr)
+      : "memory");
+}
+
+/// Waits until at most N vector memory operations of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  static_assert(N >= 0 && N <= 63, "vmcnt holds 0..63");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+/// wait_vmem<n>() for n in [LO, HI]; a constant n (an unrolled loop's) folds to the one wait.
+template <int LO, int HI>
+__device__ __forceinline__ void wait_vmem_n(int n) {
+  if constexpr (LO <= HI) {
+    if (n == LO) {
+      wait_vmem<LO>();
+    } else {
+      wait_vmem_n<LO + 1, HI>(n);
+    }
+  }
+}
+
+/// Ring loads in the group of quarter qq of a block: four for the quarter's rows, and with quarter
+/// 0 one more for the block's row norms and the queries' shared bounds.
+__host__ __device__ constexpr int ring_group_loads(int qq) { return 4 + (qq == 0 ? 1 : 0); }
+
+/// Loads that may still be outstanding once the group after quarter qq's has landed, the refill of
+/// quarter qq + R - 1 having just been issued: those of the R - 2 groups issued after that group
+/// (quarters qq + 2 .. qq + R - 1, modulo NQ).
+template <int NQ>
+__host__ __device__ constexpr int ring_wait_count(int qq) {
+  int n = 0;
+  for (int d = 2; d <= kRingSlots - 1; ++d) n += ring_group_loads((qq + d) % NQ);
+  return n;
+}
+
+/// The value of lane (lane ^ 32), by one v_permlane32_swap (no LDS round trip).
+__device__ __forceinline__ uint32_t lane_swap32_u32(uint32_t v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return (threadIdx.x & 32) ? r[0] : r[1];
+}
+__device__ __forceinline__ float lane_swap32_f(float v) { return __uint_as_float(lane_swap32_u32(__float_as_uint(v))); }
+
+/// The key of an empty list entry: +inf distance, QVH_EMPTY_ROW (after every real entry).
+constexpr uint64_t kRingEmptyKey = (uint64_t{0xFF800000u} << 32) | QVH_EMPTY_ROW;
+
+/// Inserts `key` into the ascending (distance, row) key list K, dropping the last entry. Every entry
+/// takes one compare and two selects, none waiting on another's (the list is sorted, so the
+/// entries above the key form a suffix that shifts up by one); the empty key changes nothing.
+template <int KL>
+__device__ __forceinline__ void key_insert(uint64_t (&K)[KL], uint64_t key) {
+  bool gt[KL];
+#pragma unroll
+  for (int x = 0; x < KL; ++x) gt[x] = K[x] > key;
+#pragma unroll
+  for (int x = KL - 1; x > 0; --x) K[x] = gt[x] ? (gt[x - 1] ? K[x - 1] : key) : K[x];
+  K[0] = gt[0] ? key : K[0];
+}
+
+/// Distance of a (distance, row) key.
+__device__ __forceinline__ float key_distance(uint64_t k) { return ordered_to_float(static_cast<uint32_t>(k >> 32)); }
+
+/// Merges the sorted key list at sk (entry x of this lane at x * 64 + lane) into K: the KL best of
+/// the union. An entry that would not enter ends the lane's part (every later one is after it),
+/// and the wave stops once no lane takes one.
+template <int KL>
+__device__ __forceinline__ void ring_merge_list(uint64_t (&K)[KL], const uint64_t* sk, int lane) {
+  for (int x = 0; x < KL; ++x) {
+    const uint64_t k = sk[x * 64 + lane];
+    const bool take = k < K[KL - 1];
+    if (!__builtin_amdgcn_ballot_w64(take)) break;
+    key_insert<KL>(K, take ? k : kRingEmptyKey);
+  }
+}
+
+template <int DP, int KL, bool L2>
+__global__ void __launch_bounds__(kRingThreads) flat_ring_kernel(ScanArgs a) {
+  static_assert(DP % 32 == 0 && DP <= kMaxDp, "the ring scan takes whole 32-dim quarters");
+  static_assert(2 * KL * 64 * 2 <= kRingWaves * kRingSlots * kRingSlotFloats, "list hand-off fits the rings");
+  if (gate_closed(a.gate, a.gate_want)) return;  // the same for every thread of the grid
+  constexpr int NQ = DP / 32;  // quarters per block
+  constexpr int R = kRingSlots;
+  constexpr int CAP = kRingCap;
+  constexpr int SLOT_BYTES = kRingSlotFloats * 4;
+  __shared__ __attribute__((aligned(16))) float s_ring[kRingWaves][R][kRingSlotFloats];
+  __shared__ float s_norm[kRingWaves][R][64];
+  __shared__ float s_qd[kRingWaves][CAP * 64];
+  __shared__ uint32_t s_qr[kRingWaves][CAP * 64];
+  __shared__ uint32_t s_thr[32];
+  // Per query, the ceil(KL / 8)-th entry of each of the work-group's eight lists (four waves, two
+  // lane halves, disjoint rows): the union of the eight holds KL entries at or below the largest.
+  __shared__ __attribute__((aligned(16))) float s_part[32][8];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 31, h = lane >> 5;
+  const uint32_t split = blockIdx.x;
+  const uint32_t q = static_cast<uint32_t>(j);
+  const bool qvalid = q < a.nq;
+
+  // This split's rows (the grid has no empty split) and this wave's blocks: wave, wave + 4, ...
+  const uint64_t r0 = static_cast<uint64_t>(split) * a.rows_per_split;
+  const uint64_t r1 = a.n < r0 + a.rows_per_split ? a.n : r0 + a.rows_per_split;
+  const uint32_t nblk = static_cast<uint32_t>(ceil_div(r1 - r0, 32));
+  const uint32_t myblk = nblk > static_cast<uint32_t>(wave) ? (nblk - wave + kRingWaves - 1) / kRingWaves : 0u;
+
+  constexpr float kScale = L2 ? -2.0f : -1.0f;
+  float qreg[DP / 2];
+  {
+    const float* qp = a.Q + static_cast<size_t>(qvalid ? q : 0) * DP;
+#pragma unroll
+    for (int qq = 0; qq < NQ; ++qq)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const f32x4 v = qvalid ? *reinterpret_cast<const f32x4*>(qp + 32 * qq + 8 * u + 4 * h)
+                               : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qreg[qq * 16 + 4 * u + i] = kScale * v[i];
+      }
+  }
+  const float qaug = h == 0 ? 1.0f : (L2 && qvalid ? a.qnorm[q] : 0.0f);
+  // Uses that make the compiler wait for these loads here, before any ring load is in flight.
+#pragma unroll
+  for (int i = 0; i < DP / 2; ++i) asm volatile("" ::"v"(qreg[i]));
+  asm volatile("" ::"v"(qaug));
+
+  if (tid < 32) s_thr[tid] = 0xFF800000u;  // ordered bits of +inf
+  s_part[tid >> 3][tid & 7] = __builtin_huge_valf();
+  __syncthreads();
+
+  uint64_t Lk[KL];  // this lane's list: the KL best (distance, row) keys of its rows, ascending
+#pragma unroll
+  for (int x = 0; x < KL; ++x) Lk[x] = kRingEmptyKey;
+  float pthr = __builtin_huge_valf();
+  float* qd = s_qd[wave];
+  uint32_t* qr = s_qr[wave];
+  int qcount = 0;
+  // Queued candidates into the list (NaN as +inf), all lanes at once, for as long as some lane
+  // has one left; a lane past its count inserts the empty key.
+  auto flush_queue = [&]() {
+    for (int e = 0; __builtin_amdgcn_ballot_w64(e < qcount); ++e) {
+      const int at = e < qcount ? e : 0;
+      float v = qd[at * 64 + lane];
+      v = v == v ? v : __builtin_huge_valf();
+      key_insert<KL>(Lk, e < qcount ? make_key(v, qr[at * 64 + lane]) : kRingEmptyKey);
+    }
+    qcount = 0;
+  };
+
+  if (myblk > 0) {
+    const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_address(&s_ring[wave][0][0]));
+    const uint32_t norm_lds = __builtin_amdgcn_readfirstlane(lds_address(&s_norm[wave][0][0]));
+    const float* ring = &s_ring[wave][0][0];
+    const float* norms = &s_norm[wave][0][0];
+    // Byte offsets of this lane's 16-byte units in a whole block's quarter, and of its row norm.
+    uint32_t voff[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const uint32_t P = 64 * m + lane, r = P >> 3, c = (P & 7) ^ (r & 7);
+      voff[m] = (r * DP + 4 * c) * 4;
+    }
+    // Quarter qq of block b (clamped to the wave's last block: the loads past the end repeat it,
+    // so every group has its fixed number of loads) into slot `slot`, once every LDS read this
+    // wave has issued is complete (among them the last reads of that slot).
+    auto issue = [&](uint32_t b, int qq, uint32_t slot) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      b = b < myblk ? b : myblk - 1;
+      const uint64_t row0 = r0 + 32ull * (static_cast<uint64_t>(wave) + kRingWaves * static_cast<uint64_t>(b));
+      const uint64_t left = r1 - row0;  // >= 1
+      const float* sbase = a.X + row0 * DP + 32 * qq;
+      const uint32_t lds = ring_lds + slot * SLOT_BYTES;
+      if (left >= 32) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) lds_load16(lds + 1024 * m, sbase, voff[m]);
+      } else {  // the split's last block: rows past its end repeat its last row
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const uint32_t P = 64 * m + lane, r = P >> 3, c = (P & 7) ^ (r & 7);
+          const uint32_t rc = r < left ? r : static_cast<uint32_t>(left - 1);
+          lds_load16(lds + 1024 * m, sbase, (rc * DP + 4 * c) * 4);
+        }
+      }
+      if (qq == 0) {  // lanes 0-31: the block's row norms (L2); 32-63: the queries' shared bounds
+        const uint32_t rn = static_cast<uint32_t>(j) < left ? static_cast<uint32_t>(j) : static_cast<uint32_t>(left - 1);
+        const void* src = L2 && h == 0 ? static_cast<const void*>(a.xnorm + row0 + rn)
+                                       : static_cast<const void*>(a.qthr + (qvalid ? q : 0u) * kRingBoundStride);
+        lds_load4(norm_lds + slot * 256, src);
+      }
+    };
+    auto read = [&](uint32_t slot, f32x4 (&x)[4]) {
+      const float* sp = ring + slot * kRingSlotFloats;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int c = 2 * u + h;
+        x[u] = *reinterpret_cast<const f32x4*>(sp + (j * 8 + (c ^ (j & 7))) * 4);
+      }
+    };
+
+    // Prologue: groups 0 .. R - 2 in flight, then group 0 in registers.
+#pragma unroll
+    for (int g = 0; g < R - 1; ++g) issue(static_cast<uint32_t>(g / NQ), g % NQ, static_cast<uint32_t>(g));
+    uint32_t slot_read = 0, slot_issue = R - 1;
+    {
+      constexpr int kFirst = [] {
+        int n = 0;
+        for (int d = 1; d <= kRingSlots - 2; ++d) n += ring_group_loads(d % NQ);
+        return n;
+      }();
+      wait_vmem<kFirst>();
+    }
+    f32x4 xa[4], xb[4];
+    read(0, xa);
+    float na = L2 ? norms[j] : 1.0f, nb = na;
+    uint32_t ga = __float_as_uint(norms[32 + j]), gb = ga;  // the shared bound as the block's load saw it
+
+    for (uint32_t b = 0; b < myblk; ++b) {
+      f32x16 acc = {};
+#pragma unroll
+      for (int qq = 0; qq < NQ; ++qq) {
+        if (qq == 0) {
+          acc = __builtin_amdgcn_mfma_f32_32x32x2f32(h == 0 ? na : 1.0f, qaug, acc, 0, 0, 0);
+          pthr = fminf(pthr, ordered_to_float(ga));
+        }
+        // Refill the slot this quarter's predecessor used (read in the iteration before last), then
+        // wait for the next group and read it while this quarter's MFMAs run.
+        issue(b + (qq + R - 1) / NQ, (qq + R - 1) % NQ, slot_issue);
+        slot_issue = slot_issue + 1 == R ? 0 : slot_issue + 1;
+        wait_vmem_n<4 * (kRingSlots - 2), 5 * (kRingSlots - 2)>(ring_wait_count<NQ>(qq));
+        const uint32_t slot_next = slot_read + 1 == R ? 0 : slot_read + 1;
+        read(slot_next, xb);
+        if ((qq + 1) % NQ == 0) {
+          if (L2) nb = norms[slot_next * 64 + j];
+          gb = __float_as_uint(norms[slot_next * 64 + 32 + j]);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[u][i], qreg[qq * 16 + 4 * u + i], acc, 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) xa[u] = xb[u];
+        if ((qq + 1) % NQ == 0) {
+          na = nb;
+          ga = gb;
+        }
+        slot_read = slot_next;
+      }
+      // Selection over the block: register r holds row 8 (r / 4) + 4 h + r % 4 of the block.
+      const uint64_t row0 = r0 + 32ull * (static_cast<uint64_t>(wave) + kRingWaves * static_cast<uint64_t>(b));
+      const uint64_t left = r1 - row0;
+      const bool masked = left < 32;
+      const uint32_t lane_bits = (masked ? ((1u << left) - 1u) : 0xFFFFFFFFu) >> (4 * h);
+      const float thr = fminf(pthr, key_distance(Lk[KL - 1]));
+      bool any = false;
+      if (!masked) {
+        float m = acc[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) m = fminf(m, acc[r]);
+        any = !(m > thr);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) any = any || (!(acc[r] > thr) && ((lane_bits >> (8 * (r >> 2) + (r & 3))) & 1u));
+      }
+      any = any && qvalid;
+      if (__builtin_amdgcn_ballot_w64(qcount > CAP - 16)) flush_queue();
+      if (any) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int bit = 8 * (r >> 2) + (r & 3);
+          bool p = !(acc[r] > thr);
+          if (masked) p = p && ((lane_bits >> bit) & 1u);
+          qd[qcount * 64 + lane] = acc[r];
+          qr[qcount * 64 + lane] = static_cast<uint32_t>(row0 + 4 * h + bit);
+          qcount += p ? 1 : 0;
+        }
+      }
+      if (b % kRingShareEvery == kRingShareEvery - 1) {
+        // The two lanes of a query hold disjoint rows, and so do the four waves and the splits: any
+        // list's KL-th (or the pair's bound) bounds the KL-th of the union of all of the query's
+        // lists. Shared through LDS with the work-group at once, and through a per-query word in
+        // device memory (one 128-byte line per query) with the other splits, which read it with
+        // their blocks' norm loads. Only the first wave writes that word, with the work-group's
+        // bound, and only when it is below what this block's load saw: an atomic that returns
+        // nothing, so no wait is for its return, but one that the ring's in-order waits may still
+        // wait behind, so they must stay few.
+        flush_queue();
+        const float own_k = key_distance(Lk[KL - 1]), own_h = key_distance(Lk[KL / 2 - 1]);
+        const float oth_k = lane_swap32_f(own_k), oth_h = lane_swap32_f(own_h);
+        float t = fminf(fminf(own_k, oth_k), fmaxf(own_h, oth_h));
+        // The work-group's union: the other waves' entries may be older (larger) values of their
+        // lists, which keeps the largest of the eight an upper bound.
+        s_part[j][2 * wave + h] = key_distance(Lk[(KL + 7) / 8 - 1]);
+        {
+          const f32x4 p0 = *reinterpret_cast<const f32x4*>(&s_part[j][0]);
+          const f32x4 p1 = *reinterpret_cast<const f32x4*>(&s_part[j][4]);
+          const float u = fmaxf(fmaxf(fmaxf(p0[0], p0[1]), fmaxf(p0[2], p0[3])),
+                                fmaxf(fmaxf(p1[0], p1[1]), fmaxf(p1[2], p1[3])));
+          t = fminf(t, u);
+        }
+        uint32_t g = 0xFF800000u;
+        if (h == 0) {
+          const uint32_t ot = float_to_ordered(t);
+          g = atomicMin(&s_thr[j], ot);
+          const uint32_t wg = g < ot ? g : ot;
+          if (wave == 0 && qvalid && wg < ga) {
+            __hip_atomic_fetch_min(a.qthr + q * kRingBoundStride, wg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+        const uint32_t gs = lane_swap32_u32(g);
+        g = h == 0 ? g : gs;
+        pthr = fminf(pthr, fminf(t, ordered_to_float(g)));
+      }
+    }
+    wait_vmem<0>();  // the loads past the end, before the LDS is reused or released
+  }
+  flush_queue();
+
+  // The four waves' lists into the first wave's, through the ring slots: waves 2 and 3 hand theirs
+  // to waves 0 and 1, then wave 1 to wave 0.
+  __syncthreads();
+  uint64_t* hk = reinterpret_cast<uint64_t*>(&s_ring[0][0][0]);
+  if (wave >= 2) {
+#pragma unroll
+    for (int x = 0; x < KL; ++x) hk[((wave - 2) * KL + x) * 64 + lane] = Lk[x];
+  }
+  __syncthreads();
+  if (wave < 2) ring_merge_list<KL>(Lk, hk + wave * KL * 64, lane);
+  __syncthreads();
+  if (wave == 1) {
+#pragma unroll
+    for (int x = 0; x < KL; ++x) hk[x * 64 + lane] = Lk[x];
+  }
+  __syncthreads();
+  if (wave == 0) {
+    ring_merge_list<KL>(Lk, hk, lane);
+    if (qvalid) {
+      const size_t o = (static_cast<size_t>(q) * (2 * a.nsplit) + 2 * split + h) * KL;
+#pragma unroll
+      for (int x = 0; x < KL; ++x) {
+        a.part_d[o + x] = key_distance(Lk[x]);
+        a.part_r[o + x] = static_cast<uint32_t>(Lk[x]);
+      }
     }
   }
 }
@@ -1919,6 +2336,37 @@ void launch_scan(uint32_t dp, int kl, dim3 grid, const ScanArgs& a, hipStream_t 
   }
 }
 
+template <int DP>
+void launch_ring_dp(int kl, bool l2, dim3 grid, const ScanArgs& a, hipStream_t s) {
+  auto go = [&](auto klc) {
+    constexpr int KL = decltype(klc)::value;
+    if (l2) {
+      hipLaunchKernelGGL((flat_ring_kernel<DP, KL, true>), grid, dim3(kRingThreads), 0, s, a);
+    } else {
+      hipLaunchKernelGGL((flat_ring_kernel<DP, KL, false>), grid, dim3(kRingThreads), 0, s, a);
+    }
+  };
+  if (kl == 10) {
+    go(std::integral_constant<int, 10>{});
+  } else if (kl == 16) {
+    go(std::integral_constant<int, 16>{});
+  } else {
+    go(std::integral_constant<int, 32>{});
+  }
+}
+
+/// The ring scan for padded width dp (a multiple of 32 up to kMaxDp), one work-group per split.
+void launch_ring(uint32_t dp, int kl, dim3 grid, const ScanArgs& a, hipStream_t s) {
+  const bool l2 = a.l2 != 0;
+  switch (dp) {
+    case 32: launch_ring_dp<32>(kl, l2, grid, a, s); break;
+    case 64: launch_ring_dp<64>(kl, l2, grid, a, s); break;
+    case 96: launch_ring_dp<96>(kl, l2, grid, a, s); break;
+    case 128: launch_ring_dp<128>(kl, l2, grid, a, s); break;
+    default: throw Failure(QVH_EUNSUPPORTED, "ring scan: padded dimension is not a multiple of 32 up to 128");
+  }
+}
+
 }  // namespace
 
 struct qvh_flat {
@@ -1981,6 +2429,7 @@ void flat_grow(qvh_flat* f, uint64_t need) {
 struct FlatPlan {
   enum Path { kFew, kSplit, kExactOnly, kMfma, kSorted } path = kMfma;
   bool wide = false;
+  bool ring = false;  // kMfma: the ring scan (one 32-query group, unfiltered) instead of the MFMA scan
   int kl = 16;
   // List length when every query's distances turn out exact (exact_list_length), or 0: the scan
   // and merge are then launched for both lengths, and the device runs the one that applies.
@@ -2020,7 +2469,8 @@ struct FlatBuffers {
 };
 
 /// d_idx (listed admitted rows) is in use when n_idx > 0 or `indexed`.
-FlatPlan plan_flat_search(const qvh_flat* f, uint64_t nq, uint32_t k, bool indexed, uint64_t n_idx, int cus) {
+FlatPlan plan_flat_search(const qvh_flat* f, uint64_t nq, uint32_t k, bool indexed, bool filtered, uint64_t n_idx,
+                          int cus) {
   QVH_REQUIRE(nq <= 0xFFFFFFFFull, "flat search: too many queries in one call");
   FlatPlan p;
   if (k > kExactMaxK) {
@@ -2044,10 +2494,16 @@ FlatPlan plan_flat_search(const qvh_flat* f, uint64_t nq, uint32_t k, bool index
   // or 32 and a shared bound; larger k up to kWideMaxK: the same scan without the shared bound and
   // the wide merge (its rare fallback queries on the exact kernel); larger k or dim: the exact kernel.
   // Rows wider than kMaxDp (up to kMaxChunkedDp) take the chunked form of the MFMA scan.
+  // kRingMinQueries to kRingMaxQueries unfiltered queries whose rows are whole 32-dim quarters,
+  // with k in the shared-bound lists: the ring scan (its lists go to the same merge as the MFMA
+  // scan's); fewer queries too when the rows are too few to split for the few-query kernel.
+  const bool ring = !indexed && !filtered && f->n >= 1 && nq <= kRingMaxQueries && shared_list_length(k) != 0 &&
+                    f->dp % 32 == 0 && f->dp <= static_cast<uint32_t>(kMaxDp) &&
+                    (nq >= kRingMinQueries || f->n < 2 * kMinSplitRows);
   const bool splittable = !indexed && f->n >= 2 * kMinSplitRows;
-  const bool few = splittable && nq <= kFewMaxBatch && k <= (f->dim % 32 == 0 ? kFewMaxK : 64u) && f->dim >= 32 &&
-                   f->dim <= kFewMaxDim;
-  const bool split = splittable && !few && nq <= kSplitMaxQueries;
+  const bool few = !ring && splittable && nq <= kFewMaxBatch && k <= (f->dim % 32 == 0 ? kFewMaxK : 64u) &&
+                   f->dim >= 32 && f->dim <= kFewMaxDim;
+  const bool split = !ring && splittable && !few && nq <= kSplitMaxQueries;
   p.wide = !few && !split && shared_list_length(k) == 0 && k <= kWideMaxK && f->dp <= kMaxChunkedDp &&
            !indexed;
   const bool exact_only = !few && !split && !p.wide && (shared_list_length(k) == 0 || f->dp > kMaxChunkedDp);
@@ -2084,33 +2540,43 @@ FlatPlan plan_flat_search(const qvh_flat* f, uint64_t nq, uint32_t k, bool index
   p.kl_exact = !p.wide && f->integral_rows ? exact_list_length(k) : 0;
   p.qblocks = static_cast<uint32_t>(ceil_div(nq, kQueriesPerBlock));
   p.scan_rows = indexed ? n_idx : f->n;
-  const uint64_t tiles = std::max<uint64_t>(1, ceil_div(p.scan_rows, kTileRows));
-  // One workgroup per CU at a time: pick the split count (a multiple of 8 for the XCD mapping)
-  // whose workgroup count best fills whole rounds of the CUs; fewer splits on ties. A split keeps
-  // at least four tiles: with fewer rows per split the per-split top-k lists take in most rows
-  // (1.18M x 100 cosine with 0.5% of the ids allowed: 32 splits 0.47 ms, 16 splits 0.37 ms).
-  {
-    const uint64_t cap = std::max<uint64_t>(1, std::min<uint64_t>(tiles / 4, kMaxSplits));
-    double best = -1.0;
-    for (uint64_t c = 1; c <= cap; c = c < 8 ? c + 1 : c + 8) {
-      if (c >= 8 && c % 8) continue;
-      const uint64_t total = p.qblocks * c;
-      const uint64_t rounds = ceil_div(total, static_cast<uint64_t>(cus));
-      // prefer enough parallelism (>= 4 rounds when the rows allow) and full rounds
-      const double fill = static_cast<double>(total) / static_cast<double>(rounds * cus);
-      const double par = std::min(1.0, static_cast<double>(total) / (4.0 * cus));
-      const double score = fill * par;
-      if (score > best + 1e-9) {
-        best = score;
-        p.nsplit = c;
+  if (ring) {
+    // One work-group (160 KB of LDS: one per CU) per split of whole 32-row blocks, as many splits
+    // as CUs (at most kRingMaxSplits) while each keeps kRingMinSplitRows rows.
+    p.ring = true;
+    p.nsplit = std::min<uint64_t>({kRingMaxSplits, static_cast<uint64_t>(std::max(cus, 1)),
+                                   std::max<uint64_t>(1, p.scan_rows / kRingMinSplitRows)});
+    p.rows_per_split = ceil_div(ceil_div(p.scan_rows, p.nsplit), 32) * 32;
+    p.nsplit = ceil_div(p.scan_rows, p.rows_per_split);
+  } else {
+    const uint64_t tiles = std::max<uint64_t>(1, ceil_div(p.scan_rows, kTileRows));
+    // One workgroup per CU at a time: pick the split count (a multiple of 8 for the XCD mapping)
+    // whose workgroup count best fills whole rounds of the CUs; fewer splits on ties. A split keeps
+    // at least four tiles: with fewer rows per split the per-split top-k lists take in most rows
+    // (1.18M x 100 cosine with 0.5% of the ids allowed: 32 splits 0.47 ms, 16 splits 0.37 ms).
+    {
+      const uint64_t cap = std::max<uint64_t>(1, std::min<uint64_t>(tiles / 4, kMaxSplits));
+      double best = -1.0;
+      for (uint64_t c = 1; c <= cap; c = c < 8 ? c + 1 : c + 8) {
+        if (c >= 8 && c % 8) continue;
+        const uint64_t total = p.qblocks * c;
+        const uint64_t rounds = ceil_div(total, static_cast<uint64_t>(cus));
+        // prefer enough parallelism (>= 4 rounds when the rows allow) and full rounds
+        const double fill = static_cast<double>(total) / static_cast<double>(rounds * cus);
+        const double par = std::min(1.0, static_cast<double>(total) / (4.0 * cus));
+        const double score = fill * par;
+        if (score > best + 1e-9) {
+          best = score;
+          p.nsplit = c;
+        }
       }
     }
+    p.rows_per_split = ceil_div(tiles, p.nsplit) * kTileRows;
   }
-  p.rows_per_split = ceil_div(tiles, p.nsplit) * kTileRows;
   const size_t parts = static_cast<size_t>(nq) * 2 * p.nsplit * p.kl;
   p.pd = parts * sizeof(float);
   p.pr = parts * sizeof(uint32_t);
-  p.thr = nq * sizeof(uint32_t);
+  p.thr = nq * (p.ring ? kRingBoundStride : 1) * sizeof(uint32_t);
   p.fb = (nq + 2) * sizeof(uint32_t);  // count, listed queries, then the launch gate word
   return p;
 }
@@ -2288,16 +2754,24 @@ void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const
   // One query block of at most 128 queries, unfiltered, register-resident queries: the row-split
   // form of the scan (two waves per 32-query group).
   a.rowsplit = nq <= static_cast<uint64_t>(kQueriesPerBlock / 2) && !d_idx && !d_bitmap && f->dp <= kMaxDp ? 1 : 0;
-  hipLaunchKernelGGL(fill_u32_kernel, dim3(static_cast<unsigned>(ceil_div(nq, 256))), dim3(256), 0, s,
-                     a.qthr, nq, 0xFF800000u);  // ordered bits of +inf
+  const uint64_t nthr = nq * (p.ring ? kRingBoundStride : 1);  // the ring scan's words are strided
+  hipLaunchKernelGGL(fill_u32_kernel, dim3(static_cast<unsigned>(ceil_div(nthr, 256))), dim3(256), 0, s,
+                     a.qthr, nthr, 0xFF800000u);  // ordered bits of +inf
   const dim3 sgrid(static_cast<unsigned>(p.qblocks * p.nsplit));
+  auto scan = [&](int kl) {
+    if (p.ring) {
+      launch_ring(f->dp, kl, sgrid, a, s);
+    } else {
+      launch_scan(f->dp, kl, sgrid, a, s);
+    }
+  };
   if (gate) {  // exact distances for every query: the short lists; otherwise the margin's
     a.gate = gate;
     a.gate_want = 0;
-    launch_scan(f->dp, p.kl_exact, sgrid, a, s);
+    scan(p.kl_exact);
     a.gate_want = 1;
   }
-  launch_scan(f->dp, p.kl, sgrid, a, s);
+  scan(p.kl);
   QVH_HIP(hipGetLastError());
   if (f->timed) QVH_HIP(hipEventRecord(f->ev[2], s));
   f->last_nsplit = p.nsplit;
@@ -2376,7 +2850,7 @@ void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const
 void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t k,
                       const uint64_t* d_bitmap, uint32_t* d_rows, float* d_dist, hipStream_t s,
                       const uint32_t* d_idx = nullptr, uint64_t n_idx = 0) {
-  const FlatPlan p = plan_flat_search(f, nq, k, d_idx != nullptr, n_idx, device_cus(f->device));
+  const FlatPlan p = plan_flat_search(f, nq, k, d_idx != nullptr, d_bitmap != nullptr, n_idx, device_cus(f->device));
   flat_search_run(f, p, handle_buffers(f, p), d_queries, nq, k, d_bitmap, d_rows, d_dist, s, d_idx, n_idx);
 }
 
@@ -2701,7 +3175,7 @@ qvh_status qvh_flat_search_device_noalloc(qvh_flat* f, const float* d_queries, u
     ScratchSlot& slot = scratch_on(f->device);
     std::lock_guard<std::mutex> use(slot.use);  // after the handle's lock, never before it
     unsigned char* base = static_cast<unsigned char*>(slot.ptr);
-    const FlatPlan p = plan_flat_search(f, nq, k, false, 0, device_cus(f->device));
+    const FlatPlan p = plan_flat_search(f, nq, k, false, d_row_bitmap != nullptr, 0, device_cus(f->device));
     if (p.total() > kScratchBytes) {
       throw Failure(QVH_EINVAL, "qvh_flat_search_device_noalloc: this search needs " + std::to_string(p.total()) +
                                     " bytes of workspace, above the fixed scratch of " +

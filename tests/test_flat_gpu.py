@@ -259,15 +259,44 @@ def test_few_query_coalesced_scan(oracle, metric, dim, nq, k, n):
 @pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
 @pytest.mark.parametrize("nq", [9, 16, 32, 64, 100])
 def test_small_batches_on_256_row_splits(oracle, metric, nq):
-    """9 to 128 queries: one block of the MFMA scan in its row-split form (the two waves of a 32-query
-    group take the two halves of each tile, and the odd wave's lists join the even wave's through
-    LDS), its rows over 256 splits (512 lane lists per query in the merge, eight per merge lane).
-    Integer data adds exact ties across splits and tile halves."""
+    """Up to 32 queries: the ring scan over 73 splits of 4,096 rows; 33 to 128: one block of the
+    MFMA scan in its row-split form (the two waves of a 32-query group take the two halves of each
+    tile, and the odd wave's lists join the even wave's through LDS) over up to 256 splits. Either
+    way the merge takes two lane lists per query and split. Integer data adds exact ties across
+    splits, waves and tile halves."""
     base = D.gaussian(300_000, 128, seed=35)
     q = D.gaussian(nq, 128, seed=36)
     print(_check(oracle, base, q, 10, metric))
     ib, iq = D.int_mix(300_000, nq)
     print(_check(oracle, ib, iq, 10, metric))
+
+
+@pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
+@pytest.mark.parametrize("dim,nq,k,n", [(128, 5, 10, 1_000_003), (128, 32, 10, 300_000), (128, 31, 1, 70_001),
+                                        (96, 17, 21, 65_632), (64, 8, 11, 4_200), (32, 5, 16, 100),
+                                        (128, 2, 10, 33), (64, 3, 10, 4_097)])
+def test_ring_scan(oracle, metric, dim, nq, k, n):
+    """The ring scan (5 to 32 unfiltered queries, or fewer over rows too few to split; rows of
+    whole 32-dim quarters; k up to 21): 1,000,003 rows make 255 splits of 3,936 rows, the last of
+    259 (a 3-row block); 4,200 rows four splits whose waves stream 9, 8, 8 and 8 blocks; 100 rows
+    one split of four blocks, the last of 4 rows; 33 rows leave two waves without a block; 4,097
+    rows end on a 1-row block. k = 21 takes the 32-entry lists, k = 1, 10 and 11 the 16-entry ones."""
+    base = D.gaussian(n, dim, seed=51)
+    q = D.gaussian(nq, dim, seed=52)
+    print(_check(oracle, base, q, k, metric))
+
+
+@pytest.mark.parametrize("metric", ["l2", "ip"])
+def test_ring_scan_integer_store(oracle, metric):
+    """Integer store and queries take the ring scan's 10-entry lists behind the launch gate; one
+    real-valued query in the batch switches the whole batch to the 16-entry lists. Exact ties
+    across splits and waves resolve to the smaller row. (One query: the few-query kernel.)"""
+    base, q = D.int_mix(200_000, 32)
+    print(_check(oracle, base, q, 10, metric))
+    q2 = q.copy()
+    q2[7, 3] += np.float32(0.25)
+    print(_check(oracle, base, q2, 10, metric))
+    print(_check(oracle, base, q[:1], 10, metric))
 
 
 @pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
