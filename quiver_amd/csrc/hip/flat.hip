@@ -603,17 +603,21 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
 // merged into the first wave's, which writes two lists per query and split in the MFMA scan's
 // format for the same merge, re-score and certificate.
 
-constexpr int kRingWaves = 4;
+constexpr int kRingWaves = 8;           // two per SIMD: one's selection runs beside the other's MFMAs
 constexpr int kRingThreads = kRingWaves * 64;
-constexpr int kRingSlots = 7;           // quarter-block slots per wave
-constexpr int kRingCap = 18;            // queued candidates per lane
+constexpr int kRingSlots = 4;           // quarter-block slots per wave
 constexpr int kRingSlotFloats = 32 * 32;
 constexpr int kRingShareEvery = 2;      // blocks between exchanges of the shared bound
+constexpr int kRingEarlyShares = 4;     // exchanges after each of a wave's first blocks
+// With one wave per SIMD the next quarter is read into registers while this one's MFMAs run; with
+// two, the other wave covers that read, and waiting for the next quarter only after the MFMAs
+// keeps one more group of loads in flight meanwhile.
+constexpr bool kRingLateWait = kRingWaves > 4;
 constexpr uint32_t kRingMinQueries = 5;   // up to four queries the few-query kernel is faster
 constexpr uint32_t kRingMaxQueries = 32;
 constexpr uint64_t kRingMinSplitRows = 1024;  // rows per split at least (eight blocks per wave)
 constexpr uint32_t kRingMaxSplits = 256;   // two lists per query and split: the merge's 512
-constexpr uint32_t kRingBoundStride = 32;  // words between queries' shared bounds (one 128-byte line each)
+constexpr uint32_t kRingBoundStride = 32;  // words between queries' bound slots (one 128-byte line each)
 
 /// LDS byte address of a shared-memory pointer.
 __device__ __forceinline__ uint32_t lds_address(const void* p) {
@@ -649,6 +653,12 @@ __device__ __forceinline__ void lds_load4(uint32_t lds, const void* addr) {
       : "=&s"(save)
       : "s"(lds), "v"(addr)
       : "memory");
+}
+
+/// The bound slot that wave `wave`'s load for block b brings (the waves of a work-group and its
+/// successive blocks go round the ns slots).
+__device__ __forceinline__ uint32_t ring_slot_of(uint32_t b, int wave, int ns) {
+  return (b * static_cast<uint32_t>(kRingWaves) + static_cast<uint32_t>(wave)) % static_cast<uint32_t>(ns);
 }
 
 /// Waits until at most N vector memory operations of this wave are outstanding.
@@ -707,6 +717,27 @@ __device__ __forceinline__ void key_insert(uint64_t (&K)[KL], uint64_t key) {
   K[0] = gt[0] ? key : K[0];
 }
 
+/// Sorts 16 keys ascending in registers (a bitonic network, 80 compare-exchanges).
+__device__ __forceinline__ void sort16_keys(uint64_t (&k)[16]) {
+#pragma unroll
+  for (int w = 2; w <= 16; w <<= 1) {
+#pragma unroll
+    for (int s = w >> 1; s > 0; s >>= 1) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int l = i ^ s;
+        if (l > i) {
+          const bool up = (i & w) == 0;
+          const uint64_t x = k[i], y = k[l];
+          const bool sw = up ? (x > y) : (x < y);
+          k[i] = sw ? y : x;
+          k[l] = sw ? x : y;
+        }
+      }
+    }
+  }
+}
+
 /// Distance of a (distance, row) key.
 __device__ __forceinline__ float key_distance(uint64_t k) { return ordered_to_float(static_cast<uint32_t>(k >> 32)); }
 
@@ -726,20 +757,28 @@ __device__ __forceinline__ void ring_merge_list(uint64_t (&K)[KL], const uint64_
 template <int DP, int KL, bool L2>
 __global__ void __launch_bounds__(kRingThreads) flat_ring_kernel(ScanArgs a) {
   static_assert(DP % 32 == 0 && DP <= kMaxDp, "the ring scan takes whole 32-dim quarters");
-  static_assert(2 * KL * 64 * 2 <= kRingWaves * kRingSlots * kRingSlotFloats, "list hand-off fits the rings");
+  static_assert(kRingWaves / 2 * KL * 64 * 2 <= kRingWaves * kRingSlots * kRingSlotFloats, "list hand-off fits the rings");
+  static_assert((kRingWaves & (kRingWaves - 1)) == 0 && kRingWaves >= 2, "the hand-off halves the waves");
   if (gate_closed(a.gate, a.gate_want)) return;  // the same for every thread of the grid
   constexpr int NQ = DP / 32;  // quarters per block
   constexpr int R = kRingSlots;
-  constexpr int CAP = kRingCap;
   constexpr int SLOT_BYTES = kRingSlotFloats * 4;
   __shared__ __attribute__((aligned(16))) float s_ring[kRingWaves][R][kRingSlotFloats];
   __shared__ float s_norm[kRingWaves][R][64];
-  __shared__ float s_qd[kRingWaves][CAP * 64];
-  __shared__ uint32_t s_qr[kRingWaves][CAP * 64];
   __shared__ uint32_t s_thr[32];
-  // Per query, the ceil(KL / 8)-th entry of each of the work-group's eight lists (four waves, two
-  // lane halves, disjoint rows): the union of the eight holds KL entries at or below the largest.
-  __shared__ __attribute__((aligned(16))) float s_part[32][8];
+  // Per query, the ceil(KL / NL)-th entry of each of the work-group's NL lists (two lane halves
+  // per wave, disjoint rows): their union holds KL entries at or below the largest.
+  constexpr int NL = 2 * kRingWaves;
+  __shared__ __attribute__((aligned(16))) float s_part[32][NL];
+  // Per query, NS bound slots in device memory (a.qthr, kRingBoundStride words per query): slot s
+  // holds the smallest distance any split of class s (split % NS) has found, so the NS slots are
+  // distances of NS different rows and their largest bounds the KL-th (NS >= KL). Each block's
+  // norm load brings one slot of each query (rotating over the slots); s_slot keeps the smallest
+  // value seen per slot, and the work-group's best distance goes to its own slot.
+  constexpr int NS = KL <= 16 ? 16 : 32;
+  static_assert(NS <= static_cast<int>(kRingBoundStride), "the slots fit a query's line");
+  __shared__ __attribute__((aligned(16))) uint32_t s_slot[32][NS];
+  __shared__ uint32_t s_best[32];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -776,27 +815,15 @@ __global__ void __launch_bounds__(kRingThreads) flat_ring_kernel(ScanArgs a) {
   asm volatile("" ::"v"(qaug));
 
   if (tid < 32) s_thr[tid] = 0xFF800000u;  // ordered bits of +inf
-  s_part[tid >> 3][tid & 7] = __builtin_huge_valf();
+  for (int i = tid; i < 32 * NL; i += kRingThreads) s_part[i / NL][i % NL] = __builtin_huge_valf();
+  for (int i = tid; i < 32 * NS; i += kRingThreads) s_slot[i / NS][i % NS] = 0xFF800000u;
+  if (tid < 32) s_best[tid] = 0xFF800000u;
   __syncthreads();
 
   uint64_t Lk[KL];  // this lane's list: the KL best (distance, row) keys of its rows, ascending
 #pragma unroll
   for (int x = 0; x < KL; ++x) Lk[x] = kRingEmptyKey;
   float pthr = __builtin_huge_valf();
-  float* qd = s_qd[wave];
-  uint32_t* qr = s_qr[wave];
-  int qcount = 0;
-  // Queued candidates into the list (NaN as +inf), all lanes at once, for as long as some lane
-  // has one left; a lane past its count inserts the empty key.
-  auto flush_queue = [&]() {
-    for (int e = 0; __builtin_amdgcn_ballot_w64(e < qcount); ++e) {
-      const int at = e < qcount ? e : 0;
-      float v = qd[at * 64 + lane];
-      v = v == v ? v : __builtin_huge_valf();
-      key_insert<KL>(Lk, e < qcount ? make_key(v, qr[at * 64 + lane]) : kRingEmptyKey);
-    }
-    qcount = 0;
-  };
 
   if (myblk > 0) {
     const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_address(&s_ring[wave][0][0]));
@@ -815,6 +842,7 @@ __global__ void __launch_bounds__(kRingThreads) flat_ring_kernel(ScanArgs a) {
     // wave has issued is complete (among them the last reads of that slot).
     auto issue = [&](uint32_t b, int qq, uint32_t slot) {
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      const uint32_t b_virtual = b;
       b = b < myblk ? b : myblk - 1;
       const uint64_t row0 = r0 + 32ull * (static_cast<uint64_t>(wave) + kRingWaves * static_cast<uint64_t>(b));
       const uint64_t left = r1 - row0;  // >= 1
@@ -831,10 +859,11 @@ __global__ void __launch_bounds__(kRingThreads) flat_ring_kernel(ScanArgs a) {
           lds_load16(lds + 1024 * m, sbase, (rc * DP + 4 * c) * 4);
         }
       }
-      if (qq == 0) {  // lanes 0-31: the block's row norms (L2); 32-63: the queries' shared bounds
+      if (qq == 0) {  // lanes 0-31: the block's row norms (L2); 32-63: one bound slot per query
         const uint32_t rn = static_cast<uint32_t>(j) < left ? static_cast<uint32_t>(j) : static_cast<uint32_t>(left - 1);
         const void* src = L2 && h == 0 ? static_cast<const void*>(a.xnorm + row0 + rn)
-                                       : static_cast<const void*>(a.qthr + (qvalid ? q : 0u) * kRingBoundStride);
+                                       : static_cast<const void*>(a.qthr + (qvalid ? q : 0u) * kRingBoundStride +
+                                                                  ring_slot_of(b_virtual, wave, NS));
         lds_load4(norm_lds + slot * 256, src);
       }
     };
@@ -862,7 +891,7 @@ __global__ void __launch_bounds__(kRingThreads) flat_ring_kernel(ScanArgs a) {
     f32x4 xa[4], xb[4];
     read(0, xa);
     float na = L2 ? norms[j] : 1.0f, nb = na;
-    uint32_t ga = __float_as_uint(norms[32 + j]), gb = ga;  // the shared bound as the block's load saw it
+    uint32_t ga = __float_as_uint(norms[32 + j]), gb = ga;  // the block's bound slot as its load saw it
 
     for (uint32_t b = 0; b < myblk; ++b) {
       f32x16 acc = {};
@@ -870,24 +899,28 @@ __global__ void __launch_bounds__(kRingThreads) flat_ring_kernel(ScanArgs a) {
       for (int qq = 0; qq < NQ; ++qq) {
         if (qq == 0) {
           acc = __builtin_amdgcn_mfma_f32_32x32x2f32(h == 0 ? na : 1.0f, qaug, acc, 0, 0, 0);
-          pthr = fminf(pthr, ordered_to_float(ga));
+          if (h == 0) atomicMin(&s_slot[j][ring_slot_of(b, wave, NS)], ga);
         }
         // Refill the slot this quarter's predecessor used (read in the iteration before last), then
         // wait for the next group and read it while this quarter's MFMAs run.
         issue(b + (qq + R - 1) / NQ, (qq + R - 1) % NQ, slot_issue);
         slot_issue = slot_issue + 1 == R ? 0 : slot_issue + 1;
-        wait_vmem_n<4 * (kRingSlots - 2), 5 * (kRingSlots - 2)>(ring_wait_count<NQ>(qq));
         const uint32_t slot_next = slot_read + 1 == R ? 0 : slot_read + 1;
-        read(slot_next, xb);
-        if ((qq + 1) % NQ == 0) {
-          if (L2) nb = norms[slot_next * 64 + j];
-          gb = __float_as_uint(norms[slot_next * 64 + 32 + j]);
-        }
+        auto next = [&]() {
+          wait_vmem_n<4 * (kRingSlots - 2), 5 * (kRingSlots - 2)>(ring_wait_count<NQ>(qq));
+          read(slot_next, xb);
+          if ((qq + 1) % NQ == 0) {
+            if (L2) nb = norms[slot_next * 64 + j];
+            gb = __float_as_uint(norms[slot_next * 64 + 32 + j]);
+          }
+        };
+        if (!kRingLateWait) next();
 #pragma unroll
         for (int u = 0; u < 4; ++u)
 #pragma unroll
           for (int i = 0; i < 4; ++i)
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[u][i], qreg[qq * 16 + 4 * u + i], acc, 0, 0, 0);
+        if (kRingLateWait) next();
 #pragma unroll
         for (int u = 0; u < 4; ++u) xa[u] = xb[u];
         if ((qq + 1) % NQ == 0) {
@@ -913,49 +946,83 @@ __global__ void __launch_bounds__(kRingThreads) flat_ring_kernel(ScanArgs a) {
         for (int r = 0; r < 16; ++r) any = any || (!(acc[r] > thr) && ((lane_bits >> (8 * (r >> 2) + (r & 3))) & 1u));
       }
       any = any && qvalid;
-      if (__builtin_amdgcn_ballot_w64(qcount > CAP - 16)) flush_queue();
-      if (any) {
+      if (b == 0) {
+        // The wave's first block, into empty lists: its 16 candidates sorted (NaN as +inf), the
+        // KL smallest kept; rows that do not pass (outside the split) are empty keys.
+        uint64_t k16[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int bit = 8 * (r >> 2) + (r & 3);
-          bool p = !(acc[r] > thr);
+          const bool p = qvalid && (!masked || ((lane_bits >> bit) & 1u));
+          const float v = acc[r] == acc[r] ? acc[r] : __builtin_huge_valf();
+          k16[r] = p ? make_key(v, static_cast<uint32_t>(row0 + 4 * h + bit)) : kRingEmptyKey;
+        }
+        sort16_keys(k16);
+#pragma unroll
+        for (int x = 0; x < KL; ++x) Lk[x] = x < 16 ? k16[x < 16 ? x : 0] : kRingEmptyKey;
+      } else if (__builtin_amdgcn_ballot_w64(any)) {
+        // Passing candidates straight into the list (NaN as +inf), one register at a time across
+        // the wave, for the registers where some lane has one (the other wave of the SIMD runs its
+        // MFMAs meanwhile).
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int bit = 8 * (r >> 2) + (r & 3);
+          bool p = any && !(acc[r] > thr);
           if (masked) p = p && ((lane_bits >> bit) & 1u);
-          qd[qcount * 64 + lane] = acc[r];
-          qr[qcount * 64 + lane] = static_cast<uint32_t>(row0 + 4 * h + bit);
-          qcount += p ? 1 : 0;
+          if (__builtin_amdgcn_ballot_w64(p)) {
+            const float v = acc[r] == acc[r] ? acc[r] : __builtin_huge_valf();
+            key_insert<KL>(Lk, p ? make_key(v, static_cast<uint32_t>(row0 + 4 * h + bit)) : kRingEmptyKey);
+          }
         }
       }
-      if (b % kRingShareEvery == kRingShareEvery - 1) {
-        // The two lanes of a query hold disjoint rows, and so do the four waves and the splits: any
-        // list's KL-th (or the pair's bound) bounds the KL-th of the union of all of the query's
-        // lists. Shared through LDS with the work-group at once, and through a per-query word in
-        // device memory (one 128-byte line per query) with the other splits, which read it with
-        // their blocks' norm loads. Only the first wave writes that word, with the work-group's
-        // bound, and only when it is below what this block's load saw: an atomic that returns
-        // nothing, so no wait is for its return, but one that the ring's in-order waits may still
-        // wait behind, so they must stay few.
-        flush_queue();
+      if (b < kRingEarlyShares || b % kRingShareEvery == kRingShareEvery - 1) {
+        // The two lanes of a query hold disjoint rows, and so do the waves and the splits: any
+        // list's KL-th (or the lane pair's bound, or the work-group's union bound, or the largest
+        // bound slot) bounds the KL-th of the union of all of the query's lists; the smallest of
+        // them goes to the work-group through LDS.
         const float own_k = key_distance(Lk[KL - 1]), own_h = key_distance(Lk[KL / 2 - 1]);
         const float oth_k = lane_swap32_f(own_k), oth_h = lane_swap32_f(own_h);
         float t = fminf(fminf(own_k, oth_k), fmaxf(own_h, oth_h));
         // The work-group's union: the other waves' entries may be older (larger) values of their
         // lists, which keeps the largest of the eight an upper bound.
-        s_part[j][2 * wave + h] = key_distance(Lk[(KL + 7) / 8 - 1]);
+        s_part[j][2 * wave + h] = key_distance(Lk[(KL + NL - 1) / NL - 1]);
         {
-          const f32x4 p0 = *reinterpret_cast<const f32x4*>(&s_part[j][0]);
-          const f32x4 p1 = *reinterpret_cast<const f32x4*>(&s_part[j][4]);
-          const float u = fmaxf(fmaxf(fmaxf(p0[0], p0[1]), fmaxf(p0[2], p0[3])),
-                                fmaxf(fmaxf(p1[0], p1[1]), fmaxf(p1[2], p1[3])));
+          float u = -__builtin_huge_valf();
+#pragma unroll
+          for (int c = 0; c < NL; c += 4) {
+            const f32x4 pc = *reinterpret_cast<const f32x4*>(&s_part[j][c]);
+            u = fmaxf(u, fmaxf(fmaxf(pc[0], pc[1]), fmaxf(pc[2], pc[3])));
+          }
           t = fminf(t, u);
         }
+        // The slots: the largest of the smallest values seen per slot.
+        {
+          uint32_t smax = 0u;
+#pragma unroll
+          for (int c = 0; c < NS; c += 4) {
+            const uint32_t* sp = &s_slot[j][c];
+            smax = max(smax, max(max(sp[0], sp[1]), max(sp[2], sp[3])));
+          }
+          t = fminf(t, ordered_to_float(smax));
+        }
+        // This work-group's best distance per query, into its slot when below the slot's value as
+        // last seen here (an atomic that returns nothing: the ring's waits never wait for a return,
+        // but may wait behind it, so these stay few).
+        const uint32_t mine = float_to_ordered(key_distance(Lk[0]));
         uint32_t g = 0xFF800000u;
         if (h == 0) {
           const uint32_t ot = float_to_ordered(t);
           g = atomicMin(&s_thr[j], ot);
-          const uint32_t wg = g < ot ? g : ot;
-          if (wave == 0 && qvalid && wg < ga) {
-            __hip_atomic_fetch_min(a.qthr + q * kRingBoundStride, wg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          const uint32_t best = atomicMin(&s_best[j], mine);
+          const uint32_t wb = best < mine ? best : mine;
+          const uint32_t own = split % NS;
+          if (wave == 0 && qvalid && wb < s_slot[j][own]) {
+            atomicMin(&s_slot[j][own], wb);
+            __hip_atomic_fetch_min(a.qthr + q * kRingBoundStride + own, wb, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
           }
+        } else {
+          atomicMin(&s_best[j], mine);
         }
         const uint32_t gs = lane_swap32_u32(g);
         g = h == 0 ? g : gs;
@@ -964,26 +1031,21 @@ __global__ void __launch_bounds__(kRingThreads) flat_ring_kernel(ScanArgs a) {
     }
     wait_vmem<0>();  // the loads past the end, before the LDS is reused or released
   }
-  flush_queue();
 
-  // The four waves' lists into the first wave's, through the ring slots: waves 2 and 3 hand theirs
-  // to waves 0 and 1, then wave 1 to wave 0.
-  __syncthreads();
+  // The waves' lists into the first wave's, through the ring slots, halving the waves each round:
+  // waves [s, 2s) hand theirs to waves [0, s).
   uint64_t* hk = reinterpret_cast<uint64_t*>(&s_ring[0][0][0]);
-  if (wave >= 2) {
 #pragma unroll
-    for (int x = 0; x < KL; ++x) hk[((wave - 2) * KL + x) * 64 + lane] = Lk[x];
-  }
-  __syncthreads();
-  if (wave < 2) ring_merge_list<KL>(Lk, hk + wave * KL * 64, lane);
-  __syncthreads();
-  if (wave == 1) {
+  for (int s = kRingWaves / 2; s >= 1; s /= 2) {
+    __syncthreads();
+    if (wave >= s && wave < 2 * s) {
 #pragma unroll
-    for (int x = 0; x < KL; ++x) hk[x * 64 + lane] = Lk[x];
+      for (int x = 0; x < KL; ++x) hk[((wave - s) * KL + x) * 64 + lane] = Lk[x];
+    }
+    __syncthreads();
+    if (wave < s) ring_merge_list<KL>(Lk, hk + wave * KL * 64, lane);
   }
-  __syncthreads();
   if (wave == 0) {
-    ring_merge_list<KL>(Lk, hk, lane);
     if (qvalid) {
       const size_t o = (static_cast<size_t>(q) * (2 * a.nsplit) + 2 * split + h) * KL;
 #pragma unroll
@@ -1159,7 +1221,7 @@ struct MergeArgs {
   const uint32_t* idx;  // list positions -> rows (indexed scan), or null
   uint32_t* out_rows;
   float* out_dist;
-  const float* delta;   // [nq] bound on |GEMM-form distance - exact distance| (query_norms_kernel)
+  const float* delta;   // [nq] bound on |GEMM-form distance - exact distance| (prep_queries_kernel)
   uint32_t* fallback;   // queries the exact kernel recomputes (uncertified selections)
   uint32_t* nfallback;  // their count
   const uint32_t* gate;  // as ScanArgs::gate
@@ -1420,9 +1482,11 @@ __global__ void row_norms_kernel(const float* __restrict__ rows, float* __restri
   }
 }
 
-/// Squared norms of the prepared queries and each query's bound on |GEMM-form distance - exact
-/// distance| over every stored row (the certificate of the MFMA scan's re-score; n = dp rounding
-/// steps on any product's path, u = 2^-24, P = ||q||, R = the largest stored ||x||):
+/// The queries in the scans' layout, one wave per query: row q of src (dim floats) into qp (dp
+/// floats, zero padded). With qn, also ||q||^2 into qn (summed in any order: the GEMM form and the
+/// bound take any) and the query's bound on |GEMM-form distance - exact distance| over every stored
+/// row into delta (the certificate of the MFMA scan's re-score; n = dp rounding steps on any
+/// product's path, u = 2^-24, P = ||q||, R = the largest stored ||x||):
 ///   L2:            |g - e| <= (2n + 4) u (P + R)^2 (1 + O(nu))
 ///   inner product: |g - e| <= (2n + 2) u (1 + P R) (1 + O(nu))
 /// from the standard bound gamma_n = nu / (1 - nu) on a sum of n rounded terms, applied to the
@@ -1432,14 +1496,28 @@ __global__ void row_norms_kernel(const float* __restrict__ rows, float* __restri
 /// unit whose accumulation rounds faithfully rather than to nearest. delta is 0 when the query
 /// and every stored row are small integers and (P + R)^2 <= 2^24: every product, partial sum and
 /// difference of either form is then an integer below 2^24, so both forms are exact.
-/// any_delta (nullable) becomes nonzero when some query's delta is not 0.
-__global__ void query_norms_kernel(const float* __restrict__ qp, float* __restrict__ qn, uint32_t nq, uint32_t dp,
-                                   const uint32_t* __restrict__ meta, int l2, float* __restrict__ delta,
-                                   uint32_t* __restrict__ any_delta) {
-  const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
-  if (q >= nq) return;
-  bool integral = true;
-  const float s = padded_norm(qp + static_cast<uint64_t>(q) * dp, dp, integral);
+/// *any_delta (nullable) is raised when some query's delta is not 0.
+__global__ void __launch_bounds__(256) prep_queries_kernel(const float* __restrict__ src, float* __restrict__ qp,
+                                                           uint64_t nq, uint32_t dim, uint32_t dp,
+                                                           float* __restrict__ qn, const uint32_t* __restrict__ meta,
+                                                           int l2, float* __restrict__ delta,
+                                                           uint32_t* __restrict__ any_delta) {
+  const uint64_t q = static_cast<uint64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (q >= nq) return;  // the whole wave
+  const uint32_t lane = threadIdx.x & 63u;
+  float s = 0.0f;
+  bool ok = true;
+  for (uint32_t c = lane; c < dp; c += 64) {
+    const float v = c < dim ? src[q * dim + c] : 0.0f;
+    qp[q * dp + c] = v;
+    s = fmaf(v, v, s);
+    ok = ok && small_integer(v);
+  }
+  if (qn == nullptr) return;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+  const bool integral = __builtin_amdgcn_ballot_w64(!ok) == 0;
+  if (lane != 0) return;
   qn[q] = s;
   const double P = sqrt(static_cast<double>(s));
   const double R = sqrt(static_cast<double>(__uint_as_float(meta[0])));
@@ -1453,15 +1531,20 @@ __global__ void query_norms_kernel(const float* __restrict__ qp, float* __restri
   } else {
     d = coef * (1.0 + P * R);
   }
-  // Rounded up to float; an overflowing or NaN bound stays non-finite and fails every check.
   const float df = static_cast<float>(d);
   delta[q] = static_cast<double>(df) < d ? __uint_as_float(__float_as_uint(df) + 1u) : df;
-  if (any_delta != nullptr) {
-    const uint64_t inexact = __ballot(d != 0.0);  // one atomic per wave
-    if (inexact != 0 && (threadIdx.x & 63u) == static_cast<uint32_t>(__builtin_ctzll(inexact))) {
-      atomicOr(any_delta, 1u);
-    }
+  if (any_delta != nullptr && d != 0.0) atomicOr(any_delta, 1u);
+}
+
+/// One search's words before its kernels run: the fallback count fb[0] and the launch gate (gate,
+/// nullable) to zero, and the n_thr shared prune bounds thr to +inf (ordered bits).
+__global__ void reset_search_words_kernel(uint32_t* fb, uint32_t* gate, uint32_t* thr, uint64_t n_thr) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i == 0) {
+    fb[0] = 0u;
+    if (gate != nullptr) *gate = 0u;
   }
+  if (i < n_thr) thr[i] = 0xFF800000u;
 }
 
 __global__ void fill_u32_kernel(uint32_t* p, uint64_t n, uint32_t v) {
@@ -2537,7 +2620,9 @@ FlatPlan plan_flat_search(const qvh_flat* f, uint64_t nq, uint32_t k, bool index
   p.qn = nq * sizeof(float);
   p.delta = nq * sizeof(float);
   p.kl = p.wide ? 32 : shared_list_length(k);
-  p.kl_exact = !p.wide && f->integral_rows ? exact_list_length(k) : 0;
+  // The ring scan takes the margin's lists for integer stores too (exact distances certify with any
+  // list length): a second, gated launch of its scan and merge would cost more than it saves.
+  p.kl_exact = !p.wide && !ring && f->integral_rows ? exact_list_length(k) : 0;
   p.qblocks = static_cast<uint32_t>(ceil_div(nq, kQueriesPerBlock));
   p.scan_rows = indexed ? n_idx : f->n;
   if (ring) {
@@ -2602,8 +2687,8 @@ FlatBuffers handle_buffers(qvh_flat* f, const FlatPlan& p) {
 }
 
 /// Queries into b.q ([nq][dp], normalized for cosine in b.stage) and, for the MFMA scan, their
-/// squared norms into b.qn and their re-score bounds into b.delta; any_delta (nullable) is cleared
-/// and then set when some query's bound is not 0.
+/// squared norms into b.qn and their re-score bounds into b.delta; any_delta (nullable, cleared
+/// beforehand) is set when some query's bound is not 0.
 void flat_prep_queries(qvh_flat* f, const FlatBuffers& b, const float* d_raw, uint64_t nq, hipStream_t s,
                        uint32_t* any_delta = nullptr) {
   const float* qs = d_raw;
@@ -2614,15 +2699,9 @@ void flat_prep_queries(qvh_flat* f, const FlatBuffers& b, const float* d_raw, ui
     launch_normalize_rows(b.stage, nq, f->dim, s);
     qs = b.stage;
   }
-  const uint64_t total = nq * f->dp;
-  hipLaunchKernelGGL(pack_rows_kernel, dim3(static_cast<unsigned>(ceil_div(total, 256))), dim3(256), 0, s,
-                     qs, b.q, nq, f->dim, f->dp);
-  if (b.qn) {
-    if (any_delta) hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, s, any_delta, 1, 0u);
-    hipLaunchKernelGGL(query_norms_kernel, dim3(static_cast<unsigned>(ceil_div(nq, 256))), dim3(256), 0, s,
-                       b.q, b.qn, static_cast<uint32_t>(nq), f->dp, f->meta.as<uint32_t>(),
-                       f->metric == QVH_METRIC_L2 ? 1 : 0, b.delta, any_delta);
-  }
+  hipLaunchKernelGGL(prep_queries_kernel, dim3(static_cast<unsigned>(ceil_div(nq, 4))), dim3(256), 0, s, qs, b.q, nq,
+                     f->dim, f->dp, b.qn, f->meta.as<uint32_t>(), f->metric == QVH_METRIC_L2 ? 1 : 0, b.delta,
+                     any_delta);
   QVH_HIP(hipGetLastError());
 }
 
@@ -2637,6 +2716,12 @@ void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const
   f->timed = f->timing;
   if (f->timed) QVH_HIP(hipEventRecord(f->ev[0], s));
   uint32_t* gate = p.path == FlatPlan::kMfma && p.kl_exact ? b.fb + nq + 1 : nullptr;
+  if (p.path == FlatPlan::kMfma) {
+    // The fallback count and the gate to zero, the shared bounds (strided for the ring scan) to +inf.
+    const uint64_t nthr = nq * (p.ring ? kRingBoundStride : 1);
+    hipLaunchKernelGGL(reset_search_words_kernel, dim3(static_cast<unsigned>(ceil_div(nthr, 256))), dim3(256), 0, s,
+                       b.fb, gate, b.thr, nthr);
+  }
   flat_prep_queries(f, b, d_queries, nq, s, gate);
   if (f->timed) QVH_HIP(hipEventRecord(f->ev[1], s));
   ExactArgs e{};
@@ -2754,9 +2839,6 @@ void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const
   // One query block of at most 128 queries, unfiltered, register-resident queries: the row-split
   // form of the scan (two waves per 32-query group).
   a.rowsplit = nq <= static_cast<uint64_t>(kQueriesPerBlock / 2) && !d_idx && !d_bitmap && f->dp <= kMaxDp ? 1 : 0;
-  const uint64_t nthr = nq * (p.ring ? kRingBoundStride : 1);  // the ring scan's words are strided
-  hipLaunchKernelGGL(fill_u32_kernel, dim3(static_cast<unsigned>(ceil_div(nthr, 256))), dim3(256), 0, s,
-                     a.qthr, nthr, 0xFF800000u);  // ordered bits of +inf
   const dim3 sgrid(static_cast<unsigned>(p.qblocks * p.nsplit));
   auto scan = [&](int kl) {
     if (p.ring) {
@@ -2795,8 +2877,7 @@ void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const
   m.delta = b.delta;
   // fb[0] counts the queries whose selection the merge could not certify (or, in the wide merge,
   // whose list ran out), fb[1..] lists them; the exact kernel then recomputes only those.
-  uint32_t* fb = b.fb;
-  hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(256), 0, s, fb, 1, 0u);
+  uint32_t* fb = b.fb;  // reset before the prep
   m.fallback = fb + 1;
   m.nfallback = fb;
   const dim3 mgrid(static_cast<unsigned>(ceil_div(nq, 4)));

@@ -288,9 +288,10 @@ def test_ring_scan(oracle, metric, dim, nq, k, n):
 
 @pytest.mark.parametrize("metric", ["l2", "ip"])
 def test_ring_scan_integer_store(oracle, metric):
-    """Integer store and queries take the ring scan's 10-entry lists behind the launch gate; one
-    real-valued query in the batch switches the whole batch to the 16-entry lists. Exact ties
-    across splits and waves resolve to the smaller row. (One query: the few-query kernel.)"""
+    """Integer store and queries: the ring scan's GEMM-form distances are exact (every bound 0), so
+    its lists certify without the margin; one real-valued query in the batch has a bound above 0
+    and its selection is certified against it. Exact ties across splits and waves resolve to the
+    smaller row. (One query: the few-query kernel.)"""
     base, q = D.int_mix(200_000, 32)
     print(_check(oracle, base, q, 10, metric))
     q2 = q.copy()
