@@ -613,7 +613,7 @@ constexpr int kRingEarlyShares = 4;     // exchanges after each of a wave's firs
 // two, the other wave covers that read, and waiting for the next quarter only after the MFMAs
 // keeps one more group of loads in flight meanwhile.
 constexpr bool kRingLateWait = kRingWaves > 4;
-constexpr uint32_t kRingMinQueries = 5;   // up to four queries the few-query kernel is faster
+constexpr uint32_t kRingMinQueries = 4;   // up to three queries the few-query kernel is faster
 constexpr uint32_t kRingMaxQueries = 32;
 constexpr uint64_t kRingMinSplitRows = 1024;  // rows per split at least (eight blocks per wave)
 constexpr uint32_t kRingMaxSplits = 256;   // two lists per query and split: the merge's 512
@@ -1241,6 +1241,34 @@ __device__ __forceinline__ bool selection_certified(uint32_t count, uint32_t sel
   return static_cast<double>(e_k) < static_cast<double>(g_last) - static_cast<double>(delta);
 }
 
+/// Keys held per list by the merge before it reloads.
+constexpr int kMergeHeld = 4;
+
+/// Keys p .. p + kMergeHeld - 1 of one list (positions at or past KL read the list's start: in
+/// bounds, never used), as 16-byte loads when KL keeps them aligned.
+template <int KL>
+__device__ __forceinline__ void merge_load_held(const float* ld, const uint32_t* lr, uint32_t p, float (&d)[kMergeHeld],
+                                                uint32_t (&r)[kMergeHeld]) {
+  static_assert(kMergeHeld == 4, "one 16-byte load per list");
+  if constexpr (KL % 4 == 0) {
+    const uint32_t at = p + 4 <= KL ? p : 0u;
+    const f32x4 dv = *reinterpret_cast<const f32x4*>(ld + at);
+    const f32x4 rv = *reinterpret_cast<const f32x4*>(lr + at);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      d[i] = dv[i];
+      r[i] = __float_as_uint(rv[i]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t at = p + i < KL ? p + i : 0u;
+      d[i] = ld[at];
+      r[i] = lr[at];
+    }
+  }
+}
+
 template <int KL>
 __global__ void __launch_bounds__(256) flat_merge_kernel(MergeArgs m) {
   if (gate_closed(m.gate, m.gate_want)) return;
@@ -1250,23 +1278,34 @@ __global__ void __launch_bounds__(256) flat_merge_kernel(MergeArgs m) {
   const float* pd = m.part_d + static_cast<size_t>(q) * m.nlists * KL;
   const uint32_t* pr = m.part_r + static_cast<size_t>(q) * m.nlists * KL;
 
-  uint32_t ptr[kMaxListsPerLane];
-  uint64_t head[kMaxListsPerLane];
+  // The first kMergeHeld keys of each list are loaded up front (unconditional loads, clamped to a
+  // list that exists, so none waits behind a branch) and popped from registers; a list whose held
+  // keys run out before its KL-th loads its next ones there and then. The pop loop itself issues
+  // no other memory access, so no pop waits for an earlier one's load.
+  constexpr int H = kMergeHeld;
+  uint64_t kk[kMaxListsPerLane][H];
+  uint32_t ptr[kMaxListsPerLane];  // the position of kk[u][0] in list u
 #pragma unroll
   for (int u = 0; u < kMaxListsPerLane; ++u) {
     const uint32_t li = lane + 64 * u;
+    const bool ok = li < m.nlists;
+    const uint32_t lc = ok ? li : 0u;
+    float d[H];
+    uint32_t r[H];
+    merge_load_held<KL>(pd + static_cast<size_t>(lc) * KL, pr + static_cast<size_t>(lc) * KL, 0, d, r);
+#pragma unroll
+    for (int i = 0; i < H; ++i) kk[u][i] = ok && i < KL ? make_key(d[i], r[i]) : ~0ull;
     ptr[u] = 0;
-    head[u] = li < m.nlists ? make_key(pd[li * KL], pr[li * KL]) : ~0ull;
   }
   uint64_t sel = ~0ull;
   int count = 0;
   for (int x = 0; x < KL; ++x) {
-    uint64_t mine = head[0];
+    uint64_t mine = kk[0][0];
     int arg = 0;
 #pragma unroll
     for (int u = 1; u < kMaxListsPerLane; ++u) {
-      if (head[u] < mine) {
-        mine = head[u];
+      if (kk[u][0] < mine) {
+        mine = kk[u][0];
         arg = u;
       }
     }
@@ -1278,9 +1317,18 @@ __global__ void __launch_bounds__(256) flat_merge_kernel(MergeArgs m) {
 #pragma unroll
       for (int u = 0; u < kMaxListsPerLane; ++u) {
         if (u == arg) {
-          const uint32_t li = lane + 64 * u;
+#pragma unroll
+          for (int i = 0; i + 1 < H; ++i) kk[u][i] = kk[u][i + 1];
+          kk[u][H - 1] = ~0ull;
           const uint32_t p = ++ptr[u];
-          head[u] = p < KL ? make_key(pd[li * KL + p], pr[li * KL + p]) : ~0ull;
+          if (p % H == 0 && p < KL) {  // held keys used up: the list's next ones
+            float d[H];
+            uint32_t r[H];
+            merge_load_held<KL>(pd + static_cast<size_t>(lane + 64 * u) * KL,
+                                pr + static_cast<size_t>(lane + 64 * u) * KL, p, d, r);
+#pragma unroll
+            for (int i = 0; i < H; ++i) kk[u][i] = p + i < KL ? make_key(d[i], r[i]) : ~0ull;
+          }
         }
       }
     }
@@ -1483,7 +1531,8 @@ __global__ void row_norms_kernel(const float* __restrict__ rows, float* __restri
 }
 
 /// The queries in the scans' layout, one wave per query: row q of src (dim floats) into qp (dp
-/// floats, zero padded). With qn, also ||q||^2 into qn (summed in any order: the GEMM form and the
+/// floats, zero padded); thr_stride words of thr (nullable) per query to +inf and fb[0]
+/// (nullable) to zero. With qn, also ||q||^2 into qn (summed in any order: the GEMM form and the
 /// bound take any) and the query's bound on |GEMM-form distance - exact distance| over every stored
 /// row into delta (the certificate of the MFMA scan's re-score; n = dp rounding steps on any
 /// product's path, u = 2^-24, P = ||q||, R = the largest stored ||x||):
@@ -1501,10 +1550,15 @@ __global__ void __launch_bounds__(256) prep_queries_kernel(const float* __restri
                                                            uint64_t nq, uint32_t dim, uint32_t dp,
                                                            float* __restrict__ qn, const uint32_t* __restrict__ meta,
                                                            int l2, float* __restrict__ delta,
-                                                           uint32_t* __restrict__ any_delta) {
+                                                           uint32_t* __restrict__ any_delta, uint32_t* __restrict__ fb,
+                                                           uint32_t* __restrict__ thr, uint32_t thr_stride) {
   const uint64_t q = static_cast<uint64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (q >= nq) return;  // the whole wave
   const uint32_t lane = threadIdx.x & 63u;
+  // The search's words for the kernels after this one: the query's shared prune bounds to +inf
+  // (ordered bits) and the fallback count to zero.
+  if (thr != nullptr && lane < thr_stride) thr[q * thr_stride + lane] = 0xFF800000u;
+  if (fb != nullptr && q == 0 && lane == 0) fb[0] = 0u;
   float s = 0.0f;
   bool ok = true;
   for (uint32_t c = lane; c < dp; c += 64) {
@@ -1534,17 +1588,6 @@ __global__ void __launch_bounds__(256) prep_queries_kernel(const float* __restri
   const float df = static_cast<float>(d);
   delta[q] = static_cast<double>(df) < d ? __uint_as_float(__float_as_uint(df) + 1u) : df;
   if (any_delta != nullptr && d != 0.0) atomicOr(any_delta, 1u);
-}
-
-/// One search's words before its kernels run: the fallback count fb[0] and the launch gate (gate,
-/// nullable) to zero, and the n_thr shared prune bounds thr to +inf (ordered bits).
-__global__ void reset_search_words_kernel(uint32_t* fb, uint32_t* gate, uint32_t* thr, uint64_t n_thr) {
-  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i == 0) {
-    fb[0] = 0u;
-    if (gate != nullptr) *gate = 0u;
-  }
-  if (i < n_thr) thr[i] = 0xFF800000u;
 }
 
 __global__ void fill_u32_kernel(uint32_t* p, uint64_t n, uint32_t v) {
@@ -2688,9 +2731,10 @@ FlatBuffers handle_buffers(qvh_flat* f, const FlatPlan& p) {
 
 /// Queries into b.q ([nq][dp], normalized for cosine in b.stage) and, for the MFMA scan, their
 /// squared norms into b.qn and their re-score bounds into b.delta; any_delta (nullable, cleared
-/// beforehand) is set when some query's bound is not 0.
+/// beforehand) is set when some query's bound is not 0. With thr, also the MFMA scan's words:
+/// thr_stride prune bounds per query in thr and the fallback count in b.fb.
 void flat_prep_queries(qvh_flat* f, const FlatBuffers& b, const float* d_raw, uint64_t nq, hipStream_t s,
-                       uint32_t* any_delta = nullptr) {
+                       uint32_t* any_delta = nullptr, uint32_t* thr = nullptr, uint32_t thr_stride = 0) {
   const float* qs = d_raw;
   if (f->metric == QVH_METRIC_COSINE) {  // normalized in a copy
     if (b.stage != d_raw) {
@@ -2701,7 +2745,7 @@ void flat_prep_queries(qvh_flat* f, const FlatBuffers& b, const float* d_raw, ui
   }
   hipLaunchKernelGGL(prep_queries_kernel, dim3(static_cast<unsigned>(ceil_div(nq, 4))), dim3(256), 0, s, qs, b.q, nq,
                      f->dim, f->dp, b.qn, f->meta.as<uint32_t>(), f->metric == QVH_METRIC_L2 ? 1 : 0, b.delta,
-                     any_delta);
+                     any_delta, thr != nullptr ? b.fb : nullptr, thr, thr_stride);
   QVH_HIP(hipGetLastError());
 }
 
@@ -2716,13 +2760,14 @@ void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const
   f->timed = f->timing;
   if (f->timed) QVH_HIP(hipEventRecord(f->ev[0], s));
   uint32_t* gate = p.path == FlatPlan::kMfma && p.kl_exact ? b.fb + nq + 1 : nullptr;
+  // The launch gate is cleared before the prep raises it; the MFMA scan's other words are set by the
+  // prep (its shared bounds, strided for the ring scan, and the fallback count).
+  if (gate) hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, s, gate, 1, 0u);
   if (p.path == FlatPlan::kMfma) {
-    // The fallback count and the gate to zero, the shared bounds (strided for the ring scan) to +inf.
-    const uint64_t nthr = nq * (p.ring ? kRingBoundStride : 1);
-    hipLaunchKernelGGL(reset_search_words_kernel, dim3(static_cast<unsigned>(ceil_div(nthr, 256))), dim3(256), 0, s,
-                       b.fb, gate, b.thr, nthr);
+    flat_prep_queries(f, b, d_queries, nq, s, gate, b.thr, p.ring ? kRingBoundStride : 1);
+  } else {
+    flat_prep_queries(f, b, d_queries, nq, s);
   }
-  flat_prep_queries(f, b, d_queries, nq, s, gate);
   if (f->timed) QVH_HIP(hipEventRecord(f->ev[1], s));
   ExactArgs e{};
   e.X = f->rows.as<float>();
@@ -2923,7 +2968,8 @@ void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const
     QVH_HIP(hipGetLastError());
     e.qskip = kFallbackSplitQueries;
   }
-  launch_exact(e, nq, s);
+  // At most nq queries fall back: with no more than the split form takes, none is left for this.
+  if (e.qskip < nq) launch_exact(e, nq, s);
   if (f->timed) QVH_HIP(hipEventRecord(f->ev[3], s));
 }
 

@@ -276,7 +276,7 @@ def test_small_batches_on_256_row_splits(oracle, metric, nq):
                                         (96, 17, 21, 65_632), (64, 8, 11, 4_200), (32, 5, 16, 100),
                                         (128, 2, 10, 33), (64, 3, 10, 4_097)])
 def test_ring_scan(oracle, metric, dim, nq, k, n):
-    """The ring scan (5 to 32 unfiltered queries, or fewer over rows too few to split; rows of
+    """The ring scan (4 to 32 unfiltered queries, or fewer over rows too few to split; rows of
     whole 32-dim quarters; k up to 21): 1,000,003 rows make 255 splits of 3,936 rows, the last of
     259 (a 3-row block); 4,200 rows four splits whose waves stream 9, 8, 8 and 8 blocks; 100 rows
     one split of four blocks, the last of 4 rows; 33 rows leave two waves without a block; 4,097
