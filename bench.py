@@ -232,9 +232,9 @@ def bench_flat(args, hip: Hip, qvh: Qvh):
                           "note": "FlatIndex::search_batch, host numpy buffers in and out (PCIe included)"}
     del host_index
     if not args.no_extra:
-        # Small batches (the first 1 and 8 queries: the few-query kernel; 32 and 128: the row-split
-        # MFMA scan): device time of one search from its stage events, and the caller's wall time
-        # of search + sync.
+        # Small batches (the first query: the few-query kernel; 8 and 32: the ring scan; 128: the
+        # row-split MFMA scan): device time of one search from its stage events, and the caller's
+        # wall time of search + sync.
         small = {}
         for b in (1, 8, 32, 128):
             dev, wall = [], []

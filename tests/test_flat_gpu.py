@@ -274,7 +274,7 @@ def test_small_batches_on_256_row_splits(oracle, metric, nq):
 @pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
 @pytest.mark.parametrize("dim,nq,k,n", [(128, 5, 10, 1_000_003), (128, 32, 10, 300_000), (128, 31, 1, 70_001),
                                         (96, 17, 21, 65_632), (64, 8, 11, 4_200), (32, 5, 16, 100),
-                                        (128, 2, 10, 33), (64, 3, 10, 4_097)])
+                                        (128, 2, 10, 33), (64, 4, 10, 4_097)])
 def test_ring_scan(oracle, metric, dim, nq, k, n):
     """The ring scan (4 to 32 unfiltered queries, or fewer over rows too few to split; rows of
     whole 32-dim quarters; k up to 21): 1,000,003 rows make 255 splits of 3,936 rows, the last of
