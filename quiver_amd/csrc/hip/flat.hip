@@ -61,10 +61,13 @@ struct ScanArgs {
   const uint32_t* idx;      // admitted rows, ascending (indexed mode), or null
   float* part_d;            // [nq][2*nsplit][KL]
   uint32_t* part_r;
-  uint32_t* qthr;           // [nq] shared prune threshold (ordered float bits), starts at +inf
+  uint32_t* qthr;           // shared prune bounds (ordered float bits, +inf at the start): the
+                            // register and chunked scans kScanBoundStride words per query, the
+                            // ring scan kRingBoundStride
   int share;                // 0: every lane list keeps its own KL best (k > KL: no shared bound)
   uint32_t dp;              // row width (the chunked scan; the register scan has it as DP)
   int rowsplit;             // register scan, unfiltered, at most 128 queries: two waves per query group
+  int bound_slots;          // register scan: publish and read the per-query bound slots
   // Launch gate: when set, the launch does nothing unless (*gate != 0) == (gate_want != 0), read
   // once at the start. Two list lengths are launched back to back and the device picks one.
   const uint32_t* gate;
@@ -76,6 +79,21 @@ __device__ __forceinline__ bool gate_closed(const uint32_t* gate, uint32_t want)
 }
 
 constexpr int kShareEvery = 8;  // tiles between exchanges of the shared per-query threshold
+// The MFMA scan's words per query in ScanArgs::qthr: word 0 the union bound, words kScanSlotBase
+// and up the bound slots (one per list source, at most 32), on the query's second 128-byte line.
+constexpr uint32_t kScanBoundStride = 64;
+constexpr uint32_t kScanSlotBase = 32;
+// Splits per query up to which the register scan uses the bound slots: with more, the atomics of
+// its many lists on the query's slot line queue up (1M x 128, 128 queries on 256 splits: 0.39 ms
+// without the slots, 0.49 ms with them; 10,000 queries on 32 splits: 21.50 ms without, 21.23 ms with).
+constexpr uint64_t kScanSlotMaxSplits = 64;
+
+/// Tiles after which the register scan exchanges bounds: 0, 1 and 3 (the lists' first rows move a
+/// bound the most, and a split of a few tiles would otherwise never take the shared one), then
+/// every kShareEvery.
+__device__ __forceinline__ bool scan_share_after(uint32_t t) {
+  return t == 0 || t == 1 || t == 3 || t % kShareEvery == kShareEvery - 1;
+}
 constexpr int kQueueCap = 20;   // queued candidates per lane before a wave-wide flush
 
 /// Inserts (d, r) into the ascending list (Ld, Lr) in (distance, row) order, dropping the last.
@@ -310,7 +328,18 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
   // Prune threshold: the smaller of this lane's KL-th best and the shared per-query value. Any
   // list's KL-th best bounds the KL-th best of the union of all lists, so candidates above it can
   // never be among the query's KL best (equal distances pass: ties are decided by row).
-  float pthr = qvalid ? ordered_to_float(a.qthr[q]) : __builtin_huge_valf();
+  uint32_t* const qw = a.qthr + static_cast<size_t>(qvalid ? q : 0u) * kScanBoundStride;
+  float pthr = qvalid ? ordered_to_float(qw[0]) : __builtin_huge_valf();
+  // Bound slots: every list of the query (one per split, row half rb and lane half h) publishes
+  // its best distance, atomic min, to slot src of NS = KL. A slot holds one row's distance at any
+  // time, and different lists hold different rows, so once every slot is written the largest slot
+  // is at or above the query's NS-th best distance; unwritten slots hold +inf. Slots read stale
+  // are larger, still bounds. With many splits running at once this bound falls long before any
+  // one list holds KL good rows.
+  constexpr int NS = KL;
+  static_assert(NS % 2 == 0 && kScanSlotBase + NS <= kScanBoundStride, "a query's slots fit its words");
+  const uint32_t src = (split * (RS ? 4u : 2u) + static_cast<uint32_t>(rb) * 2u + static_cast<uint32_t>(h)) % NS;
+  float published = __builtin_huge_valf();
   auto share_threshold = [&]() {
     // The two lanes of a query hold disjoint rows: their union has KL candidates at or below
     // max(own[KL/2-1], other[KL/2-1]) as well as below either list's KL-th.
@@ -319,9 +348,25 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
     float t = fminf(fminf(own_k, oth_k), fmaxf(own_h, oth_h));
     if (qvalid) {
       uint32_t g = 0;
-      if (h == 0) g = atomicMin(&a.qthr[q], float_to_ordered(t));
+      if (h == 0) g = atomicMin(qw, float_to_ordered(t));
+      uint32_t m = 0xFF800000u;  // +inf
+      if (a.bound_slots) {
+        if (Ld[0] < published) {
+          published = Ld[0];
+          __hip_atomic_fetch_min(qw + kScanSlotBase + src, float_to_ordered(published), __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+        }
+        // Each lane half reads half of the slots; the pair's maximum is over all NS.
+        m = 0;
+#pragma unroll
+        for (int i = 0; i < NS / 2; ++i) {
+          m = max(m, __hip_atomic_load(qw + kScanSlotBase + h * (NS / 2) + i, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT));
+        }
+        m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), 32, 64)));
+      }
       g = __shfl(g, j, 64);
-      t = fminf(t, ordered_to_float(g));
+      t = fminf(t, fminf(ordered_to_float(g), ordered_to_float(m)));
     }
     pthr = fminf(pthr, t);
   };
@@ -354,6 +399,27 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
   // load sits under an exec-mask branch and the prefetch of the next tile stays in flight while
   // this tile's MFMAs run.
   const uint64_t last_row = r1 > r0 ? r1 - 1 : r0;
+  // MODE 2: the list entries (row numbers) a tile's loads read, fetched one tile earlier than its
+  // rows, so the row loads never wait on the list load in front of them (a wait that would stall
+  // the wave's MFMAs for a memory latency on every tile).
+  uint32_t lrow[MODE == 2 ? PER_THREAD : 1];
+  uint32_t lrow_norm = 0;
+  auto load_list = [&](uint32_t t) {
+    if constexpr (MODE == 2) {
+      const uint64_t base = r0 + static_cast<uint64_t>(t) * kTileRows;
+#pragma unroll
+      for (int p = 0; p < PER_THREAD; ++p) {
+        int c = tid + p * kThreads;
+        if (CHUNKS % kThreads != 0) c = c < CHUNKS ? c : CHUNKS - 1;
+        const uint64_t pos = base + c / C4;
+        lrow[p] = a.idx[pos < last_row ? pos : last_row];
+      }
+      if constexpr (L2) {
+        const uint64_t pos = base + (tid & (kTileRows - 1));
+        lrow_norm = a.idx[pos < last_row ? pos : last_row];
+      }
+    }
+  };
   auto load_tile = [&](uint32_t t) {
     const uint64_t base = r0 + static_cast<uint64_t>(t) * kTileRows;
 #pragma unroll
@@ -363,16 +429,22 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
       const int row = c / C4, col = c % C4;
       uint64_t gr = base + row;
       gr = gr < last_row ? gr : last_row;
-      if constexpr (MODE == 2) gr = a.idx[gr];
+      if constexpr (MODE == 2) gr = lrow[p];
       stage[p] = *reinterpret_cast<const f32x4*>(a.X + gr * DP + 4 * col);
     }
     if constexpr (L2) {
       uint64_t gn = base + (tid & (kTileRows - 1));
       gn = gn < last_row ? gn : last_row;
-      if constexpr (MODE == 2) gn = a.idx[gn];
+      if constexpr (MODE == 2) gn = lrow_norm;
       stage_norm = a.xnorm[gn];
     }
     if constexpr (FILTER) stage_bits = a.bitmap[base >> 6];
+  };
+  // The next tile's loads, then (MODE 2) the list entries of the tile after it; past the last tile
+  // the entries of the last one are loaded again (unconditional, like the row loads).
+  auto fetch_next = [&](uint32_t t) {
+    load_tile(t + 1);
+    load_list(t + 2 < ntiles ? t + 2 : ntiles - 1);
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
@@ -390,15 +462,17 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
   };
 
   if (ntiles > 0) {
+    load_list(0);
     load_tile(0);
     store_tile(0);
+    load_list(ntiles > 1 ? 1 : 0);
   }
   __syncthreads();
 
   for (uint32_t t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
     const bool prefetch = t + 1 < ntiles;
-    if (!wave_active && prefetch) load_tile(t + 1);
+    if (!wave_active && prefetch) fetch_next(t);
     if (wave_active && RS) {
       // One 32-row half per wave: a single accumulation chain, four MFMAs per pair of b128 reads.
       f32x16 acc = {};
@@ -415,7 +489,7 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
         acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x0[3], qreg[s + 3], acc, 0, 0, 0);
         x0 = n0;
         __builtin_amdgcn_sched_barrier(0);
-        if (s == 4 && prefetch) load_tile(t + 1);
+        if (s == 4 && prefetch) fetch_next(t);
         if (s == 4) __builtin_amdgcn_sched_barrier(0);
       }
       acc = __builtin_amdgcn_mfma_f32_32x32x2f32(augr, qaug, acc, 0, 0, 0);
@@ -482,7 +556,7 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         // The next tile's global loads go out once the MFMA pipe is busy, so no wait for them
         // lands in front of this tile's first MFMAs.
-        if (s == 4 && prefetch) load_tile(t + 1);
+        if (s == 4 && prefetch) fetch_next(t);
         if (s == 4) __builtin_amdgcn_sched_barrier(0);
       }
       acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(aug0, qaug, acc0, 0, 0, 0);
@@ -538,7 +612,7 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
         }
       }
     }
-    if (wave_active && (t % kShareEvery) == kShareEvery - 1) {
+    if (wave_active && scan_share_after(t)) {
       flush_queue();
       if (a.share) share_threshold();
     }
@@ -1068,6 +1142,8 @@ constexpr int kKc = 32;              // dims per chunk
 constexpr int kKcStride = kKc + 4;   // LDS row stride of a row chunk (floats)
 constexpr int kKcQueueCap = 18;      // queue entries per lane (LDS holds both chunk buffers too)
 constexpr uint32_t kMaxChunkedDp = 4096;
+// Largest contiguous copy of listed rows the MFMA scan takes (above it the scan reads through the list).
+constexpr uint64_t kCompactMaxBytes = 4ull << 30;
 
 template <int KL, bool L2, int MODE>
 __global__ void __launch_bounds__(kThreads) flat_scan_k_kernel(ScanArgs a) {
@@ -1095,7 +1171,7 @@ __global__ void __launch_bounds__(kThreads) flat_scan_k_kernel(ScanArgs a) {
   const float qaug = h == 0 ? 1.0f : (L2 && qvalid ? a.qnorm[q] : 0.0f);
 
   LaneScan<KL, kKcQueueCap> ls;
-  ls.init(tid, qvalid ? ordered_to_float(a.qthr[q]) : __builtin_huge_valf());
+  ls.init(tid, qvalid ? ordered_to_float(a.qthr[static_cast<size_t>(q) * kScanBoundStride]) : __builtin_huge_valf());
 
   const uint64_t r0 = static_cast<uint64_t>(split) * a.rows_per_split;
   const uint64_t r1 = r0 < a.n ? (a.n < r0 + a.rows_per_split ? a.n : r0 + a.rows_per_split) : r0;
@@ -1197,7 +1273,7 @@ __global__ void __launch_bounds__(kThreads) flat_scan_k_kernel(ScanArgs a) {
         ls.tile(acc0, acc1, tile_row0, r1 - tile_row0, FILTER ? s_bits[t & 1] : ~0ull, FILTER, qvalid, h, s_qd, s_qr);
         if ((t % kShareEvery) == kShareEvery - 1) {
           ls.flush(s_qd, s_qr);
-          if (a.share) ls.share(qvalid ? &a.qthr[q] : nullptr, h, j);
+          if (a.share) ls.share(qvalid ? &a.qthr[static_cast<size_t>(q) * kScanBoundStride] : nullptr, h, j);
         }
       }
     }
@@ -1588,6 +1664,23 @@ __global__ void __launch_bounds__(256) prep_queries_kernel(const float* __restri
   const float df = static_cast<float>(d);
   delta[q] = static_cast<double>(df) < d ? __uint_as_float(__float_as_uint(df) + 1u) : df;
   if (any_delta != nullptr && d != 0.0) atomicOr(any_delta, 1u);
+}
+
+/// Copies the listed rows idx[0..n) of a [rows][4 * c4] store into a contiguous [n][4 * c4] copy,
+/// 16 bytes per thread and step (a row's chunks on adjacent lanes), and their squared norms into
+/// norms_out when that is set.
+__global__ void gather_rows_kernel(const float* __restrict__ X, const float* __restrict__ norms,
+                                   const uint32_t* __restrict__ idx, uint64_t n, uint32_t c4, float* __restrict__ out,
+                                   float* __restrict__ norms_out) {
+  const uint64_t total = n * c4;
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const uint64_t pos = i / c4;
+    const uint32_t col = static_cast<uint32_t>(i - pos * c4);
+    const uint64_t row = idx[pos];
+    reinterpret_cast<f32x4*>(out)[i] = reinterpret_cast<const f32x4*>(X)[row * c4 + col];
+    if (norms_out != nullptr && col == 0) norms_out[pos] = norms[row];
+  }
 }
 
 __global__ void fill_u32_kernel(uint32_t* p, uint64_t n, uint32_t v) {
@@ -2513,6 +2606,7 @@ struct qvh_flat {
   // per-call workspace (grown on demand, serialized by mu)
   DeviceBuffer w_stage, w_q, w_qn, w_pd, w_pr, w_rows, w_dist, w_bits, w_thr, w_idx, w_fb, w_mflag, w_delta;
   DeviceBuffer w_skin, w_skout, w_soff, w_stmp;  // k above kExactMaxK: sort keys and scratch
+  DeviceBuffer w_cx, w_cn;                        // listed rows gathered for the MFMA scan, their norms
   // optional per-stage timing of the last search: events before prep, scan, merge and after
   bool timing = false;
   bool timed = false;
@@ -2566,6 +2660,8 @@ struct FlatPlan {
   uint64_t scan_rows = 0;
   // Bytes of each workspace buffer (0 = unused).
   size_t stage = 0, q = 0, qn = 0, delta = 0, pd = 0, pr = 0, thr = 0, fb = 0, mflag = 0;
+  // Listed rows for the MFMA scan: their contiguous copy and (L2) its squared norms.
+  size_t cx = 0, cn = 0;
   // k above kExactMaxK: sort_chunk queries per pass; two key buffers, segment offsets, sort scratch.
   uint64_t sort_chunk = 0;
   size_t skeys = 0, soff = 0, stmp = 0;
@@ -2573,7 +2669,8 @@ struct FlatPlan {
   static size_t aligned(size_t b) { return (b + 255) / 256 * 256; }
   size_t total() const {
     return aligned(stage) + aligned(q) + aligned(qn) + aligned(delta) + aligned(pd) + aligned(pr) + aligned(thr) +
-           aligned(fb) + aligned(mflag) + 2 * aligned(skeys) + aligned(soff) + aligned(stmp);
+           aligned(fb) + aligned(mflag) + 2 * aligned(skeys) + aligned(soff) + aligned(stmp) + aligned(cx) +
+           aligned(cn);
   }
 };
 
@@ -2592,6 +2689,8 @@ struct FlatBuffers {
   uint64_t* skout = nullptr;
   uint32_t* soff = nullptr;
   void* stmp = nullptr;
+  float* cx = nullptr;
+  float* cn = nullptr;
 };
 
 /// d_idx (listed admitted rows) is in use when n_idx > 0 or `indexed`.
@@ -2704,8 +2803,15 @@ FlatPlan plan_flat_search(const qvh_flat* f, uint64_t nq, uint32_t k, bool index
   const size_t parts = static_cast<size_t>(nq) * 2 * p.nsplit * p.kl;
   p.pd = parts * sizeof(float);
   p.pr = parts * sizeof(uint32_t);
-  p.thr = nq * (p.ring ? kRingBoundStride : 1) * sizeof(uint32_t);
+  p.thr = nq * (p.ring ? kRingBoundStride : kScanBoundStride) * sizeof(uint32_t);
   p.fb = (nq + 2) * sizeof(uint32_t);  // count, listed queries, then the launch gate word
+  // Listed rows are gathered once into a contiguous copy: the scan reads every row once per query
+  // block, and through the list each of those reads would be a scattered gather (1.18M x 100
+  // cosine, 10% listed, 10,000 queries: 2.97 ms through the list).
+  if (indexed && n_idx > 0 && n_idx * f->dp * sizeof(float) <= kCompactMaxBytes) {
+    p.cx = n_idx * f->dp * sizeof(float);
+    p.cn = f->metric == QVH_METRIC_L2 ? n_idx * sizeof(float) : 0;
+  }
   return p;
 }
 
@@ -2726,6 +2832,8 @@ FlatBuffers handle_buffers(qvh_flat* f, const FlatPlan& p) {
   b.skout = static_cast<uint64_t*>(take(f->w_skout, p.skeys));
   b.soff = static_cast<uint32_t*>(take(f->w_soff, p.soff));
   b.stmp = take(f->w_stmp, p.stmp);
+  b.cx = static_cast<float*>(take(f->w_cx, p.cx));
+  b.cn = static_cast<float*>(take(f->w_cn, p.cn));
   return b;
 }
 
@@ -2764,7 +2872,7 @@ void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const
   // prep (its shared bounds, strided for the ring scan, and the fallback count).
   if (gate) hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, s, gate, 1, 0u);
   if (p.path == FlatPlan::kMfma) {
-    flat_prep_queries(f, b, d_queries, nq, s, gate, b.thr, p.ring ? kRingBoundStride : 1);
+    flat_prep_queries(f, b, d_queries, nq, s, gate, b.thr, p.ring ? kRingBoundStride : kScanBoundStride);
   } else {
     flat_prep_queries(f, b, d_queries, nq, s);
   }
@@ -2873,6 +2981,19 @@ void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const
   a.bitmap = d_idx ? nullptr : d_bitmap;
   a.idx = d_idx;
   a.l2 = f->metric == QVH_METRIC_L2;
+  if (d_idx && b.cx) {
+    // The listed rows in list order: positions stay what the list gives, so the merge and the
+    // fallback map them to rows through d_idx as before.
+    const uint64_t chunks = n_idx * (f->dp / 4);
+    const unsigned blocks = static_cast<unsigned>(
+        std::min<uint64_t>(ceil_div(chunks, 256), static_cast<uint64_t>(device_cus(f->device)) * 16));
+    hipLaunchKernelGGL(gather_rows_kernel, dim3(blocks), dim3(256), 0, s, f->rows.as<float>(),
+                       a.l2 ? f->norms.as<float>() : nullptr, d_idx, n_idx, f->dp / 4, b.cx, b.cn);
+    QVH_HIP(hipGetLastError());
+    a.X = b.cx;
+    if (a.l2) a.xnorm = b.cn;
+    a.idx = nullptr;
+  }
   a.nsplit = static_cast<uint32_t>(p.nsplit);
   a.qblocks = p.qblocks;
   a.rows_per_split = p.rows_per_split;
@@ -2884,6 +3005,7 @@ void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const
   // One query block of at most 128 queries, unfiltered, register-resident queries: the row-split
   // form of the scan (two waves per 32-query group).
   a.rowsplit = nq <= static_cast<uint64_t>(kQueriesPerBlock / 2) && !d_idx && !d_bitmap && f->dp <= kMaxDp ? 1 : 0;
+  a.bound_slots = p.nsplit <= kScanSlotMaxSplits ? 1 : 0;
   const dim3 sgrid(static_cast<unsigned>(p.qblocks * p.nsplit));
   auto scan = [&](int kl) {
     if (p.ring) {
@@ -2906,7 +3028,7 @@ void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const
   MergeArgs m;
   m.gate = nullptr;
   m.gate_want = 0;
-  m.X = a.X;
+  m.X = f->rows.as<float>();
   m.dim = f->dim;
   m.dp = f->dp;
   m.Q = a.Q;
@@ -3283,6 +3405,8 @@ FlatBuffers scratch_buffers(unsigned char* base, const FlatPlan& p) {
   b.skout = static_cast<uint64_t*>(take(p.skeys));
   b.soff = static_cast<uint32_t*>(take(p.soff));
   b.stmp = take(p.stmp);
+  b.cx = static_cast<float*>(take(p.cx));
+  b.cn = static_cast<float*>(take(p.cn));
   return b;
 }
 
