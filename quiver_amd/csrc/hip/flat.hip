@@ -58,7 +58,6 @@ struct ScanArgs {
   uint32_t nsplit;
   uint32_t qblocks;
   uint64_t rows_per_split;  // multiple of kTileRows (of 32 for the ring scan)
-  const uint32_t* idx;      // admitted rows, ascending (indexed mode), or null
   float* part_d;            // [nq][2*nsplit][KL]
   uint32_t* part_r;
   uint32_t* qthr;           // shared prune bounds (ordered float bits, +inf at the start): the
@@ -248,8 +247,8 @@ __device__ __forceinline__ void scan_block_coords(const ScanArgs& a, uint32_t& q
   }
 }
 
-// MODE: 0 every row, 1 rows admitted by a bitmap (tested per tile), 2 the admitted rows listed in
-// a.idx (positions 0..n-1 index that list; candidates carry positions, the merge maps them to rows).
+// MODE: 0 every row of a.X (the store, or a contiguous copy of listed rows: candidates then carry
+// positions in the list, which the merge maps to rows), 1 rows admitted by a bitmap (tested per tile).
 // RS (row split, small batches): the block serves 128 queries, and the two waves of a 32-query group
 // take the two 32-row halves of every tile, so a batch of 32 queries keeps two SIMDs of a CU busy
 // rather than one; at the end the odd wave's lists go through LDS into the even wave's.
@@ -399,27 +398,6 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
   // load sits under an exec-mask branch and the prefetch of the next tile stays in flight while
   // this tile's MFMAs run.
   const uint64_t last_row = r1 > r0 ? r1 - 1 : r0;
-  // MODE 2: the list entries (row numbers) a tile's loads read, fetched one tile earlier than its
-  // rows, so the row loads never wait on the list load in front of them (a wait that would stall
-  // the wave's MFMAs for a memory latency on every tile).
-  uint32_t lrow[MODE == 2 ? PER_THREAD : 1];
-  uint32_t lrow_norm = 0;
-  auto load_list = [&](uint32_t t) {
-    if constexpr (MODE == 2) {
-      const uint64_t base = r0 + static_cast<uint64_t>(t) * kTileRows;
-#pragma unroll
-      for (int p = 0; p < PER_THREAD; ++p) {
-        int c = tid + p * kThreads;
-        if (CHUNKS % kThreads != 0) c = c < CHUNKS ? c : CHUNKS - 1;
-        const uint64_t pos = base + c / C4;
-        lrow[p] = a.idx[pos < last_row ? pos : last_row];
-      }
-      if constexpr (L2) {
-        const uint64_t pos = base + (tid & (kTileRows - 1));
-        lrow_norm = a.idx[pos < last_row ? pos : last_row];
-      }
-    }
-  };
   auto load_tile = [&](uint32_t t) {
     const uint64_t base = r0 + static_cast<uint64_t>(t) * kTileRows;
 #pragma unroll
@@ -429,22 +407,14 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
       const int row = c / C4, col = c % C4;
       uint64_t gr = base + row;
       gr = gr < last_row ? gr : last_row;
-      if constexpr (MODE == 2) gr = lrow[p];
       stage[p] = *reinterpret_cast<const f32x4*>(a.X + gr * DP + 4 * col);
     }
     if constexpr (L2) {
       uint64_t gn = base + (tid & (kTileRows - 1));
       gn = gn < last_row ? gn : last_row;
-      if constexpr (MODE == 2) gn = lrow_norm;
       stage_norm = a.xnorm[gn];
     }
     if constexpr (FILTER) stage_bits = a.bitmap[base >> 6];
-  };
-  // The next tile's loads, then (MODE 2) the list entries of the tile after it; past the last tile
-  // the entries of the last one are loaded again (unconditional, like the row loads).
-  auto fetch_next = [&](uint32_t t) {
-    load_tile(t + 1);
-    load_list(t + 2 < ntiles ? t + 2 : ntiles - 1);
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
@@ -462,17 +432,15 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
   };
 
   if (ntiles > 0) {
-    load_list(0);
     load_tile(0);
     store_tile(0);
-    load_list(ntiles > 1 ? 1 : 0);
   }
   __syncthreads();
 
   for (uint32_t t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
     const bool prefetch = t + 1 < ntiles;
-    if (!wave_active && prefetch) fetch_next(t);
+    if (!wave_active && prefetch) load_tile(t + 1);
     if (wave_active && RS) {
       // One 32-row half per wave: a single accumulation chain, four MFMAs per pair of b128 reads.
       f32x16 acc = {};
@@ -489,7 +457,7 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
         acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x0[3], qreg[s + 3], acc, 0, 0, 0);
         x0 = n0;
         __builtin_amdgcn_sched_barrier(0);
-        if (s == 4 && prefetch) fetch_next(t);
+        if (s == 4 && prefetch) load_tile(t + 1);
         if (s == 4) __builtin_amdgcn_sched_barrier(0);
       }
       acc = __builtin_amdgcn_mfma_f32_32x32x2f32(augr, qaug, acc, 0, 0, 0);
@@ -556,7 +524,7 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         // The next tile's global loads go out once the MFMA pipe is busy, so no wait for them
         // lands in front of this tile's first MFMAs.
-        if (s == 4 && prefetch) fetch_next(t);
+        if (s == 4 && prefetch) load_tile(t + 1);
         if (s == 4) __builtin_amdgcn_sched_barrier(0);
       }
       acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(aug0, qaug, acc0, 0, 0, 0);
@@ -1142,7 +1110,8 @@ constexpr int kKc = 32;              // dims per chunk
 constexpr int kKcStride = kKc + 4;   // LDS row stride of a row chunk (floats)
 constexpr int kKcQueueCap = 18;      // queue entries per lane (LDS holds both chunk buffers too)
 constexpr uint32_t kMaxChunkedDp = 4096;
-// Largest contiguous copy of listed rows the MFMA scan takes (above it the scan reads through the list).
+// Largest contiguous copy of listed rows for the MFMA scan; a filter admitting more rows goes to
+// the scan as its bitmap.
 constexpr uint64_t kCompactMaxBytes = 4ull << 30;
 
 template <int KL, bool L2, int MODE>
@@ -1193,12 +1162,10 @@ __global__ void __launch_bounds__(kThreads) flat_scan_k_kernel(ScanArgs a) {
     if (c == 0) {
       uint64_t gr = base + xrow;
       gr = gr < last_row ? gr : last_row;
-      if constexpr (MODE == 2) gr = a.idx[gr];
       xg = gr;
       if (L2 && tid < kTileRows) {
         uint64_t gn = base + tid;
         gn = gn < last_row ? gn : last_row;
-        if constexpr (MODE == 2) gn = a.idx[gn];
         sn = a.xnorm[gn];
       }
       if (FILTER && tid == kTileRows) sb = a.bitmap[base >> 6];
@@ -2443,9 +2410,6 @@ uint32_t padded_dim(uint32_t dim) {
   return (dim + 15u) / 16u * 16u;
 }
 
-/// Per-lane list length of the MFMA scan with the shared bound for top-k: the re-score selects the
-/// KL best by GEMM-form distance, and the certificate needs some of them beyond the k-th, so KL
-/// leaves a margin of max(5, k / 2). 0: k is above that (the wide merge without a shared bound).
 /// Per-lane list length of the MFMA scan for k, or 0 when k needs the wide merge. A margin of
 /// max(5, k/2) candidates past k lets the merge's re-score certify the selection when the GEMM-form
 /// distances differ from the exact ones in rounding.
@@ -2473,16 +2437,12 @@ void launch_scan_kl(bool l2, int mode, dim3 grid, const ScanArgs& a, hipStream_t
   if (l2) {
     if (mode == 1) {
       hipLaunchKernelGGL((flat_scan_kernel<DP, KL, true, 1>), grid, dim3(kThreads), 0, s, a);
-    } else if (mode == 2) {
-      hipLaunchKernelGGL((flat_scan_kernel<DP, KL, true, 2>), grid, dim3(kThreads), 0, s, a);
     } else {
       hipLaunchKernelGGL((flat_scan_kernel<DP, KL, true, 0>), grid, dim3(kThreads), 0, s, a);
     }
   } else {
     if (mode == 1) {
       hipLaunchKernelGGL((flat_scan_kernel<DP, KL, false, 1>), grid, dim3(kThreads), 0, s, a);
-    } else if (mode == 2) {
-      hipLaunchKernelGGL((flat_scan_kernel<DP, KL, false, 2>), grid, dim3(kThreads), 0, s, a);
     } else {
       hipLaunchKernelGGL((flat_scan_kernel<DP, KL, false, 0>), grid, dim3(kThreads), 0, s, a);
     }
@@ -2505,16 +2465,12 @@ void launch_scan_chunked_kl(bool l2, int mode, dim3 grid, const ScanArgs& a, hip
   if (l2) {
     if (mode == 1) {
       hipLaunchKernelGGL((flat_scan_k_kernel<KL, true, 1>), grid, dim3(kThreads), 0, s, a);
-    } else if (mode == 2) {
-      hipLaunchKernelGGL((flat_scan_k_kernel<KL, true, 2>), grid, dim3(kThreads), 0, s, a);
     } else {
       hipLaunchKernelGGL((flat_scan_k_kernel<KL, true, 0>), grid, dim3(kThreads), 0, s, a);
     }
   } else {
     if (mode == 1) {
       hipLaunchKernelGGL((flat_scan_k_kernel<KL, false, 1>), grid, dim3(kThreads), 0, s, a);
-    } else if (mode == 2) {
-      hipLaunchKernelGGL((flat_scan_k_kernel<KL, false, 2>), grid, dim3(kThreads), 0, s, a);
     } else {
       hipLaunchKernelGGL((flat_scan_k_kernel<KL, false, 0>), grid, dim3(kThreads), 0, s, a);
     }
@@ -2524,7 +2480,7 @@ void launch_scan_chunked_kl(bool l2, int mode, dim3 grid, const ScanArgs& a, hip
 /// The MFMA scan for padded width dp: register-resident queries up to kMaxDp, chunked above.
 void launch_scan(uint32_t dp, int kl, dim3 grid, const ScanArgs& a, hipStream_t s) {
   const bool l2 = a.l2 != 0;
-  const int filter = a.idx ? 2 : a.bitmap ? 1 : 0;
+  const int filter = a.bitmap ? 1 : 0;
   if (dp > static_cast<uint32_t>(kMaxDp)) {
     if (kl == 10) {
       launch_scan_chunked_kl<10>(l2, filter, grid, a, s);
@@ -2807,8 +2763,9 @@ FlatPlan plan_flat_search(const qvh_flat* f, uint64_t nq, uint32_t k, bool index
   p.fb = (nq + 2) * sizeof(uint32_t);  // count, listed queries, then the launch gate word
   // Listed rows are gathered once into a contiguous copy: the scan reads every row once per query
   // block, and through the list each of those reads would be a scattered gather (1.18M x 100
-  // cosine, 10% listed, 10,000 queries: 2.97 ms through the list).
-  if (indexed && n_idx > 0 && n_idx * f->dp * sizeof(float) <= kCompactMaxBytes) {
+  // cosine, 10% listed, 10,000 queries: 2.97 ms through the list, 2.86 ms on the copy).
+  if (indexed && n_idx > 0) {
+    QVH_REQUIRE(n_idx * f->dp * sizeof(float) <= kCompactMaxBytes, "flat search: too many listed rows");
     p.cx = n_idx * f->dp * sizeof(float);
     p.cn = f->metric == QVH_METRIC_L2 ? n_idx * sizeof(float) : 0;
   }
@@ -2979,11 +2936,11 @@ void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const
   a.qnorm = b.qn;
   a.nq = static_cast<uint32_t>(nq);
   a.bitmap = d_idx ? nullptr : d_bitmap;
-  a.idx = d_idx;
   a.l2 = f->metric == QVH_METRIC_L2;
-  if (d_idx && b.cx) {
-    // The listed rows in list order: positions stay what the list gives, so the merge and the
-    // fallback map them to rows through d_idx as before.
+  if (d_idx && n_idx > 0) {
+    // The listed rows in list order: the scan's positions are positions in the list, which the
+    // merge and the fallback map to rows through d_idx.
+    QVH_REQUIRE(b.cx != nullptr, "flat search: no workspace for the listed rows");
     const uint64_t chunks = n_idx * (f->dp / 4);
     const unsigned blocks = static_cast<unsigned>(
         std::min<uint64_t>(ceil_div(chunks, 256), static_cast<uint64_t>(device_cus(f->device)) * 16));
@@ -2992,7 +2949,6 @@ void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const
     QVH_HIP(hipGetLastError());
     a.X = b.cx;
     if (a.l2) a.xnorm = b.cn;
-    a.idx = nullptr;
   }
   a.nsplit = static_cast<uint32_t>(p.nsplit);
   a.qblocks = p.qblocks;
@@ -3261,7 +3217,8 @@ qvh_status qvh_flat_search(qvh_flat* f, const float* queries, uint64_t nq, uint3
         if (w + 1 == words && f->n % 64) bits &= (1ull << (f->n % 64)) - 1;
         admitted += static_cast<uint64_t>(__builtin_popcountll(bits));
       }
-      if (shared_list_length(k) != 0 && f->dp <= kMaxChunkedDp && 2 * admitted < f->n) {
+      if (shared_list_length(k) != 0 && f->dp <= kMaxChunkedDp && 2 * admitted < f->n &&
+          admitted * f->dp * sizeof(float) <= kCompactMaxBytes) {
         listed.reserve(admitted);
         for (size_t w = 0; w < words; ++w) {
           uint64_t bits = row_bitmap[w];
