@@ -110,6 +110,49 @@ __device__ __forceinline__ void list_insert(float (&Ld)[KL], uint32_t (&Lr)[KL],
   }
 }
 
+/// Inserts (d, r) into the sorted list (the caller has checked d <= Ld[KL - 1]) for a lane whose
+/// candidates come in increasing row order: a listed entry of equal distance then holds a smaller
+/// row and stays ahead, so the new entry goes before the first entry of larger distance or the
+/// first empty one (an empty entry, +inf and QVH_EMPTY_ROW, gives way to a row at +inf). Every
+/// compare reads the old list and every entry's new value depends on its own compare and its
+/// neighbour's, so the insertion is one parallel step rather than a chain through the list.
+template <int KL>
+__device__ __forceinline__ void list_insert_ordered(float (&Ld)[KL], uint32_t (&Lr)[KL], float d, uint32_t r) {
+  bool lt[KL];
+#pragma unroll
+  for (int x = 0; x < KL; ++x) lt[x] = (d < Ld[x]) | (Lr[x] == QVH_EMPTY_ROW);
+#pragma unroll
+  for (int x = KL - 1; x > 0; --x) {
+    Ld[x] = lt[x] ? (lt[x - 1] ? Ld[x - 1] : d) : Ld[x];
+    Lr[x] = lt[x] ? (lt[x - 1] ? Lr[x - 1] : r) : Lr[x];
+  }
+  Ld[0] = lt[0] ? d : Ld[0];
+  Lr[0] = lt[0] ? r : Lr[0];
+}
+
+/// Appends a lane's passing candidates of one 32x32 distance block to its queue (entry e at
+/// s_qd / s_qr[e * kThreads + tid], room for 16 left by the caller). Register r holds row
+/// row0 + 8*(r/4) + r%4; it passes when lane_ok, !(d > thr) (ties and NaN pass) and, with MASKED,
+/// bit 8*(r/4) + r%4 of lane_bits is set. An element that no lane of the wave passes costs a
+/// compare and a skipped branch.
+template <bool MASKED>
+__device__ __forceinline__ void queue_block(const f32x16& acc, float thr, bool lane_ok, uint32_t lane_bits,
+                                            uint32_t row0, int tid, int& qcount, float* s_qd, uint32_t* s_qr) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int bit = 8 * (r >> 2) + (r & 3);
+    bool p = lane_ok && !(acc[r] > thr);
+    if (MASKED) p = p && ((lane_bits >> bit) & 1u);
+    if (__builtin_amdgcn_ballot_w64(p)) {
+      if (p) {
+        s_qd[qcount * kThreads + tid] = acc[r];
+        s_qr[qcount * kThreads + tid] = row0 + static_cast<uint32_t>(bit);
+        ++qcount;
+      }
+    }
+  }
+}
+
 /// A scan lane's selection state: its list of the KL best (distance, row) among the rows it has
 /// seen, its candidate queue (CAP entries in LDS, entry-major: entry e of thread t at e * kThreads
 /// + t, so lanes appending at different depths never share a bank) and its prune threshold.
@@ -147,7 +190,7 @@ struct LaneScan {
       if (e < qcount) {
         float v = s_qd[e * kThreads + tid];
         v = v == v ? v : __builtin_huge_valf();
-        if (v <= Ld[KL - 1]) list_insert<KL>(Ld, Lr, v, s_qr[e * kThreads + tid]);
+        if (v <= Ld[KL - 1]) list_insert_ordered<KL>(Ld, Lr, v, s_qr[e * kThreads + tid]);
       }
     }
     qcount = 0;
@@ -194,18 +237,12 @@ struct LaneScan {
     // Lanes past the last query never queue: their zero query makes every inner-product
     // distance 1 exactly, a tie with their own list that would admit every row.
     any = any && qvalid;
-    if (__builtin_amdgcn_ballot_w64(qcount > CAP - 16)) flush(s_qd, s_qr);
-    if (any) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int bit = 8 * (r >> 2) + (r & 3);
-        bool p = !(acc[r] > thr);
-        if (masked) p = p && ((lane_bits >> bit) & 1u);
-        // Written whether or not it passes (no branch per element); a failing entry is
-        // overwritten by the next. The flush above leaves room for all 16.
-        s_qd[qcount * kThreads + tid] = acc[r];
-        s_qr[qcount * kThreads + tid] = row0 + static_cast<uint32_t>(bit);
-        qcount += p ? 1 : 0;
+    if (__builtin_amdgcn_ballot_w64(any)) {
+      if (__builtin_amdgcn_ballot_w64(qcount > CAP - 16)) flush(s_qd, s_qr);
+      if (masked) {
+        queue_block<true>(acc, thr, any, lane_bits, row0, tid, qcount, s_qd, s_qr);
+      } else {
+        queue_block<false>(acc, thr, any, lane_bits, row0, tid, qcount, s_qd, s_qr);
       }
     }
   }
@@ -381,7 +418,7 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
       if (e < qcount) {
         float v = s_qd[e * kThreads + tid];
         v = v == v ? v : __builtin_huge_valf();
-        if (v <= Ld[KL - 1]) list_insert<KL>(Ld, Lr, v, s_qr[e * kThreads + tid]);
+        if (v <= Ld[KL - 1]) list_insert_ordered<KL>(Ld, Lr, v, s_qr[e * kThreads + tid]);
       }
     }
     qcount = 0;
@@ -479,16 +516,13 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
         for (int r = 0; r < 16; ++r) any = any || (!(acc[r] > thr) && ((lane_bits >> (8 * (r >> 2) + (r & 3))) & 1u));
       }
       any = any && qvalid;
-      if (__builtin_amdgcn_ballot_w64(qcount > kQueueCap - 16)) flush_queue();
-      if (any) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int bit = 8 * (r >> 2) + (r & 3);
-          bool p = !(acc[r] > thr);
-          if (masked) p = p && ((lane_bits >> bit) & 1u);
-          s_qd[qcount * kThreads + tid] = acc[r];
-          s_qr[qcount * kThreads + tid] = static_cast<uint32_t>(tile_row0 + 32 * rb + 4 * h + bit);
-          qcount += p ? 1 : 0;
+      if (__builtin_amdgcn_ballot_w64(any)) {
+        if (__builtin_amdgcn_ballot_w64(qcount > kQueueCap - 16)) flush_queue();
+        const uint32_t row0 = static_cast<uint32_t>(tile_row0 + 32 * rb + 4 * h);
+        if (masked) {
+          queue_block<true>(acc, thr, any, lane_bits, row0, tid, qcount, s_qd, s_qr);
+        } else {
+          queue_block<false>(acc, thr, any, lane_bits, row0, tid, qcount, s_qd, s_qr);
         }
       }
     } else if (wave_active) {
@@ -564,18 +598,13 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
         // distance 1 exactly, a tie with their own list that would admit every row.
         any = any && qvalid;
         // Slow path: append this lane's passing, admitted candidates to its queue.
-        if (__builtin_amdgcn_ballot_w64(qcount > kQueueCap - 16)) flush_queue();
-        if (any) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int bit = 8 * (r >> 2) + (r & 3);
-            bool p = !(d[r] > thr);
-            if (masked) p = p && ((lane_bits >> bit) & 1u);
-            // Written whether or not it passes (no branch per element); a failing entry is
-            // overwritten by the next. The flush above leaves room for all 16.
-            s_qd[qcount * kThreads + tid] = d[r];
-            s_qr[qcount * kThreads + tid] = static_cast<uint32_t>(tile_row0 + 32 * blk + 4 * h + bit);
-            qcount += p ? 1 : 0;
+        if (__builtin_amdgcn_ballot_w64(any)) {
+          if (__builtin_amdgcn_ballot_w64(qcount > kQueueCap - 16)) flush_queue();
+          const uint32_t row0 = static_cast<uint32_t>(tile_row0 + 32 * blk + 4 * h);
+          if (masked) {
+            queue_block<true>(acc, thr, any, lane_bits, row0, tid, qcount, s_qd, s_qr);
+          } else {
+            queue_block<false>(acc, thr, any, lane_bits, row0, tid, qcount, s_qd, s_qr);
           }
         }
       }
