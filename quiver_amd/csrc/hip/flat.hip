@@ -82,6 +82,7 @@ constexpr int kShareEvery = 8;  // tiles between exchanges of the shared per-que
 // and up the bound slots (one per list source, at most 32), on the query's second 128-byte line.
 constexpr uint32_t kScanBoundStride = 64;
 constexpr uint32_t kScanSlotBase = 32;
+constexpr int kScanSlots = 32;
 // Splits per query up to which the register scan uses the bound slots: with more, the atomics of
 // its many lists on the query's slot line queue up (1M x 128, 128 queries on 256 splits: 0.39 ms
 // without the slots, 0.49 ms with them; 10,000 queries on 32 splits: 21.50 ms without, 21.23 ms with).
@@ -128,6 +129,50 @@ __device__ __forceinline__ void list_insert_ordered(float (&Ld)[KL], uint32_t (&
   }
   Ld[0] = lt[0] ? d : Ld[0];
   Lr[0] = lt[0] ? r : Lr[0];
+}
+
+/// Sorts 16 values ascending in registers (a bitonic network of 80 compare-exchanges).
+__device__ __forceinline__ void sort16_u32(uint32_t (&v)[16]) {
+#pragma unroll
+  for (int size = 2; size <= 16; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int l = i ^ stride;
+        if (l > i) {
+          const uint32_t lo = min(v[i], v[l]), hi = max(v[i], v[l]);
+          const bool up = (i & size) == 0;
+          v[i] = up ? lo : hi;
+          v[l] = up ? hi : lo;
+        }
+      }
+    }
+  }
+}
+
+/// The K-th smallest of the 32 values held 16 by this lane and 16 by its partner (lane ^ 32),
+/// the same in both lanes. K = 32 is the maximum; below it both halves are sorted and the K-th
+/// smallest of the union is min over i of max(S[i - 1], P[K - 1 - i]) (i values from this lane's
+/// sorted S, the rest from the partner's P).
+template <int K>
+__device__ __forceinline__ uint32_t pair_kth_smallest(uint32_t (&v)[16]) {
+  static_assert(K >= 1 && (K <= 16 || K == 32), "K-th of 32");
+  if constexpr (K == 32) {
+    uint32_t m = v[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) m = max(m, v[i]);
+    return max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), 32, 64)));
+  } else {
+    sort16_u32(v);
+    uint32_t p[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) p[i] = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v[i]), 32, 64));
+    uint32_t r = min(v[K - 1], p[K - 1]);
+#pragma unroll
+    for (int i = 1; i < K; ++i) r = min(r, max(v[i - 1], p[K - 1 - i]));
+    return r;
+  }
 }
 
 /// Appends a lane's passing candidates of one 32x32 distance block to its queue (entry e at
@@ -367,14 +412,14 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
   uint32_t* const qw = a.qthr + static_cast<size_t>(qvalid ? q : 0u) * kScanBoundStride;
   float pthr = qvalid ? ordered_to_float(qw[0]) : __builtin_huge_valf();
   // Bound slots: every list of the query (one per split, row half rb and lane half h) publishes
-  // its best distance, atomic min, to slot src of NS = KL. A slot holds one row's distance at any
-  // time, and different lists hold different rows, so once every slot is written the largest slot
-  // is at or above the query's NS-th best distance; unwritten slots hold +inf. Slots read stale
-  // are larger, still bounds. With many splits running at once this bound falls long before any
-  // one list holds KL good rows.
-  constexpr int NS = KL;
-  static_assert(NS % 2 == 0 && kScanSlotBase + NS <= kScanBoundStride, "a query's slots fit its words");
-  const uint32_t src = (split * (RS ? 4u : 2u) + static_cast<uint32_t>(rb) * 2u + static_cast<uint32_t>(h)) % NS;
+  // its best distance, atomic min, to slot src of kScanSlots. A slot holds one row's distance at
+  // any time, and different slots come from different lists, which hold different rows, so the
+  // KL-th smallest slot value is at or above the query's KL-th best distance (KL distinct rows lie
+  // at or below it); unwritten slots hold +inf. Slots read stale are larger, still bounds. With
+  // many splits running at once this bound falls long before any one list holds KL good rows.
+  static_assert(KL <= kScanSlots && kScanSlotBase + kScanSlots <= kScanBoundStride, "a query's slots fit its words");
+  const uint32_t src =
+      (split * (RS ? 4u : 2u) + static_cast<uint32_t>(rb) * 2u + static_cast<uint32_t>(h)) % kScanSlots;
   float published = __builtin_huge_valf();
   auto share_threshold = [&]() {
     // The two lanes of a query hold disjoint rows: their union has KL candidates at or below
@@ -392,14 +437,18 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
           __hip_atomic_fetch_min(qw + kScanSlotBase + src, float_to_ordered(published), __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_AGENT);
         }
-        // Each lane half reads half of the slots; the pair's maximum is over all NS.
-        m = 0;
+        // Each lane half reads half of the slots (ordered bits compare as the distances do) and
+        // sorts them; the pair then takes the KL-th smallest of all kScanSlots.
+        constexpr int kHalf = kScanSlots / 2;
+        uint32_t sv[kHalf];
+        uint64_t* sw = reinterpret_cast<uint64_t*>(qw + kScanSlotBase + h * kHalf);
 #pragma unroll
-        for (int i = 0; i < NS / 2; ++i) {
-          m = max(m, __hip_atomic_load(qw + kScanSlotBase + h * (NS / 2) + i, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT));
+        for (int i = 0; i < kHalf / 2; ++i) {
+          const uint64_t w = __hip_atomic_load(sw + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          sv[2 * i] = static_cast<uint32_t>(w);
+          sv[2 * i + 1] = static_cast<uint32_t>(w >> 32);
         }
-        m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), 32, 64)));
+        m = pair_kth_smallest<KL>(sv);
       }
       g = __shfl(g, j, 64);
       t = fminf(t, fminf(ordered_to_float(g), ordered_to_float(m)));
