@@ -510,9 +510,14 @@ def bench_ivfpq_cosine_refine(args, hip: Hip, qvh: Qvh):
         elapsed = time.perf_counter() - t0
         st = np.array(steps)
         scan_ms = float(st[:, 1].mean())
+        # The re-ranking reads each query's k * refine_factor candidates' stored vectors (dim fp32
+        # each) beside the codes: algorithmic bytes of the same scan stage.
+        refine_bytes = nq * k * 8 * dim * 4
         out[str(nprobe)] = {"qps": nq * 5 / elapsed, "select_ms": float(st[:, 0].mean()), "scan_ms": scan_ms,
-                            "code_bytes": nb.value,
-                            "scan_hbm_frac": nb.value / (scan_ms * 1e-3) / (HBM_PEAK_GBS * 1e9)}
+                            "code_bytes": nb.value, "refine_bytes": refine_bytes,
+                            "scan_hbm_frac": nb.value / (scan_ms * 1e-3) / (HBM_PEAK_GBS * 1e9),
+                            "scan_hbm_frac_with_refine":
+                                (nb.value + refine_bytes) / (scan_ms * 1e-3) / (HBM_PEAK_GBS * 1e9)}
     for ptr in (d_q, d_refs, d_dist):
         hip.lib.hipFree(ptr)
     return {"config": {"workload": "IVF-PQ cosine k=10 refine_factor 8: 1,183,514 x 100 unit-norm mixture, "

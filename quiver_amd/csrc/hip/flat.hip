@@ -77,7 +77,7 @@ __device__ __forceinline__ bool gate_closed(const uint32_t* gate, uint32_t want)
   return gate != nullptr && ((*gate != 0u) != (want != 0u));
 }
 
-constexpr int kShareEvery = 8;  // tiles between exchanges of the shared per-query threshold
+constexpr int kShareEvery = 8;  // chunked scan: tiles between exchanges of the shared per-query bound
 // The MFMA scan's words per query in ScanArgs::qthr: word 0 the union bound, words kScanSlotBase
 // and up the bound slots (one per list source, at most 32), on the query's second 128-byte line.
 constexpr uint32_t kScanBoundStride = 64;
@@ -88,11 +88,13 @@ constexpr int kScanSlots = 32;
 // without the slots, 0.49 ms with them; 10,000 queries on 32 splits: 21.50 ms without, 21.23 ms with).
 constexpr uint64_t kScanSlotMaxSplits = 64;
 
-/// Tiles after which the register scan exchanges bounds: 0, 1 and 3 (the lists' first rows move a
-/// bound the most, and a split of a few tiles would otherwise never take the shared one), then
-/// every kShareEvery.
+/// Tiles after which the register scan exchanges bounds: 0, 1, 3, 7, 15, 31 and 63 (the lists' first
+/// rows move a bound the most, and a split of a few tiles would otherwise never take the shared
+/// one), then every 64. An exchange stalls the wave for a device-scope round trip, and late in a
+/// split the bounds move little (1M x 128, 10,000 queries: every 8 tiles 21.07 ms, every 16 20.58,
+/// every 32 20.30, this schedule 20.22, every 128 after 127 20.21).
 __device__ __forceinline__ bool scan_share_after(uint32_t t) {
-  return t == 0 || t == 1 || t == 3 || t % kShareEvery == kShareEvery - 1;
+  return t < 64 ? (t & (t + 1)) == 0 : t % 64 == 63;
 }
 constexpr int kQueueCap = 20;   // queued candidates per lane before a wave-wide flush
 
