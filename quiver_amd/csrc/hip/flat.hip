@@ -83,9 +83,12 @@ constexpr int kShareEvery = 8;  // chunked scan: tiles between exchanges of the 
 constexpr uint32_t kScanBoundStride = 64;
 constexpr uint32_t kScanSlotBase = 32;
 constexpr int kScanSlots = 32;
-// Splits per query up to which the register scan uses the bound slots: with more, the atomics of
-// its many lists on the query's slot line queue up (1M x 128, 128 queries on 256 splits: 0.39 ms
-// without the slots, 0.49 ms with them; 10,000 queries on 32 splits: 21.50 ms without, 21.23 ms with).
+// Splits per query up to which the row-split form of the register scan (four lists per split and
+// query) uses the bound slots: with more, the atomics of its many lists on the query's slot line
+// queue up (1M x 128, 128 queries on 256 splits: 0.39 ms without the slots, 0.49 ms with them). The
+// register scan's full-block form (two lists per split and query) uses them at any split count
+// (10,000 queries on 32 splits: 21.50 ms without, 21.23 ms with; 512 queries on 256 splits 1.33 ->
+// 1.23 ms, 1,024 on 256 2.46 -> 2.30 ms, 2,048 on 128 4.71 -> 4.26 ms).
 constexpr uint64_t kScanSlotMaxSplits = 64;
 
 /// Tiles after which the register scan exchanges bounds: 0, 1, 3, 7, 15, 31 and 63 (the lists' first
@@ -2813,18 +2816,35 @@ FlatPlan plan_flat_search(const qvh_flat* f, uint64_t nq, uint32_t k, bool index
     p.nsplit = ceil_div(p.scan_rows, p.rows_per_split);
   } else {
     const uint64_t tiles = std::max<uint64_t>(1, ceil_div(p.scan_rows, kTileRows));
-    // One workgroup per CU at a time: pick the split count (a multiple of 8 for the XCD mapping)
-    // whose workgroup count best fills whole rounds of the CUs; fewer splits on ties. A split keeps
-    // at least four tiles: with fewer rows per split the per-split top-k lists take in most rows
-    // (1.18M x 100 cosine with 0.5% of the ids allowed: 32 splits 0.47 ms, 16 splits 0.37 ms).
+    // One workgroup per CU at a time: the split count (1 to 7, or a multiple of 8 for the XCD
+    // mapping) is the smallest whose workgroups fill whole rounds of the CUs to 97%: longer splits
+    // start fewer lists and exchange bounds with fewer others. 1M x 128, scan at k = 10 (the earlier
+    // choice, which preferred four rounds, without bound slots above 64 splits -> this one): 512
+    // queries 256 -> 128 splits 1.33 -> 1.18 ms, 1,024 queries 256 -> 64 splits 2.46 -> 2.14 ms,
+    // 2,048 queries 128 -> 32 splits 4.71 -> 4.12 ms, 8,192 queries 32 -> 8 splits 16.04 -> 15.97 ms;
+    // 10,000 queries keep 32 (24 splits: 21.27 ms, 32: 20.22, 40: 22.35). When no count fills 97%
+    // of its rounds, the best fill weighted by parallelism (at least four rounds when the rows
+    // allow) decides, fewer splits on ties. A split keeps at least four tiles: with fewer
+    // rows per split the per-split top-k lists take in most rows (1.18M x 100 cosine with 0.5% of
+    // the ids allowed: 32 splits 0.47 ms, 16 splits 0.37 ms).
     {
       const uint64_t cap = std::max<uint64_t>(1, std::min<uint64_t>(tiles / 4, kMaxSplits));
       double best = -1.0;
-      for (uint64_t c = 1; c <= cap; c = c < 8 ? c + 1 : c + 8) {
+      bool full = false;
+      for (uint64_t c = 1; c <= cap && !full; c = c < 8 ? c + 1 : c + 8) {
         if (c >= 8 && c % 8) continue;
         const uint64_t total = p.qblocks * c;
         const uint64_t rounds = ceil_div(total, static_cast<uint64_t>(cus));
-        // prefer enough parallelism (>= 4 rounds when the rows allow) and full rounds
+        const double fill = static_cast<double>(total) / static_cast<double>(rounds * cus);
+        if (fill >= 0.97) {
+          p.nsplit = c;
+          full = true;
+        }
+      }
+      for (uint64_t c = 1; c <= cap && !full; c = c < 8 ? c + 1 : c + 8) {
+        if (c >= 8 && c % 8) continue;
+        const uint64_t total = p.qblocks * c;
+        const uint64_t rounds = ceil_div(total, static_cast<uint64_t>(cus));
         const double fill = static_cast<double>(total) / static_cast<double>(rounds * cus);
         const double par = std::min(1.0, static_cast<double>(total) / (4.0 * cus));
         const double score = fill * par;
@@ -3041,7 +3061,7 @@ void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const
   // One query block of at most 128 queries, unfiltered, register-resident queries: the row-split
   // form of the scan (two waves per 32-query group).
   a.rowsplit = nq <= static_cast<uint64_t>(kQueriesPerBlock / 2) && !d_idx && !d_bitmap && f->dp <= kMaxDp ? 1 : 0;
-  a.bound_slots = p.nsplit <= kScanSlotMaxSplits ? 1 : 0;
+  a.bound_slots = !a.rowsplit || p.nsplit <= kScanSlotMaxSplits ? 1 : 0;
   const dim3 sgrid(static_cast<unsigned>(p.qblocks * p.nsplit));
   auto scan = [&](int kl) {
     if (p.ring) {

@@ -271,6 +271,21 @@ def test_small_batches_on_256_row_splits(oracle, metric, nq):
     print(_check(oracle, ib, iq, 10, metric))
 
 
+@pytest.mark.parametrize("metric", ["l2", "cosine"])
+@pytest.mark.parametrize("nq", [384, 768, 1280, 1792])
+def test_mid_batches_whole_round_splits(oracle, metric, nq):
+    """Batches of 2, 3, 5 and 7 query blocks take the smallest row-split count whose work-groups
+    fill whole rounds of the CUs (on 256 CUs: 128, 168, 152 and 72 splits of 300,000 rows, none a
+    power of two but the first), with the bound slots shared by every list of a query. Integer data
+    adds exact ties across splits."""
+    base = D.gaussian(300_000, 128, seed=37)
+    q = D.gaussian(nq, 128, seed=38)
+    print(_check(oracle, base, q, 10, metric))
+    if metric == "l2":
+        ib, iq = D.int_mix(300_000, nq)
+        print(_check(oracle, ib, iq, 10, metric))
+
+
 @pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
 @pytest.mark.parametrize("dim,nq,k,n", [(128, 5, 10, 1_000_003), (128, 32, 10, 300_000), (128, 31, 1, 70_001),
                                         (96, 17, 21, 65_632), (64, 8, 11, 4_200), (32, 5, 16, 100),
