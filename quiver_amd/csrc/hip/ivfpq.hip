@@ -1895,12 +1895,13 @@ __global__ void __launch_bounds__(kScanThreads) ivf_scan_kernel(ScanArgs a) {
 #endif
 // Default waves per streaming block: 4 with 128- or 192-entry wave queues (four blocks of ~37 KB
 // LDS per CU, 128 registers per lane), 8 with 256-entry queues (three blocks of ~49 KB per CU, 80
-// registers) or with 512-entry queues for candidate sets of 129..256 (two blocks of ~66 KB per
-// CU). The host also runs 256-entry queues on 4 waves (inner product and cosine).
+// registers), with 512-entry queues for candidate sets of 129..256 (two blocks of ~66 KB per CU)
+// or with 1024-entry queues for 257..512 (one block of ~98 KB per CU, codes of up to 32 bytes).
+// The host also runs 256-entry queues on 4 waves (inner product and cosine).
 template <int CAP>
 constexpr int stream_waves() { return CAP <= 192 ? 4 : 8; }
 constexpr uint32_t kStreamMaxProbes = 256;
-constexpr uint32_t kStreamMaxSel = 256;
+constexpr uint32_t kStreamMaxSel = 512;
 constexpr uint32_t kStreamMaxM = 64;  // code bytes of the widest streaming kernel
 // Slices per query of a batch smaller than one resident generation of blocks.
 constexpr uint64_t kMaxSlices = 16;
@@ -2532,7 +2533,7 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
     if (static_cast<uint32_t>(lane) < a.k) emit(lane, static_cast<uint32_t>(lane) < min(cnt_f, a.k), key);
     return;
   }
-  // Queues of 256 or 512 entries (keep_sel <= CAP / 2): each wave sorts its list (<= CAP / 2
+  // Queues of 256, 512 or 1024 entries (keep_sel <= CAP / 2): each wave sorts its list (<= CAP / 2
   // keys, NK per lane) in registers; log2(waves) rounds of pairwise merges then keep the CAP / 2
   // smallest: the elementwise minimum of one sorted list and the other reversed holds the CAP / 2
   // smallest of both as a bitonic sequence, which a register bitonic merge orders. Wave 0's region
@@ -2571,12 +2572,20 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
   }
   uint32_t cnt_f = min(merged, keep_sel);
   bool certified = true;
-  // Sorts s_queue[0, count) (count <= 256) ascending in wave 0's registers (no block barriers inside
-  // the sort); slots past count read as empty. The block waits before and after.
+  // Sorts s_queue[0, count) (count <= CAP / 2, at most 512) ascending in wave 0's registers (no
+  // block barriers inside the sort); slots past count read as empty. The block waits before and
+  // after.
   auto sort_front = [&](uint32_t count) {
     __syncthreads();
     if (wave == 0) {
-      if (count <= 128) {
+      if (CAP >= 1024 && count > 256) {
+        uint64_t t[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) t[i] = static_cast<uint32_t>(i * 64 + lane) < count ? s_queue[i * 64 + lane] : ~0ull;
+        wave_sort<8>(t);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s_queue[i * 64 + lane] = t[i];
+      } else if (count <= 128) {
         uint64_t t[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i) t[i] = static_cast<uint32_t>(i * 64 + lane) < count ? s_queue[i * 64 + lane] : ~0ull;
@@ -2710,7 +2719,7 @@ __device__ __forceinline__ void stream_scan(const ScanArgs& a) {
 // either for 256).
 template <int MPW, bool FULL, int CAP, bool ROT = false, int W = stream_waves<CAP>()>
 __global__ void __launch_bounds__(W * 64)
-__attribute__((amdgpu_waves_per_eu(W == 4 || CAP == 512 ? 4 : 6))) ivf_stream_kernel(ScanArgs a) {
+__attribute__((amdgpu_waves_per_eu(W == 4 || CAP == 512 ? 4 : CAP >= 1024 ? 2 : 6))) ivf_stream_kernel(ScanArgs a) {
   stream_scan<MPW, FULL, CAP, ROT, W>(a);
 }
 
@@ -3199,11 +3208,15 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   const bool full = h->mp == 4 * mpw_t;
   const bool small_sel = a.keep_sel <= 64 && k <= 64;
   const bool big_sel = !small_sel && (a.keep_sel > 128 || k > 128);  // 512-entry wave queues
+  // 1024-entry wave queues for 257..512 candidates (codes of up to 32 bytes; wider codes take the
+  // block-buffer scan). 1M x 128 L2, nprobe 32, 10k queries, k = 200 (300 candidates): 8.80 ms on
+  // the block-buffer scan.
+  const bool huge_sel = a.keep_sel > 256 || k > 256;
   // Four-wave blocks take 192-entry queues past 48 candidates, so that at least 64 candidates
   // arrive between two cuts of a queue (1M x 128, nprobe 16: 60 candidates 0.97 -> 0.84 ms; at 36-40
   // candidates the 128-entry queues measured 1-2% faster).
   const bool mid_sel = small_sel && a.keep_sel > 48;
-  const uint32_t cap = small_sel ? (mid_sel ? 192 : 128) : big_sel ? 512 : 256;
+  const uint32_t cap = small_sel ? (mid_sel ? 192 : 128) : huge_sel ? 1024 : big_sel ? 512 : 256;
   // 256-entry queues run on four waves, except for L2 with the precomputed table, whose block
   // re-scores its selection: 1.18M x 100 cosine, refine 8 (80 candidates), nprobe 16 0.69 ->
   // 0.66 ms and nprobe 64 1.86 -> 1.81 ms on four waves; 1M x 128 L2, k = 50 (75 candidates),
@@ -3218,7 +3231,7 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
                            (4 * static_cast<size_t>(nprobe) + 2 + waves) * sizeof(uint32_t);
   const size_t lds2 = mpw_t > 8 ? lds_total : lds_total - lds_table;
   if (!exact_all && mode != kModeResidual && h->mp <= kStreamMaxM && nprobe <= kStreamMaxProbes && a.keep_sel >= 1 &&
-      a.keep_sel <= kStreamMaxSel && k <= kStreamMaxSel && lds_total <= 150 * 1024) {
+      a.keep_sel <= kStreamMaxSel && k <= kStreamMaxSel && !(huge_sel && mpw_t > 8) && lds_total <= 150 * 1024) {
     a.order = order;
     auto launch2 = [&](auto kernel) {
       const void* fn = reinterpret_cast<const void*>(kernel);
@@ -3255,7 +3268,8 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   (small_sel ? (mid_sel ? launch2(KERNEL<__VA_ARGS__, 192>) : launch2(KERNEL<__VA_ARGS__, 128>))          \
    : big_sel ? launch2(KERNEL<__VA_ARGS__, 512>)                                                          \
    : four256 ? launch2(KERNEL<__VA_ARGS__, 256, false, 4>) : launch2(KERNEL<__VA_ARGS__, 256>))
-#define QVH_STREAM(MPW_) QVH_STREAM_CAP(ivf_stream_kernel, MPW_, true)
+#define QVH_STREAM(MPW_)                                                                                  \
+  (huge_sel ? launch2(ivf_stream_kernel<MPW_, true, 1024>) : QVH_STREAM_CAP(ivf_stream_kernel, MPW_, true))
     // Bank-rotated lookups: L2 with the precomputed table (re-scored exactly afterwards), four
     // dims per sub-space, 16- or 32-byte codes.
     const bool rot =

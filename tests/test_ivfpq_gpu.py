@@ -171,6 +171,19 @@ def test_ivfpq_large_candidate_sets(oracle, metric, k, refine):
         print(k, refine, qs.shape[0], compare_search(oracle, idx, st, qs, k, 16, refine))
 
 
+@pytest.mark.parametrize("metric,k,refine", [("l2", 200, 0), ("l2", 341, 0), ("ip", 300, 0), ("ip", 512, 0),
+                                             ("cosine", 400, 0), ("l2", 30, 10), ("cosine", 50, 8), ("ip", 257, 0)])
+def test_ivfpq_1024_entry_queues(oracle, metric, k, refine):
+    """Candidate sets of 257..512 (L2 k = 341: 341 + 170 = 511 with the re-score margin; k = 30 with
+    refine 10: 450) stream through 1024-entry wave queues on eight-wave blocks: the same results as
+    the oracle, for a batch of whole queries and a sliced small batch."""
+    base = clustered(12_000, 32, 24, seed=45)
+    q = clustered(700, 32, 24, seed=46)
+    idx, st = build_pair(oracle, base, metric, 64, 8, refine > 0)
+    for qs in (q, q[:3]):
+        print(k, refine, qs.shape[0], compare_search(oracle, idx, st, qs, k, 16, refine))
+
+
 @pytest.mark.parametrize("metric,k,refine", [("ip", 65, 0), ("ip", 100, 0), ("cosine", 128, 0), ("cosine", 12, 8),
                                              ("l2", 50, 0)])
 def test_ivfpq_256_entry_queues(oracle, metric, k, refine):
