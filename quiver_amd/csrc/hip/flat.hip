@@ -3310,15 +3310,22 @@ qvh_status qvh_flat_search(qvh_flat* f, const float* queries, uint64_t nq, uint3
     std::vector<uint32_t> listed;
     if (row_bitmap) {
       const size_t words = ceil_div(std::max<uint64_t>(f->n, 1), 64);
-      // Few admitted rows: hand the MFMA scan the list of them, so its work follows their count.
+      // The admitted rows, counted.
       uint64_t admitted = 0;
       for (size_t w = 0; w < words; ++w) {
         uint64_t bits = row_bitmap[w];
         if (w + 1 == words && f->n % 64) bits &= (1ull << (f->n % 64)) - 1;
         admitted += static_cast<uint64_t>(__builtin_popcountll(bits));
       }
-      if (shared_list_length(k) != 0 && f->dp <= kMaxChunkedDp && 2 * admitted < f->n &&
-          admitted * f->dp * sizeof(float) <= kCompactMaxBytes) {
+      // A filter that admits every row is no filter. Any other goes to the MFMA scan as the list of
+      // its rows while their contiguous copy fits: the scan then reads only admitted rows, where
+      // the bitmap form reads every row and tests it (1.18M x 100 cosine, 10,000 queries: 55% of
+      // the rows admitted 23.8 ms as a bitmap, 90% 23.8 ms, none filtered 21.0 ms; listed rows
+      // run in proportion to their count, 45% in 10.3 ms).
+      if (admitted == f->n) {
+        row_bitmap = nullptr;
+      } else if (shared_list_length(k) != 0 && f->dp <= kMaxChunkedDp &&
+                 admitted * f->dp * sizeof(float) <= kCompactMaxBytes) {
         listed.reserve(admitted);
         for (size_t w = 0; w < words; ++w) {
           uint64_t bits = row_bitmap[w];

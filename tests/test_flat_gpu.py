@@ -25,6 +25,18 @@ def _true_dist(oracle, stored, queries, metric):
     return f
 
 
+def _bitmap_form_matches_listed_rows(idx, queries, k, allowed):
+    """The same filtered search through device buffers (the filter as a device bitmap tested in the
+    scan) and through host buffers (the admitted rows listed and copied): identical rows and
+    bit-identical distances."""
+    import torch
+
+    hl, hd = idx.search(queries, k, filter=allowed)
+    dl, dd = idx.search(torch.from_numpy(np.ascontiguousarray(queries)).to("cuda:0"), k, filter=allowed)
+    assert np.array_equal(dl.cpu().numpy(), hl)
+    assert np.array_equal(dd.cpu().numpy().view(np.uint32), hd.view(np.uint32))
+
+
 def _check(oracle, base, queries, k, metric, allowed=None, labels=None):
     print(f"case: n={base.shape[0]} dim={base.shape[1]} nq={queries.shape[0]} k={k} "
           f"metric={metric} filtered={allowed is not None}", flush=True)
@@ -87,16 +99,21 @@ def test_integer_stores_short_lists(oracle, metric, k):
     for n_allowed in (4_000, 24_000):
         allowed = np.sort(rng.choice(40_000, n_allowed, replace=False)).astype(np.uint64)
         print(_check(oracle, base, q_int, k, metric, allowed))
+        _bitmap_form_matches_listed_rows(idx, q_int, k, allowed)
 
 
-@pytest.mark.parametrize("fraction", [0.005, 0.3, 0.49, 0.7])
+@pytest.mark.parametrize("fraction", [0.005, 0.3, 0.49, 0.7, 0.97, 1.0])
 @pytest.mark.parametrize("metric", ["l2", "cosine"])
 def test_filter_densities(oracle, fraction, metric):
-    """Below half the rows admitted the scan runs over the list of admitted rows; above, over all
-    rows with the bitmap tested per tile. Both give the oracle's answer."""
+    """Through host buffers a filter runs over the list of admitted rows at any density (a filter
+    admitting every row runs as no filter); with device buffers over all rows with the bitmap tested
+    per tile. Both give the oracle's answer."""
     base, q = D.unit_mix(30_000, 50)
     allowed = D.allowed_ids(base.shape[0], fraction, seed=17)
     print(_check(oracle, base, q, 10, metric, allowed))
+    idx = quiver.FlatIndex(base.shape[1], metric)
+    idx.add(base)
+    _bitmap_form_matches_listed_rows(idx, q, 10, allowed)
 
 
 def test_cosine_rows_are_normalized_like_the_reference(oracle):
@@ -319,12 +336,16 @@ def test_ring_scan_integer_store(oracle, metric):
 @pytest.mark.parametrize("fraction", [0.6, 0.95])
 def test_small_batches_split_rows_filtered_and_ties(oracle, fraction, metric):
     """Integer data (many exactly equal distances across splits) with a row filter above half
-    density (the bitmap is tested per row)."""
+    density: the listed rows through host buffers, the bitmap tested per row with device buffers."""
     base, q = D.int_mix(300_000, 12)
     allowed = D.allowed_ids(base.shape[0], fraction, seed=41)
     print(_check(oracle, base, q[:4], 10, metric, allowed))
     print(_check(oracle, base, q, 10, metric, allowed))
     print(_check(oracle, base, q[:1], 50, metric))
+    idx = quiver.FlatIndex(base.shape[1], metric)
+    idx.add(base)
+    for qs in (q[:4], q):
+        _bitmap_form_matches_listed_rows(idx, qs, 10, allowed)
 
 
 def test_integer_data_exact_ties(oracle):
