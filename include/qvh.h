@@ -98,8 +98,9 @@ uint64_t qvh_flat_size(const qvh_flat* flat);
 
 /* The scan of FlatIndex::search_batch (src/flat_index.cc:84-106) for nq raw queries (normalized
  * here for cosine, as search_one does at :74-78). `row_bitmap` (nullable, ceil(size/64) words,
- * bit r of word r/64 set = row r admitted) is the Filter materialized over rows (:85); when it
- * admits fewer than half of the rows, the scan runs over the list of admitted rows only.
+ * bit r of word r/64 set = row r admitted) is the Filter materialized over rows (:85): unless it
+ * admits every row (then it is no filter), the scan runs over the list of admitted rows only, while
+ * their contiguous copy stays within 4 GiB (else it tests the bitmap over every row).
  * Outputs: nq*k rows (QVH_EMPTY_ROW when fewer than k rows are admitted) and distances (+inf). */
 qvh_status qvh_flat_search(qvh_flat* flat, const float* queries, uint64_t nq, uint32_t k,
                            const uint64_t* row_bitmap, uint32_t* out_rows, float* out_dist);
@@ -113,10 +114,23 @@ qvh_status qvh_flat_search_rows(qvh_flat* flat, const float* queries, uint64_t n
                                 const uint32_t* rows, uint64_t nrows, uint32_t* out_rows,
                                 float* out_dist);
 
-/* Same, on device-resident buffers, enqueued on `stream` (a hipStream_t; NULL = the handle's). */
+/* Same, on device-resident buffers, enqueued on `stream` (a hipStream_t; NULL = the handle's).
+ * The device bitmap is tested per tile over every row. */
 qvh_status qvh_flat_search_device(qvh_flat* flat, const float* d_queries, uint64_t nq,
                                   uint32_t k, const uint64_t* d_row_bitmap, uint32_t* d_out_rows,
                                   float* d_out_dist, void* stream);
+
+/* qvh_flat_search_device with the admitted rows given as a device list instead of a bitmap: no
+ * counterpart in the reference (its search takes the Filter on the host, src/flat_index.cc:85);
+ * for device-resident callers, whose filter the host turns into rows once. `d_row_list` holds
+ * `nrows` rows in ascending order, without repeats, each below the stored row count (at most that
+ * count, else QVH_EINVAL; rows past the last stored one are read as the last). The scan reads only
+ * the listed rows, as qvh_flat_search does with a host filter; all stored rows listed is no filter.
+ * Where the listed-row scan does not apply (its copy above 4 GiB, or a k it does not serve) the list
+ * becomes a device bitmap first. Enqueued on `stream` (NULL = the handle's). */
+qvh_status qvh_flat_search_device_rows(qvh_flat* flat, const float* d_queries, uint64_t nq,
+                                       uint32_t k, const uint32_t* d_row_list, uint64_t nrows,
+                                       uint32_t* d_out_rows, float* d_out_dist, void* stream);
 
 /* qvh_flat_search_device without any allocation: no counterpart in the reference; for callers that
  * cannot allocate device memory during a search (code under HIP graph capture, tight serving loops,

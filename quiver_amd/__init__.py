@@ -135,6 +135,16 @@ def _device_bitmap(bits: np.ndarray, device):
     return torch.from_numpy(np.ascontiguousarray(bits).view(np.int64)).to(device)
 
 
+def _device_rows(bits: np.ndarray, n: int, device):
+    """The rows among the first n that a row bitmap admits (bit r % 64 of word r // 64), ascending,
+    as an int32 tensor on `device` holding the rows' uint32 bits (empty when none is admitted)."""
+    import torch
+
+    flags = np.unpackbits(np.ascontiguousarray(bits).view(np.uint8), bitorder="little")[:n]
+    rows = np.flatnonzero(flags).astype(np.uint32)
+    return torch.from_numpy(rows.view(np.int32)).to(device)
+
+
 _MAX_LABEL = 2**63 - 1  # labels come back as int64, and -1 marks an empty slot
 
 
@@ -336,13 +346,18 @@ class FlatIndex:
         n = len(self)
         if q.shape[0] == 0 or n == 0:
             return labels, dist
-        bitmap = None
-        if filter is not None:
-            bitmap = _device_bitmap(self._index._row_bitmap(_as_labels(filter)), q.device)
         rows = torch.empty((q.shape[0], k), dtype=torch.int32, device=q.device)
-        _on_torch_stream(q.device, (q, bitmap, rows, dist), lambda stream: self._index._search_device(
-            q.data_ptr(), q.shape[0], k, 0 if bitmap is None else bitmap.data_ptr(), rows.data_ptr(), dist.data_ptr(),
-            stream))
+        listed = None
+        if filter is not None:
+            # The admitted rows, ascending, as a device list: the scan then reads only those rows.
+            listed = _device_rows(self._index._row_bitmap(_as_labels(filter)), n, q.device)
+        if listed is None:
+            _on_torch_stream(q.device, (q, rows, dist), lambda stream: self._index._search_device(
+                q.data_ptr(), q.shape[0], k, 0, rows.data_ptr(), dist.data_ptr(), stream))
+        else:
+            _on_torch_stream(q.device, (q, listed, rows, dist), lambda stream: self._index._search_device_rows(
+                q.data_ptr(), q.shape[0], k, listed.data_ptr(), listed.numel(), rows.data_ptr(), dist.data_ptr(),
+                stream))
         table = self._label_table(q.device, n)
         return torch.where(rows != -1, table[rows.clamp(0, n - 1).long()], labels), dist
 

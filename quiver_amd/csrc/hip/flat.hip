@@ -3159,6 +3159,37 @@ void flat_search_impl(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t
   flat_search_run(f, p, handle_buffers(f, p), d_queries, nq, k, d_bitmap, d_rows, d_dist, s, d_idx, n_idx);
 }
 
+/// True when a filter of `admitted` rows can run as listed rows: the MFMA scan serves k, and the
+/// rows' contiguous copy fits kCompactMaxBytes.
+bool listed_scan_applies(const qvh_flat* f, uint32_t k, uint64_t admitted) {
+  return shared_list_length(k) != 0 && f->dp <= kMaxChunkedDp && admitted * f->dp * sizeof(float) <= kCompactMaxBytes;
+}
+
+/// A caller's list of admitted rows into the handle's copy, each row clamped below n (a row past
+/// the store reads the last stored row instead of memory past it).
+__global__ void clamp_rows_kernel(const uint32_t* __restrict__ src, uint64_t count, uint64_t n,
+                                  uint32_t* __restrict__ dst) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < count) {
+    const uint32_t r = src[i];
+    dst[i] = r < n ? r : static_cast<uint32_t>(n - 1);
+  }
+}
+
+__global__ void zero_words_kernel(uint64_t* __restrict__ p, uint64_t count) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < count) p[i] = 0;
+}
+
+/// Sets the bit of every listed row (below n, as clamp_rows_kernel leaves them) in a cleared bitmap.
+__global__ void rows_to_bitmap_kernel(const uint32_t* __restrict__ rows, uint64_t count, uint64_t* bits) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < count) {
+    const uint32_t r = rows[i];
+    atomicOr(reinterpret_cast<unsigned long long*>(bits + (r >> 6)), 1ull << (r & 63));
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -3324,8 +3355,7 @@ qvh_status qvh_flat_search(qvh_flat* f, const float* queries, uint64_t nq, uint3
       // run in proportion to their count, 45% in 10.3 ms).
       if (admitted == f->n) {
         row_bitmap = nullptr;
-      } else if (shared_list_length(k) != 0 && f->dp <= kMaxChunkedDp &&
-                 admitted * f->dp * sizeof(float) <= kCompactMaxBytes) {
+      } else if (listed_scan_applies(f, k, admitted)) {
         listed.reserve(admitted);
         for (size_t w = 0; w < words; ++w) {
           uint64_t bits = row_bitmap[w];
@@ -3391,6 +3421,49 @@ qvh_status qvh_flat_search_device(qvh_flat* f, const float* d_queries, uint64_t 
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : f->stream;
     on_handle_timeline(f->stream, f->join, s, [&](hipStream_t st) {
       flat_search_impl(f, d_queries, nq, k, d_row_bitmap, d_out_rows, d_out_dist, st);
+    });
+  });
+}
+
+qvh_status qvh_flat_search_device_rows(qvh_flat* f, const float* d_queries, uint64_t nq, uint32_t k,
+                                       const uint32_t* d_row_list, uint64_t nrows, uint32_t* d_out_rows,
+                                       float* d_out_dist, void* stream) {
+  return guarded([&] {
+    QVH_REQUIRE(f != nullptr, "qvh_flat_search_device_rows: null handle");
+    if (nq == 0 || k == 0) return;
+    QVH_REQUIRE(d_queries && d_out_rows && d_out_dist, "qvh_flat_search_device_rows: null buffer");
+    QVH_REQUIRE(d_row_list != nullptr || nrows == 0, "qvh_flat_search_device_rows: null row list");
+    std::lock_guard<std::mutex> lock(f->mu);
+    QVH_REQUIRE(nrows <= f->n, "qvh_flat_search_device_rows: " + std::to_string(nrows) + " listed rows but " +
+                                   std::to_string(f->n) + " stored");
+    QVH_HIP(hipSetDevice(f->device));
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : f->stream;
+    on_handle_timeline(f->stream, f->join, s, [&](hipStream_t st) {
+      if (nrows == f->n) {  // every stored row listed: no filter
+        flat_search_impl(f, d_queries, nq, k, nullptr, d_out_rows, d_out_dist, st);
+        return;
+      }
+      uint32_t* li = static_cast<uint32_t*>(f->w_idx.reserve(std::max<uint64_t>(nrows, 1) * sizeof(uint32_t)));
+      if (nrows > 0) {
+        hipLaunchKernelGGL(clamp_rows_kernel, dim3(static_cast<unsigned>(ceil_div(nrows, 256))), dim3(256), 0, st,
+                           d_row_list, nrows, f->n, li);
+        QVH_HIP(hipGetLastError());
+      }
+      if (listed_scan_applies(f, k, nrows)) {
+        flat_search_impl(f, d_queries, nq, k, nullptr, d_out_rows, d_out_dist, st, li, nrows);
+        return;
+      }
+      // The scan over every row with the list as a bitmap.
+      const uint64_t words = ceil_div(std::max<uint64_t>(f->n, 1), 64);
+      uint64_t* b = static_cast<uint64_t*>(f->w_bits.reserve(words * sizeof(uint64_t)));
+      hipLaunchKernelGGL(zero_words_kernel, dim3(static_cast<unsigned>(ceil_div(words, 256))), dim3(256), 0, st, b,
+                         words);
+      if (nrows > 0) {
+        hipLaunchKernelGGL(rows_to_bitmap_kernel, dim3(static_cast<unsigned>(ceil_div(nrows, 256))), dim3(256), 0, st,
+                           li, nrows, b);
+      }
+      QVH_HIP(hipGetLastError());
+      flat_search_impl(f, d_queries, nq, k, b, d_out_rows, d_out_dist, st);
     });
   });
 }

@@ -63,6 +63,11 @@ class FlatIndex {
   void search_batch_device(const float* d_queries, std::size_t nq, std::size_t k,
                            const std::uint64_t* d_row_bitmap, std::uint32_t* d_rows,
                            float* d_distances, void* stream = nullptr) const;
+  /// search_batch_device with the admitted rows as a device list (ascending, no repeats, each
+  /// below size()) instead of a bitmap: the scan reads only the listed rows.
+  void search_batch_device_rows(const float* d_queries, std::size_t nq, std::size_t k,
+                                const std::uint32_t* d_row_list, std::size_t nrows, std::uint32_t* d_rows,
+                                float* d_distances, void* stream = nullptr) const;
   /// The filter as bits over rows (bit i = labels()[i] admitted), as search_batch builds it.
   std::vector<std::uint64_t> row_bitmap(const Filter& filter) const;
   /// Labels by row.

@@ -136,6 +136,20 @@ void FlatIndex::search_batch_device(const float* d_queries, std::size_t nq, std:
             "FlatIndex::search_batch_device");
 }
 
+void FlatIndex::search_batch_device_rows(const float* d_queries, std::size_t nq, std::size_t k,
+                                         const std::uint32_t* d_row_list, std::size_t nrows, std::uint32_t* d_rows,
+                                         float* d_distances, void* stream) const {
+  if (nq == 0 || k == 0) return;
+  QUIVER_CHECK(d_queries != nullptr && d_rows != nullptr && d_distances != nullptr,
+               "search_batch_device_rows: null buffer");
+  QUIVER_CHECK(k <= 0xFFFFFFFFull, "k is too large");
+  std::shared_lock lock(*mu_);
+  QUIVER_CHECK(dev_ != nullptr && !labels_.empty(), "search_batch_device_rows: the index is empty");
+  qvh_check(qvh_flat_search_device_rows(dev_.get(), d_queries, nq, static_cast<std::uint32_t>(k), d_row_list, nrows,
+                                        d_rows, d_distances, stream),
+            "FlatIndex::search_batch_device_rows");
+}
+
 std::vector<std::uint64_t> FlatIndex::row_bitmap(const Filter& filter) const {
   std::shared_lock lock(*mu_);
   return internal::filter_bitmap(filter, labels_.size(), [&](std::size_t i) { return labels_[i]; },

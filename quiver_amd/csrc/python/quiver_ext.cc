@@ -206,6 +206,18 @@ PYBIND11_MODULE(_quiver, m) {
           },
           py::arg("queries"), py::arg("nq"), py::arg("k"), py::arg("bitmap"), py::arg("rows"), py::arg("distances"),
           py::arg("stream"))
+      .def(
+          "_search_device_rows",
+          [](const quiver::FlatIndex& self, std::uintptr_t q, std::size_t nq, std::size_t k, std::uintptr_t row_list,
+             std::size_t nrows, std::uintptr_t rows, std::uintptr_t dist, std::uintptr_t stream) {
+            py::gil_scoped_release release;
+            self.search_batch_device_rows(reinterpret_cast<const float*>(q), nq, k,
+                                          reinterpret_cast<const std::uint32_t*>(row_list), nrows,
+                                          reinterpret_cast<std::uint32_t*>(rows), reinterpret_cast<float*>(dist),
+                                          reinterpret_cast<void*>(stream));
+          },
+          py::arg("queries"), py::arg("nq"), py::arg("k"), py::arg("row_list"), py::arg("nrows"), py::arg("rows"),
+          py::arg("distances"), py::arg("stream"))
       .def("_row_bitmap",
            [](const quiver::FlatIndex& self, const LabelArray& allowed) {
              const auto filter = allowed_filter(allowed);

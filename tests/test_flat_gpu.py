@@ -25,10 +25,10 @@ def _true_dist(oracle, stored, queries, metric):
     return f
 
 
-def _bitmap_form_matches_listed_rows(idx, queries, k, allowed):
-    """The same filtered search through device buffers (the filter as a device bitmap tested in the
-    scan) and through host buffers (the admitted rows listed and copied): identical rows and
-    bit-identical distances."""
+def _device_path_matches_host_path(idx, queries, k, allowed):
+    """The same filtered search with torch device queries (the admitted rows as a device list) and
+    with host queries (the rows listed on the host): identical rows and bit-identical distances.
+    The device bitmap form is compared with both in test_device_filters_gpu.py."""
     import torch
 
     hl, hd = idx.search(queries, k, filter=allowed)
@@ -76,9 +76,9 @@ def test_integer_stores_short_lists(oracle, metric, k):
     """On a store of small integers, a batch of small-integer queries has exact GEMM-form distances
     and scans with 10-entry lane lists for k <= 10 (no margin, nothing to certify: no fallback); a
     batch holding any real-valued query takes the 16-entry lists with the margin instead (the
-    device picks between the two launches). Integer, real-valued and mixed batches, and the
-    listed-row and bitmap forms of the filtered scan, against the oracle, with ties (integer data
-    has many) resolved by row."""
+    device picks between the two launches). Integer, real-valued and mixed batches, and filtered
+    searches through host and device buffers, against the oracle, with ties (integer data has many)
+    resolved by row."""
     base, q_int = D.int_mix(40_000, 150)
     q_real = q_int[:100] + np.random.default_rng(3).standard_normal((100, base.shape[1])).astype(np.float32) * 0.37
     q_mixed = np.concatenate([q_int[100:], q_real[:3]])
@@ -99,21 +99,20 @@ def test_integer_stores_short_lists(oracle, metric, k):
     for n_allowed in (4_000, 24_000):
         allowed = np.sort(rng.choice(40_000, n_allowed, replace=False)).astype(np.uint64)
         print(_check(oracle, base, q_int, k, metric, allowed))
-        _bitmap_form_matches_listed_rows(idx, q_int, k, allowed)
+        _device_path_matches_host_path(idx, q_int, k, allowed)
 
 
 @pytest.mark.parametrize("fraction", [0.005, 0.3, 0.49, 0.7, 0.97, 1.0])
 @pytest.mark.parametrize("metric", ["l2", "cosine"])
 def test_filter_densities(oracle, fraction, metric):
-    """Through host buffers a filter runs over the list of admitted rows at any density (a filter
-    admitting every row runs as no filter); with device buffers over all rows with the bitmap tested
-    per tile. Both give the oracle's answer."""
+    """A filter runs over the list of admitted rows at any density, through host and device buffers
+    alike (a filter admitting every row runs as no filter). Both give the oracle's answer."""
     base, q = D.unit_mix(30_000, 50)
     allowed = D.allowed_ids(base.shape[0], fraction, seed=17)
     print(_check(oracle, base, q, 10, metric, allowed))
     idx = quiver.FlatIndex(base.shape[1], metric)
     idx.add(base)
-    _bitmap_form_matches_listed_rows(idx, q, 10, allowed)
+    _device_path_matches_host_path(idx, q, 10, allowed)
 
 
 def test_cosine_rows_are_normalized_like_the_reference(oracle):
@@ -336,7 +335,7 @@ def test_ring_scan_integer_store(oracle, metric):
 @pytest.mark.parametrize("fraction", [0.6, 0.95])
 def test_small_batches_split_rows_filtered_and_ties(oracle, fraction, metric):
     """Integer data (many exactly equal distances across splits) with a row filter above half
-    density: the listed rows through host buffers, the bitmap tested per row with device buffers."""
+    density, through host and device buffers."""
     base, q = D.int_mix(300_000, 12)
     allowed = D.allowed_ids(base.shape[0], fraction, seed=41)
     print(_check(oracle, base, q[:4], 10, metric, allowed))
@@ -345,7 +344,7 @@ def test_small_batches_split_rows_filtered_and_ties(oracle, fraction, metric):
     idx = quiver.FlatIndex(base.shape[1], metric)
     idx.add(base)
     for qs in (q[:4], q):
-        _bitmap_form_matches_listed_rows(idx, qs, 10, allowed)
+        _device_path_matches_host_path(idx, qs, 10, allowed)
 
 
 def test_integer_data_exact_ties(oracle):
