@@ -865,7 +865,8 @@ __global__ void __launch_bounds__(256) probe_select_any_kernel(const float* __re
 
 // ---- search: coarse scores on the matrix unit ----------------------------------------------------
 //
-// Batches of at least kCgMinQueries queries score the centroids on the matrix unit: g_c =
+// Batches of at least kCgMinQueries queries (kCgMinQueriesWide above 32 probes) score the
+// centroids on the matrix unit: g_c =
 // ||c||^2 - 2<q,c> for L2 (the query enters scaled by -2, exact, and one more MFMA step adds the
 // augmented column ||c||^2 of the assignment operand) or -<q,c> for inner product and cosine. g
 // differs from the reference's in-order sum e_c (src/internal/centroid_table.h:65-85) by the
@@ -886,7 +887,12 @@ constexpr uint32_t kCgTileC = 128;        // centroids per work-group tile (64 p
 constexpr uint32_t kCgKC = 32;            // dims per LDS chunk
 constexpr int kCgPitch = kCgKC + 4;       // LDS row pitch in floats: conflict-free 16-byte reads
 constexpr int kCgOutPitch = 64 + 4;       // the epilogue's per-wave block of 32 queries x 64 centroids
-constexpr uint64_t kCgMinQueries = 1024;  // smaller batches: coarse_kernel
+// Smallest batches scored on the matrix unit (smaller ones: coarse_kernel); the matrix path costs a
+// nearly fixed 34-39 us at nprobe <= 32 and 45 us at 64, the in-order kernel grows with the batch
+// (1M x 128, 2048 lists, select stage: 200 queries 42.4 -> 34.4 us, 1,000 queries 52.5 -> 35.1 us
+// at nprobe 8; 100 queries 35.9 vs 38.6 us at nprobe 32; 300 queries 44.6 vs 45.3 us at nprobe 64).
+constexpr uint64_t kCgMinQueries = 192;
+constexpr uint64_t kCgMinQueriesWide = 512;  // nprobe above 32
 constexpr uint32_t kCgMaxProbes = 64;
 constexpr uint32_t kCgMaxLists = 64 * 32;
 constexpr int kBandCap = 128;             // band members re-scored and sorted in registers
@@ -3015,7 +3021,8 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   const bool ordered = nq > 1 && nq <= 65536 && h->nlist <= 32768 && mode != kModeResidual && h->mp <= kStreamMaxM &&
                        nprobe <= kStreamMaxProbes;
   uint32_t* min_probe = ordered ? static_cast<uint32_t*>(h->w_key.reserve(nq * sizeof(uint32_t))) : nullptr;
-  const bool mfma_coarse = h->asg.ready && h->asg.dim == h->dim && nq >= kCgMinQueries && nq < 0xFFFFFFFFull &&
+  const uint64_t cg_min = nprobe > 32 ? kCgMinQueriesWide : kCgMinQueries;
+  const bool mfma_coarse = h->asg.ready && h->asg.dim == h->dim && nq >= cg_min && nq < 0xFFFFFFFFull &&
                            nprobe <= kCgMaxProbes && h->nlist <= kCgMaxLists;
   if (mfma_coarse) {
     const bool ip = h->metric != QVH_METRIC_L2;
