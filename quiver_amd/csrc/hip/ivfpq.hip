@@ -2909,6 +2909,9 @@ struct qvh_ivfpq {
   DeviceBuffer w_q, w_scores, w_probes, w_bits, w_refs, w_dist, w_bytes, w_key, w_order, w_lut, w_cand;
   DeviceBuffer w_pkeys, w_pcnt, w_pdone;  // sliced queries of the streaming scan
   DeviceBuffer w_delta, w_fb;             // certificate bounds; uncertified queries (count, list)
+  // A filtered search's admitted codes as a store of their own: per-list counts, offsets, the
+  // original position of each, and their codes, t1 terms and stored vectors.
+  DeviceBuffer w_fcnt, w_foff, w_fpos, w_fcodes, w_ft1, w_fvec;
   bool last_certified = false;            // the last search ranked approximately (w_fb holds its count)
   int cus = 0;                             // compute units of the device
   int timing = 0;               // 0 off, 1 stage events, 2 events and probed code bytes
@@ -2966,6 +2969,99 @@ void ivf_encode_device(const qvh_ivfpq* h, EncodeSpace& es, const float* d_x, ui
 
 void ivf_check_trained(const qvh_ivfpq* h) {
   if (!h->trained) throw Failure(QVH_EINVAL, "IVF-PQ index must be trained before add()");
+}
+
+/// Admitted positions of list l (bit p % 64 of word p / 64 of the position bitmap), counted by one
+/// wave per list.
+__global__ void __launch_bounds__(256) filter_count_kernel(const uint64_t* __restrict__ off, uint32_t nlist,
+                                                           const uint64_t* __restrict__ bits, uint32_t* __restrict__ cnt) {
+  const uint32_t l = blockIdx.x * 4 + threadIdx.x / 64;
+  const int lane = threadIdx.x & 63;
+  if (l >= nlist) return;
+  uint32_t c = 0;
+  for (uint64_t p = off[l] + lane; p < off[l + 1]; p += 64) c += static_cast<uint32_t>((bits[p >> 6] >> (p & 63)) & 1ull);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o, 64);
+  if (lane == 0) cnt[l] = c;
+}
+
+/// off_f[l] = sum of cnt[0, l) for l <= nlist (one block of 1024 threads, each a contiguous chunk).
+__global__ void __launch_bounds__(1024) filter_offsets_kernel(const uint32_t* __restrict__ cnt, uint32_t nlist,
+                                                              uint64_t* __restrict__ off_f) {
+  __shared__ uint64_t s_sum[1024];
+  const uint32_t t = threadIdx.x;
+  const uint32_t chunk = (nlist + 1023) / 1024;
+  const uint32_t b = min(nlist, t * chunk), e = min(nlist, b + chunk);
+  uint64_t own = 0;
+  for (uint32_t i = b; i < e; ++i) own += cnt[i];
+  s_sum[t] = own;
+  __syncthreads();
+  for (uint32_t d = 1; d < 1024; d <<= 1) {  // inclusive scan
+    const uint64_t v = t >= d ? s_sum[t - d] : 0;
+    __syncthreads();
+    s_sum[t] += v;
+    __syncthreads();
+  }
+  uint64_t run = s_sum[t] - own;
+  for (uint32_t i = b; i < e; ++i) {
+    off_f[i] = run;
+    run += cnt[i];
+  }
+  if (t == 1023) off_f[nlist] = s_sum[1023];
+}
+
+struct FilterGatherArgs {
+  const uint64_t* off;     // [nlist + 1] the store's list offsets
+  const uint64_t* bits;    // position bitmap
+  const uint64_t* off_f;   // [nlist + 1] the admitted codes' offsets
+  uint32_t nlist;
+  uint32_t mw;             // code dwords (mp / 4)
+  uint32_t dim;
+  const uint32_t* codes;   // [count][mw]
+  const float* t1;         // [count] or null
+  const float* vec;        // [count][dim] or null
+  uint32_t* pos;           // [admitted] original positions
+  uint32_t* codes_f;       // [admitted][mw]
+  float* t1_f;             // [admitted] or null
+  float* vec_f;            // [admitted][dim] or null
+};
+
+/// The admitted codes of list l, in position order, into the compact store (one wave per list).
+__global__ void __launch_bounds__(256) filter_gather_kernel(FilterGatherArgs g) {
+  const uint32_t l = blockIdx.x * 4 + threadIdx.x / 64;
+  const int lane = threadIdx.x & 63;
+  if (l >= g.nlist) return;
+  uint64_t dst = g.off_f[l];
+  const uint64_t end = g.off[l + 1];
+  for (uint64_t base = g.off[l]; base < end; base += 64) {
+    const uint64_t p = base + static_cast<uint64_t>(lane);
+    const bool in = p < end && ((g.bits[p >> 6] >> (p & 63)) & 1ull);
+    const uint64_t mask = __ballot(in);
+    if (in) {
+      const uint64_t d = dst + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                         __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+      g.pos[d] = static_cast<uint32_t>(p);
+      for (uint32_t w = 0; w < g.mw; ++w) g.codes_f[d * g.mw + w] = g.codes[p * g.mw + w];
+      if (g.t1_f) g.t1_f[d] = g.t1[p];
+      if (g.vec_f) {
+        for (uint32_t j = 0; j < g.dim; ++j) g.vec_f[d * g.dim + j] = g.vec[p * g.dim + j];
+      }
+    }
+    dst += static_cast<uint64_t>(__popcll(mask));
+  }
+}
+
+/// Refs over the compact store ((list << 32) | rank among the list's admitted codes) back to the
+/// store's ((list << 32) | offset in the list).
+__global__ void filter_remap_kernel(uint64_t* __restrict__ refs, uint64_t total, const uint64_t* __restrict__ off,
+                                    const uint64_t* __restrict__ off_f, const uint32_t* __restrict__ pos) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const uint64_t ref = refs[i];
+  if (ref == QVH_EMPTY_REF) return;
+  const uint64_t l = ref >> 32;
+  const uint64_t orig = pos[off_f[l] + (ref & 0xFFFFFFFFull)];
+  refs[i] = (l << 32) | (orig - off[l]);
 }
 
 void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k, uint32_t nprobe_req,
@@ -3123,6 +3219,46 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   }
   h->last_certified = certify;
   QVH_HIP(hipGetLastError());
+  // A filter: the admitted codes (and t1 terms and stored vectors) become a store of their own,
+  // which the scans read like an unfiltered one, so their work follows the admitted count as the
+  // reference's skip of filtered labels does (src/ivfpq_index.cc:349); the refs they write are
+  // mapped back to the store's afterwards. Buffers are sized for every stored code (no count read
+  // back), and grow once.
+  const uint64_t* off_use = h->off.as<uint64_t>();
+  const uint8_t* codes_use = h->codes.as<uint8_t>();
+  const float* t1_use = h->t1.as<float>();
+  const float* vec_use = h->vec.as<float>();
+  uint64_t* off_f = nullptr;
+  uint32_t* fpos = nullptr;
+  if (d_bitmap != nullptr && count > 0) {
+    const uint32_t nl = h->nlist;
+    uint32_t* fcnt = static_cast<uint32_t*>(h->w_fcnt.reserve(nl * sizeof(uint32_t)));
+    off_f = static_cast<uint64_t*>(h->w_foff.reserve((nl + 1) * sizeof(uint64_t)));
+    fpos = static_cast<uint32_t*>(h->w_fpos.reserve(count * sizeof(uint32_t)));
+    FilterGatherArgs g{};
+    g.off = off_use;
+    g.bits = d_bitmap;
+    g.off_f = off_f;
+    g.nlist = nl;
+    g.mw = h->mp / 4;
+    g.dim = h->dim;
+    g.codes = reinterpret_cast<const uint32_t*>(codes_use);
+    g.t1 = h->has_pre ? t1_use : nullptr;
+    g.vec = h->store_vectors ? vec_use : nullptr;
+    g.pos = fpos;
+    g.codes_f = static_cast<uint32_t*>(h->w_fcodes.reserve(count * h->mp));
+    g.t1_f = g.t1 ? static_cast<float*>(h->w_ft1.reserve(count * sizeof(float))) : nullptr;
+    g.vec_f = g.vec ? static_cast<float*>(h->w_fvec.reserve(count * h->dim * sizeof(float))) : nullptr;
+    const dim3 wave_grid(static_cast<unsigned>(ceil_div(nl, 4)));
+    hipLaunchKernelGGL(filter_count_kernel, wave_grid, dim3(256), 0, s, off_use, nl, d_bitmap, fcnt);
+    hipLaunchKernelGGL(filter_offsets_kernel, dim3(1), dim3(1024), 0, s, fcnt, nl, off_f);
+    hipLaunchKernelGGL(filter_gather_kernel, wave_grid, dim3(256), 0, s, g);
+    QVH_HIP(hipGetLastError());
+    off_use = off_f;
+    codes_use = reinterpret_cast<const uint8_t*>(g.codes_f);
+    t1_use = g.t1_f;
+    vec_use = g.vec_f;
+  }
   if (h->timed) QVH_HIP(hipEventRecord(h->ev[1], s));
   ScanArgs a{};
   a.delta = delta;
@@ -3140,15 +3276,15 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
   a.Q = dq;
   a.scores = scores;
   a.probes = probes;
-  a.off = h->off.as<uint64_t>();
-  a.codes = h->codes.as<uint8_t>();
-  a.t1 = h->t1.as<float>();
+  a.off = off_use;
+  a.codes = codes_use;
+  a.t1 = t1_use;
   a.pre = h->pre.as<float>();
   a.cbt = h->cbt.as<float>();
   a.cbc = h->cbc.as<float>();
   a.cent = h->cent.as<float>();
-  a.vec = h->vec.as<float>();
-  a.bitmap = d_bitmap;
+  a.vec = vec_use;
+  a.bitmap = off_f != nullptr ? nullptr : d_bitmap;
   a.keep = static_cast<uint32_t>(keep);
   a.keep_sel = static_cast<uint32_t>(keep_sel);
   a.refine = refine && !exact_all ? 1 : 0;
@@ -3325,6 +3461,11 @@ void ivf_search_impl(qvh_ivfpq* h, const float* d_q_raw, uint64_t nq, uint32_t k
     fa.qcount = fb;
     launch_block_scan(fa, dim3(static_cast<unsigned>(bounded_grid ? block_grid
                                                                   : std::min<uint64_t>(nq, 2 * static_cast<uint64_t>(std::max(h->cus, 1))))));
+    QVH_HIP(hipGetLastError());
+  }
+  if (off_f != nullptr) {
+    hipLaunchKernelGGL(filter_remap_kernel, dim3(static_cast<unsigned>(ceil_div(nq * k, 256))), dim3(256), 0, s, d_refs,
+                       nq * k, h->off.as<uint64_t>(), off_f, fpos);
     QVH_HIP(hipGetLastError());
   }
   if (h->timed_bytes) {

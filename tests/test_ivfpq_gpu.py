@@ -320,6 +320,23 @@ def test_ivfpq_filter_matches_oracle(oracle):
         print(frac, compare_search(oracle, idx, st, q, 10, 32, 2, allowed))
 
 
+@pytest.mark.parametrize("metric,refine", [("l2", 0), ("l2", 4), ("ip", 0), ("cosine", 3)])
+def test_ivfpq_filtered_codes_as_their_own_store(oracle, metric, refine):
+    """A filtered search scans the admitted codes gathered into a store of their own (per-list
+    counts, offsets, codes, t1 terms and stored vectors) and maps the refs back: the oracle's
+    answer at densities from no admitted code to every code, for a batch of whole queries, a sliced
+    small batch, k = 10 and k = 100, and nprobe 1 and 16 (lists with no admitted code included)."""
+    base = clustered(12_000, 32, 24, seed=47)
+    q = clustered(300, 32, 24, seed=48)
+    idx, st = build_pair(oracle, base, metric, 64, 8, refine > 0)
+    rng = np.random.default_rng(2)
+    for frac in (0.0, 0.002, 0.05, 0.6, 1.0):
+        n_allowed = int(round(12_000 * frac))
+        allowed = np.sort(rng.choice(12_000, n_allowed, replace=False)).astype(np.uint64)
+        for qs, k, nprobe in ((q, 10, 16), (q[:3], 10, 16), (q, 100, 16), (q, 10, 1)):
+            print(frac, qs.shape[0], k, nprobe, compare_search(oracle, idx, st, qs, k, nprobe, refine, allowed))
+
+
 def test_ivfpq_without_precomputed_table(oracle):
     """nlist * m * 256 floats above 256 MiB: per-list residual tables (src/ivfpq_index.cc:338-342)."""
     base = clustered(8_400, 32, 40, 10)
