@@ -67,6 +67,10 @@ struct ScanArgs {
   uint32_t dp;              // row width (the chunked scan; the register scan has it as DP)
   int rowsplit;             // register scan, unfiltered, at most 128 queries: two waves per query group
   int bound_slots;          // register scan: publish and read the per-query bound slots
+  // Register scan with 32-entry lists for k above 21 (the wide merge takes R = k + max(16, k / 2)
+  // keys): when nonzero, c = ceil(R / 2) <= 32, and the shared bound is the larger of the lane
+  // pair's c-th entries (2c >= R rows of the pair lie at or below it, so it bounds the R-th best).
+  uint32_t share_rank;
   // Launch gate: when set, the launch does nothing unless (*gate != 0) == (gate_want != 0), read
   // once at the start. Two list lengths are launched back to back and the device picks one.
   const uint32_t* gate;
@@ -432,6 +436,14 @@ __global__ void __launch_bounds__(kThreads) flat_scan_kernel(ScanArgs a) {
     const float own_k = Ld[KL - 1], own_h = Ld[KL / 2 - 1];
     const float oth_k = __shfl_xor(own_k, 32, 64), oth_h = __shfl_xor(own_h, 32, 64);
     float t = fminf(fminf(own_k, oth_k), fmaxf(own_h, oth_h));
+    if (a.share_rank != 0) {
+      // k above KL (the wide merge): the pair's union has 2c >= R rows at or below the larger of
+      // the two lanes' c-th entries.
+      float own_c = Ld[0];
+#pragma unroll
+      for (int x = 1; x < KL; ++x) own_c = static_cast<uint32_t>(x) + 1 == a.share_rank ? Ld[x] : own_c;
+      t = fmaxf(own_c, __shfl_xor(own_c, 32, 64));
+    }
     if (qvalid) {
       uint32_t g = 0;
       if (h == 0) g = atomicMin(qw, float_to_ordered(t));
@@ -3056,12 +3068,16 @@ void flat_search_run(qvh_flat* f, const FlatPlan& p, const FlatBuffers& b, const
   a.part_d = b.pd;
   a.part_r = b.pr;
   a.qthr = b.thr;
-  a.share = p.wide ? 0 : 1;
+  // The wide merge's R = k + max(16, k / 2) keys: up to R = 64 the register scan shares a bound of
+  // rank ceil(R / 2) (1M x 128 integer mixture, 10k queries, k = 32: 28.9 ms with no shared bound).
+  const uint32_t wide_sel = k + std::max<uint32_t>(16, k / 2);
+  a.share_rank = p.wide && wide_sel <= 64 && f->dp <= static_cast<uint32_t>(kMaxDp) ? (wide_sel + 1) / 2 : 0;
+  a.share = !p.wide || a.share_rank != 0 ? 1 : 0;
   a.dp = f->dp;
   // One query block of at most 128 queries, unfiltered, register-resident queries: the row-split
   // form of the scan (two waves per 32-query group).
   a.rowsplit = nq <= static_cast<uint64_t>(kQueriesPerBlock / 2) && !d_idx && !d_bitmap && f->dp <= kMaxDp ? 1 : 0;
-  a.bound_slots = !a.rowsplit || p.nsplit <= kScanSlotMaxSplits ? 1 : 0;
+  a.bound_slots = !p.wide && (!a.rowsplit || p.nsplit <= kScanSlotMaxSplits) ? 1 : 0;
   const dim3 sgrid(static_cast<unsigned>(p.qblocks * p.nsplit));
   auto scan = [&](int kl) {
     if (p.ring) {

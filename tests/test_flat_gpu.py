@@ -287,6 +287,21 @@ def test_small_batches_on_256_row_splits(oracle, metric, nq):
     print(_check(oracle, ib, iq, 10, metric))
 
 
+@pytest.mark.parametrize("metric", ["l2", "ip", "cosine"])
+@pytest.mark.parametrize("k", [22, 32, 43, 44])
+def test_wide_k_shared_bound(oracle, metric, k):
+    """k from 22 to 43 (the wide merge's k + max(16, k / 2) keys at most 64): the register scan's
+    32-entry lane lists share a bound of rank ceil(R / 2) across the lane pair and the row splits;
+    k = 44 keeps no shared bound. Real-valued and integer data (exact ties across splits), a full
+    query block and a partial one, against the oracle."""
+    base = D.gaussian(300_000, 96, seed=71)
+    q = D.gaussian(300, 96, seed=72)
+    print(_check(oracle, base, q, k, metric))
+    if metric == "l2":
+        ib, iq = D.int_mix(300_000, 300)
+        print(_check(oracle, ib, iq, k, metric))
+
+
 @pytest.mark.parametrize("metric", ["l2", "cosine"])
 @pytest.mark.parametrize("nq", [384, 768, 1280, 1792])
 def test_mid_batches_whole_round_splits(oracle, metric, nq):
